@@ -1,0 +1,222 @@
+"""Benchmark of the fused fwd+bwd Naju scan on one MI355X.
+
+A step is one forward (naju_scan_fwd) plus one backward (naju_scan_bwd) of the
+scan over one batch of synthetic input resident in HBM, through the C ABI on
+preallocated buffers (the hot path itself, no autograd bookkeeping). The
+default workload is BASELINE configuration 2: B=8, L=4096, D=1024, bf16
+streams with fp32 state, N=1 (B=C=1), h0 ~ N(0, 0.1^2), dy ~ N(0,1).
+
+value = algorithmic bytes of fwd+bwd per step * K / wall time of K steps
+(GB/s). The roofline object reports the dominant kernel (the backward) from
+HIP events recorded on the launch stream inside the timed region. The
+cpu_baseline leg times the sequential torch-CPU restatement of the
+reference's scan (oracle/scan_ref.py: scan_loop_torch, the algorithm of
+reference naju/scan.py:79-93) with autograd on a bounded sample of the same
+workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--N 1]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+_ROOT = os.path.dirname(os.path.abspath(__file__))
+if _ROOT not in sys.path:
+    sys.path.insert(0, _ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "fwd+bwd scan GB/s (% of HBM peak) at B8 L4096 D1024; LM tokens/s"
+
+
+def _dt_size(dt):
+    import torch
+    return 4 if dt == torch.float32 else 2
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--flush", action="store_true",
+                    help="also time steps with a 1 GiB cache-flush write before each step")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
+              "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+
+    import ctypes
+    import torch
+    from naju_amd import _lib
+    from naju_amd.workloads import CONFIGS, algorithmic_bytes, config_inputs
+
+    L = _lib.lib()
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    Bsz, T, D, N = cfg["batch"], cfg["T"], cfg["D"], args.N
+    ins = config_inputs(args.config, N=N, seed=0, device=dev)
+    xdt = ins["u"].dtype
+    DT = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+    dts = (DT[xdt], DT[ins["f_logit"].dtype], DT[ins["B"].dtype])
+    u, fl, il, Bm, Cm, Dk, h0, dy = (ins[k] for k in ("u", "f_logit", "i_logit", "B", "C", "D_skip", "h0", "dy"))
+    y = torch.empty_like(u)
+    ck = torch.empty(L.naju_scan_ckpt_elems(Bsz, T, D, N, *dts), dtype=torch.float32, device=dev)
+    du, dfl, dil = torch.empty_like(u), torch.empty_like(fl), torch.empty_like(il)
+    dB, dC = torch.empty_like(Bm), torch.empty_like(Cm)
+    dD = torch.empty(D, dtype=torch.float32, device=dev)
+    dh0 = torch.empty_like(h0) if h0 is not None else None
+    ws_bytes = L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    def fwd():
+        _lib.check(L.naju_scan_fwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(h0), p(y), p(ck), None,
+                                   Bsz, T, D, N, *dts, p(ws), ws_bytes, sh))
+
+    def bwd():
+        _lib.check(L.naju_scan_bwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(ck), p(dy), p(du), p(dfl),
+                                   p(dil), p(dB), p(dC), p(dD), p(dh0), Bsz, T, D, N, *dts, p(ws), ws_bytes,
+                                   sh))
+
+    s_x, s_g, s_bc = _dt_size(xdt), _dt_size(fl.dtype), _dt_size(Bm.dtype)
+    has_h0 = h0 is not None
+    bytes_fwd = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=True, bwd=False)
+    bytes_bwd = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=False, bwd=True)
+    bytes_step = bytes_fwd + bytes_bwd
+
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(K):
+        ev[k][0].record(stream)
+        fwd()
+        ev[k][1].record(stream)
+        bwd()
+        ev[k][2].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / K
+    t_fwd = sorted(e[0].elapsed_time(e[1]) for e in ev)
+    t_bwd = sorted(e[1].elapsed_time(e[2]) for e in ev)
+    avg_fwd = sum(t_fwd) / K
+    avg_bwd = sum(t_bwd) / K
+    med = lambda xs: xs[len(xs) // 2]  # noqa: E731
+
+    st = ctypes.c_uint32(0)
+    _lib.check(L.naju_scan_workspace_status(p(ws), sh, ctypes.byref(st)))
+    if st.value != 0:
+        raise RuntimeError("workspace status nonzero: a carry hand-off timed out")
+
+    value = bytes_step / (ms_step * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[xdt]
+        + " streams, f32 state/accum",
+        "data": "synthetic (seeded; BASELINE.json config recipe)",
+        "config": {"workload": f"naju scan fwd+bwd {args.config}: B={Bsz} L={T} D={D} N={N}"
+                   + (" B=C=1" if N == 1 else " B,C~N(0,1/N)") + (" with h0" if has_h0 else ""),
+                   "batch": Bsz, "seq_len": T, "channels": D, "d_state": N,
+                   "parallelism": "single GPU", "cache_flush": False},
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "elements_per_s": round(Bsz * T * D / (ms_step * 1e-3), 1),
+        "algorithmic_bytes_per_step": bytes_step,
+        "fwd_ms_avg": round(avg_fwd, 5), "fwd_ms_median": round(med(t_fwd), 5),
+        "bwd_ms_avg": round(avg_bwd, 5), "bwd_ms_median": round(med(t_bwd), 5),
+        "fwd_GBs": round(bytes_fwd / (avg_fwd * 1e-3) / 1e9, 1),
+        "roofline": {
+            "kernel": "n1_bwd_kernel (+ fold_partials_kernel, same call)" if N == 1 else "bwd",
+            "bound": "hbm",
+            "achieved": round(bytes_bwd / (avg_bwd * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(bytes_bwd / (avg_bwd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": _traffic(args.config, N),
+        },
+    }
+    if args.flush:
+        scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        tf = []
+        for k in range(min(K, 20)):
+            scratch.fill_(k & 0xFF)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fwd()
+            bwd()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            tf.append(e0.elapsed_time(e1))
+        tf.sort()
+        out["flushed_ms_median"] = round(med(tf), 5)
+        out["flushed_GBs"] = round(bytes_step / (med(tf) * 1e-3) / 1e9, 1)
+        del scratch
+    out["cpu_baseline"] = None if args.no_cpu else _cpu_baseline(args.config, N)
+    print(json.dumps(out), flush=True)
+
+
+def _traffic(config, N):
+    """HBM bytes per launch of the backward kernel, from the committed
+    rocprofv3 --pmc summary (profiles/traffic.json), or None."""
+    path = os.path.join(_ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(f"{config}_N{N}_bwd")
+    except (OSError, ValueError):
+        return None
+
+
+def _cpu_baseline(config, N):
+    """The reference's sequential scan algorithm (torch CPU, autograd) on a
+    bounded sample of the workload: all batch rows and channels, the first
+    T_s timesteps. GB/s with the same algorithmic-byte formula."""
+    import torch
+    from naju_amd.workloads import CONFIGS, algorithmic_bytes, make_inputs
+    from oracle.scan_ref import scan_loop_torch
+    cfg = CONFIGS[config]
+    Bsz, D = cfg["batch"], cfg["D"]
+    Ts = 1024 if config in ("c1", "c2") else 256
+    Ts = min(Ts, cfg["T"])
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    ins = make_inputs(Bsz, Ts, D, N=N, dtype=torch.float32, gate=cfg["gate"], h0_std=cfg["h0_std"], seed=0,
+                      device="cpu")
+    names = ("u", "f_logit", "i_logit", "B", "C", "D_skip")
+    xs = [ins[k].requires_grad_(True) for k in names]
+    h0 = ins["h0"].requires_grad_(True) if ins["h0"] is not None else None
+    t0 = time.perf_counter()
+    yv = scan_loop_torch(*xs, h0=h0)
+    yv.backward(ins["dy"])
+    dt = time.perf_counter() - t0
+    s = 4 if cfg["dtype"] == torch.float32 else 2
+    nbytes = algorithmic_bytes(Bsz, Ts, D, N, s, s, s, h0 is not None)
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "seconds": round(dt, 2),
+            "sample": f"{config} fwd+bwd, all {Bsz} batch rows x {D} channels, first {Ts} of {cfg['T']} "
+                      f"timesteps, N={N}; torch-CPU loop restating naju/scan.py:79-93 with autograd, fp32 "
+                      f"arithmetic; bytes counted at the workload's dtypes"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,120 @@
+/*
+ * naju_scan.h -- C ABI of the MI355X (gfx950) Naju gated state-space scan.
+ *
+ * Recurrence (per batch b, channel d, state n), the contract of
+ * /root/reference/naju/scan.py:3-19:
+ *   f_t = sigmoid(f_logit_t)          i_t = sigmoid(i_logit_t)
+ *   x_t[n] = f_t * x_{t-1}[n] + i_t * B_t[n] * u_t        x_{-1} = h0 (or 0)
+ *   y_t    = sum_n C_t[n] * x_t[n] + D_skip * u_t
+ *
+ * Tensor layouts (row-major, contiguous, last index fastest), scan.py:7-11:
+ *   u, f_logit, i_logit, y, dy, du, dfl, dil : [batch, T, D]
+ *   B, C, dB, dC                             : [batch, T, N]
+ *   D_skip, dD                               : [D]        (float32)
+ *   h0, hT, dh0                              : [batch, D, N] (float32)
+ *   ckpt                                     : naju_scan_ckpt_elems() floats
+ * All pointers are device pointers. Every call is asynchronous on `stream`
+ * (a hipStream_t; NULL = the default stream), allocates nothing and never
+ * synchronises the host.
+ *
+ * dtype codes: the u-stream dtype covers u, y, dy and du; the gate dtype
+ * covers f_logit, i_logit, dfl and dil; the bc dtype covers B, C, dB and dC.
+ * Supported: u in {F32, BF16, F16}; gate and bc each either F32 or equal to
+ * the u dtype. Arithmetic and the state are float32 throughout.
+ *
+ * Workspace: naju_scan_workspace_bytes() bytes of device memory that MUST be
+ * zero-filled once before its first use; every call leaves it reusable
+ * (its counters return to zero), so one zeroed workspace serves any number of
+ * stream-ordered calls. Calls that overlap in time (different streams) need
+ * different workspaces.
+ *
+ * Return codes: 0 on success, a negative NAJU_ERR_* otherwise, with a message
+ * in naju_scan_last_error() (thread-local). Argument checks run on the host,
+ * before any device work, so they are testable without a GPU.
+ */
+#ifndef NAJU_SCAN_H
+#define NAJU_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NAJU_DTYPE_F32 0
+#define NAJU_DTYPE_BF16 1
+#define NAJU_DTYPE_F16 2
+
+#define NAJU_OK 0
+#define NAJU_ERR_INVALID -1     /* bad pointer, shape or dtype code        */
+#define NAJU_ERR_UNSUPPORTED -2 /* valid request this build does not serve */
+#define NAJU_ERR_WORKSPACE -3   /* workspace missing or too small          */
+#define NAJU_ERR_LAUNCH -4      /* the HIP runtime rejected a launch       */
+
+/* Library version, (major << 16) | minor. */
+int naju_scan_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* naju_scan_last_error(void);
+
+/* Number of float32 values of the forward's state checkpoint, which the
+ * backward consumes. Depends only on the shape and the dtype codes. Replaces
+ * the ckpt tensor of reference naju/cuda/naju_cuda.cu:241-259 (there
+ * [B,D,ceil(T/32),N]). */
+int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N,
+                             int x_dtype, int gate_dtype, int bc_dtype);
+
+/* Bytes of workspace needed by naju_scan_fwd / naju_scan_bwd at this shape
+ * (the same figure serves both). */
+size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D,
+                                 int64_t N, int x_dtype, int gate_dtype,
+                                 int bc_dtype);
+
+/* Forward scan. Replaces the forward of every reference backend: the
+ * sequential loop of naju/scan.py:79-93, _ChunkScanTriton.forward
+ * (naju/chunk_triton.py:148-181), _AffineChunkScan.forward
+ * (naju/chunk_affine_triton.py:257-288) and naju_fwd / naju_fwd_chunked
+ * (naju/cuda/naju_cuda.cu:241-259, :211-238).
+ *   h0   : optional initial state (NULL = zeros, the reference behaviour)
+ *   y    : output, u dtype
+ *   ckpt : optional (NULL under no_grad); state checkpoint for the backward
+ *   hT   : optional final state x_{T-1}
+ */
+int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit,
+                  const void* B, const void* C, const float* D_skip,
+                  const float* h0, void* y, float* ckpt, float* hT,
+                  int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
+                  int gate_dtype, int bc_dtype, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* Fused backward scan. Replaces naju_bwd (naju/cuda/naju_cuda.cu:261-286),
+ * naju_chunk_backward (naju/chunk_bwd_triton.py:187-243) and the affine
+ * backward (naju/chunk_affine_triton.py:290-342): one reverse pass yields
+ *   du, dfl, dil [batch,T,D]  (gradients of u, f_logit, i_logit)
+ *   dB, dC       [batch,T,N]  (reduced over D, deterministic order)
+ *   dD           [D] float32  (reduced over batch and T)
+ *   dh0          [batch,D,N] float32 (gradient of h0)
+ * Every gradient pointer may be NULL to skip it. ckpt must come from
+ * naju_scan_fwd with the same inputs, shape and dtype codes.
+ */
+int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
+                  const void* B, const void* C, const float* D_skip,
+                  const float* ckpt, const void* dy, void* du, void* dfl,
+                  void* dil, void* dB, void* dC, float* dD, float* dh0,
+                  int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
+                  int gate_dtype, int bc_dtype, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* Reads the workspace's device-side status word (synchronises `stream`).
+ * 0 = healthy; nonzero = a carry hand-off between workgroups exceeded its
+ * bounded wait and the affected outputs were set to NaN. No counterpart in
+ * the reference (its kernels have no cross-workgroup waits). */
+int naju_scan_workspace_status(const void* workspace, void* stream,
+                               uint32_t* status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NAJU_SCAN_H */

@@ -1,0 +1,70 @@
+"""ctypes binding of the C ABI declared in include/naju_scan.h.
+
+The library is naju_amd/libnaju_scan.so (built by naju_amd/build.py). Nothing
+here falls back to another implementation: if the library is missing or a
+call fails, an exception is raised.
+"""
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnaju_scan.so")
+
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = 0, -1, -2, -3, -4
+
+EXPORTED = (
+    "naju_scan_version",
+    "naju_scan_last_error",
+    "naju_scan_ckpt_elems",
+    "naju_scan_workspace_bytes",
+    "naju_scan_fwd",
+    "naju_scan_bwd",
+    "naju_scan_workspace_status",
+)
+
+_lib = None
+
+
+class NajuScanError(RuntimeError):
+    """A C-ABI call returned a nonzero code."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"naju_scan error {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    """Load (once) and return the ctypes handle; raises if not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build the HIP library first "
+            "(python -m naju_amd.build, or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I64, I, SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+    L.naju_scan_version.argtypes = []
+    L.naju_scan_version.restype = I
+    L.naju_scan_last_error.argtypes = []
+    L.naju_scan_last_error.restype = ctypes.c_char_p
+    L.naju_scan_ckpt_elems.argtypes = [I64] * 4 + [I] * 3
+    L.naju_scan_ckpt_elems.restype = I64
+    L.naju_scan_workspace_bytes.argtypes = [I64] * 4 + [I] * 3
+    L.naju_scan_workspace_bytes.restype = SZ
+    # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, ws, ws_bytes, stream
+    L.naju_scan_fwd.argtypes = [P] * 10 + [I64] * 4 + [I] * 3 + [P, SZ, P]
+    L.naju_scan_fwd.restype = I
+    # u, fl, il, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N, dts, ws, ws_bytes, stream
+    L.naju_scan_bwd.argtypes = [P] * 15 + [I64] * 4 + [I] * 3 + [P, SZ, P]
+    L.naju_scan_bwd.restype = I
+    L.naju_scan_workspace_status.argtypes = [P, P, ctypes.POINTER(ctypes.c_uint32)]
+    L.naju_scan_workspace_status.restype = I
+    _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != OK:
+        raise NajuScanError(rc, lib().naju_scan_last_error().decode(errors="replace"))
+    return rc

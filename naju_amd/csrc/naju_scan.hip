@@ -1,0 +1,961 @@
+// naju_scan.hip -- MI355X (gfx950) kernels and C ABI of the Naju gated scan.
+//
+// Recurrence (reference naju/scan.py:15-19, naju_scan_reference :79-93):
+//   f_t = sigmoid(fl_t), i_t = sigmoid(il_t)
+//   x_t = f_t * x_{t-1} + i_t * B_t * u_t ,  y_t = sum_n C_t x_t + D u_t
+//
+// Design (one HBM pass per direction):
+//  * Lanes run over channels d (the contiguous axis of [B,T,D]), V channels
+//    per lane, so every load and store of the u / gate / dy / grad streams is
+//    a coalesced 8- or 16-byte vector access. B_t and C_t are uniform across
+//    the lanes of a batch row and come in through scalar loads.
+//  * A workgroup owns a tile of 64*V channels and a chunk of L = W*R
+//    timesteps; wave w holds rows [w*R, w*R+R) of the chunk in registers.
+//  * Each wave scans its rows from a zero state and reduces them to an affine
+//    map s -> F*s + Z (the composition rule of reference
+//    naju/chunk_affine_triton.py:3-5). The W maps are composed through LDS.
+//  * Chunks hand their carries to each other through a decoupled look-back:
+//    a workgroup publishes its chunk map (the "aggregate"), then walks back
+//    over its predecessors' published maps until it meets an "inclusive"
+//    carry, and publishes its own inclusive carry. Published words are
+//    64-bit {float value, 32-bit tag} pairs written and read with relaxed
+//    device-scope atomics, so no cache-wide fences are needed and stale words
+//    from earlier launches (older tags) are never mistaken for fresh ones.
+//    Chunks are handed out in order through an atomic ticket, so a workgroup
+//    waits only on workgroups that are already running: no deadlock at any
+//    occupancy. Every wait is bounded.
+//  * The backward is the same machinery run in reverse time for the adjoint
+//    x̄_t = C_t dy_t + f_{t+1} x̄_{t+1}; the forward state inside a chunk is
+//    recomputed from the checkpoint the forward wrote at the chunk start.
+//    du, dfl, dil come out of that single pass; dB, dC (sums over channels)
+//    and dD (sum over batch and time) are written as per-tile partial sums
+//    and folded by one small kernel in a fixed order (deterministic).
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "naju_scan.h"
+
+namespace {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+// ------------------------------------------------------------------ helpers
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  return (T)x;
+}
+
+// sigmoid(x) = 1 / (1 + 2^(-x*log2 e)); exact 0 and 1 at -inf and +inf,
+// so hard-reset (f=0) and pure-retention (f=1) gates stay exact.
+__device__ __forceinline__ float sigm(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
+// Load with a runtime dtype code (B_t / C_t scalars and other small streams).
+__device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
+  if (dt == NAJU_DTYPE_F32) return ((const float*)p)[i];
+  if (dt == NAJU_DTYPE_BF16) return (float)((const bf16_t*)p)[i];
+  return (float)((const f16_t*)p)[i];
+}
+__device__ __forceinline__ void st_any(void* p, int dt, int64_t i, float v) {
+  if (dt == NAJU_DTYPE_F32)
+    ((float*)p)[i] = v;
+  else if (dt == NAJU_DTYPE_BF16)
+    ((bf16_t*)p)[i] = (bf16_t)v;
+  else
+    ((f16_t*)p)[i] = (f16_t)v;
+}
+
+// V consecutive elements starting at element d0 of row `p`. VEC: one aligned
+// vector access, valid iff d0 < D (the host guarantees D % V == 0).
+// Otherwise each element is checked against D. Out-of-range elements read 0.
+template <typename T, int V, bool VEC>
+__device__ __forceinline__ void ld_row(const T* __restrict__ p, int64_t d0, int64_t D, float (&o)[V]) {
+  if constexpr (VEC) {
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    if (d0 < D) {
+      const vec_t v = *reinterpret_cast<const vec_t*>(p + d0);
+#pragma unroll
+      for (int j = 0; j < V; ++j) o[j] = to_f32(v[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) o[j] = 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) o[j] = (d0 + j < D) ? to_f32(p[d0 + j]) : 0.f;
+  }
+}
+
+template <typename T, int V, bool VEC>
+__device__ __forceinline__ void st_row(T* __restrict__ p, int64_t d0, int64_t D, const float (&x)[V]) {
+  if constexpr (VEC) {
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    if (d0 < D) {
+      vec_t v;
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[j] = from_f32<T>(x[j]);
+      *reinterpret_cast<vec_t*>(p + d0) = v;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      if (d0 + j < D) p[d0 + j] = from_f32<T>(x[j]);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+// Tagged words of the look-back: {value bits, tag} in one 64-bit atomic.
+__device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_word(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool word_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Workspace header words.
+enum { HDR_TICKET = 0, HDR_DONE = 1, HDR_EPOCH = 2, HDR_STATUS = 3 };
+// Bound on idle polls of one look-back. A poll is a few device-scope loads
+// plus a short sleep (~1 us), so the bound is about a second, far beyond any
+// legitimate wait (microseconds); past it the carry becomes NaN and the
+// status word records the failure, so every wave still exits.
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+// Decoupled look-back for the V channels of one lane.
+//   aggF/aggZ/incl point at this lane's words of the first predecessor chunk;
+//   consecutive predecessors are `agg_step` / `incl_step` words apart (the
+//   sign gives the direction). At most `max_steps` predecessors exist, the
+//   last of which always publishes an inclusive carry.
+// Result: s = the inclusive carry of the nearest predecessor mapped through
+//   the aggregates in between (Z_acc + F_acc * s).
+template <int V>
+__device__ void look_back(const uint64_t* aggF, const uint64_t* aggZ, const uint64_t* incl, int64_t agg_step,
+                          int64_t incl_step, int max_steps, uint32_t tag, uint32_t* hdr, float (&s)[V]) {
+  float aF[V], aZ[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    aF[j] = 1.f;
+    aZ[j] = 0.f;
+  }
+  int m = 0;
+  bool done = false;
+  uint32_t idle = 0;
+  while (true) {
+    bool moved = false;
+    if (!done) {
+      const uint64_t* pi = incl + (int64_t)m * incl_step;
+      uint64_t wi[V];
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        wi[j] = ld_word(pi + j);
+        ok = ok && word_ok(wi[j], tag);
+      }
+      if (ok) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) s[j] = fmaf(aF[j], word_val(wi[j]), aZ[j]);
+        done = true;
+        moved = true;
+      } else if (m + 1 < max_steps) {
+        const uint64_t* pf = aggF + (int64_t)m * agg_step;
+        const uint64_t* pz = aggZ + (int64_t)m * agg_step;
+        uint64_t wf[V], wz[V];
+        bool ok2 = true;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          wf[j] = ld_word(pf + j);
+          wz[j] = ld_word(pz + j);
+          ok2 = ok2 && word_ok(wf[j], tag) && word_ok(wz[j], tag);
+        }
+        if (ok2) {
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            aZ[j] = fmaf(aF[j], word_val(wz[j]), aZ[j]);
+            aF[j] *= word_val(wf[j]);
+          }
+          ++m;
+          moved = true;
+        }
+      }
+      if (!moved && ++idle > kSpinLimit) {
+        __hip_atomic_store(hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int j = 0; j < V; ++j) s[j] = __builtin_nanf("");
+        done = true;
+      }
+    }
+    if (__all(done)) break;
+    if (!moved) __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Kernel arguments (one struct for every kernel; unused fields are null).
+struct ScanArgs {
+  const void* u;
+  const void* fl;
+  const void* il;
+  const void* Bm;
+  const void* Cm;
+  const float* Dsk;
+  const float* h0;
+  const void* dy;
+  void* y;
+  float* ckpt;
+  float* hT;
+  void* du;
+  void* dfl;
+  void* dil;
+  float* dh0;
+  float* partB;  // [n_dtiles][batch][T][N]
+  float* partC;
+  float* partD;  // [batch][K][D]
+  uint32_t* hdr;
+  uint64_t* agg;   // [K][n_tiles][2][CH]
+  uint64_t* incl;  // [K][n_tiles][CH]
+  int64_t T;
+  int64_t D;
+  int batch;
+  int bc_dt;
+  int n_dtiles;
+  int n_tiles;
+  int K;
+  uint32_t total_wgs;
+};
+
+__device__ __forceinline__ void take_ticket(const ScanArgs& a, uint32_t* s_unit, uint32_t* s_tag) {
+  if (threadIdx.x == 0) {
+    *s_unit = __hip_atomic_fetch_add(a.hdr + HDR_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_tag = __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  }
+  __syncthreads();
+}
+
+// The workgroup that finishes last rewinds the ticket and completion counters
+// and advances the epoch, leaving the workspace ready for the next launch.
+__device__ __forceinline__ void finish(const ScanArgs& a, uint32_t tag) {
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == a.total_wgs - 1) {
+      __hip_atomic_store(a.hdr + HDR_TICKET, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.hdr + HDR_EPOCH, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ------------------------------------------------------------ N = 1 forward
+//
+// One workgroup = (batch row b, tile of CH = 64*V channels, chunk k of
+// L = W*R timesteps). Forward chunk order: ticket -> (k, tile), chunk-major,
+// so every predecessor (k-1, same tile) holds a smaller ticket.
+template <typename TU, typename TG, int V, int R, int W, bool VEC>
+__global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
+  constexpr int CH = 64 * V;
+  constexpr int L = W * R;
+  __shared__ uint32_t s_unit, s_tag;
+  __shared__ float s_F[W][CH];
+  __shared__ float s_Z[W][CH];
+  __shared__ float s_in[CH];
+
+  take_ticket(a, &s_unit, &s_tag);
+  const uint32_t unit = __builtin_amdgcn_readfirstlane(s_unit);
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int k = (int)(unit / (uint32_t)a.n_tiles);
+  const int tile = (int)unit - k * a.n_tiles;
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
+  const int c0 = lane * V;
+  const int64_t T = a.T, D = a.D;
+  const int64_t d0 = (int64_t)dtile * CH + c0;
+  const int t0 = k * L + wv * R;
+
+  const TU* __restrict__ pu = (const TU*)a.u;
+  const TG* __restrict__ pf = (const TG*)a.fl;
+  const TG* __restrict__ pi = (const TG*)a.il;
+
+  float Dv[V];
+  bool dok[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    dok[j] = d0 + j < D;
+    Dv[j] = dok[j] ? a.Dsk[d0 + j] : 0.f;
+  }
+
+  // ---- load the wave's R rows
+  float xu[R][V], xf[R][V], xi[R][V];
+  float Bt[R], Ct[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r;
+    const bool tv = t < T;
+    const int64_t row = ((int64_t)b * T + t) * D;
+    if (tv) {
+      ld_row<TU, V, VEC>(pu + row, d0, D, xu[r]);
+      ld_row<TG, V, VEC>(pf + row, d0, D, xf[r]);
+      ld_row<TG, V, VEC>(pi + row, d0, D, xi[r]);
+      Bt[r] = ld_any(a.Bm, a.bc_dt, (int64_t)b * T + t);
+      Ct[r] = ld_any(a.Cm, a.bc_dt, (int64_t)b * T + t);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) xu[r][j] = xf[r][j] = xi[r][j] = 0.f;
+      Bt[r] = Ct[r] = 0.f;
+    }
+  }
+
+  // ---- pass 1: local scan from zero; keep y = yl + q * s_in per element
+  float F[V], Z[V];
+  float yl[R][V], q[R][V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    F[j] = 1.f;
+    Z[j] = 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool tv = t0 + r < T;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const bool v = tv && dok[j];
+      const float f = v ? sigm(xf[r][j]) : 1.f;
+      const float ig = v ? sigm(xi[r][j]) : 0.f;
+      const float x = xu[r][j];
+      Z[j] = fmaf(f, Z[j], ig * Bt[r] * x);
+      F[j] *= f;
+      yl[r][j] = fmaf(Ct[r], Z[j], Dv[j] * x);
+      q[r][j] = Ct[r] * F[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    s_F[wv][c0 + j] = F[j];
+    s_Z[wv][c0 + j] = Z[j];
+  }
+  __syncthreads();
+
+  // ---- wave 0: chunk map, publish, look back, publish inclusive carry
+  if (wv == 0) {
+    float Fw[V], Zw[V], sin[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      Fw[j] = 1.f;
+      Zw[j] = 0.f;
+    }
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float f = s_F[w][c0 + j];
+        Zw[j] = fmaf(f, Zw[j], s_Z[w][c0 + j]);
+        Fw[j] *= f;
+      }
+    const int64_t agg_step = (int64_t)a.n_tiles * 2 * CH;
+    const int64_t incl_step = (int64_t)a.n_tiles * CH;
+    uint64_t* my_agg = a.agg + ((int64_t)k * a.n_tiles + tile) * 2 * CH + c0;
+    uint64_t* my_incl = a.incl + ((int64_t)k * a.n_tiles + tile) * CH + c0;
+    if (k == 0) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) sin[j] = (a.h0 && dok[j]) ? a.h0[(int64_t)b * D + d0 + j] : 0.f;
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        st_word(my_agg + j, Fw[j], tag);
+        st_word(my_agg + CH + j, Zw[j], tag);
+      }
+      look_back<V>(my_agg - agg_step, my_agg - agg_step + CH, my_incl - incl_step, -agg_step, -incl_step, k, tag,
+                   a.hdr, sin);
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      st_word(my_incl + j, fmaf(Fw[j], sin[j], Zw[j]), tag);
+      s_in[c0 + j] = sin[j];
+    }
+    if (a.ckpt) {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if (dok[j]) a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] = sin[j];
+    }
+    if (a.hT && k == a.K - 1) {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if (dok[j]) a.hT[(int64_t)b * D + d0 + j] = fmaf(Fw[j], sin[j], Zw[j]);
+    }
+  }
+  __syncthreads();
+
+  // ---- pass 2: this wave's carry, then y
+  float s[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) s[j] = s_in[c0 + j];
+  for (int w = 0; w < wv; ++w)
+#pragma unroll
+    for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][c0 + j], s[j], s_Z[w][c0 + j]);
+  TU* __restrict__ py = (TU*)a.y;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r;
+    if (t < T) {
+      float o[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) o[j] = fmaf(q[r][j], s[j], yl[r][j]);
+      st_row<TU, V, VEC>(py + ((int64_t)b * T + t) * D, d0, D, o);
+    }
+  }
+  finish(a, tag);
+}
+
+// ----------------------------------------------------------- N = 1 backward
+//
+// Adjoint in carry form: with g = f_{t+1} x̄_{t+1} entering row t from the
+// future, x̄_t = C_t dy_t + g and the carry leaving is f_t x̄_t. Rows [t0,t1)
+// map g_in -> A g_in + Zb with A = prod f. Chunks run in reverse order
+// (ticket -> chunk K-1-k), so the look-back walks towards larger t.
+template <typename TU, typename TG, int V, int R, int W, bool VEC>
+__global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
+  constexpr int CH = 64 * V;
+  constexpr int L = W * R;
+  __shared__ uint32_t s_unit, s_tag;
+  __shared__ float s_F[W][CH];
+  __shared__ float s_Z[W][CH];
+  __shared__ float s_Zb[W][CH];
+  __shared__ float s_g[CH];
+
+  take_ticket(a, &s_unit, &s_tag);
+  const uint32_t unit = __builtin_amdgcn_readfirstlane(s_unit);
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int kk = (int)(unit / (uint32_t)a.n_tiles);
+  const int tile = (int)unit - kk * a.n_tiles;
+  const int k = a.K - 1 - kk;
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
+  const int c0 = lane * V;
+  const int64_t T = a.T, D = a.D;
+  const int64_t d0 = (int64_t)dtile * CH + c0;
+  const int t0 = k * L + wv * R;
+
+  const TU* __restrict__ pu = (const TU*)a.u;
+  const TG* __restrict__ pfl = (const TG*)a.fl;
+  const TG* __restrict__ pil = (const TG*)a.il;
+  const TU* __restrict__ pdy = (const TU*)a.dy;
+
+  float Dv[V];
+  bool dok[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    dok[j] = d0 + j < D;
+    Dv[j] = dok[j] ? a.Dsk[d0 + j] : 0.f;
+  }
+
+  float xu[R][V], xf[R][V], xi[R][V], xg[R][V];
+  float Bt[R], Ct[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r;
+    const bool tv = t < T;
+    const int64_t row = ((int64_t)b * T + t) * D;
+    if (tv) {
+      ld_row<TU, V, VEC>(pu + row, d0, D, xu[r]);
+      ld_row<TG, V, VEC>(pfl + row, d0, D, xf[r]);
+      ld_row<TG, V, VEC>(pil + row, d0, D, xi[r]);
+      ld_row<TU, V, VEC>(pdy + row, d0, D, xg[r]);
+      Bt[r] = ld_any(a.Bm, a.bc_dt, (int64_t)b * T + t);
+      Ct[r] = ld_any(a.Cm, a.bc_dt, (int64_t)b * T + t);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) xu[r][j] = xf[r][j] = xi[r][j] = xg[r][j] = 0.f;
+      Bt[r] = Ct[r] = 0.f;
+    }
+  }
+
+  // ---- pass 1: gates, forward map (F, Z) and adjoint map (F, Zb) of the rows
+  float F[V], Z[V], G[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    F[j] = 1.f;
+    Z[j] = 0.f;
+    G[j] = 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool tv = t0 + r < T;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const bool v = tv && dok[j];
+      xf[r][j] = v ? sigm(xf[r][j]) : 1.f;  // f
+      xi[r][j] = v ? sigm(xi[r][j]) : 0.f;  // i
+      Z[j] = fmaf(xf[r][j], Z[j], xi[r][j] * Bt[r] * xu[r][j]);
+      F[j] *= xf[r][j];
+    }
+  }
+#pragma unroll
+  for (int r = R - 1; r >= 0; --r)
+#pragma unroll
+    for (int j = 0; j < V; ++j) G[j] = xf[r][j] * fmaf(xg[r][j], Ct[r], G[j]);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    s_F[wv][c0 + j] = F[j];
+    s_Z[wv][c0 + j] = Z[j];
+    s_Zb[wv][c0 + j] = G[j];
+  }
+  __syncthreads();
+
+  // ---- wave 0: chunk adjoint map, publish, look ahead, publish inclusive
+  if (wv == 0) {
+    float A[V], Zb[V], gin[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      A[j] = 1.f;
+      Zb[j] = 0.f;
+    }
+#pragma unroll
+    for (int w = W - 1; w >= 0; --w)
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float f = s_F[w][c0 + j];
+        Zb[j] = fmaf(f, Zb[j], s_Zb[w][c0 + j]);
+        A[j] *= f;
+      }
+    const int64_t agg_step = (int64_t)a.n_tiles * 2 * CH;
+    const int64_t incl_step = (int64_t)a.n_tiles * CH;
+    uint64_t* my_agg = a.agg + ((int64_t)k * a.n_tiles + tile) * 2 * CH + c0;
+    uint64_t* my_incl = a.incl + ((int64_t)k * a.n_tiles + tile) * CH + c0;
+    if (k == a.K - 1) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) gin[j] = 0.f;
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        st_word(my_agg + j, A[j], tag);
+        st_word(my_agg + CH + j, Zb[j], tag);
+      }
+      look_back<V>(my_agg + agg_step, my_agg + agg_step + CH, my_incl + incl_step, agg_step, incl_step,
+                   a.K - 1 - k, tag, a.hdr, gin);
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float gout = fmaf(A[j], gin[j], Zb[j]);
+      st_word(my_incl + j, gout, tag);
+      s_g[c0 + j] = gin[j];
+      if (a.dh0 && k == 0 && dok[j]) a.dh0[(int64_t)b * D + d0 + j] = gout;
+    }
+  }
+  __syncthreads();
+
+  // ---- pass 2: exact carries of this wave's rows
+  float s[V], g[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    s[j] = dok[j] ? a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] : 0.f;
+    g[j] = s_g[c0 + j];
+  }
+  for (int w = 0; w < wv; ++w)
+#pragma unroll
+    for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][c0 + j], s[j], s_Z[w][c0 + j]);
+  for (int w = W - 1; w > wv; --w)
+#pragma unroll
+    for (int j = 0; j < V; ++j) g[j] = fmaf(s_F[w][c0 + j], g[j], s_Zb[w][c0 + j]);
+
+  // forward states x_{t-1} of every row (x_{t0-1} = s)
+  float xp[R][V];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      xp[r][j] = s[j];
+      s[j] = fmaf(xf[r][j], s[j], xi[r][j] * Bt[r] * xu[r][j]);
+    }
+
+  // reverse sweep: gradients (naju/cuda/naju_cuda.cu:116-140 restated)
+  float pB[R], pC[R], dDs[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) dDs[j] = 0.f;
+#pragma unroll
+  for (int r = R - 1; r >= 0; --r) {
+    pB[r] = 0.f;
+    pC[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float f = xf[r][j], ig = xi[r][j], x = xu[r][j], gy = xg[r][j];
+      const float xb = fmaf(gy, Ct[r], g[j]);
+      const float xt = fmaf(f, xp[r][j], ig * Bt[r] * x);
+      const float dws = xb * Bt[r];
+      pB[r] = fmaf(xb, ig * x, pB[r]);
+      pC[r] = fmaf(gy, xt, pC[r]);
+      dDs[j] = fmaf(gy, x, dDs[j]);
+      g[j] = f * xb;
+      xf[r][j] = f * (1.f - f) * xb * xp[r][j];  // dfl
+      xi[r][j] = dws * x * (ig * (1.f - ig));     // dil
+      xu[r][j] = fmaf(ig, dws, Dv[j] * gy);       // du
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r;
+    if (t < T) {
+      const int64_t row = ((int64_t)b * T + t) * D;
+      if (a.du) st_row<TU, V, VEC>((TU*)a.du + row, d0, D, xu[r]);
+      if (a.dfl) st_row<TG, V, VEC>((TG*)a.dfl + row, d0, D, xf[r]);
+      if (a.dil) st_row<TG, V, VEC>((TG*)a.dil + row, d0, D, xi[r]);
+    }
+  }
+  if (a.partB || a.partC) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float sb = wave_sum(pB[r]);
+      const float sc = wave_sum(pC[r]);
+      const int64_t t = t0 + r;
+      if (lane == 0 && t < T) {
+        const int64_t o = ((int64_t)dtile * a.batch + b) * T + t;
+        if (a.partB) a.partB[o] = sb;
+        if (a.partC) a.partC[o] = sc;
+      }
+    }
+  }
+  if (a.partD) {
+    __syncthreads();  // every wave has read s_Z for its carry
+#pragma unroll
+    for (int j = 0; j < V; ++j) s_Z[wv][c0 + j] = dDs[j];
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float acc = 0.f;
+        for (int w = 0; w < W; ++w) acc += s_Z[w][c0 + j];
+        if (dok[j]) a.partD[((int64_t)b * a.K + k) * D + d0 + j] = acc;
+      }
+    }
+  }
+  finish(a, tag);
+}
+
+// Folds the per-tile partial sums: dB/dC over channel tiles, dD over
+// (batch, chunk). Fixed summation order, so results are run-to-run identical.
+__global__ void fold_partials_kernel(const float* __restrict__ partB, const float* __restrict__ partC,
+                                     int n_parts, int64_t btn, void* dB, void* dC, int bc_dt,
+                                     const float* __restrict__ partD, int64_t n_rows, int64_t D, float* dD) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
+    if (dB) {
+      float s = 0.f;
+      for (int p = 0; p < n_parts; ++p) s += partB[(int64_t)p * btn + i];
+      st_any(dB, bc_dt, i, s);
+    }
+    if (dC) {
+      float s = 0.f;
+      for (int p = 0; p < n_parts; ++p) s += partC[(int64_t)p * btn + i];
+      st_any(dC, bc_dt, i, s);
+    }
+  }
+  if (dD) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < D; i += stride) {
+      float s = 0.f;
+      for (int64_t r = 0; r < n_rows; ++r) s += partD[r * D + i];
+      dD[i] = s;
+    }
+  }
+}
+
+// Fills n float32 values with src[i] (or 0 when src is null); used for the
+// empty-shape edge cases (hT = h0 when T == 0, zero gradients).
+__global__ void fill_kernel(float* dst, const float* src, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    dst[i] = src ? src[i] : 0.f;
+}
+__global__ void zero_any_kernel(void* dst, int dt, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) st_any(dst, dt, i, 0.f);
+}
+
+// ------------------------------------------------------------- host side
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
+
+// Tile geometry of the N = 1 kernels: R rows per wave, W waves per
+// workgroup, V channels per lane (16-byte loads when every stream is 2-byte).
+constexpr int kR = 4;
+constexpr int kW = 8;
+
+// The backward keeps four streams and the forward states of its rows in
+// registers, so it uses V = 4 throughout; the chunk length L (which fixes the
+// checkpoint layout) is the same in both directions.
+int n1_vec_width(int x_dt, int g_dt, bool bwd) {
+  return (!bwd && dsize(x_dt) == 2 && dsize(g_dt) == 2) ? 8 : 4;
+}
+
+struct Layout {
+  int V, CH, L, K, n_dtiles, n_tiles;
+  size_t off_agg, off_incl, off_partB, off_partC, off_partD, total;
+};
+
+size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd) {
+  Layout l{};
+  l.V = n1_vec_width(x_dt, g_dt, bwd);
+  l.CH = 64 * l.V;
+  l.L = kR * kW;
+  l.K = (int)((T + l.L - 1) / l.L);
+  l.n_dtiles = (int)((D + l.CH - 1) / l.CH);
+  l.n_tiles = (int)(batch * l.n_dtiles);
+  const size_t units = (size_t)l.K * l.n_tiles;
+  size_t off = 256;  // header
+  l.off_agg = off;
+  off = align_up(off + units * 2 * l.CH * sizeof(uint64_t));
+  l.off_incl = off;
+  off = align_up(off + units * l.CH * sizeof(uint64_t));
+  l.off_partB = off;
+  off = align_up(off + (size_t)l.n_dtiles * batch * T * N * sizeof(float));
+  l.off_partC = off;
+  off = align_up(off + (size_t)l.n_dtiles * batch * T * N * sizeof(float));
+  l.off_partD = off;
+  off = align_up(off + (size_t)batch * l.K * D * sizeof(float));
+  l.total = off;
+  return l;
+}
+
+bool dt_ok(int dt) { return dt == NAJU_DTYPE_F32 || dt == NAJU_DTYPE_BF16 || dt == NAJU_DTYPE_F16; }
+
+int check_common(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, int bc_dt) {
+  if (batch < 0 || T < 0 || D < 0) return fail(NAJU_ERR_INVALID, "negative shape (batch=%lld T=%lld D=%lld)",
+                                               (long long)batch, (long long)T, (long long)D);
+  if (N < 1) return fail(NAJU_ERR_INVALID, "N (d_state) must be >= 1, got %lld", (long long)N);
+  if (!dt_ok(x_dt) || !dt_ok(g_dt) || !dt_ok(bc_dt))
+    return fail(NAJU_ERR_INVALID, "unknown dtype code (x=%d gate=%d bc=%d)", x_dt, g_dt, bc_dt);
+  if (g_dt != NAJU_DTYPE_F32 && g_dt != x_dt)
+    return fail(NAJU_ERR_UNSUPPORTED, "gate dtype must be float32 or equal to the u dtype");
+  if (bc_dt != NAJU_DTYPE_F32 && bc_dt != x_dt)
+    return fail(NAJU_ERR_UNSUPPORTED, "B/C dtype must be float32 or equal to the u dtype");
+  if (x_dt == NAJU_DTYPE_F32 && g_dt != NAJU_DTYPE_F32)
+    return fail(NAJU_ERR_UNSUPPORTED, "float32 u needs float32 gates");
+  if (N != 1) return fail(NAJU_ERR_UNSUPPORTED, "this build serves N == 1 only (got N=%lld)", (long long)N);
+  if (T > (1ll << 30) || D > (1ll << 30) || batch > (1ll << 30))
+    return fail(NAJU_ERR_INVALID, "dimension exceeds 2^30");
+  return NAJU_OK;
+}
+
+bool aligned(const void* p, size_t a) { return p == nullptr || ((uintptr_t)p % a) == 0; }
+
+typedef void (*kern_t)(ScanArgs);
+
+template <typename TU, typename TG, bool VEC>
+kern_t pick_n1(bool bwd) {
+  constexpr int VF = (sizeof(TU) == 2 && sizeof(TG) == 2) ? 8 : 4;
+  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, 4, kR, kW, VEC> : (kern_t)n1_fwd_kernel<TU, TG, VF, kR, kW, VEC>;
+}
+
+template <bool VEC>
+kern_t pick_n1_dt(int x_dt, int g_dt, bool bwd) {
+  if (x_dt == NAJU_DTYPE_F32) return pick_n1<float, float, VEC>(bwd);
+  if (x_dt == NAJU_DTYPE_BF16)
+    return g_dt == NAJU_DTYPE_F32 ? pick_n1<bf16_t, float, VEC>(bwd) : pick_n1<bf16_t, bf16_t, VEC>(bwd);
+  return g_dt == NAJU_DTYPE_F32 ? pick_n1<f16_t, float, VEC>(bwd) : pick_n1<f16_t, f16_t, VEC>(bwd);
+}
+
+int launch(kern_t k, unsigned grid, unsigned block, hipStream_t st, const ScanArgs& a) {
+  hipLaunchKernelGGL(k, dim3(grid), dim3(block), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+unsigned small_grid(int64_t n) {
+  const int64_t g = (n + 255) / 256;
+  return (unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g));
+}
+
+}  // namespace
+
+extern "C" {
+
+int naju_scan_version(void) { return (0 << 16) | 1; }
+
+const char* naju_scan_last_error(void) { return g_err; }
+
+int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
+                             int bc_dtype) {
+  if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return -1;
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false);
+  return batch * (int64_t)l.K * D * N;
+}
+
+size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
+                                 int bc_dtype) {
+  if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return 0;
+  const size_t f = make_layout(batch, T, D, N, x_dtype, gate_dtype, false).total;
+  const size_t b = make_layout(batch, T, D, N, x_dtype, gate_dtype, true).total;
+  return f > b ? f : b;
+}
+
+int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                  const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch, int64_t T,
+                  int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (batch == 0 || D == 0) return NAJU_OK;
+  if (T == 0) {
+    if (hT) {
+      hipLaunchKernelGGL(fill_kernel, dim3(small_grid(batch * D * N)), dim3(256), 0, st, hT, h0, batch * D * N);
+      if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fill launch failed");
+    }
+    return NAJU_OK;
+  }
+  if (!u || !f_logit || !i_logit || !B || !C || !D_skip || !y)
+    return fail(NAJU_ERR_INVALID, "null input/output pointer (u, f_logit, i_logit, B, C, D_skip and y are required)");
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", l.total,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!aligned(workspace, 256)) return fail(NAJU_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  const size_t va_x = l.V * dsize(x_dtype), va_g = l.V * dsize(gate_dtype);
+  const bool vec = (D % l.V == 0) && aligned(u, va_x) && aligned(y, va_x) && aligned(f_logit, va_g) &&
+                   aligned(i_logit, va_g);
+  ScanArgs a{};
+  a.u = u;
+  a.fl = f_logit;
+  a.il = i_logit;
+  a.Bm = B;
+  a.Cm = C;
+  a.Dsk = D_skip;
+  a.h0 = h0;
+  a.y = y;
+  a.ckpt = ckpt;
+  a.hT = hT;
+  char* ws = (char*)workspace;
+  a.hdr = (uint32_t*)ws;
+  a.agg = (uint64_t*)(ws + l.off_agg);
+  a.incl = (uint64_t*)(ws + l.off_incl);
+  a.T = T;
+  a.D = D;
+  a.batch = (int)batch;
+  a.bc_dt = bc_dtype;
+  a.n_dtiles = l.n_dtiles;
+  a.n_tiles = l.n_tiles;
+  a.K = l.K;
+  const int64_t wgs = (int64_t)l.K * l.n_tiles;
+  if (wgs > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups)", (long long)wgs);
+  a.total_wgs = (uint32_t)wgs;
+  kern_t k = vec ? pick_n1_dt<true>(x_dtype, gate_dtype, false) : pick_n1_dt<false>(x_dtype, gate_dtype, false);
+  return launch(k, (unsigned)wgs, 64 * kW, st, a);
+}
+
+int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                  const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil, void* dB,
+                  void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
+                  int gate_dtype, int bc_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (batch == 0 || T == 0 || D == 0) {
+    // Gradients of an empty scan: the reductions over the empty axes are 0.
+    if (dD) hipLaunchKernelGGL(fill_kernel, dim3(small_grid(D)), dim3(256), 0, st, dD, (const float*)nullptr, D);
+    if (dh0)
+      hipLaunchKernelGGL(fill_kernel, dim3(small_grid(batch * D * N)), dim3(256), 0, st, dh0,
+                         (const float*)nullptr, batch * D * N);
+    if (dB) hipLaunchKernelGGL(zero_any_kernel, dim3(small_grid(batch * T * N)), dim3(256), 0, st, dB, bc_dtype,
+                               batch * T * N);
+    if (dC) hipLaunchKernelGGL(zero_any_kernel, dim3(small_grid(batch * T * N)), dim3(256), 0, st, dC, bc_dtype,
+                               batch * T * N);
+    if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fill launch failed");
+    return NAJU_OK;
+  }
+  if (!u || !f_logit || !i_logit || !B || !C || !D_skip || !dy)
+    return fail(NAJU_ERR_INVALID, "null input pointer (u, f_logit, i_logit, B, C, D_skip and dy are required)");
+  if (!ckpt) return fail(NAJU_ERR_INVALID, "ckpt is required (write it with naju_scan_fwd)");
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", l.total,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!aligned(workspace, 256)) return fail(NAJU_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  const size_t va_x = l.V * dsize(x_dtype), va_g = l.V * dsize(gate_dtype);
+  const bool vec = (D % l.V == 0) && aligned(u, va_x) && aligned(dy, va_x) && aligned(du, va_x) &&
+                   aligned(f_logit, va_g) && aligned(i_logit, va_g) && aligned(dfl, va_g) && aligned(dil, va_g);
+  ScanArgs a{};
+  a.u = u;
+  a.fl = f_logit;
+  a.il = i_logit;
+  a.Bm = B;
+  a.Cm = C;
+  a.Dsk = D_skip;
+  a.dy = dy;
+  a.ckpt = (float*)ckpt;
+  a.du = du;
+  a.dfl = dfl;
+  a.dil = dil;
+  a.dh0 = dh0;
+  char* ws = (char*)workspace;
+  a.hdr = (uint32_t*)ws;
+  a.agg = (uint64_t*)(ws + l.off_agg);
+  a.incl = (uint64_t*)(ws + l.off_incl);
+  a.partB = dB ? (float*)(ws + l.off_partB) : nullptr;
+  a.partC = dC ? (float*)(ws + l.off_partC) : nullptr;
+  a.partD = dD ? (float*)(ws + l.off_partD) : nullptr;
+  a.T = T;
+  a.D = D;
+  a.batch = (int)batch;
+  a.bc_dt = bc_dtype;
+  a.n_dtiles = l.n_dtiles;
+  a.n_tiles = l.n_tiles;
+  a.K = l.K;
+  const int64_t wgs = (int64_t)l.K * l.n_tiles;
+  if (wgs > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups)", (long long)wgs);
+  a.total_wgs = (uint32_t)wgs;
+  kern_t k = vec ? pick_n1_dt<true>(x_dtype, gate_dtype, true) : pick_n1_dt<false>(x_dtype, gate_dtype, true);
+  rc = launch(k, (unsigned)wgs, 64 * kW, st, a);
+  if (rc) return rc;
+  if (dB || dC || dD) {
+    const int64_t btn = batch * T * N;
+    hipLaunchKernelGGL(fold_partials_kernel, dim3(small_grid(btn > D ? btn : D)), dim3(256), 0, st, a.partB,
+                       a.partC, l.n_dtiles, btn, dB, dC, bc_dtype, a.partD, batch * (int64_t)l.K, D, dD);
+    if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
+  }
+  return NAJU_OK;
+}
+
+int naju_scan_workspace_status(const void* workspace, void* stream, uint32_t* status) {
+  if (!workspace || !status) return fail(NAJU_ERR_INVALID, "null workspace or status pointer");
+  uint32_t hdr[4];
+  if (hipMemcpyAsync(hdr, workspace, sizeof(hdr), hipMemcpyDeviceToHost, (hipStream_t)stream) != hipSuccess ||
+      hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+    return fail(NAJU_ERR_LAUNCH, "could not read the workspace header");
+  *status = hdr[HDR_STATUS];
+  return NAJU_OK;
+}
+
+}  // extern "C"

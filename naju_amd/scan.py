@@ -1,0 +1,204 @@
+"""Naju scan on MI355X behind the reference's scan-backend interface.
+
+Public surface, mirroring /root/reference/naju/scan.py:
+
+* ``naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None)`` -- the backend
+  callable, same 6-tensor signature as every reference backend
+  (scan.py:3-13, chunk_triton.py:203, cuda/__init__.py:66) plus an optional
+  initial state ``h0`` [B, D, N] (the reference always starts from zero,
+  scan.py:84). Differentiable; the backward returns the gradients of all
+  inputs, including ``h0``.
+* ``naju_scan(..., backend=None)`` / ``resolve_backend`` / ``_BACKEND_CACHE``
+  -- the dispatch of scan.py:45-76 for code that runs without the reference
+  package. The only backend name served here is ``"hip"``.
+* ``register(name="hip", scan_module=None)`` -- inserts ``naju_scan_hip`` into
+  the reference's ``naju.scan._BACKEND_CACHE``. ``_get`` returns cached entries
+  before it validates names (scan.py:55-57) and ``resolve_backend`` lower-cases
+  (scan.py:52), so ``NAJU_SCAN_BACKEND=hip`` or ``NajuMixer(scan_backend="hip")``
+  then routes unmodified NajuMixer / NajuLM code to these kernels.
+
+Tensor conventions follow the reference (SURVEY of scan.py:7-11): [B,T,D]
+streams with D contiguous, [B,T,N] for B and C, [D] for D_skip. Inputs are
+never modified. ``y`` has u's dtype (the convention of the GPU training
+backends, chunk_triton.py:181 and chunk_affine_triton.py:288); each gradient
+has its input's dtype. Arithmetic and state are float32.
+"""
+import os
+
+import torch
+
+from naju_amd import _lib
+
+_BACKEND_CACHE = {}
+
+_DT = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16}
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class _Workspace:
+    """One zero-filled workspace per (device, stream), grown on demand. The
+    kernels return it to a reusable state after every call, so it is zeroed
+    only when (re)allocated."""
+
+    def __init__(self):
+        self._bufs = {}
+
+    def get(self, device, stream, nbytes):
+        key = (device.index, stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_WS = _Workspace()
+
+
+def _stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0):
+    """Contiguous tensors in a dtype combination the kernels serve:
+    u in {f32,bf16,f16}; gates and B/C each f32 or u's dtype; D_skip, h0 f32."""
+    if u.dtype not in _DT:
+        u = u.float()
+    xd = u.dtype
+    if not (f_logit.dtype == i_logit.dtype and f_logit.dtype in (xd, torch.float32)):
+        f_logit, i_logit = f_logit.float(), i_logit.float()
+    if xd == torch.float32 and f_logit.dtype != torch.float32:
+        f_logit, i_logit = f_logit.float(), i_logit.float()
+    if not (B.dtype == C.dtype and B.dtype in (xd, torch.float32)):
+        B, C = B.float(), C.float()
+    D_skip = D_skip.float()
+    if h0 is not None:
+        h0 = h0.float().contiguous()
+    return (u.contiguous(), f_logit.contiguous(), i_logit.contiguous(),
+            B.contiguous(), C.contiguous(), D_skip.contiguous(), h0)
+
+
+def _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0):
+    if u.dim() != 3:
+        raise ValueError(f"u must be [B, T, D], got shape {tuple(u.shape)}")
+    Bsz, T, D = u.shape
+    if f_logit.shape != u.shape or i_logit.shape != u.shape:
+        raise ValueError("f_logit and i_logit must have u's shape [B, T, D]")
+    if B.dim() != 3 or B.shape[:2] != u.shape[:2] or C.shape != B.shape:
+        raise ValueError("B and C must be [B, T, N] with u's batch and time sizes")
+    if D_skip.shape != (D,):
+        raise ValueError(f"D_skip must be [D]={D}, got {tuple(D_skip.shape)}")
+    N = B.shape[-1]
+    if h0 is not None and tuple(h0.shape) != (Bsz, D, N):
+        raise ValueError(f"h0 must be [B, D, N]=({Bsz}, {D}, {N}), got {tuple(h0.shape)}")
+    devs = {t.device for t in (u, f_logit, i_logit, B, C, D_skip) + ((h0,) if h0 is not None else ())}
+    if len(devs) != 1 or next(iter(devs)).type != "cuda":
+        raise ValueError("all scan inputs must live on one GPU device")
+    return Bsz, T, D, N
+
+
+class NajuScanHip(torch.autograd.Function):
+    """Autograd wrapper of naju_scan_fwd / naju_scan_bwd (include/naju_scan.h)."""
+
+    @staticmethod
+    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None):
+        Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
+        out_dtype = u.dtype
+        u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0)
+        dts = (_DT[u_.dtype], _DT[fl_.dtype], _DT[B_.dtype])
+        L = _lib.lib()
+        dev = u_.device
+        stream = _stream_handle(dev)
+        need_grad = any(ctx.needs_input_grad)
+        ckpt = None
+        if need_grad:
+            n = L.naju_scan_ckpt_elems(Bsz, T, D, N, *dts)
+            if n < 0:
+                _lib.check(_lib.ERR_INVALID)
+            ckpt = torch.empty(max(n, 1), dtype=torch.float32, device=dev)
+        nbytes = L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)
+        if nbytes == 0 and Bsz * T * D > 0:
+            _lib.check(_lib.ERR_INVALID)
+        ws = _WS.get(dev, stream, nbytes)
+        y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
+        _lib.check(L.naju_scan_fwd(
+            _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
+            _ptr(y), _ptr(ckpt), None, Bsz, T, D, N, *dts, ws.data_ptr(), ws.numel(), stream))
+        if need_grad:
+            ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
+            ctx.meta = (Bsz, T, D, N, dts, h0 is not None,
+                        (u.dtype, f_logit.dtype, i_logit.dtype, B.dtype, C.dtype, D_skip.dtype))
+        return y if y.dtype == out_dtype else y.to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        u_, fl_, il_, B_, C_, D_, ckpt = ctx.saved_tensors
+        Bsz, T, D, N, dts, has_h0, in_dtypes = ctx.meta
+        ng = ctx.needs_input_grad
+        dev = u_.device
+        dy = dy.to(u_.dtype).contiguous()
+        du = torch.empty_like(u_) if ng[0] else None
+        dfl = torch.empty_like(fl_) if ng[1] else None
+        dil = torch.empty_like(il_) if ng[2] else None
+        dB = torch.empty_like(B_) if ng[3] else None
+        dC = torch.empty_like(C_) if ng[4] else None
+        dD = torch.empty((D,), dtype=torch.float32, device=dev) if ng[5] else None
+        want_h0 = has_h0 and len(ng) > 6 and ng[6]
+        dh0 = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_h0 else None
+        L = _lib.lib()
+        stream = _stream_handle(dev)
+        ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts))
+        _lib.check(L.naju_scan_bwd(
+            _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
+            _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
+            Bsz, T, D, N, *dts, ws.data_ptr(), ws.numel(), stream))
+        grads = [du, dfl, dil, dB, dC, dD]
+        grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
+        return (*grads, dh0)
+
+
+def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None):
+    """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module doc)."""
+    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0)
+
+
+def resolve_backend(backend=None):
+    """Selection order of scan.py:48-52: explicit > NAJU_SCAN_BACKEND > "hip"."""
+    b = backend or os.environ.get("NAJU_SCAN_BACKEND") or "hip"
+    return b.lower()
+
+
+def _get(b):
+    fn = _BACKEND_CACHE.get(b)
+    if fn is None:
+        if b in ("hip", "naju_amd"):
+            fn = naju_scan_hip
+        else:
+            raise ValueError(f"unknown scan backend {b!r}; valid: hip")
+        _BACKEND_CACHE[b] = fn
+    return fn
+
+
+def naju_scan(u, f_logit, i_logit, B, C, D_skip, backend=None, h0=None):
+    """Dispatching entry point with the signature of scan.py:75-76 (+ h0)."""
+    fn = _get(resolve_backend(backend))
+    if h0 is None:
+        return fn(u, f_logit, i_logit, B, C, D_skip)
+    return fn(u, f_logit, i_logit, B, C, D_skip, h0)
+
+
+def register(name="hip", scan_module=None):
+    """Register naju_scan_hip as backend `name` of the reference dispatcher.
+
+    scan_module defaults to ``naju.scan`` (imported lazily); pass the module
+    explicitly when it lives elsewhere. Registering as "chunk" also captures
+    the reference's automatic GPU default (scan.py:51)."""
+    if scan_module is None:
+        import importlib
+        scan_module = importlib.import_module("naju.scan")
+    scan_module._BACKEND_CACHE[name.lower()] = naju_scan_hip
+    _BACKEND_CACHE[name.lower()] = naju_scan_hip
+    return naju_scan_hip

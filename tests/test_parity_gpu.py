@@ -1,0 +1,175 @@
+"""GPU parity of the HIP scan (through the C ABI) against the fp64 oracle.
+
+Tolerances (tests/_helpers.tol_for): float32 outputs 1e-5, bf16/fp16 outputs
+2e-3, as max-abs error / max|oracle| AND ||err||_2 / ||oracle||_2. The oracle
+runs on the same (already quantized) inputs, upcast -- the practice of
+reference naju/tests/test_affine_chunk.py:149-153.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests._helpers import check_all, oracle_all, rand_inputs, run_hip
+
+pytestmark = pytest.mark.gpu
+
+# (batch, T, D): single chunk, ragged T, D not a multiple of the lane width,
+# several tiles, long-ish T -- the reference's shape matrix style
+# (naju/tests/test_affine_chunk.py:84-86).
+SHAPES_N1 = [(1, 7, 32), (2, 64, 64), (2, 65, 96), (1, 129, 96), (3, 200, 40),
+             (2, 33, 1000), (2, 1024, 256), (8, 256, 512)]
+
+
+@pytest.mark.parametrize("shape", SHAPES_N1)
+def test_fp32_n1_shapes(gpu, shape):
+    b, T, D = shape
+    ins = rand_inputs(b, T, D, 1, seed=T + D)
+    y, g = run_hip(ins, gpu)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+@pytest.mark.parametrize("dtype,gate_dtype", [(torch.bfloat16, None), (torch.float16, None),
+                                              (torch.bfloat16, torch.float32),
+                                              (torch.float16, torch.float32)])
+def test_half_n1(gpu, dtype, gate_dtype):
+    ins = rand_inputs(4, 512, 128, 1, seed=5, dtype=dtype, gate_dtype=gate_dtype)
+    y, g = run_hip(ins, gpu)
+    assert y.dtype == dtype
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+def test_bf16_u_bc_f32_gates_mixer_dtypes(gpu):
+    """Autocast dtypes at the mixer's call (u, B, C bf16; logits fp32;
+    D_skip fp32)."""
+    ins = rand_inputs(2, 300, 192, 1, seed=21, dtype=torch.bfloat16, gate_dtype=torch.float32)
+    y, g = run_hip(ins, gpu)
+    assert g["dfl"].dtype == torch.float32 and g["du"].dtype == torch.bfloat16
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_h0(gpu, dtype):
+    ins = rand_inputs(3, 257, 192, 1, seed=3, dtype=dtype, h0_std=0.5)
+    y, g = run_hip(ins, gpu)
+    assert "dh0" in g and g["dh0"].shape == (3, 192, 1)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+def test_edge_gates_exact_zero_one(gpu):
+    """a forced to exactly 0 (f_logit=-inf) and 1 (+inf) on 10% each: the
+    scan stays finite and exact, and dfl is exactly 0 there (f(1-f) = 0)."""
+    ins = rand_inputs(2, 400, 256, 1, seed=11, dtype=torch.bfloat16, f_shift=0.0)
+    g = torch.Generator().manual_seed(12)
+    sel = torch.rand(2, 400, 256, generator=g)
+    fl = ins["f_logit"].float() * 2.0
+    fl[sel < 0.1] = -math.inf
+    fl[sel >= 0.9] = math.inf
+    ins["f_logit"] = fl.to(torch.bfloat16)
+    y, gr = run_hip(ins, gpu)
+    ry, rg = oracle_all(ins)
+    check_all(y, gr, ry, rg)
+    hard = (sel < 0.1) | (sel >= 0.9)
+    assert torch.all(gr["dfl"].float().cpu()[hard] == 0)
+
+
+def test_deep_gates(gpu):
+    """f ~ sigmoid(-12): the guard region of the reference chunk backend
+    (naju/tests/test_affine_chunk.py:101-115, :172-194)."""
+    ins = rand_inputs(2, 256, 64, 1, seed=7, f_shift=-12.0)
+    y, g = run_hip(ins, gpu)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+def test_long_sequence_near_one(gpu):
+    """Long T with retention near 1: cross-chunk carries dominate."""
+    ins = rand_inputs(1, 32768, 64, 1, seed=11, f_shift=4.0)
+    y, g = run_hip(ins, gpu)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+def test_deterministic_and_workspace_reusable(gpu):
+    """Two identical runs are bitwise identical (no float atomics), and the
+    workspace status word stays healthy."""
+    ins = rand_inputs(4, 700, 320, 1, seed=13, dtype=torch.bfloat16)
+    y1, g1 = run_hip(ins, gpu)
+    y2, g2 = run_hip(ins, gpu)
+    assert torch.equal(y1, y2)
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
+    from naju_amd import _lib
+    from naju_amd.scan import _WS
+    import ctypes
+    for (dev, stream), buf in _WS._bufs.items():
+        st = ctypes.c_uint32(99)
+        _lib.check(_lib.lib().naju_scan_workspace_status(buf.data_ptr(), stream, ctypes.byref(st)))
+        assert st.value == 0
+
+
+def test_needs_input_grad_subset(gpu):
+    ins = rand_inputs(2, 100, 64, 1, seed=17)
+    y, g = run_hip(ins, gpu, grad_names=["u", "f_logit"])
+    assert set(g) == {"du", "dfl"}
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+def test_no_grad_forward(gpu):
+    ins = rand_inputs(2, 300, 128, 1, seed=19)
+    y, _ = run_hip(ins, gpu, grad=False)
+    ry, _ = oracle_all(ins)
+    check_all(y, {}, ry, {})
+
+
+def test_register_into_reference_style_dispatch(gpu):
+    """register() inserts the backend into a scan module's _BACKEND_CACHE;
+    dispatch by name then reaches the HIP kernels (scan.py:55-57, :75-76)."""
+    import types
+    from naju_amd import register
+    fake = types.SimpleNamespace(_BACKEND_CACHE={})
+    fn = register("HIP", scan_module=fake)
+    assert fake._BACKEND_CACHE["hip"] is fn
+    ins = rand_inputs(1, 50, 64, 1, seed=23)
+    args = [ins[k].to(gpu) for k in ("u", "f_logit", "i_logit", "B", "C", "D_skip")]
+    y = fake._BACKEND_CACHE["hip"](*args)
+    ry, _ = oracle_all(ins)
+    check_all(y, {}, ry, {})
+
+
+def test_empty_time_axis(gpu):
+    from naju_amd import naju_scan_hip
+    u = torch.zeros(2, 0, 8, device=gpu, requires_grad=True)
+    fl = torch.zeros(2, 0, 8, device=gpu, requires_grad=True)
+    il = torch.zeros(2, 0, 8, device=gpu, requires_grad=True)
+    B = torch.zeros(2, 0, 1, device=gpu, requires_grad=True)
+    C = torch.zeros(2, 0, 1, device=gpu, requires_grad=True)
+    Dk = torch.ones(8, device=gpu, requires_grad=True)
+    y = naju_scan_hip(u, fl, il, B, C, Dk)
+    assert y.shape == (2, 0, 8)
+    y.sum().backward()
+    assert torch.all(Dk.grad == 0)
+
+
+@pytest.mark.parametrize("name", ["c2"])
+def test_full_size_batch_row_slice(gpu, name):
+    """Full BASELINE size on the GPU; batch row 0 checked in full against the
+    oracle (every output except dD depends only on its own batch row), dD
+    checked against sum(dy*u) over the whole batch."""
+    from naju_amd.workloads import config_inputs
+    ins = config_inputs(name, N=1, seed=1, device=gpu)
+    y, g = run_hip(ins, gpu)
+    row = {k: (v[:1].cpu() if v is not None and k != "D_skip" else v) for k, v in ins.items()}
+    row["D_skip"] = ins["D_skip"].cpu()
+    ry, rg = oracle_all(row)
+    g0 = {k: v[:1] for k, v in g.items() if k != "dD"}
+    check_all(y[:1], g0, ry, rg)
+    ref_dD = (ins["dy"].float() * ins["u"].float()).sum((0, 1)).double().cpu().numpy()
+    out_dD = g["dD"].double().cpu().numpy()
+    assert np.max(np.abs(out_dD - ref_dD)) <= 1e-4 * max(1.0, np.abs(ref_dD).max())
