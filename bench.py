@@ -79,12 +79,12 @@ def main():
 
     def fwd():
         _lib.check(L.naju_scan_fwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(h0), p(y), p(ck), None,
-                                   Bsz, T, D, N, *dts, p(ws), ws_bytes, sh))
+                                   Bsz, T, D, N, *dts, 0, p(ws), ws_bytes, sh))
 
     def bwd():
         _lib.check(L.naju_scan_bwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(ck), p(dy), p(du), p(dfl),
-                                   p(dil), p(dB), p(dC), p(dD), p(dh0), Bsz, T, D, N, *dts, p(ws), ws_bytes,
-                                   sh))
+                                   p(dil), p(dB), p(dC), p(dD), p(dh0), Bsz, T, D, N, *dts, 0, p(ws),
+                                   ws_bytes, sh))
 
     s_x, s_g, s_bc = _dt_size(xdt), _dt_size(fl.dtype), _dt_size(Bm.dtype)
     has_h0 = h0 is not None

@@ -21,6 +21,10 @@
  * covers f_logit, i_logit, dfl and dil; the bc dtype covers B, C, dB and dC.
  * Supported: u in {F32, BF16, F16}; gate and bc each either F32 or equal to
  * the u dtype. Arithmetic and the state are float32 throughout.
+ * out_f32 = 0: every output has its input's dtype (y and du: u dtype; dfl,
+ * dil: gate dtype; dB, dC: bc dtype). out_f32 = 1: y, du, dfl, dil, dB and dC
+ * are all float32 (bf16 storage rounding alone is up to 2^-8 relative, so
+ * this is the form in which the kernels' own accuracy is measured).
  *
  * Workspace: naju_scan_workspace_bytes() bytes of device memory that MUST be
  * zero-filled once before its first use; every call leaves it reusable
@@ -77,7 +81,7 @@ size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D,
  * (naju/chunk_affine_triton.py:257-288) and naju_fwd / naju_fwd_chunked
  * (naju/cuda/naju_cuda.cu:241-259, :211-238).
  *   h0   : optional initial state (NULL = zeros, the reference behaviour)
- *   y    : output, u dtype
+ *   y    : output, u dtype (float32 when out_f32)
  *   ckpt : optional (NULL under no_grad); state checkpoint for the backward
  *   hT   : optional final state x_{T-1}
  */
@@ -85,7 +89,7 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit,
                   const void* B, const void* C, const float* D_skip,
                   const float* h0, void* y, float* ckpt, float* hT,
                   int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, void* workspace,
+                  int gate_dtype, int bc_dtype, int out_f32, void* workspace,
                   size_t workspace_bytes, void* stream);
 
 /* Fused backward scan. Replaces naju_bwd (naju/cuda/naju_cuda.cu:261-286),
@@ -103,7 +107,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   const float* ckpt, const void* dy, void* du, void* dfl,
                   void* dil, void* dB, void* dC, float* dD, float* dh0,
                   int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, void* workspace,
+                  int gate_dtype, int bc_dtype, int out_f32, void* workspace,
                   size_t workspace_bytes, void* stream);
 
 /* Reads the workspace's device-side status word (synchronises `stream`).

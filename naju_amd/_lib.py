@@ -52,11 +52,13 @@ def lib():
     L.naju_scan_ckpt_elems.restype = I64
     L.naju_scan_workspace_bytes.argtypes = [I64] * 4 + [I] * 3
     L.naju_scan_workspace_bytes.restype = SZ
-    # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, ws, ws_bytes, stream
-    L.naju_scan_fwd.argtypes = [P] * 10 + [I64] * 4 + [I] * 3 + [P, SZ, P]
+    # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, out_f32, ws, ws_bytes,
+    # stream
+    L.naju_scan_fwd.argtypes = [P] * 10 + [I64] * 4 + [I] * 4 + [P, SZ, P]
     L.naju_scan_fwd.restype = I
-    # u, fl, il, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N, dts, ws, ws_bytes, stream
-    L.naju_scan_bwd.argtypes = [P] * 15 + [I64] * 4 + [I] * 3 + [P, SZ, P]
+    # u, fl, il, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N, dts, out_f32, ws,
+    # ws_bytes, stream
+    L.naju_scan_bwd.argtypes = [P] * 15 + [I64] * 4 + [I] * 4 + [P, SZ, P]
     L.naju_scan_bwd.restype = I
     L.naju_scan_workspace_status.argtypes = [P, P, ctypes.POINTER(ctypes.c_uint32)]
     L.naju_scan_workspace_status.restype = I

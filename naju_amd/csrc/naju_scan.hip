@@ -34,6 +34,7 @@
 
 #include <stdarg.h>
 #include <stdint.h>
+#include <type_traits>
 #include <stdio.h>
 #include <string.h>
 
@@ -267,8 +268,9 @@ __device__ __forceinline__ void finish(const ScanArgs& a, uint32_t tag) {
 // One workgroup = (batch row b, tile of CH = 64*V channels, chunk k of
 // L = W*R timesteps). Forward chunk order: ticket -> (k, tile), chunk-major,
 // so every predecessor (k-1, same tile) holds a smaller ticket.
-template <typename TU, typename TG, int V, int R, int W, bool VEC>
+template <typename TU, typename TG, int V, int R, int W, bool VEC, bool F32O>
 __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
+  using TY = std::conditional_t<F32O, float, TU>;  // y dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
   __shared__ uint32_t s_unit, s_tag;
@@ -410,7 +412,7 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   for (int w = 0; w < wv; ++w)
 #pragma unroll
     for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][c0 + j], s[j], s_Z[w][c0 + j]);
-  TU* __restrict__ py = (TU*)a.y;
+  TY* __restrict__ py = (TY*)a.y;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t = t0 + r;
@@ -418,7 +420,7 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
       float o[V];
 #pragma unroll
       for (int j = 0; j < V; ++j) o[j] = fmaf(q[r][j], s[j], yl[r][j]);
-      st_row<TU, V, VEC>(py + ((int64_t)b * T + t) * D, d0, D, o);
+      st_row<TY, V, VEC>(py + ((int64_t)b * T + t) * D, d0, D, o);
     }
   }
   finish(a, tag);
@@ -430,8 +432,10 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 // future, x̄_t = C_t dy_t + g and the carry leaving is f_t x̄_t. Rows [t0,t1)
 // map g_in -> A g_in + Zb with A = prod f. Chunks run in reverse order
 // (ticket -> chunk K-1-k), so the look-back walks towards larger t.
-template <typename TU, typename TG, int V, int R, int W, bool VEC>
+template <typename TU, typename TG, int V, int R, int W, bool VEC, bool F32O>
 __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
+  using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
+  using TDG = std::conditional_t<F32O, float, TG>;  // dfl, dil dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
   __shared__ uint32_t s_unit, s_tag;
@@ -615,9 +619,9 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
     const int64_t t = t0 + r;
     if (t < T) {
       const int64_t row = ((int64_t)b * T + t) * D;
-      if (a.du) st_row<TU, V, VEC>((TU*)a.du + row, d0, D, xu[r]);
-      if (a.dfl) st_row<TG, V, VEC>((TG*)a.dfl + row, d0, D, xf[r]);
-      if (a.dil) st_row<TG, V, VEC>((TG*)a.dil + row, d0, D, xi[r]);
+      if (a.du) st_row<TDU, V, VEC>((TDU*)a.du + row, d0, D, xu[r]);
+      if (a.dfl) st_row<TDG, V, VEC>((TDG*)a.dfl + row, d0, D, xf[r]);
+      if (a.dil) st_row<TDG, V, VEC>((TDG*)a.dil + row, d0, D, xi[r]);
     }
   }
   if (a.partB || a.partC) {
@@ -770,18 +774,25 @@ bool aligned(const void* p, size_t a) { return p == nullptr || ((uintptr_t)p % a
 
 typedef void (*kern_t)(ScanArgs);
 
-template <typename TU, typename TG, bool VEC>
+template <typename TU, typename TG, bool VEC, bool F32O>
 kern_t pick_n1(bool bwd) {
   constexpr int VF = (sizeof(TU) == 2 && sizeof(TG) == 2) ? 8 : 4;
-  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, 4, kR, kW, VEC> : (kern_t)n1_fwd_kernel<TU, TG, VF, kR, kW, VEC>;
+  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, 4, kR, kW, VEC, F32O>
+             : (kern_t)n1_fwd_kernel<TU, TG, VF, kR, kW, VEC, F32O>;
 }
 
-template <bool VEC>
+template <bool VEC, bool F32O>
 kern_t pick_n1_dt(int x_dt, int g_dt, bool bwd) {
-  if (x_dt == NAJU_DTYPE_F32) return pick_n1<float, float, VEC>(bwd);
+  if (x_dt == NAJU_DTYPE_F32) return pick_n1<float, float, VEC, F32O>(bwd);
   if (x_dt == NAJU_DTYPE_BF16)
-    return g_dt == NAJU_DTYPE_F32 ? pick_n1<bf16_t, float, VEC>(bwd) : pick_n1<bf16_t, bf16_t, VEC>(bwd);
-  return g_dt == NAJU_DTYPE_F32 ? pick_n1<f16_t, float, VEC>(bwd) : pick_n1<f16_t, f16_t, VEC>(bwd);
+    return g_dt == NAJU_DTYPE_F32 ? pick_n1<bf16_t, float, VEC, F32O>(bwd)
+                                  : pick_n1<bf16_t, bf16_t, VEC, F32O>(bwd);
+  return g_dt == NAJU_DTYPE_F32 ? pick_n1<f16_t, float, VEC, F32O>(bwd) : pick_n1<f16_t, f16_t, VEC, F32O>(bwd);
+}
+
+kern_t pick_n1_all(bool vec, bool f32o, int x_dt, int g_dt, bool bwd) {
+  if (vec) return f32o ? pick_n1_dt<true, true>(x_dt, g_dt, bwd) : pick_n1_dt<true, false>(x_dt, g_dt, bwd);
+  return f32o ? pick_n1_dt<false, true>(x_dt, g_dt, bwd) : pick_n1_dt<false, false>(x_dt, g_dt, bwd);
 }
 
 int launch(kern_t k, unsigned grid, unsigned block, hipStream_t st, const ScanArgs& a) {
@@ -821,7 +832,7 @@ size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D, int64_t N,
 
 int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                   const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch, int64_t T,
-                  int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, void* workspace,
+                  int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int out_f32, void* workspace,
                   size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
@@ -843,7 +854,8 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
                 workspace ? workspace_bytes : (size_t)0);
   if (!aligned(workspace, 256)) return fail(NAJU_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   const size_t va_x = l.V * dsize(x_dtype), va_g = l.V * dsize(gate_dtype);
-  const bool vec = (D % l.V == 0) && aligned(u, va_x) && aligned(y, va_x) && aligned(f_logit, va_g) &&
+  const size_t va_y = l.V * (out_f32 ? 4 : dsize(x_dtype));
+  const bool vec = (D % l.V == 0) && aligned(u, va_x) && aligned(y, va_y) && aligned(f_logit, va_g) &&
                    aligned(i_logit, va_g);
   ScanArgs a{};
   a.u = u;
@@ -870,14 +882,15 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   const int64_t wgs = (int64_t)l.K * l.n_tiles;
   if (wgs > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups)", (long long)wgs);
   a.total_wgs = (uint32_t)wgs;
-  kern_t k = vec ? pick_n1_dt<true>(x_dtype, gate_dtype, false) : pick_n1_dt<false>(x_dtype, gate_dtype, false);
+  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, false);
   return launch(k, (unsigned)wgs, 64 * kW, st, a);
 }
 
 int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                   const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil, void* dB,
                   void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+                  int gate_dtype, int bc_dtype, int out_f32, void* workspace, size_t workspace_bytes,
+                  void* stream) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
@@ -904,8 +917,9 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
                 workspace ? workspace_bytes : (size_t)0);
   if (!aligned(workspace, 256)) return fail(NAJU_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   const size_t va_x = l.V * dsize(x_dtype), va_g = l.V * dsize(gate_dtype);
-  const bool vec = (D % l.V == 0) && aligned(u, va_x) && aligned(dy, va_x) && aligned(du, va_x) &&
-                   aligned(f_logit, va_g) && aligned(i_logit, va_g) && aligned(dfl, va_g) && aligned(dil, va_g);
+  const size_t vo_x = out_f32 ? l.V * 4 : va_x, vo_g = out_f32 ? l.V * 4 : va_g;
+  const bool vec = (D % l.V == 0) && aligned(u, va_x) && aligned(dy, va_x) && aligned(du, vo_x) &&
+                   aligned(f_logit, va_g) && aligned(i_logit, va_g) && aligned(dfl, vo_g) && aligned(dil, vo_g);
   ScanArgs a{};
   a.u = u;
   a.fl = f_logit;
@@ -936,13 +950,14 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   const int64_t wgs = (int64_t)l.K * l.n_tiles;
   if (wgs > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups)", (long long)wgs);
   a.total_wgs = (uint32_t)wgs;
-  kern_t k = vec ? pick_n1_dt<true>(x_dtype, gate_dtype, true) : pick_n1_dt<false>(x_dtype, gate_dtype, true);
+  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, true);
   rc = launch(k, (unsigned)wgs, 64 * kW, st, a);
   if (rc) return rc;
   if (dB || dC || dD) {
     const int64_t btn = batch * T * N;
     hipLaunchKernelGGL(fold_partials_kernel, dim3(small_grid(btn > D ? btn : D)), dim3(256), 0, st, a.partB,
-                       a.partC, l.n_dtiles, btn, dB, dC, bc_dtype, a.partD, batch * (int64_t)l.K, D, dD);
+                       a.partC, l.n_dtiles, btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, a.partD,
+                       batch * (int64_t)l.K, D, dD);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;

@@ -17,7 +17,7 @@ Public surface, mirroring /root/reference/naju/scan.py:
   (scan.py:52), so ``NAJU_SCAN_BACKEND=hip`` or ``NajuMixer(scan_backend="hip")``
   then routes unmodified NajuMixer / NajuLM code to these kernels.
 
-Tensor conventions follow the reference (SURVEY of scan.py:7-11): [B,T,D]
+Tensor conventions follow the reference (scan.py:7-11): [B,T,D]
 streams with D contiguous, [B,T,N] for B and C, [D] for D_skip. Inputs are
 never modified. ``y`` has u's dtype (the convention of the GPU training
 backends, chunk_triton.py:181 and chunk_affine_triton.py:288); each gradient
@@ -126,7 +126,7 @@ class NajuScanHip(torch.autograd.Function):
         y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
         _lib.check(L.naju_scan_fwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
-            _ptr(y), _ptr(ckpt), None, Bsz, T, D, N, *dts, ws.data_ptr(), ws.numel(), stream))
+            _ptr(y), _ptr(ckpt), None, Bsz, T, D, N, *dts, 0, ws.data_ptr(), ws.numel(), stream))
         if need_grad:
             ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
             ctx.meta = (Bsz, T, D, N, dts, h0 is not None,
@@ -154,7 +154,7 @@ class NajuScanHip(torch.autograd.Function):
         _lib.check(L.naju_scan_bwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
             _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
-            Bsz, T, D, N, *dts, ws.data_ptr(), ws.numel(), stream))
+            Bsz, T, D, N, *dts, 0, ws.data_ptr(), ws.numel(), stream))
         grads = [du, dfl, dil, dB, dC, dD]
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
         return (*grads, dh0)

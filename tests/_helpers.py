@@ -10,9 +10,18 @@ GRAD_KEYS = {"u": "du", "f_logit": "dfl", "i_logit": "dil", "B": "dB", "C": "dC"
 
 
 def tol_for(dtype):
-    """Tolerance (max-abs error / max|oracle| and ||err||/||oracle||):
-    float32 1e-5; bfloat16/float16 in with float32 accumulation 2e-3."""
-    return 1e-5 if dtype in (torch.float32, torch.float64) else 2e-3
+    """(max_tol, l2_tol) on max-abs error / max|oracle| and ||err||/||oracle||.
+
+    float32 outputs: 1e-5 both -- this covers bf16/fp16 INPUTS with float32
+    outputs too, since the oracle runs on the same quantized inputs.
+    bfloat16 outputs: 2e-3 norm-wise; the max-norm bound is the storage
+    rounding itself, 2^-8 relative (bf16 keeps 8 significant bits), plus
+    float32-level slack. float16 outputs: 2e-3 both (rounding 2^-11)."""
+    if dtype in (torch.float32, torch.float64):
+        return 1e-5, 1e-5
+    if dtype == torch.bfloat16:
+        return 2.0 ** -8 + 2e-5, 2e-3
+    return 2e-3, 2e-3
 
 
 def rand_inputs(batch, T, D, N, seed=0, dtype=torch.float32, f_shift=2.0, i_shift=-1.0,
@@ -73,7 +82,8 @@ def check(name, out, ref, tol):
     out = out.detach().float().cpu().numpy().astype(np.float64) if hasattr(out, "detach") else out
     assert np.all(np.isfinite(out)), f"{name}: non-finite output"
     mx, l2 = rel_err(out, ref)
-    assert mx <= tol and l2 <= tol, f"{name}: rel err max {mx:.3e} l2 {l2:.3e} > tol {tol:.1e}"
+    tmx, tl2 = tol
+    assert mx <= tmx and l2 <= tl2, f"{name}: rel err max {mx:.3e} l2 {l2:.3e} > tol ({tmx:.2e}, {tl2:.1e})"
     return mx, l2
 
 
@@ -85,3 +95,43 @@ def check_all(y, grads, ref_y, ref_g, skip=()):
             continue
         res[k] = check(k, v, ref_g[k], tol_for(v.dtype))
     return res
+
+
+_DTC = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def run_abi(ins, device, out_f32=True):
+    """Forward + backward through the C ABI directly (naju_scan_fwd/_bwd), with
+    every output in float32 when out_f32. Returns (y, grads) like run_hip."""
+    from naju_amd import _lib
+    L = _lib.lib()
+    t = {k: (v.to(device).contiguous() if v is not None else None) for k, v in ins.items()}
+    u, fl, il, Bm, Cm = t["u"], t["f_logit"], t["i_logit"], t["B"], t["C"]
+    Dk = t["D_skip"].float().contiguous()
+    h0 = t.get("h0")
+    dy = t["dy"]
+    Bsz, T, D = u.shape
+    N = Bm.shape[-1]
+    dts = (_DTC[u.dtype], _DTC[fl.dtype], _DTC[Bm.dtype])
+    od = lambda x: torch.float32 if out_f32 else x.dtype  # noqa: E731
+    y = torch.empty(u.shape, dtype=od(u), device=device)
+    ck = torch.empty(max(1, L.naju_scan_ckpt_elems(Bsz, T, D, N, *dts)), dtype=torch.float32, device=device)
+    nb = L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)
+    ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    p = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+    _lib.check(L.naju_scan_fwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(h0), p(y), p(ck), None,
+                               Bsz, T, D, N, *dts, int(out_f32), p(ws), ws.numel(), st))
+    g = {"du": torch.empty(u.shape, dtype=od(u), device=device),
+         "dfl": torch.empty(u.shape, dtype=od(fl), device=device),
+         "dil": torch.empty(u.shape, dtype=od(il), device=device),
+         "dB": torch.empty(Bm.shape, dtype=od(Bm), device=device),
+         "dC": torch.empty(Bm.shape, dtype=od(Cm), device=device),
+         "dD": torch.empty(D, dtype=torch.float32, device=device)}
+    if h0 is not None:
+        g["dh0"] = torch.empty(h0.shape, dtype=torch.float32, device=device)
+    _lib.check(L.naju_scan_bwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(ck), p(dy), p(g["du"]),
+                               p(g["dfl"]), p(g["dil"]), p(g["dB"]), p(g["dC"]), p(g["dD"]), p(g.get("dh0")),
+                               Bsz, T, D, N, *dts, int(out_f32), p(ws), ws.numel(), st))
+    torch.cuda.synchronize()
+    return y, g
