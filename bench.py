@@ -45,6 +45,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flush", action="store_true",
                     help="also time steps with a 1 GiB cache-flush write before each step")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run 3 plain 512 MiB device copies (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -58,6 +60,14 @@ def main():
 
     L = _lib.lib()
     dev = torch.device("cuda", 0)
+    if args.calib_copy:
+        src = torch.ones(1 << 27, dtype=torch.float32, device=dev)   # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calib-copy: 3 x copy of {src.numel() * 4} bytes", file=sys.stderr, flush=True)
+        del src, dst
     cfg = CONFIGS[args.config]
     Bsz, T, D, N = cfg["batch"], cfg["T"], cfg["D"], args.N
     ins = config_inputs(args.config, N=N, seed=0, device=dev)

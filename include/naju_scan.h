@@ -111,9 +111,11 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   size_t workspace_bytes, void* stream);
 
 /* Reads the workspace's device-side status word (synchronises `stream`).
- * 0 = healthy; nonzero = a carry hand-off between workgroups exceeded its
- * bounded wait and the affected outputs were set to NaN. No counterpart in
- * the reference (its kernels have no cross-workgroup waits). */
+ * 0 = healthy; 1 = a carry hand-off between workgroups exceeded its
+ * bounded wait and the affected outputs were set to NaN; 2 = a ticket
+ * counter held a value out of range (a workspace that was not zero-filled
+ * before first use), and the affected workgroups did nothing. No counterpart
+ * in the reference (its kernels have no cross-workgroup waits). */
 int naju_scan_workspace_status(const void* workspace, void* stream,
                                uint32_t* status);
 

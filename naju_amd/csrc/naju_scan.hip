@@ -34,6 +34,7 @@
 
 #include <stdarg.h>
 #include <stdint.h>
+#include <atomic>
 #include <type_traits>
 #include <stdio.h>
 #include <string.h>
@@ -132,81 +133,20 @@ __device__ __forceinline__ void st_word(uint64_t* p, float v, uint32_t tag) {
 __device__ __forceinline__ bool word_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
-// Workspace header words.
-enum { HDR_TICKET = 0, HDR_DONE = 1, HDR_EPOCH = 2, HDR_STATUS = 3 };
+// Workspace header, a fixed-size region that no other part of any layout
+// ever overlaps (so its counters, which must start at zero, are only ever
+// written by the ticket logic below): word 0 is the status word; tile t's
+// ticket counter is word kCtrBase + t*kCtrStride, t < kMaxTiles.
+enum { HDR_STATUS = 0 };
+constexpr int kCtrBase = 64;
+constexpr int kCtrStride = 4;
+constexpr int kMaxTiles = 1 << 16;
+constexpr size_t kHeaderBytes = ((size_t)kCtrBase + (size_t)kMaxTiles * kCtrStride) * sizeof(uint32_t);
 // Bound on idle polls of one look-back. A poll is a few device-scope loads
 // plus a short sleep (~1 us), so the bound is about a second, far beyond any
 // legitimate wait (microseconds); past it the carry becomes NaN and the
 // status word records the failure, so every wave still exits.
 constexpr uint32_t kSpinLimit = 1u << 20;
-
-// Decoupled look-back for the V channels of one lane.
-//   aggF/aggZ/incl point at this lane's words of the first predecessor chunk;
-//   consecutive predecessors are `agg_step` / `incl_step` words apart (the
-//   sign gives the direction). At most `max_steps` predecessors exist, the
-//   last of which always publishes an inclusive carry.
-// Result: s = the inclusive carry of the nearest predecessor mapped through
-//   the aggregates in between (Z_acc + F_acc * s).
-template <int V>
-__device__ void look_back(const uint64_t* aggF, const uint64_t* aggZ, const uint64_t* incl, int64_t agg_step,
-                          int64_t incl_step, int max_steps, uint32_t tag, uint32_t* hdr, float (&s)[V]) {
-  float aF[V], aZ[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) {
-    aF[j] = 1.f;
-    aZ[j] = 0.f;
-  }
-  int m = 0;
-  bool done = false;
-  uint32_t idle = 0;
-  while (true) {
-    bool moved = false;
-    if (!done) {
-      const uint64_t* pi = incl + (int64_t)m * incl_step;
-      uint64_t wi[V];
-      bool ok = true;
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        wi[j] = ld_word(pi + j);
-        ok = ok && word_ok(wi[j], tag);
-      }
-      if (ok) {
-#pragma unroll
-        for (int j = 0; j < V; ++j) s[j] = fmaf(aF[j], word_val(wi[j]), aZ[j]);
-        done = true;
-        moved = true;
-      } else if (m + 1 < max_steps) {
-        const uint64_t* pf = aggF + (int64_t)m * agg_step;
-        const uint64_t* pz = aggZ + (int64_t)m * agg_step;
-        uint64_t wf[V], wz[V];
-        bool ok2 = true;
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          wf[j] = ld_word(pf + j);
-          wz[j] = ld_word(pz + j);
-          ok2 = ok2 && word_ok(wf[j], tag) && word_ok(wz[j], tag);
-        }
-        if (ok2) {
-#pragma unroll
-          for (int j = 0; j < V; ++j) {
-            aZ[j] = fmaf(aF[j], word_val(wz[j]), aZ[j]);
-            aF[j] *= word_val(wf[j]);
-          }
-          ++m;
-          moved = true;
-        }
-      }
-      if (!moved && ++idle > kSpinLimit) {
-        __hip_atomic_store(hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int j = 0; j < V; ++j) s[j] = __builtin_nanf("");
-        done = true;
-      }
-    }
-    if (__all(done)) break;
-    if (!moved) __builtin_amdgcn_s_sleep(1);
-  }
-}
 
 // Kernel arguments (one struct for every kernel; unused fields are null).
 struct ScanArgs {
@@ -238,28 +178,146 @@ struct ScanArgs {
   int n_dtiles;
   int n_tiles;
   int K;
-  uint32_t total_wgs;
+  uint32_t tag;  // this launch's tag (nonzero, new for every launch)
 };
 
-__device__ __forceinline__ void take_ticket(const ScanArgs& a, uint32_t* s_unit, uint32_t* s_tag) {
+// Workgroup blockIdx.x serves tile blockIdx.x % n_tiles; the chunk comes from
+// that tile's ticket counter, so a tile's chunks are handed out in the order
+// its workgroups start and every chunk a workgroup waits on is already held
+// by a running workgroup. The workgroup that draws the tile's last ticket
+// rewinds the counter for the next launch (all K tickets are taken by then).
+// Returns false (after recording it in the status word) if the counter held
+// a value outside [0, K): a workspace that was not zero-filled. The caller
+// then exits without touching memory.
+__device__ __forceinline__ bool take_ticket(const ScanArgs& a, int tile, uint32_t* s_ticket) {
   if (threadIdx.x == 0) {
-    *s_unit = __hip_atomic_fetch_add(a.hdr + HDR_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_tag = __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    uint32_t* ctr = a.hdr + kCtrBase + (int64_t)tile * kCtrStride;
+    const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == (uint32_t)a.K - 1) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t >= (uint32_t)a.K) __hip_atomic_store(a.hdr + HDR_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_ticket = t;
   }
   __syncthreads();
+  return *s_ticket < (uint32_t)a.K;
 }
 
-// The workgroup that finishes last rewinds the ticket and completion counters
-// and advances the epoch, leaving the workspace ready for the next launch.
-__device__ __forceinline__ void finish(const ScanArgs& a, uint32_t tag) {
-  if (threadIdx.x == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == a.total_wgs - 1) {
-      __hip_atomic_store(a.hdr + HDR_TICKET, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.hdr + HDR_EPOCH, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// ------------------------------------------------ workgroup-wide look-back
+//
+// A chunk's map, published as "aggregate" words, and its inclusive carry,
+// published as "inclusive" words, live in the workspace at
+//   agg [chunk][tile][2][CH]   (F block, then Z block)
+//   incl[chunk][tile][CH]
+// with channel slot cs = j*64 + lane (j < V), so every wave-wide access of
+// one j touches 64 consecutive 8-byte words.
+//
+// Each round, wave w polls predecessors base + dir*(p*W + w), p < P, so one
+// memory round trip covers a window of W*P predecessors. A predecessor is
+// usable when all CH channels of a word kind carry the current tag (a wave
+// vote). Wave 0 then walks the window in order: aggregates are composed
+// until the first inclusive carry, which ends the walk; a predecessor that
+// is not ready yet ends the round and the next round resumes there.
+template <int V, int W, int P>
+struct LookShared {
+  float S[W * P][64 * V];
+  float F[W * P][64 * V];
+  float Z[W * P][64 * V];
+  int stat[W * P];  // 0 = not ready, 1 = aggregate, 2 = inclusive
+  int ctl[2];       // done, number of predecessors consumed
+};
+
+// Carry entering chunk k (dir = -1: forward, predecessors k-1, k-2, ...;
+// dir = +1: backward, k+1, k+2, ...). Result valid in wave 0's lanes.
+template <int V, int W, int P>
+__device__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, int tile, int dir, uint32_t tag,
+                             int lane, int wv, float (&out)[V]) {
+  constexpr int CH = 64 * V;
+  constexpr int WP = W * P;
+  float aF[V], aZ[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    aF[j] = 1.f;
+    aZ[j] = 0.f;
+    out[j] = 0.f;
+  }
+  int base = k + dir;
+  uint32_t idle = 0;
+  while (true) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int slot = p * W + wv;
+      const int c = base + dir * slot;
+      const bool inr = c >= 0 && c < a.K;
+      bool iok = inr, aok = inr;
+      float S[V], F[V], Z[V];
+      if (inr) {
+        const uint64_t* pi = a.incl + ((int64_t)c * a.n_tiles + tile) * CH + lane;
+        const uint64_t* pa = a.agg + ((int64_t)c * a.n_tiles + tile) * 2 * CH + lane;
+        uint64_t wi[V], wf[V], wz[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          wi[j] = ld_word(pi + j * 64);
+          wf[j] = ld_word(pa + j * 64);
+          wz[j] = ld_word(pa + CH + j * 64);
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          iok = iok && word_ok(wi[j], tag);
+          aok = aok && word_ok(wf[j], tag) && word_ok(wz[j], tag);
+          S[j] = word_val(wi[j]);
+          F[j] = word_val(wf[j]);
+          Z[j] = word_val(wz[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) S[j] = F[j] = Z[j] = 0.f;
+      }
+      iok = __all(iok);
+      aok = __all(aok);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        sh.S[slot][j * 64 + lane] = S[j];
+        sh.F[slot][j * 64 + lane] = F[j];
+        sh.Z[slot][j * 64 + lane] = Z[j];
+      }
+      if (lane == 0) sh.stat[slot] = iok ? 2 : (aok ? 1 : 0);
     }
+    __syncthreads();
+    if (wv == 0) {
+      int consumed = 0, done = 0;
+      for (int slot = 0; slot < WP; ++slot) {
+        const int st = sh.stat[slot];
+        if (st == 2) {
+#pragma unroll
+          for (int j = 0; j < V; ++j) out[j] = fmaf(aF[j], sh.S[slot][j * 64 + lane], aZ[j]);
+          done = 1;
+          break;
+        }
+        if (st != 1) break;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          aZ[j] = fmaf(aF[j], sh.Z[slot][j * 64 + lane], aZ[j]);
+          aF[j] *= sh.F[slot][j * 64 + lane];
+        }
+        ++consumed;
+      }
+      if (!done && consumed == 0 && ++idle > kSpinLimit) {
+        // Bounded wait exceeded: record it and end with a NaN carry.
+        if (lane == 0) __hip_atomic_store(a.hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int j = 0; j < V; ++j) out[j] = __builtin_nanf("");
+        done = 1;
+      }
+      if (lane == 0) {
+        sh.ctl[0] = done;
+        sh.ctl[1] = consumed;
+      }
+    }
+    __syncthreads();
+    const int done = sh.ctl[0];
+    const int consumed = sh.ctl[1];
+    if (done) break;
+    base += dir * consumed;
+    if (consumed == 0) __builtin_amdgcn_s_sleep(2);
   }
 }
 
@@ -267,29 +325,30 @@ __device__ __forceinline__ void finish(const ScanArgs& a, uint32_t tag) {
 //
 // One workgroup = (batch row b, tile of CH = 64*V channels, chunk k of
 // L = W*R timesteps). Forward chunk order: ticket -> (k, tile), chunk-major,
-// so every predecessor (k-1, same tile) holds a smaller ticket.
-template <typename TU, typename TG, int V, int R, int W, bool VEC, bool F32O>
+// so every predecessor (k-1, same tile) holds a smaller ticket. Lane `lane`
+// owns channels d0 .. d0+V-1 (d0 = tile start + lane*V); its slot for
+// channel j in LDS and workspace arrays is j*64 + lane.
+template <typename TU, typename TG, int V, int R, int W, int P, bool VEC, bool F32O>
 __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   using TY = std::conditional_t<F32O, float, TU>;  // y dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
-  __shared__ uint32_t s_unit, s_tag;
+  __shared__ uint32_t s_ticket;
   __shared__ float s_F[W][CH];
   __shared__ float s_Z[W][CH];
   __shared__ float s_in[CH];
+  __shared__ LookShared<V, W, P> s_lb;
 
-  take_ticket(a, &s_unit, &s_tag);
-  const uint32_t unit = __builtin_amdgcn_readfirstlane(s_unit);
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  if (!take_ticket(a, tile, &s_ticket)) return;
+  const int k = (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  const uint32_t tag = a.tag;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int k = (int)(unit / (uint32_t)a.n_tiles);
-  const int tile = (int)unit - k * a.n_tiles;
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
-  const int c0 = lane * V;
   const int64_t T = a.T, D = a.D;
-  const int64_t d0 = (int64_t)dtile * CH + c0;
+  const int64_t d0 = (int64_t)dtile * CH + lane * V;
   const int t0 = k * L + wv * R;
 
   const TU* __restrict__ pu = (const TU*)a.u;
@@ -310,9 +369,8 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t = t0 + r;
-    const bool tv = t < T;
     const int64_t row = ((int64_t)b * T + t) * D;
-    if (tv) {
+    if (t < T) {
       ld_row<TU, V, VEC>(pu + row, d0, D, xu[r]);
       ld_row<TG, V, VEC>(pf + row, d0, D, xf[r]);
       ld_row<TG, V, VEC>(pi + row, d0, D, xi[r]);
@@ -325,7 +383,7 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
     }
   }
 
-  // ---- pass 1: local scan from zero; keep y = yl + q * s_in per element
+  // ---- pass 1: local scan from zero; keep y = yl + q * (carry) per element
   float F[V], Z[V];
   float yl[R][V], q[R][V];
 #pragma unroll
@@ -350,14 +408,16 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    s_F[wv][c0 + j] = F[j];
-    s_Z[wv][c0 + j] = Z[j];
+    s_F[wv][j * 64 + lane] = F[j];
+    s_Z[wv][j * 64 + lane] = Z[j];
   }
   __syncthreads();
 
-  // ---- wave 0: chunk map, publish, look back, publish inclusive carry
+  // ---- chunk map (wave 0), publish, look back, publish the inclusive carry
+  float Fw[V], Zw[V], sin[V];
+  uint64_t* my_agg = a.agg + ((int64_t)k * a.n_tiles + tile) * 2 * CH + lane;
+  uint64_t* my_incl = a.incl + ((int64_t)k * a.n_tiles + tile) * CH + lane;
   if (wv == 0) {
-    float Fw[V], Zw[V], sin[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       Fw[j] = 1.f;
@@ -367,30 +427,27 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
     for (int w = 0; w < W; ++w)
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float f = s_F[w][c0 + j];
-        Zw[j] = fmaf(f, Zw[j], s_Z[w][c0 + j]);
+        const float f = s_F[w][j * 64 + lane];
+        Zw[j] = fmaf(f, Zw[j], s_Z[w][j * 64 + lane]);
         Fw[j] *= f;
       }
-    const int64_t agg_step = (int64_t)a.n_tiles * 2 * CH;
-    const int64_t incl_step = (int64_t)a.n_tiles * CH;
-    uint64_t* my_agg = a.agg + ((int64_t)k * a.n_tiles + tile) * 2 * CH + c0;
-    uint64_t* my_incl = a.incl + ((int64_t)k * a.n_tiles + tile) * CH + c0;
-    if (k == 0) {
-#pragma unroll
-      for (int j = 0; j < V; ++j) sin[j] = (a.h0 && dok[j]) ? a.h0[(int64_t)b * D + d0 + j] : 0.f;
-    } else {
+    if (k > 0) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        st_word(my_agg + j, Fw[j], tag);
-        st_word(my_agg + CH + j, Zw[j], tag);
+        st_word(my_agg + j * 64, Fw[j], tag);
+        st_word(my_agg + CH + j * 64, Zw[j], tag);
       }
-      look_back<V>(my_agg - agg_step, my_agg - agg_step + CH, my_incl - incl_step, -agg_step, -incl_step, k, tag,
-                   a.hdr, sin);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) sin[j] = (a.h0 && dok[j]) ? a.h0[(int64_t)b * D + d0 + j] : 0.f;
     }
+  }
+  if (k > 0) wg_look_back<V, W, P>(a, s_lb, k, tile, -1, tag, lane, wv, sin);
+  if (wv == 0) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      st_word(my_incl + j, fmaf(Fw[j], sin[j], Zw[j]), tag);
-      s_in[c0 + j] = sin[j];
+      st_word(my_incl + j * 64, fmaf(Fw[j], sin[j], Zw[j]), tag);
+      s_in[j * 64 + lane] = sin[j];
     }
     if (a.ckpt) {
 #pragma unroll
@@ -408,10 +465,10 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   // ---- pass 2: this wave's carry, then y
   float s[V];
 #pragma unroll
-  for (int j = 0; j < V; ++j) s[j] = s_in[c0 + j];
+  for (int j = 0; j < V; ++j) s[j] = s_in[j * 64 + lane];
   for (int w = 0; w < wv; ++w)
 #pragma unroll
-    for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][c0 + j], s[j], s_Z[w][c0 + j]);
+    for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][j * 64 + lane], s[j], s_Z[w][j * 64 + lane]);
   TY* __restrict__ py = (TY*)a.y;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -423,7 +480,6 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
       st_row<TY, V, VEC>(py + ((int64_t)b * T + t) * D, d0, D, o);
     }
   }
-  finish(a, tag);
 }
 
 // ----------------------------------------------------------- N = 1 backward
@@ -431,32 +487,31 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 // Adjoint in carry form: with g = f_{t+1} x̄_{t+1} entering row t from the
 // future, x̄_t = C_t dy_t + g and the carry leaving is f_t x̄_t. Rows [t0,t1)
 // map g_in -> A g_in + Zb with A = prod f. Chunks run in reverse order
-// (ticket -> chunk K-1-k), so the look-back walks towards larger t.
-template <typename TU, typename TG, int V, int R, int W, bool VEC, bool F32O>
+// (ticket -> chunk K-1-k), so the look-back walks towards larger t. The
+// forward state entering the chunk comes from the forward's checkpoint.
+template <typename TU, typename TG, int V, int R, int W, int P, bool VEC, bool F32O>
 __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
   using TDG = std::conditional_t<F32O, float, TG>;  // dfl, dil dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
-  __shared__ uint32_t s_unit, s_tag;
+  __shared__ uint32_t s_ticket;
   __shared__ float s_F[W][CH];
   __shared__ float s_Z[W][CH];
   __shared__ float s_Zb[W][CH];
   __shared__ float s_g[CH];
+  __shared__ LookShared<V, W, P> s_lb;
 
-  take_ticket(a, &s_unit, &s_tag);
-  const uint32_t unit = __builtin_amdgcn_readfirstlane(s_unit);
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  if (!take_ticket(a, tile, &s_ticket)) return;
+  const int k = a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  const uint32_t tag = a.tag;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int kk = (int)(unit / (uint32_t)a.n_tiles);
-  const int tile = (int)unit - kk * a.n_tiles;
-  const int k = a.K - 1 - kk;
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
-  const int c0 = lane * V;
   const int64_t T = a.T, D = a.D;
-  const int64_t d0 = (int64_t)dtile * CH + c0;
+  const int64_t d0 = (int64_t)dtile * CH + lane * V;
   const int t0 = k * L + wv * R;
 
   const TU* __restrict__ pu = (const TU*)a.u;
@@ -477,9 +532,8 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t = t0 + r;
-    const bool tv = t < T;
     const int64_t row = ((int64_t)b * T + t) * D;
-    if (tv) {
+    if (t < T) {
       ld_row<TU, V, VEC>(pu + row, d0, D, xu[r]);
       ld_row<TG, V, VEC>(pfl + row, d0, D, xf[r]);
       ld_row<TG, V, VEC>(pil + row, d0, D, xi[r]);
@@ -492,6 +546,9 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
       Bt[r] = Ct[r] = 0.f;
     }
   }
+  float s[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) s[j] = dok[j] ? a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] : 0.f;
 
   // ---- pass 1: gates, forward map (F, Z) and adjoint map (F, Zb) of the rows
   float F[V], Z[V], G[V];
@@ -519,67 +576,61 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
     for (int j = 0; j < V; ++j) G[j] = xf[r][j] * fmaf(xg[r][j], Ct[r], G[j]);
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    s_F[wv][c0 + j] = F[j];
-    s_Z[wv][c0 + j] = Z[j];
-    s_Zb[wv][c0 + j] = G[j];
+    s_F[wv][j * 64 + lane] = F[j];
+    s_Z[wv][j * 64 + lane] = Z[j];
+    s_Zb[wv][j * 64 + lane] = G[j];
   }
   __syncthreads();
 
-  // ---- wave 0: chunk adjoint map, publish, look ahead, publish inclusive
+  // ---- chunk adjoint map (wave 0), publish, look ahead, publish inclusive
+  float A[V], Zb[V], gin[V];
+  uint64_t* my_agg = a.agg + ((int64_t)k * a.n_tiles + tile) * 2 * CH + lane;
+  uint64_t* my_incl = a.incl + ((int64_t)k * a.n_tiles + tile) * CH + lane;
   if (wv == 0) {
-    float A[V], Zb[V], gin[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       A[j] = 1.f;
       Zb[j] = 0.f;
+      gin[j] = 0.f;
     }
 #pragma unroll
     for (int w = W - 1; w >= 0; --w)
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float f = s_F[w][c0 + j];
-        Zb[j] = fmaf(f, Zb[j], s_Zb[w][c0 + j]);
+        const float f = s_F[w][j * 64 + lane];
+        Zb[j] = fmaf(f, Zb[j], s_Zb[w][j * 64 + lane]);
         A[j] *= f;
       }
-    const int64_t agg_step = (int64_t)a.n_tiles * 2 * CH;
-    const int64_t incl_step = (int64_t)a.n_tiles * CH;
-    uint64_t* my_agg = a.agg + ((int64_t)k * a.n_tiles + tile) * 2 * CH + c0;
-    uint64_t* my_incl = a.incl + ((int64_t)k * a.n_tiles + tile) * CH + c0;
-    if (k == a.K - 1) {
-#pragma unroll
-      for (int j = 0; j < V; ++j) gin[j] = 0.f;
-    } else {
+    if (k < a.K - 1) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        st_word(my_agg + j, A[j], tag);
-        st_word(my_agg + CH + j, Zb[j], tag);
+        st_word(my_agg + j * 64, A[j], tag);
+        st_word(my_agg + CH + j * 64, Zb[j], tag);
       }
-      look_back<V>(my_agg + agg_step, my_agg + agg_step + CH, my_incl + incl_step, agg_step, incl_step,
-                   a.K - 1 - k, tag, a.hdr, gin);
     }
+  }
+  if (k < a.K - 1) wg_look_back<V, W, P>(a, s_lb, k, tile, +1, tag, lane, wv, gin);
+  if (wv == 0) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const float gout = fmaf(A[j], gin[j], Zb[j]);
-      st_word(my_incl + j, gout, tag);
-      s_g[c0 + j] = gin[j];
+      st_word(my_incl + j * 64, gout, tag);
+      s_g[j * 64 + lane] = gin[j];
       if (a.dh0 && k == 0 && dok[j]) a.dh0[(int64_t)b * D + d0 + j] = gout;
     }
   }
   __syncthreads();
 
   // ---- pass 2: exact carries of this wave's rows
-  float s[V], g[V];
+  float g[V];
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
-    s[j] = dok[j] ? a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] : 0.f;
-    g[j] = s_g[c0 + j];
-  }
+  for (int j = 0; j < V; ++j) g[j] = s_g[j * 64 + lane];
   for (int w = 0; w < wv; ++w)
 #pragma unroll
-    for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][c0 + j], s[j], s_Z[w][c0 + j]);
+    for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][j * 64 + lane], s[j], s_Z[w][j * 64 + lane]);
   for (int w = W - 1; w > wv; --w)
 #pragma unroll
-    for (int j = 0; j < V; ++j) g[j] = fmaf(s_F[w][c0 + j], g[j], s_Zb[w][c0 + j]);
+    for (int j = 0; j < V; ++j) g[j] = fmaf(s_F[w][j * 64 + lane], g[j], s_Zb[w][j * 64 + lane]);
 
   // forward states x_{t-1} of every row (x_{t0-1} = s)
   float xp[R][V];
@@ -640,25 +691,23 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   if (a.partD) {
     __syncthreads();  // every wave has read s_Z for its carry
 #pragma unroll
-    for (int j = 0; j < V; ++j) s_Z[wv][c0 + j] = dDs[j];
+    for (int j = 0; j < V; ++j) s_Z[wv][j * 64 + lane] = dDs[j];
     __syncthreads();
     if (wv == 0) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         float acc = 0.f;
-        for (int w = 0; w < W; ++w) acc += s_Z[w][c0 + j];
+        for (int w = 0; w < W; ++w) acc += s_Z[w][j * 64 + lane];
         if (dok[j]) a.partD[((int64_t)b * a.K + k) * D + d0 + j] = acc;
       }
     }
   }
-  finish(a, tag);
 }
 
-// Folds the per-tile partial sums: dB/dC over channel tiles, dD over
-// (batch, chunk). Fixed summation order, so results are run-to-run identical.
-__global__ void fold_partials_kernel(const float* __restrict__ partB, const float* __restrict__ partC,
-                                     int n_parts, int64_t btn, void* dB, void* dC, int bc_dt,
-                                     const float* __restrict__ partD, int64_t n_rows, int64_t D, float* dD) {
+// Folds the per-tile partial sums of dB and dC over the channel tiles, in
+// tile order (run-to-run identical).
+__global__ void fold_bc_kernel(const float* __restrict__ partB, const float* __restrict__ partC, int n_parts,
+                               int64_t btn, void* dB, void* dC, int bc_dt) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
     if (dB) {
@@ -672,13 +721,29 @@ __global__ void fold_partials_kernel(const float* __restrict__ partB, const floa
       st_any(dC, bc_dt, i, s);
     }
   }
-  if (dD) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < D; i += stride) {
-      float s = 0.f;
-      for (int64_t r = 0; r < n_rows; ++r) s += partD[r * D + i];
-      dD[i] = s;
+}
+
+// dD[d] = sum over the n_rows partial rows of partD[row][d]. One block per
+// 64 channels; wave w sums rows w, w+4, ... with four interleaved
+// accumulators, then the four waves' sums are added in wave order
+// (run-to-run identical).
+__global__ __launch_bounds__(256) void fold_d_kernel(const float* __restrict__ partD, int64_t n_rows, int64_t D,
+                                                     float* __restrict__ dD) {
+  __shared__ float s_acc[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t d = (int64_t)blockIdx.x * 64 + lane;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (d < D) {
+    int64_t r = w;
+    for (; r + 12 < n_rows; r += 16) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] += partD[(r + 4 * u) * D + d];
     }
+    for (int u = 0; r < n_rows; r += 4, ++u) acc[u & 3] += partD[r * D + d];
   }
+  s_acc[w][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (w == 0 && d < D) dD[d] = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
 }
 
 // Fills n float32 values with src[i] (or 0 when src is null); used for the
@@ -697,6 +762,15 @@ __global__ void zero_any_kernel(void* dst, int dt, int64_t n) {
 
 thread_local char g_err[512] = "";
 
+// Tags of the look-back words: one new nonzero value per launch, process-wide
+// (zero-filled workspaces hold tag 0, so a fresh workspace is never misread).
+std::atomic<uint32_t> g_tag{0};
+uint32_t next_tag() {
+  uint32_t t = g_tag.fetch_add(1, std::memory_order_relaxed) + 1;
+  while (t == 0) t = g_tag.fetch_add(1, std::memory_order_relaxed) + 1;
+  return t;
+}
+
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -707,17 +781,40 @@ int fail(int code, const char* fmt, ...) {
 
 size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 
-// Tile geometry of the N = 1 kernels: R rows per wave, W waves per
-// workgroup, V channels per lane (16-byte loads when every stream is 2-byte).
-constexpr int kR = 4;
-constexpr int kW = 8;
+// Tile geometry of the N = 1 kernels, per direction: V channels per lane,
+// R rows per wave, W waves per workgroup (chunk L = W*R rows), P look-back
+// slots polled per wave and round (window W*P chunks). Both directions use
+// the same chunk length, which fixes the checkpoint layout.
+#ifndef NAJU_F_V
+#define NAJU_F_V 2
+#endif
+#ifndef NAJU_F_R
+#define NAJU_F_R 16
+#endif
+#ifndef NAJU_F_W
+#define NAJU_F_W 4
+#endif
+#ifndef NAJU_F_P
+#define NAJU_F_P 4
+#endif
+#ifndef NAJU_B_V
+#define NAJU_B_V 2
+#endif
+#ifndef NAJU_B_R
+#define NAJU_B_R 8
+#endif
+#ifndef NAJU_B_W
+#define NAJU_B_W 8
+#endif
+#ifndef NAJU_B_P
+#define NAJU_B_P 2
+#endif
+constexpr int kFV = NAJU_F_V, kFR = NAJU_F_R, kFW = NAJU_F_W, kFP = NAJU_F_P;
+constexpr int kBV = NAJU_B_V, kBR = NAJU_B_R, kBW = NAJU_B_W, kBP = NAJU_B_P;
+constexpr int kChunk = kFR * kFW;
+static_assert(kBR * kBW == kChunk, "forward and backward chunk lengths must match");
 
-// The backward keeps four streams and the forward states of its rows in
-// registers, so it uses V = 4 throughout; the chunk length L (which fixes the
-// checkpoint layout) is the same in both directions.
-int n1_vec_width(int x_dt, int g_dt, bool bwd) {
-  return (!bwd && dsize(x_dt) == 2 && dsize(g_dt) == 2) ? 8 : 4;
-}
+int n1_vec_width(bool bwd) { return bwd ? kBV : kFV; }
 
 struct Layout {
   int V, CH, L, K, n_dtiles, n_tiles;
@@ -728,14 +825,16 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd) {
   Layout l{};
-  l.V = n1_vec_width(x_dt, g_dt, bwd);
+  (void)x_dt;
+  (void)g_dt;
+  l.V = n1_vec_width(bwd);
   l.CH = 64 * l.V;
-  l.L = kR * kW;
+  l.L = kChunk;
   l.K = (int)((T + l.L - 1) / l.L);
   l.n_dtiles = (int)((D + l.CH - 1) / l.CH);
   l.n_tiles = (int)(batch * l.n_dtiles);
   const size_t units = (size_t)l.K * l.n_tiles;
-  size_t off = 256;  // header
+  size_t off = align_up(kHeaderBytes);
   l.off_agg = off;
   off = align_up(off + units * 2 * l.CH * sizeof(uint64_t));
   l.off_incl = off;
@@ -776,9 +875,8 @@ typedef void (*kern_t)(ScanArgs);
 
 template <typename TU, typename TG, bool VEC, bool F32O>
 kern_t pick_n1(bool bwd) {
-  constexpr int VF = (sizeof(TU) == 2 && sizeof(TG) == 2) ? 8 : 4;
-  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, 4, kR, kW, VEC, F32O>
-             : (kern_t)n1_fwd_kernel<TU, TG, VF, kR, kW, VEC, F32O>;
+  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, kBV, kBR, kBW, kBP, VEC, F32O>
+             : (kern_t)n1_fwd_kernel<TU, TG, kFV, kFR, kFW, kFP, VEC, F32O>;
 }
 
 template <bool VEC, bool F32O>
@@ -880,10 +978,12 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   a.n_tiles = l.n_tiles;
   a.K = l.K;
   const int64_t wgs = (int64_t)l.K * l.n_tiles;
-  if (wgs > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups)", (long long)wgs);
-  a.total_wgs = (uint32_t)wgs;
+  if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
+    return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
+                l.n_tiles);
+  a.tag = next_tag();
   kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, false);
-  return launch(k, (unsigned)wgs, 64 * kW, st, a);
+  return launch(k, (unsigned)wgs, 64 * kFW, st, a);
 }
 
 int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
@@ -948,16 +1048,21 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   a.n_tiles = l.n_tiles;
   a.K = l.K;
   const int64_t wgs = (int64_t)l.K * l.n_tiles;
-  if (wgs > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups)", (long long)wgs);
-  a.total_wgs = (uint32_t)wgs;
+  if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
+    return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
+                l.n_tiles);
+  a.tag = next_tag();
   kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, true);
-  rc = launch(k, (unsigned)wgs, 64 * kW, st, a);
+  rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
   if (rc) return rc;
   if (dB || dC || dD) {
     const int64_t btn = batch * T * N;
-    hipLaunchKernelGGL(fold_partials_kernel, dim3(small_grid(btn > D ? btn : D)), dim3(256), 0, st, a.partB,
-                       a.partC, l.n_dtiles, btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, a.partD,
-                       batch * (int64_t)l.K, D, dD);
+    if (dB || dC)
+      hipLaunchKernelGGL(fold_bc_kernel, dim3(small_grid(btn)), dim3(256), 0, st, a.partB, a.partC, l.n_dtiles, btn,
+                         dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype);
+    if (dD)
+      hipLaunchKernelGGL(fold_d_kernel, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, st, a.partD,
+                         batch * (int64_t)l.K, D, dD);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;

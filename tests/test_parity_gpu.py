@@ -133,6 +133,24 @@ def test_repeatable_and_workspace_reusable(gpu):
         assert st.value == 0
 
 
+def test_workspace_shared_across_shapes(gpu):
+    """One cached workspace serves shapes whose tile counts grow from call to
+    call (regression: the ticket counters live in a fixed header region that
+    no other part of any layout overlaps). Status stays 0 throughout."""
+    import ctypes
+    from naju_amd import _lib
+    from naju_amd.scan import _WS
+    for (b, T, D) in [(1, 40, 32), (3, 200, 40), (2, 33, 1000), (4, 130, 2000), (1, 300, 64)]:
+        ins = rand_inputs(b, T, D, 1, seed=b * T + D)
+        y, g = run_hip(ins, gpu)
+        ry, rg = oracle_all(ins)
+        check_all(y, g, ry, rg)
+    for (dev, stream), buf in _WS._bufs.items():
+        st = ctypes.c_uint32(99)
+        _lib.check(_lib.lib().naju_scan_workspace_status(buf.data_ptr(), stream, ctypes.byref(st)))
+        assert st.value == 0
+
+
 def test_needs_input_grad_subset(gpu):
     ins = rand_inputs(2, 100, 64, 1, seed=17)
     y, g = run_hip(ins, gpu, grad_names=["u", "f_logit"])
