@@ -78,13 +78,23 @@ __device__ __forceinline__ void st_any(void* p, int dt, int64_t i, float v) {
     ((f16_t*)p)[i] = (f16_t)v;
 }
 
-// V consecutive elements starting at element d0 of row `p`. VEC: one aligned
-// vector access, valid iff d0 < D (the host guarantees D % V == 0).
-// Otherwise each element is checked against D. Out-of-range elements read 0.
-template <typename T, int V, bool VEC>
+// V consecutive elements starting at element d0 of row `p`, by access mode:
+//   kVecAll : one aligned vector access, no bounds check (the caller knows
+//             the whole tile is inside [0, D));
+//   kVecLane: one aligned vector access if d0 < D (the host guarantees
+//             D % V == 0), else zeros;
+//   kElem   : element-wise, each element checked against D.
+// Out-of-range elements read as 0 and are not written.
+enum { kVecAll = 0, kVecLane = 1, kElem = 2 };
+
+template <typename T, int V, int MODE>
 __device__ __forceinline__ void ld_row(const T* __restrict__ p, int64_t d0, int64_t D, float (&o)[V]) {
-  if constexpr (VEC) {
-    typedef T vec_t __attribute__((ext_vector_type(V)));
+  typedef T vec_t __attribute__((ext_vector_type(V)));
+  if constexpr (MODE == kVecAll) {
+    const vec_t v = *reinterpret_cast<const vec_t*>(p + d0);
+#pragma unroll
+    for (int j = 0; j < V; ++j) o[j] = to_f32(v[j]);
+  } else if constexpr (MODE == kVecLane) {
     if (d0 < D) {
       const vec_t v = *reinterpret_cast<const vec_t*>(p + d0);
 #pragma unroll
@@ -99,20 +109,20 @@ __device__ __forceinline__ void ld_row(const T* __restrict__ p, int64_t d0, int6
   }
 }
 
-template <typename T, int V, bool VEC>
+template <typename T, int V, int MODE>
 __device__ __forceinline__ void st_row(T* __restrict__ p, int64_t d0, int64_t D, const float (&x)[V]) {
-  if constexpr (VEC) {
-    typedef T vec_t __attribute__((ext_vector_type(V)));
-    if (d0 < D) {
+  typedef T vec_t __attribute__((ext_vector_type(V)));
+  if constexpr (MODE == kElem) {
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      if (d0 + j < D) p[d0 + j] = from_f32<T>(x[j]);
+  } else {
+    if (MODE == kVecAll || d0 < D) {
       vec_t v;
 #pragma unroll
       for (int j = 0; j < V; ++j) v[j] = from_f32<T>(x[j]);
       *reinterpret_cast<vec_t*>(p + d0) = v;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j)
-      if (d0 + j < D) p[d0 + j] = from_f32<T>(x[j]);
   }
 }
 
@@ -242,7 +252,7 @@ __device__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, 
   int base = k + dir;
   uint32_t idle = 0;
   while (true) {
-#pragma unroll
+#pragma unroll 1
     for (int p = 0; p < P; ++p) {
       const int slot = p * W + wv;
       const int c = base + dir * slot;
@@ -321,14 +331,48 @@ __device__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, 
   }
 }
 
+// Rows [t0, t0+R) of one [batch,T,D] stream for this lane's channels
+// (rowbase = b*T + t0). ROWCHK: rows at or beyond T read as 0.
+template <typename T, int V, int R, int MODE, bool ROWCHK>
+__device__ __forceinline__ void ld_rows(const T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn, int64_t D,
+                                        int64_t d0, float (&o)[R][V]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (!ROWCHK || t0 + r < Tn) {
+      ld_row<T, V, MODE>(p + (rowbase + r) * D, d0, D, o[r]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) o[r][j] = 0.f;
+    }
+  }
+}
+
+template <typename T, int V, int R, int MODE, bool ROWCHK>
+__device__ __forceinline__ void st_rows(T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn, int64_t D,
+                                        int64_t d0, const float (&x)[R][V]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (!ROWCHK || t0 + r < Tn) st_row<T, V, MODE>(p + (rowbase + r) * D, d0, D, x[r]);
+}
+
+// B_t or C_t of rows [t0, t0+R) of batch row b (N = 1: one value per row).
+template <typename T, int R, bool ROWCHK>
+__device__ __forceinline__ void ld_scalars(const T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn,
+                                           float (&o)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) o[r] = (!ROWCHK || t0 + r < Tn) ? to_f32(p[rowbase + r]) : 0.f;
+}
+
 // ------------------------------------------------------------ N = 1 forward
 //
 // One workgroup = (batch row b, tile of CH = 64*V channels, chunk k of
 // L = W*R timesteps). Forward chunk order: ticket -> (k, tile), chunk-major,
 // so every predecessor (k-1, same tile) holds a smaller ticket. Lane `lane`
 // owns channels d0 .. d0+V-1 (d0 = tile start + lane*V); its slot for
-// channel j in LDS and workspace arrays is j*64 + lane.
-template <typename TU, typename TG, int V, int R, int W, int P, bool VEC, bool F32O>
+// channel j in LDS and workspace arrays is j*64 + lane. A workgroup whose
+// chunk and tile lie wholly inside [0,T) x [0,D) takes the branch-free path
+// (all loads issued back to back); edge workgroups check bounds.
+template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
 __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   using TY = std::conditional_t<F32O, float, TU>;  // y dtype
   constexpr int CH = 64 * V;
@@ -344,16 +388,14 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   const int k = (int)__builtin_amdgcn_readfirstlane(s_ticket);
   const uint32_t tag = a.tag;
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t d0 = (int64_t)dtile * CH + lane * V;
   const int t0 = k * L + wv * R;
-
-  const TU* __restrict__ pu = (const TU*)a.u;
-  const TG* __restrict__ pf = (const TG*)a.fl;
-  const TG* __restrict__ pi = (const TG*)a.il;
+  const int64_t rowbase = (int64_t)b * T + t0;
+  const bool full = VEC && (int64_t)(k + 1) * L <= T && (int64_t)(dtile + 1) * CH <= D;
 
   float Dv[V];
   bool dok[V];
@@ -366,21 +408,19 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   // ---- load the wave's R rows
   float xu[R][V], xf[R][V], xi[R][V];
   float Bt[R], Ct[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t t = t0 + r;
-    const int64_t row = ((int64_t)b * T + t) * D;
-    if (t < T) {
-      ld_row<TU, V, VEC>(pu + row, d0, D, xu[r]);
-      ld_row<TG, V, VEC>(pf + row, d0, D, xf[r]);
-      ld_row<TG, V, VEC>(pi + row, d0, D, xi[r]);
-      Bt[r] = ld_any(a.Bm, a.bc_dt, (int64_t)b * T + t);
-      Ct[r] = ld_any(a.Cm, a.bc_dt, (int64_t)b * T + t);
-    } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) xu[r][j] = xf[r][j] = xi[r][j] = 0.f;
-      Bt[r] = Ct[r] = 0.f;
-    }
+  if (full) {
+    ld_rows<TU, V, R, kVecAll, false>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
+    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
+    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
+    ld_scalars<TB, R, false>((const TB*)a.Bm, rowbase, t0, T, Bt);
+    ld_scalars<TB, R, false>((const TB*)a.Cm, rowbase, t0, T, Ct);
+  } else {
+    constexpr int M = VEC ? kVecLane : kElem;
+    ld_rows<TU, V, R, M, true>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
+    ld_rows<TG, V, R, M, true>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
+    ld_rows<TG, V, R, M, true>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
+    ld_scalars<TB, R, true>((const TB*)a.Bm, rowbase, t0, T, Bt);
+    ld_scalars<TB, R, true>((const TB*)a.Cm, rowbase, t0, T, Ct);
   }
 
   // ---- pass 1: local scan from zero; keep y = yl + q * (carry) per element
@@ -469,16 +509,14 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   for (int w = 0; w < wv; ++w)
 #pragma unroll
     for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][j * 64 + lane], s[j], s_Z[w][j * 64 + lane]);
-  TY* __restrict__ py = (TY*)a.y;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t t = t0 + r;
-    if (t < T) {
-      float o[V];
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int j = 0; j < V; ++j) o[j] = fmaf(q[r][j], s[j], yl[r][j]);
-      st_row<TY, V, VEC>(py + ((int64_t)b * T + t) * D, d0, D, o);
-    }
+    for (int j = 0; j < V; ++j) yl[r][j] = fmaf(q[r][j], s[j], yl[r][j]);
+  if (full) {
+    st_rows<TY, V, R, kVecAll, false>((TY*)a.y, rowbase, t0, T, D, d0, yl);
+  } else {
+    st_rows<TY, V, R, VEC ? kVecLane : kElem, true>((TY*)a.y, rowbase, t0, T, D, d0, yl);
   }
 }
 
@@ -489,7 +527,7 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 // map g_in -> A g_in + Zb with A = prod f. Chunks run in reverse order
 // (ticket -> chunk K-1-k), so the look-back walks towards larger t. The
 // forward state entering the chunk comes from the forward's checkpoint.
-template <typename TU, typename TG, int V, int R, int W, int P, bool VEC, bool F32O>
+template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
 __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
   using TDG = std::conditional_t<F32O, float, TG>;  // dfl, dil dtype
@@ -507,17 +545,14 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   const int k = a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
   const uint32_t tag = a.tag;
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t d0 = (int64_t)dtile * CH + lane * V;
   const int t0 = k * L + wv * R;
-
-  const TU* __restrict__ pu = (const TU*)a.u;
-  const TG* __restrict__ pfl = (const TG*)a.fl;
-  const TG* __restrict__ pil = (const TG*)a.il;
-  const TU* __restrict__ pdy = (const TU*)a.dy;
+  const int64_t rowbase = (int64_t)b * T + t0;
+  const bool full = VEC && (int64_t)(k + 1) * L <= T && (int64_t)(dtile + 1) * CH <= D;
 
   float Dv[V];
   bool dok[V];
@@ -529,22 +564,21 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
 
   float xu[R][V], xf[R][V], xi[R][V], xg[R][V];
   float Bt[R], Ct[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t t = t0 + r;
-    const int64_t row = ((int64_t)b * T + t) * D;
-    if (t < T) {
-      ld_row<TU, V, VEC>(pu + row, d0, D, xu[r]);
-      ld_row<TG, V, VEC>(pfl + row, d0, D, xf[r]);
-      ld_row<TG, V, VEC>(pil + row, d0, D, xi[r]);
-      ld_row<TU, V, VEC>(pdy + row, d0, D, xg[r]);
-      Bt[r] = ld_any(a.Bm, a.bc_dt, (int64_t)b * T + t);
-      Ct[r] = ld_any(a.Cm, a.bc_dt, (int64_t)b * T + t);
-    } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) xu[r][j] = xf[r][j] = xi[r][j] = xg[r][j] = 0.f;
-      Bt[r] = Ct[r] = 0.f;
-    }
+  if (full) {
+    ld_rows<TU, V, R, kVecAll, false>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
+    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
+    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
+    ld_rows<TU, V, R, kVecAll, false>((const TU*)a.dy, rowbase, t0, T, D, d0, xg);
+    ld_scalars<TB, R, false>((const TB*)a.Bm, rowbase, t0, T, Bt);
+    ld_scalars<TB, R, false>((const TB*)a.Cm, rowbase, t0, T, Ct);
+  } else {
+    constexpr int M = VEC ? kVecLane : kElem;
+    ld_rows<TU, V, R, M, true>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
+    ld_rows<TG, V, R, M, true>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
+    ld_rows<TG, V, R, M, true>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
+    ld_rows<TU, V, R, M, true>((const TU*)a.dy, rowbase, t0, T, D, d0, xg);
+    ld_scalars<TB, R, true>((const TB*)a.Bm, rowbase, t0, T, Bt);
+    ld_scalars<TB, R, true>((const TB*)a.Cm, rowbase, t0, T, Ct);
   }
   float s[V];
 #pragma unroll
@@ -665,15 +699,15 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
       xu[r][j] = fmaf(ig, dws, Dv[j] * gy);       // du
     }
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t t = t0 + r;
-    if (t < T) {
-      const int64_t row = ((int64_t)b * T + t) * D;
-      if (a.du) st_row<TDU, V, VEC>((TDU*)a.du + row, d0, D, xu[r]);
-      if (a.dfl) st_row<TDG, V, VEC>((TDG*)a.dfl + row, d0, D, xf[r]);
-      if (a.dil) st_row<TDG, V, VEC>((TDG*)a.dil + row, d0, D, xi[r]);
-    }
+  if (full) {
+    if (a.du) st_rows<TDU, V, R, kVecAll, false>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
+    if (a.dfl) st_rows<TDG, V, R, kVecAll, false>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
+    if (a.dil) st_rows<TDG, V, R, kVecAll, false>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
+  } else {
+    constexpr int M = VEC ? kVecLane : kElem;
+    if (a.du) st_rows<TDU, V, R, M, true>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
+    if (a.dfl) st_rows<TDG, V, R, M, true>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
+    if (a.dil) st_rows<TDG, V, R, M, true>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
   }
   if (a.partB || a.partC) {
 #pragma unroll
@@ -873,24 +907,31 @@ bool aligned(const void* p, size_t a) { return p == nullptr || ((uintptr_t)p % a
 
 typedef void (*kern_t)(ScanArgs);
 
-template <typename TU, typename TG, bool VEC, bool F32O>
+template <typename TU, typename TG, typename TB, bool VEC, bool F32O>
 kern_t pick_n1(bool bwd) {
-  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, kBV, kBR, kBW, kBP, VEC, F32O>
-             : (kern_t)n1_fwd_kernel<TU, TG, kFV, kFR, kFW, kFP, VEC, F32O>;
+  return bwd ? (kern_t)n1_bwd_kernel<TU, TG, TB, kBV, kBR, kBW, kBP, VEC, F32O>
+             : (kern_t)n1_fwd_kernel<TU, TG, TB, kFV, kFR, kFW, kFP, VEC, F32O>;
+}
+
+template <typename TU, typename TG, bool VEC, bool F32O>
+kern_t pick_n1_bc(int bc_dt, bool bwd) {
+  return bc_dt == NAJU_DTYPE_F32 ? pick_n1<TU, TG, float, VEC, F32O>(bwd) : pick_n1<TU, TG, TU, VEC, F32O>(bwd);
 }
 
 template <bool VEC, bool F32O>
-kern_t pick_n1_dt(int x_dt, int g_dt, bool bwd) {
-  if (x_dt == NAJU_DTYPE_F32) return pick_n1<float, float, VEC, F32O>(bwd);
+kern_t pick_n1_dt(int x_dt, int g_dt, int bc_dt, bool bwd) {
+  if (x_dt == NAJU_DTYPE_F32) return pick_n1<float, float, float, VEC, F32O>(bwd);
   if (x_dt == NAJU_DTYPE_BF16)
-    return g_dt == NAJU_DTYPE_F32 ? pick_n1<bf16_t, float, VEC, F32O>(bwd)
-                                  : pick_n1<bf16_t, bf16_t, VEC, F32O>(bwd);
-  return g_dt == NAJU_DTYPE_F32 ? pick_n1<f16_t, float, VEC, F32O>(bwd) : pick_n1<f16_t, f16_t, VEC, F32O>(bwd);
+    return g_dt == NAJU_DTYPE_F32 ? pick_n1_bc<bf16_t, float, VEC, F32O>(bc_dt, bwd)
+                                  : pick_n1_bc<bf16_t, bf16_t, VEC, F32O>(bc_dt, bwd);
+  return g_dt == NAJU_DTYPE_F32 ? pick_n1_bc<f16_t, float, VEC, F32O>(bc_dt, bwd)
+                                : pick_n1_bc<f16_t, f16_t, VEC, F32O>(bc_dt, bwd);
 }
 
-kern_t pick_n1_all(bool vec, bool f32o, int x_dt, int g_dt, bool bwd) {
-  if (vec) return f32o ? pick_n1_dt<true, true>(x_dt, g_dt, bwd) : pick_n1_dt<true, false>(x_dt, g_dt, bwd);
-  return f32o ? pick_n1_dt<false, true>(x_dt, g_dt, bwd) : pick_n1_dt<false, false>(x_dt, g_dt, bwd);
+kern_t pick_n1_all(bool vec, bool f32o, int x_dt, int g_dt, int bc_dt, bool bwd) {
+  if (vec)
+    return f32o ? pick_n1_dt<true, true>(x_dt, g_dt, bc_dt, bwd) : pick_n1_dt<true, false>(x_dt, g_dt, bc_dt, bwd);
+  return f32o ? pick_n1_dt<false, true>(x_dt, g_dt, bc_dt, bwd) : pick_n1_dt<false, false>(x_dt, g_dt, bc_dt, bwd);
 }
 
 int launch(kern_t k, unsigned grid, unsigned block, hipStream_t st, const ScanArgs& a) {
@@ -982,7 +1023,7 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
     return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                 l.n_tiles);
   a.tag = next_tag();
-  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, false);
+  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, false);
   return launch(k, (unsigned)wgs, 64 * kFW, st, a);
 }
 
@@ -1052,7 +1093,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                 l.n_tiles);
   a.tag = next_tag();
-  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, true);
+  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, true);
   rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
   if (rc) return rc;
   if (dB || dC || dD) {
