@@ -1,0 +1,188 @@
+"""CPU tests of the C ABI boundary and of the host-side Python mirror.
+
+No GPU is touched: every call here either only queries sizes or fails the
+host-side argument checks (which run before any device work), or returns
+before launching (empty batch / channel axes).
+"""
+import ctypes
+import os
+import re
+import types
+
+import pytest
+import torch
+
+from naju_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "naju_scan.h")
+F32, BF16, F16 = 0, 1, 2
+
+
+def header_functions():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(naju_scan_\w+)\s*\(", txt)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.lib()
+    names = header_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/naju_scan.h but not exported"
+    assert set(names) == set(_lib.EXPORTED)
+    assert lib.naju_scan_version() >= 1
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", os.path.join(ROOT, "no_such_lib.so"))
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()
+
+
+def test_size_queries():
+    L = _lib.lib()
+    # BASELINE config 2 at N=1: ckpt = one float per (b, chunk, d)
+    n = L.naju_scan_ckpt_elems(8, 4096, 1024, 1, BF16, BF16, BF16)
+    assert n > 0 and n % (8 * 1024) == 0 and n <= 8 * 1024 * 4096
+    ws = L.naju_scan_workspace_bytes(8, 4096, 1024, 1, BF16, BF16, BF16)
+    assert ws > 0 and ws % 256 == 0
+    # invalid requests report 0 / -1 and set the message
+    assert L.naju_scan_workspace_bytes(8, 4096, 1024, 0, BF16, BF16, BF16) == 0
+    assert b"N" in L.naju_scan_last_error()
+    assert L.naju_scan_ckpt_elems(-1, 4, 4, 1, F32, F32, F32) == -1
+
+
+def _fwd(L, **kw):
+    a = dict(u=1, fl=1, il=1, B=1, C=1, Dk=1, h0=None, y=1, ck=None, hT=None, batch=2, T=8, D=16, N=1,
+             x=F32, g=F32, bc=F32, of=0, ws=None, wsb=0, st=None)
+    a.update(kw)
+    return L.naju_scan_fwd(a["u"], a["fl"], a["il"], a["B"], a["C"], a["Dk"], a["h0"], a["y"], a["ck"], a["hT"],
+                           a["batch"], a["T"], a["D"], a["N"], a["x"], a["g"], a["bc"], a["of"], a["ws"],
+                           a["wsb"], a["st"])
+
+
+def _bwd(L, **kw):
+    a = dict(u=1, fl=1, il=1, B=1, C=1, Dk=1, ck=1, dy=1, du=None, dfl=None, dil=None, dB=None, dC=None, dD=None,
+             dh0=None, batch=2, T=8, D=16, N=1, x=F32, g=F32, bc=F32, of=0, ws=None, wsb=0, st=None)
+    a.update(kw)
+    return L.naju_scan_bwd(a["u"], a["fl"], a["il"], a["B"], a["C"], a["Dk"], a["ck"], a["dy"], a["du"],
+                           a["dfl"], a["dil"], a["dB"], a["dC"], a["dD"], a["dh0"], a["batch"], a["T"], a["D"],
+                           a["N"], a["x"], a["g"], a["bc"], a["of"], a["ws"], a["wsb"], a["st"])
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(batch=-1), _lib.ERR_INVALID, "negative"),
+    (dict(N=0), _lib.ERR_INVALID, "N"),
+    (dict(x=7), _lib.ERR_INVALID, "dtype"),
+    (dict(x=BF16, g=F16), _lib.ERR_UNSUPPORTED, "gate"),
+    (dict(x=F32, g=BF16), _lib.ERR_UNSUPPORTED, "gate"),
+    (dict(x=BF16, g=BF16, bc=F16), _lib.ERR_UNSUPPORTED, "B/C"),
+    (dict(N=3), _lib.ERR_UNSUPPORTED, "N"),
+    (dict(u=None), _lib.ERR_INVALID, "null"),
+    (dict(y=None), _lib.ERR_INVALID, "null"),
+    (dict(ws=None), _lib.ERR_WORKSPACE, "workspace"),
+    (dict(ws=256, wsb=16), _lib.ERR_WORKSPACE, "workspace"),
+])
+def test_fwd_argument_checks(kw, code, msg):
+    L = _lib.lib()
+    assert _fwd(L, **kw) == code
+    assert msg.encode() in L.naju_scan_last_error()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(ck=None), _lib.ERR_INVALID, "ckpt"),
+    (dict(dy=None), _lib.ERR_INVALID, "null"),
+    (dict(T=-3), _lib.ERR_INVALID, "negative"),
+    (dict(ws=None), _lib.ERR_WORKSPACE, "workspace"),
+])
+def test_bwd_argument_checks(kw, code, msg):
+    L = _lib.lib()
+    assert _bwd(L, **kw) == code
+    assert msg.encode() in L.naju_scan_last_error()
+
+
+def test_misaligned_workspace_rejected():
+    L = _lib.lib()
+    need = L.naju_scan_workspace_bytes(2, 8, 16, 1, F32, F32, F32)
+    assert _fwd(L, ws=256 + 8, wsb=need + 64) == _lib.ERR_WORKSPACE
+    assert b"aligned" in L.naju_scan_last_error()
+
+
+def test_empty_axes_return_without_work():
+    L = _lib.lib()
+    assert _fwd(L, batch=0, u=None, y=None) == _lib.OK
+    assert _fwd(L, D=0, u=None, y=None) == _lib.OK
+    # T == 0 with no final-state output: nothing to write
+    assert _fwd(L, T=0) == _lib.OK
+    assert L.naju_scan_last_error() == b""
+
+
+def test_check_raises_with_message():
+    L = _lib.lib()
+    _fwd(L, N=0)
+    with pytest.raises(_lib.NajuScanError, match="d_state"):
+        _lib.check(_lib.ERR_INVALID)
+
+
+# ------------------------------------------------------- Python mirror
+
+def test_resolve_backend_order(monkeypatch):
+    from naju_amd.scan import resolve_backend
+    monkeypatch.delenv("NAJU_SCAN_BACKEND", raising=False)
+    assert resolve_backend() == "hip"
+    monkeypatch.setenv("NAJU_SCAN_BACKEND", "HIP")
+    assert resolve_backend() == "hip"
+    assert resolve_backend("Other") == "other"
+
+
+def test_unknown_backend_raises():
+    from naju_amd.scan import naju_scan
+    x = torch.zeros(1, 2, 3)
+    with pytest.raises(ValueError, match="unknown scan backend"):
+        naju_scan(x, x, x, torch.zeros(1, 2, 1), torch.zeros(1, 2, 1), torch.zeros(3), backend="chunk")
+
+
+def test_register_inserts_into_dispatch_cache():
+    from naju_amd import naju_scan_hip, register
+    fake = types.SimpleNamespace(_BACKEND_CACHE={})
+    assert register("HIP", scan_module=fake) is naju_scan_hip
+    assert fake._BACKEND_CACHE["hip"] is naju_scan_hip
+    register("chunk", scan_module=fake)
+    assert fake._BACKEND_CACHE["chunk"] is naju_scan_hip
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(u=torch.zeros(2, 3)), r"\[B, T, D\]"),
+    (dict(f_logit=torch.zeros(2, 3, 5)), "f_logit"),
+    (dict(B=torch.zeros(2, 4, 1)), "B and C"),
+    (dict(D_skip=torch.zeros(3)), "D_skip"),
+    (dict(h0=torch.zeros(2, 4, 2)), "h0"),
+    ({}, "GPU"),
+])
+def test_shape_and_device_checks(bad, msg):
+    from naju_amd import naju_scan_hip
+    a = dict(u=torch.zeros(2, 3, 4), f_logit=torch.zeros(2, 3, 4), i_logit=torch.zeros(2, 3, 4),
+             B=torch.zeros(2, 3, 1), C=torch.zeros(2, 3, 1), D_skip=torch.zeros(4), h0=None)
+    a.update(bad)
+    with pytest.raises(ValueError, match=msg):
+        naju_scan_hip(a["u"], a["f_logit"], a["i_logit"], a["B"], a["C"], a["D_skip"], a["h0"])
+
+
+def test_algorithmic_bytes_headline():
+    """22 B per element at bf16 (fwd 8 + bwd 14) plus B/C and h0 terms."""
+    from naju_amd.workloads import algorithmic_bytes
+    E = 8 * 4096 * 1024
+    tot = algorithmic_bytes(8, 4096, 1024, 1, 2, 2, 2, False)
+    assert tot == 22 * E + 6 * 2 * 8 * 4096
+    with_h0 = algorithmic_bytes(8, 4096, 1024, 1, 2, 2, 2, True)
+    assert with_h0 - tot == 12 * 8 * 1024
+
+
+def test_build_flags_disable_packed_fp32():
+    from naju_amd import build
+    flags = " ".join(build.HIPCC_FLAGS)
+    assert "--offload-arch=gfx950" in flags
+    assert "-target-feature -Xclang -packed-fp32-ops" in flags
