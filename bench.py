@@ -157,7 +157,7 @@ def main():
         "bwd_ms_avg": round(avg_bwd, 5), "bwd_ms_median": round(med(t_bwd), 5),
         "fwd_GBs": round(bytes_fwd / (avg_fwd * 1e-3) / 1e9, 1),
         "roofline": {
-            "kernel": "n1_bwd_kernel (+ fold_partials_kernel, same call)" if N == 1 else "bwd",
+            "kernel": "naju_scan_bwd call = n1_bwd_kernel + fold_kernel" if N == 1 else "naju_scan_bwd call",
             "bound": "hbm",
             "achieved": round(bytes_bwd / (avg_bwd * 1e-3) / 1e9, 1),
             "peak": HBM_PEAK_GBS,

@@ -370,58 +370,40 @@ __device__ __forceinline__ void ld_scalars(const T* __restrict__ p, int64_t rowb
 // so every predecessor (k-1, same tile) holds a smaller ticket. Lane `lane`
 // owns channels d0 .. d0+V-1 (d0 = tile start + lane*V); its slot for
 // channel j in LDS and workspace arrays is j*64 + lane. A workgroup whose
-// chunk and tile lie wholly inside [0,T) x [0,D) takes the branch-free path
-// (all loads issued back to back); edge workgroups check bounds.
-template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
-__global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
+// chunk and tile lie wholly inside [0,T) x [0,D) runs the FULL body: no
+// bounds checks, all loads issued back to back; edge workgroups check.
+template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O, bool FULL>
+__device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, int lane, int wv,
+                                            float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V], float (&s_in)[64 * V],
+                                            LookShared<V, W, P>& s_lb) {
   using TY = std::conditional_t<F32O, float, TU>;  // y dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
-  __shared__ uint32_t s_ticket;
-  __shared__ float s_F[W][CH];
-  __shared__ float s_Z[W][CH];
-  __shared__ float s_in[CH];
-  __shared__ LookShared<V, W, P> s_lb;
-
-  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  if (!take_ticket(a, tile, &s_ticket)) return;
-  const int k = (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  constexpr int M = FULL ? kVecAll : (VEC ? kVecLane : kElem);
   const uint32_t tag = a.tag;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t d0 = (int64_t)dtile * CH + lane * V;
   const int t0 = k * L + wv * R;
   const int64_t rowbase = (int64_t)b * T + t0;
-  const bool full = VEC && (int64_t)(k + 1) * L <= T && (int64_t)(dtile + 1) * CH <= D;
 
   float Dv[V];
   bool dok[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    dok[j] = d0 + j < D;
+    dok[j] = FULL || d0 + j < D;
     Dv[j] = dok[j] ? a.Dsk[d0 + j] : 0.f;
   }
 
   // ---- load the wave's R rows
   float xu[R][V], xf[R][V], xi[R][V];
   float Bt[R], Ct[R];
-  if (full) {
-    ld_rows<TU, V, R, kVecAll, false>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
-    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
-    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
-    ld_scalars<TB, R, false>((const TB*)a.Bm, rowbase, t0, T, Bt);
-    ld_scalars<TB, R, false>((const TB*)a.Cm, rowbase, t0, T, Ct);
-  } else {
-    constexpr int M = VEC ? kVecLane : kElem;
-    ld_rows<TU, V, R, M, true>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
-    ld_rows<TG, V, R, M, true>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
-    ld_rows<TG, V, R, M, true>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
-    ld_scalars<TB, R, true>((const TB*)a.Bm, rowbase, t0, T, Bt);
-    ld_scalars<TB, R, true>((const TB*)a.Cm, rowbase, t0, T, Ct);
-  }
+  ld_rows<TU, V, R, M, !FULL>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
+  ld_rows<TG, V, R, M, !FULL>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
+  ld_rows<TG, V, R, M, !FULL>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
+  ld_scalars<TB, R, !FULL>((const TB*)a.Bm, rowbase, t0, T, Bt);
+  ld_scalars<TB, R, !FULL>((const TB*)a.Cm, rowbase, t0, T, Ct);
 
   // ---- pass 1: local scan from zero; keep y = yl + q * (carry) per element
   float F[V], Z[V];
@@ -433,7 +415,7 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const bool tv = t0 + r < T;
+    const bool tv = FULL || t0 + r < T;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const bool v = tv && dok[j];
@@ -513,11 +495,32 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < V; ++j) yl[r][j] = fmaf(q[r][j], s[j], yl[r][j]);
-  if (full) {
-    st_rows<TY, V, R, kVecAll, false>((TY*)a.y, rowbase, t0, T, D, d0, yl);
-  } else {
-    st_rows<TY, V, R, VEC ? kVecLane : kElem, true>((TY*)a.y, rowbase, t0, T, D, d0, yl);
+  st_rows<TY, V, R, M, !FULL>((TY*)a.y, rowbase, t0, T, D, d0, yl);
+}
+
+template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
+__global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
+  constexpr int CH = 64 * V;
+  constexpr int L = W * R;
+  __shared__ uint32_t s_ticket;
+  __shared__ float s_F[W][CH];
+  __shared__ float s_Z[W][CH];
+  __shared__ float s_in[CH];
+  __shared__ LookShared<V, W, P> s_lb;
+
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  if (!take_ticket(a, tile, &s_ticket)) return;
+  const int k = (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int dtile = tile % a.n_dtiles;
+  if constexpr (VEC) {
+    if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
+      n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, s_F, s_Z, s_in, s_lb);
+      return;
+    }
   }
+  n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, s_F, s_Z, s_in, s_lb);
 }
 
 // ----------------------------------------------------------- N = 1 backward
@@ -527,64 +530,45 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 // map g_in -> A g_in + Zb with A = prod f. Chunks run in reverse order
 // (ticket -> chunk K-1-k), so the look-back walks towards larger t. The
 // forward state entering the chunk comes from the forward's checkpoint.
-template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
-__global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
+template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O, bool FULL>
+__device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, int lane, int wv,
+                                            float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
+                                            float (&s_Zb)[W][64 * V], float (&s_g)[64 * V],
+                                            LookShared<V, W, P>& s_lb) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
   using TDG = std::conditional_t<F32O, float, TG>;  // dfl, dil dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
-  __shared__ uint32_t s_ticket;
-  __shared__ float s_F[W][CH];
-  __shared__ float s_Z[W][CH];
-  __shared__ float s_Zb[W][CH];
-  __shared__ float s_g[CH];
-  __shared__ LookShared<V, W, P> s_lb;
-
-  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  if (!take_ticket(a, tile, &s_ticket)) return;
-  const int k = a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  constexpr int M = FULL ? kVecAll : (VEC ? kVecLane : kElem);
   const uint32_t tag = a.tag;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t d0 = (int64_t)dtile * CH + lane * V;
   const int t0 = k * L + wv * R;
   const int64_t rowbase = (int64_t)b * T + t0;
-  const bool full = VEC && (int64_t)(k + 1) * L <= T && (int64_t)(dtile + 1) * CH <= D;
 
   float Dv[V];
   bool dok[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    dok[j] = d0 + j < D;
+    dok[j] = FULL || d0 + j < D;
     Dv[j] = dok[j] ? a.Dsk[d0 + j] : 0.f;
   }
 
   float xu[R][V], xf[R][V], xi[R][V], xg[R][V];
   float Bt[R], Ct[R];
-  if (full) {
-    ld_rows<TU, V, R, kVecAll, false>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
-    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
-    ld_rows<TG, V, R, kVecAll, false>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
-    ld_rows<TU, V, R, kVecAll, false>((const TU*)a.dy, rowbase, t0, T, D, d0, xg);
-    ld_scalars<TB, R, false>((const TB*)a.Bm, rowbase, t0, T, Bt);
-    ld_scalars<TB, R, false>((const TB*)a.Cm, rowbase, t0, T, Ct);
-  } else {
-    constexpr int M = VEC ? kVecLane : kElem;
-    ld_rows<TU, V, R, M, true>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
-    ld_rows<TG, V, R, M, true>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
-    ld_rows<TG, V, R, M, true>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
-    ld_rows<TU, V, R, M, true>((const TU*)a.dy, rowbase, t0, T, D, d0, xg);
-    ld_scalars<TB, R, true>((const TB*)a.Bm, rowbase, t0, T, Bt);
-    ld_scalars<TB, R, true>((const TB*)a.Cm, rowbase, t0, T, Ct);
-  }
+  ld_rows<TU, V, R, M, !FULL>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
+  ld_rows<TG, V, R, M, !FULL>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
+  ld_rows<TG, V, R, M, !FULL>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
+  ld_rows<TU, V, R, M, !FULL>((const TU*)a.dy, rowbase, t0, T, D, d0, xg);
+  ld_scalars<TB, R, !FULL>((const TB*)a.Bm, rowbase, t0, T, Bt);
+  ld_scalars<TB, R, !FULL>((const TB*)a.Cm, rowbase, t0, T, Ct);
   float s[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) s[j] = dok[j] ? a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] : 0.f;
 
-  // ---- pass 1: gates, forward map (F, Z) and adjoint map (F, Zb) of the rows
+  // ---- pass 1: gates, w = i*B*u, forward map (F, Z) and adjoint map (F, Zb)
   float F[V], Z[V], G[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
@@ -594,7 +578,7 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const bool tv = t0 + r < T;
+    const bool tv = FULL || t0 + r < T;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const bool v = tv && dok[j];
@@ -676,7 +660,8 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
       s[j] = fmaf(xf[r][j], s[j], xi[r][j] * Bt[r] * xu[r][j]);
     }
 
-  // reverse sweep: gradients (naju/cuda/naju_cuda.cu:116-140 restated)
+  // reverse sweep: gradients (naju/cuda/naju_cuda.cu:116-140 restated);
+  // f(1-f) and i(1-i) as fma(-f, f, f), exactly 0 at f in {0, 1}.
   float pB[R], pC[R], dDs[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) dDs[j] = 0.f;
@@ -688,35 +673,30 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
     for (int j = 0; j < V; ++j) {
       const float f = xf[r][j], ig = xi[r][j], x = xu[r][j], gy = xg[r][j];
       const float xb = fmaf(gy, Ct[r], g[j]);
-      const float xt = fmaf(f, xp[r][j], ig * Bt[r] * x);
+      const float iu = ig * x;
+      const float xt = fmaf(f, xp[r][j], iu * Bt[r]);
       const float dws = xb * Bt[r];
-      pB[r] = fmaf(xb, ig * x, pB[r]);
+      pB[r] = fmaf(xb, iu, pB[r]);
       pC[r] = fmaf(gy, xt, pC[r]);
       dDs[j] = fmaf(gy, x, dDs[j]);
       g[j] = f * xb;
-      xf[r][j] = f * (1.f - f) * xb * xp[r][j];  // dfl
-      xi[r][j] = dws * x * (ig * (1.f - ig));     // dil
-      xu[r][j] = fmaf(ig, dws, Dv[j] * gy);       // du
+      xf[r][j] = fmaf(-f, f, f) * (xb * xp[r][j]);  // dfl
+      xi[r][j] = fmaf(-ig, ig, ig) * (dws * x);     // dil
+      xu[r][j] = fmaf(ig, dws, Dv[j] * gy);         // du
     }
   }
-  if (full) {
-    if (a.du) st_rows<TDU, V, R, kVecAll, false>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
-    if (a.dfl) st_rows<TDG, V, R, kVecAll, false>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
-    if (a.dil) st_rows<TDG, V, R, kVecAll, false>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
-  } else {
-    constexpr int M = VEC ? kVecLane : kElem;
-    if (a.du) st_rows<TDU, V, R, M, true>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
-    if (a.dfl) st_rows<TDG, V, R, M, true>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
-    if (a.dil) st_rows<TDG, V, R, M, true>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
-  }
+  if (a.du) st_rows<TDU, V, R, M, !FULL>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
+  if (a.dfl) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
+  if (a.dil) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
   if (a.partB || a.partC) {
+    // partial sums over this tile's channels, stored [b*T + t][dtile]
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float sb = wave_sum(pB[r]);
       const float sc = wave_sum(pC[r]);
       const int64_t t = t0 + r;
-      if (lane == 0 && t < T) {
-        const int64_t o = ((int64_t)dtile * a.batch + b) * T + t;
+      if (lane == 0 && (FULL || t < T)) {
+        const int64_t o = ((int64_t)b * T + t) * a.n_dtiles + dtile;
         if (a.partB) a.partB[o] = sb;
         if (a.partC) a.partC[o] = sc;
       }
@@ -738,46 +718,80 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   }
 }
 
-// Folds the per-tile partial sums of dB and dC over the channel tiles, in
-// tile order (run-to-run identical).
-__global__ void fold_bc_kernel(const float* __restrict__ partB, const float* __restrict__ partC, int n_parts,
-                               int64_t btn, void* dB, void* dC, int bc_dt) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
-    if (dB) {
-      float s = 0.f;
-      for (int p = 0; p < n_parts; ++p) s += partB[(int64_t)p * btn + i];
-      st_any(dB, bc_dt, i, s);
-    }
-    if (dC) {
-      float s = 0.f;
-      for (int p = 0; p < n_parts; ++p) s += partC[(int64_t)p * btn + i];
-      st_any(dC, bc_dt, i, s);
+template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
+__global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
+  constexpr int CH = 64 * V;
+  constexpr int L = W * R;
+  __shared__ uint32_t s_ticket;
+  __shared__ float s_F[W][CH];
+  __shared__ float s_Z[W][CH];
+  __shared__ float s_Zb[W][CH];
+  __shared__ float s_g[CH];
+  __shared__ LookShared<V, W, P> s_lb;
+
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  if (!take_ticket(a, tile, &s_ticket)) return;
+  const int k = a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int dtile = tile % a.n_dtiles;
+  if constexpr (VEC) {
+    if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
+      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, s_F, s_Z, s_Zb, s_g, s_lb);
+      return;
     }
   }
+  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, s_F, s_Z, s_Zb, s_g, s_lb);
 }
 
-// dD[d] = sum over the n_rows partial rows of partD[row][d]. One block per
-// 64 channels; wave w sums rows w, w+4, ... with four interleaved
-// accumulators, then the four waves' sums are added in wave order
-// (run-to-run identical).
-__global__ __launch_bounds__(256) void fold_d_kernel(const float* __restrict__ partD, int64_t n_rows, int64_t D,
-                                                     float* __restrict__ dD) {
-  __shared__ float s_acc[4][64];
+// Folds the backward's partial sums, in a fixed order (run-to-run
+// identical), in one launch:
+//   blocks [0, n_bc_blocks): dB, dC [i] = sum over the channel tiles p of
+//     partB/partC[i*n_parts + p] (contiguous per output);
+//   blocks [n_bc_blocks, ...): dD[d] = sum over the n_rows rows of
+//     partD[row][d], 64 channels per block; wave w of 16 sums rows
+//     w, w+16, ... with four interleaved accumulators, then the 16 wave
+//     sums are added in wave order.
+__global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ partB,
+                                                    const float* __restrict__ partC, int n_parts, int64_t btn,
+                                                    void* dB, void* dC, int bc_dt, int n_bc_blocks,
+                                                    const float* __restrict__ partD, int64_t n_rows, int64_t D,
+                                                    float* __restrict__ dD) {
+  __shared__ float s_acc[16][64];
+  if ((int)blockIdx.x < n_bc_blocks) {
+    const int64_t stride = (int64_t)n_bc_blocks * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
+      if (dB) {
+        float sm = 0.f;
+        for (int q = 0; q < n_parts; ++q) sm += partB[i * n_parts + q];
+        st_any(dB, bc_dt, i, sm);
+      }
+      if (dC) {
+        float sm = 0.f;
+        for (int q = 0; q < n_parts; ++q) sm += partC[i * n_parts + q];
+        st_any(dC, bc_dt, i, sm);
+      }
+    }
+    return;
+  }
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t d = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t d = (int64_t)(blockIdx.x - n_bc_blocks) * 64 + lane;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (d < D) {
     int64_t r = w;
-    for (; r + 12 < n_rows; r += 16) {
+    for (; r + 48 < n_rows; r += 64) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] += partD[(r + 4 * u) * D + d];
+      for (int u = 0; u < 4; ++u) acc[u] += partD[(r + 16 * u) * D + d];
     }
-    for (int u = 0; r < n_rows; r += 4, ++u) acc[u & 3] += partD[r * D + d];
+    for (int u = 0; r < n_rows; r += 16, ++u) acc[u & 3] += partD[r * D + d];
   }
   s_acc[w][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
-  if (w == 0 && d < D) dD[d] = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
+  if (w == 0 && d < D) {
+    float sm = 0.f;
+    for (int q = 0; q < 16; ++q) sm += s_acc[q][lane];
+    dD[d] = sm;
+  }
 }
 
 // Fills n float32 values with src[i] (or 0 when src is null); used for the
@@ -1098,12 +1112,11 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   if (rc) return rc;
   if (dB || dC || dD) {
     const int64_t btn = batch * T * N;
-    if (dB || dC)
-      hipLaunchKernelGGL(fold_bc_kernel, dim3(small_grid(btn)), dim3(256), 0, st, a.partB, a.partC, l.n_dtiles, btn,
-                         dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype);
-    if (dD)
-      hipLaunchKernelGGL(fold_d_kernel, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, st, a.partD,
-                         batch * (int64_t)l.K, D, dD);
+    const int n_bc = (dB || dC) ? (int)((btn + 1023) / 1024 < 256 ? (btn + 1023) / 1024 : 256) : 0;
+    const int n_d = dD ? (int)((D + 63) / 64) : 0;
+    hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
+                       btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD, batch * (int64_t)l.K, D,
+                       dD);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;
