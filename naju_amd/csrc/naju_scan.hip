@@ -183,6 +183,7 @@ struct ScanArgs {
   uint64_t* incl;  // [K][n_tiles][CH]
   int64_t T;
   int64_t D;
+  int N;
   int batch;
   int bc_dt;
   int n_dtiles;
@@ -689,14 +690,14 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   if (a.dfl) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
   if (a.dil) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
   if (a.partB || a.partC) {
-    // partial sums over this tile's channels, stored [b*T + t][dtile]
+    // partial sums over this tile's channels, stored [dtile][b*T + t]
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float sb = wave_sum(pB[r]);
       const float sc = wave_sum(pC[r]);
       const int64_t t = t0 + r;
       if (lane == 0 && (FULL || t < T)) {
-        const int64_t o = ((int64_t)b * T + t) * a.n_dtiles + dtile;
+        const int64_t o = (int64_t)dtile * a.batch * T + (int64_t)b * T + t;
         if (a.partB) a.partB[o] = sb;
         if (a.partC) a.partC[o] = sc;
       }
@@ -744,10 +745,26 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, s_F, s_Z, s_Zb, s_g, s_lb);
 }
 
+// Sum over q < n_parts of p[q*stride + i], in q order, with the loads of
+// eight parts issued together.
+__device__ __forceinline__ float sum_parts(const float* __restrict__ p, int n_parts, int64_t stride, int64_t i) {
+  float sm = 0.f;
+  int q = 0;
+  for (; q + 8 <= n_parts; q += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(q + u) * stride + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sm += v[u];
+  }
+  for (; q < n_parts; ++q) sm += p[(int64_t)q * stride + i];
+  return sm;
+}
+
 // Folds the backward's partial sums, in a fixed order (run-to-run
 // identical), in one launch:
-//   blocks [0, n_bc_blocks): dB, dC [i] = sum over the channel tiles p of
-//     partB/partC[i*n_parts + p] (contiguous per output);
+//   blocks [0, n_bc_blocks): dB, dC [i] = sum over the channel tiles q of
+//     partB/partC[q*btn + i] (consecutive threads read consecutive i);
 //   blocks [n_bc_blocks, ...): dD[d] = sum over the n_rows rows of
 //     partD[row][d], 64 channels per block; wave w of 16 sums rows
 //     w, w+16, ... with four interleaved accumulators, then the 16 wave
@@ -761,16 +778,8 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
   if ((int)blockIdx.x < n_bc_blocks) {
     const int64_t stride = (int64_t)n_bc_blocks * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
-      if (dB) {
-        float sm = 0.f;
-        for (int q = 0; q < n_parts; ++q) sm += partB[i * n_parts + q];
-        st_any(dB, bc_dt, i, sm);
-      }
-      if (dC) {
-        float sm = 0.f;
-        for (int q = 0; q < n_parts; ++q) sm += partC[i * n_parts + q];
-        st_any(dC, bc_dt, i, sm);
-      }
+      if (dB) st_any(dB, bc_dt, i, sum_parts(partB, n_parts, btn, i));
+      if (dC) st_any(dC, bc_dt, i, sum_parts(partC, n_parts, btn, i));
     }
     return;
   }
@@ -791,6 +800,313 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
     float sm = 0.f;
     for (int q = 0; q < 16; ++q) sm += s_acc[q][lane];
     dD[d] = sm;
+  }
+}
+
+// ------------------------------------------------------ general N (N >= 2)
+//
+// Lanes run over the state index n (a wave instruction covers G = 64/LG
+// channels, LG = min(NP, 64) lanes each, S = NP/LG states per lane; NP is
+// N rounded up to a power of two, states n >= N stay 0). One workgroup owns
+// a tile of 64 channels of one batch row for the whole sequence and walks T
+// in sub-chunks of kGnCK rows. Per-channel gates and inputs of a sub-chunk
+// are staged in LDS with coalesced loads and read back as broadcasts; B_t and
+// C_t rows are staged as [row][n]. Sums over n use fixed-order butterflies.
+//   forward : x_t = f x_{t-1} + i u B_t per lane; y_t = sum_n C_t x_t + D u;
+//             the state entering every sub-chunk is checkpointed.
+//   backward: sub-chunks in reverse; the forward states of a sub-chunk are
+//             recomputed from its checkpoint into registers, then the adjoint
+//             x̄_t = C_t dy_t + f_{t+1} x̄_{t+1} runs backwards with its carry
+//             kept in registers across sub-chunks (no inter-workgroup waits).
+//             dB, dC are summed over the tile's channels (lanes of other
+//             channel groups, then waves in wave order) into per-tile partials.
+constexpr int kGnCK = 32;  // rows per sub-chunk = checkpoint interval
+constexpr int kGnDT = 64;  // channels per workgroup
+constexpr int kGnW = 8;    // waves per workgroup
+
+template <int LG>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = LG / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Loads a [kGnCK][kGnDT] tile of one [batch,T,D] stream (rows t0.., channels
+// d0..) as float; out-of-range entries take `fill`.
+__device__ __forceinline__ float gn_ld(const ScanArgs& a, const void* p, int dt, int b, int64_t t, int64_t d,
+                                      float fill) {
+  return (t < a.T && d < a.D) ? ld_any(p, dt, ((int64_t)b * a.T + t) * a.D + d) : fill;
+}
+
+template <int NP>
+__global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int x_dt, int g_dt, int y_dt) {
+  constexpr int LG = NP < 64 ? NP : 64;
+  constexpr int S = NP / LG;
+  constexpr int G = 64 / LG;
+  constexpr int NPASS = kGnDT / G;
+  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
+  __shared__ float s_f[kGnCK][kGnDT], s_iu[kGnCK][kGnDT], s_du[kGnCK][kGnDT], s_y[kGnCK][kGnDT];
+  __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP];
+  const int N = a.N;
+  const int b = blockIdx.x / a.n_dtiles;
+  const int dtile = blockIdx.x - b * a.n_dtiles;
+  const int64_t T = a.T, D = a.D;
+  const int64_t dbase = (int64_t)dtile * kGnDT;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane / LG, nl = lane - gl * LG;
+  const int KC = (int)((T + kGnCK - 1) / kGnCK);
+
+  float x[PPW][S];
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) {
+      const int n = nl + 64 * s2;
+      x[q][s2] = (a.h0 && n < N && d < D) ? a.h0[((int64_t)b * D + d) * N + n] : 0.f;
+    }
+  }
+  for (int sc = 0; sc < KC; ++sc) {
+    const int64_t t0 = (int64_t)sc * kGnCK;
+    __syncthreads();  // the previous sub-chunk's tiles are consumed
+    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
+      const int r = e / kGnDT, c = e - r * kGnDT;
+      const int64_t t = t0 + r, d = dbase + c;
+      const bool ok = t < T && d < D;
+      const float u = gn_ld(a, a.u, x_dt, b, t, d, 0.f);
+      s_f[r][c] = ok ? sigm(gn_ld(a, a.fl, g_dt, b, t, d, 0.f)) : 1.f;
+      s_iu[r][c] = ok ? sigm(gn_ld(a, a.il, g_dt, b, t, d, 0.f)) * u : 0.f;
+      s_du[r][c] = (d < D) ? a.Dsk[d] * u : 0.f;
+    }
+    for (int e = threadIdx.x; e < kGnCK * NP; e += 64 * kGnW) {
+      const int r = e / NP, n = e - r * NP;
+      const int64_t t = t0 + r;
+      const bool ok = t < T && n < N;
+      s_B[r][n] = ok ? ld_any(a.Bm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
+      s_C[r][n] = ok ? ld_any(a.Cm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
+    }
+    __syncthreads();
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const int pass = wv + q * kGnW;
+      if (pass >= NPASS) break;
+      const int c = pass * G + gl;
+      const int64_t d = dbase + c;
+      if (a.ckpt) {
+#pragma unroll
+        for (int s2 = 0; s2 < S; ++s2) {
+          const int n = nl + 64 * s2;
+          if (n < N && d < D) a.ckpt[(((int64_t)b * KC + sc) * D + d) * N + n] = x[q][s2];
+        }
+      }
+      for (int r = 0; r < rows; ++r) {
+        const float f = s_f[r][c], iu = s_iu[r][c];
+        float acc = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < S; ++s2) {
+          const int n = nl + 64 * s2;
+          x[q][s2] = fmaf(f, x[q][s2], iu * s_B[r][n]);
+          acc = fmaf(s_C[r][n], x[q][s2], acc);
+        }
+        acc = group_sum<LG>(acc);
+        if (nl == 0) s_y[r][c] = acc + s_du[r][c];
+      }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
+      const int r = e / kGnDT, c = e - r * kGnDT;
+      const int64_t t = t0 + r, d = dbase + c;
+      if (t < T && d < D) st_any(a.y, y_dt, ((int64_t)b * T + t) * D + d, s_y[r][c]);
+    }
+  }
+  if (a.hT) {
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const int pass = wv + q * kGnW;
+      if (pass >= NPASS) break;
+      const int64_t d = dbase + (int64_t)pass * G + gl;
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+        const int n = nl + 64 * s2;
+        if (n < N && d < D) a.hT[((int64_t)b * D + d) * N + n] = x[q][s2];
+      }
+    }
+  }
+}
+
+template <int NP>
+__global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int x_dt, int g_dt, int du_dt,
+                                                           int dg_dt) {
+  constexpr int LG = NP < 64 ? NP : 64;
+  constexpr int S = NP / LG;
+  constexpr int G = 64 / LG;
+  constexpr int NPASS = kGnDT / G;
+  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
+  __shared__ float s_f[kGnCK][kGnDT], s_i[kGnCK][kGnDT], s_u[kGnCK][kGnDT], s_dy[kGnCK][kGnDT];
+  __shared__ float s_o0[kGnCK][kGnDT], s_o1[kGnCK][kGnDT], s_o2[kGnCK][kGnDT];
+  __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP], s_pB[kGnCK][NP], s_pC[kGnCK][NP];
+  const int N = a.N;
+  const int b = blockIdx.x / a.n_dtiles;
+  const int dtile = blockIdx.x - b * a.n_dtiles;
+  const int64_t T = a.T, D = a.D;
+  const int64_t dbase = (int64_t)dtile * kGnDT;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane / LG, nl = lane - gl * LG;
+  const int KC = (int)((T + kGnCK - 1) / kGnCK);
+  const int64_t btn = (int64_t)a.batch * T * N;
+
+  float gc[PPW][S];  // adjoint carry f_{t+1} x̄_{t+1} per channel pass
+  float dDs[PPW];
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    dDs[q] = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = 0.f;
+  }
+  for (int sc = KC - 1; sc >= 0; --sc) {
+    const int64_t t0 = (int64_t)sc * kGnCK;
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+    __syncthreads();  // the previous sub-chunk's tiles are consumed
+    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
+      const int r = e / kGnDT, c = e - r * kGnDT;
+      const int64_t t = t0 + r, d = dbase + c;
+      const bool ok = t < T && d < D;
+      s_f[r][c] = ok ? sigm(gn_ld(a, a.fl, g_dt, b, t, d, 0.f)) : 1.f;
+      s_i[r][c] = ok ? sigm(gn_ld(a, a.il, g_dt, b, t, d, 0.f)) : 0.f;
+      s_u[r][c] = gn_ld(a, a.u, x_dt, b, t, d, 0.f);
+      s_dy[r][c] = gn_ld(a, a.dy, x_dt, b, t, d, 0.f);
+    }
+    for (int e = threadIdx.x; e < kGnCK * NP; e += 64 * kGnW) {
+      const int r = e / NP, n = e - r * NP;
+      const int64_t t = t0 + r;
+      const bool ok = t < T && n < N;
+      s_B[r][n] = ok ? ld_any(a.Bm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
+      s_C[r][n] = ok ? ld_any(a.Cm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
+    }
+    __syncthreads();
+    float accB[kGnCK][S], accC[kGnCK][S];
+#pragma unroll
+    for (int r = 0; r < kGnCK; ++r)
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) accB[r][s2] = accC[r][s2] = 0.f;
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const int pass = wv + q * kGnW;
+      if (pass >= NPASS) break;
+      const int c = pass * G + gl;
+      const int64_t d = dbase + c;
+      const float Dv = d < D ? a.Dsk[d] : 0.f;
+      float x0[S], hist[kGnCK][S];
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+        const int n = nl + 64 * s2;
+        x0[s2] = (n < N && d < D) ? a.ckpt[(((int64_t)b * KC + sc) * D + d) * N + n] : 0.f;
+      }
+      {
+        float xs[S];
+#pragma unroll
+        for (int s2 = 0; s2 < S; ++s2) xs[s2] = x0[s2];
+#pragma unroll
+        for (int r = 0; r < kGnCK; ++r) {
+          if (r < rows) {
+            const float f = s_f[r][c], iu = s_i[r][c] * s_u[r][c];
+#pragma unroll
+            for (int s2 = 0; s2 < S; ++s2) xs[s2] = fmaf(f, xs[s2], iu * s_B[r][nl + 64 * s2]);
+          }
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) hist[r][s2] = xs[s2];
+        }
+      }
+#pragma unroll
+      for (int r = kGnCK - 1; r >= 0; --r) {
+        if (r < rows) {
+          const float f = s_f[r][c], ig = s_i[r][c], uu = s_u[r][c], gy = s_dy[r][c];
+          const float iu = ig * uu;
+          float sf = 0.f, sw = 0.f;
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) {
+            const int n = nl + 64 * s2;
+            const float xprev = r > 0 ? hist[r - 1][s2] : x0[s2];
+            const float xb = fmaf(gy, s_C[r][n], gc[q][s2]);
+            sf = fmaf(xb, xprev, sf);
+            sw = fmaf(xb, s_B[r][n], sw);
+            accB[r][s2] = fmaf(xb, iu, accB[r][s2]);
+            accC[r][s2] = fmaf(gy, hist[r][s2], accC[r][s2]);
+            gc[q][s2] = f * xb;
+          }
+          sf = group_sum<LG>(sf);
+          sw = group_sum<LG>(sw);
+          if (nl == 0) {
+            s_o0[r][c] = fmaf(ig, sw, Dv * gy);            // du
+            s_o1[r][c] = fmaf(-f, f, f) * sf;              // dfl
+            s_o2[r][c] = fmaf(-ig, ig, ig) * (sw * uu);    // dil
+            dDs[q] = fmaf(gy, uu, dDs[q]);
+          }
+        }
+      }
+    }
+    // dB/dC partials: sum over the channel groups of this wave, then over the
+    // waves in wave order.
+#pragma unroll
+    for (int r = 0; r < kGnCK; ++r)
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+#pragma unroll
+        for (int m = 32; m >= LG; m >>= 1) {
+          accB[r][s2] += __shfl_xor(accB[r][s2], m, 64);
+          accC[r][s2] += __shfl_xor(accC[r][s2], m, 64);
+        }
+      }
+    for (int w = 0; w < kGnW; ++w) {
+      if (wv == w && gl == 0) {
+#pragma unroll
+        for (int r = 0; r < kGnCK; ++r)
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) {
+            const int n = nl + 64 * s2;
+            s_pB[r][n] = (w == 0 ? 0.f : s_pB[r][n]) + accB[r][s2];
+            s_pC[r][n] = (w == 0 ? 0.f : s_pC[r][n]) + accC[r][s2];
+          }
+      }
+      __syncthreads();
+    }
+    for (int e = threadIdx.x; e < kGnCK * NP; e += 64 * kGnW) {
+      const int r = e / NP, n = e - r * NP;
+      const int64_t t = t0 + r;
+      if (t < T && n < N) {
+        const int64_t i = ((int64_t)b * T + t) * N + n;
+        if (a.partB) a.partB[(int64_t)dtile * btn + i] = s_pB[r][n];
+        if (a.partC) a.partC[(int64_t)dtile * btn + i] = s_pC[r][n];
+      }
+    }
+    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
+      const int r = e / kGnDT, c = e - r * kGnDT;
+      const int64_t t = t0 + r, d = dbase + c;
+      if (t < T && d < D) {
+        const int64_t o = ((int64_t)b * T + t) * D + d;
+        if (a.du) st_any(a.du, du_dt, o, s_o0[r][c]);
+        if (a.dfl) st_any(a.dfl, dg_dt, o, s_o1[r][c]);
+        if (a.dil) st_any(a.dil, dg_dt, o, s_o2[r][c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    const int pass = wv + q * kGnW;
+    if (pass >= NPASS) break;
+    const int64_t d = dbase + (int64_t)pass * G + gl;
+    if (d >= D) continue;
+    if (a.dh0) {
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+        const int n = nl + 64 * s2;
+        if (n < N) a.dh0[((int64_t)b * D + d) * N + n] = gc[q][s2];
+      }
+    }
+    if (a.partD && nl == 0) a.partD[(int64_t)b * D + d] = dDs[q];
   }
 }
 
@@ -875,14 +1191,20 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   Layout l{};
   (void)x_dt;
   (void)g_dt;
-  l.V = n1_vec_width(bwd);
-  l.CH = 64 * l.V;
-  l.L = kChunk;
+  size_t off = align_up(kHeaderBytes);
+  if (N == 1) {
+    l.V = n1_vec_width(bwd);
+    l.CH = 64 * l.V;
+    l.L = kChunk;
+  } else {  // general N: 64-channel tiles walking T, checkpoint every kGnCK rows
+    l.V = 1;
+    l.CH = kGnDT;
+    l.L = kGnCK;
+  }
   l.K = (int)((T + l.L - 1) / l.L);
   l.n_dtiles = (int)((D + l.CH - 1) / l.CH);
   l.n_tiles = (int)(batch * l.n_dtiles);
-  const size_t units = (size_t)l.K * l.n_tiles;
-  size_t off = align_up(kHeaderBytes);
+  const size_t units = N == 1 ? (size_t)l.K * l.n_tiles : 0;
   l.off_agg = off;
   off = align_up(off + units * 2 * l.CH * sizeof(uint64_t));
   l.off_incl = off;
@@ -892,7 +1214,7 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.off_partC = off;
   off = align_up(off + (size_t)l.n_dtiles * batch * T * N * sizeof(float));
   l.off_partD = off;
-  off = align_up(off + (size_t)batch * l.K * D * sizeof(float));
+  off = align_up(off + (size_t)batch * (N == 1 ? l.K : 1) * D * sizeof(float));
   l.total = off;
   return l;
 }
@@ -911,7 +1233,7 @@ int check_common(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g
     return fail(NAJU_ERR_UNSUPPORTED, "B/C dtype must be float32 or equal to the u dtype");
   if (x_dt == NAJU_DTYPE_F32 && g_dt != NAJU_DTYPE_F32)
     return fail(NAJU_ERR_UNSUPPORTED, "float32 u needs float32 gates");
-  if (N != 1) return fail(NAJU_ERR_UNSUPPORTED, "this build serves N == 1 only (got N=%lld)", (long long)N);
+  if (N > 128) return fail(NAJU_ERR_UNSUPPORTED, "N (d_state) must be <= 128, got %lld", (long long)N);
   if (T > (1ll << 30) || D > (1ll << 30) || batch > (1ll << 30))
     return fail(NAJU_ERR_INVALID, "dimension exceeds 2^30");
   return NAJU_OK;
@@ -946,6 +1268,39 @@ kern_t pick_n1_all(bool vec, bool f32o, int x_dt, int g_dt, int bc_dt, bool bwd)
   if (vec)
     return f32o ? pick_n1_dt<true, true>(x_dt, g_dt, bc_dt, bwd) : pick_n1_dt<true, false>(x_dt, g_dt, bc_dt, bwd);
   return f32o ? pick_n1_dt<false, true>(x_dt, g_dt, bc_dt, bwd) : pick_n1_dt<false, false>(x_dt, g_dt, bc_dt, bwd);
+}
+
+typedef void (*gn_fwd_t)(ScanArgs, int, int, int);
+typedef void (*gn_bwd_t)(ScanArgs, int, int, int, int);
+
+int np_of(int64_t N) {
+  int np = 2;
+  while (np < N) np <<= 1;
+  return np;
+}
+
+gn_fwd_t pick_gn_fwd(int np) {
+  switch (np) {
+    case 2: return gn_fwd_kernel<2>;
+    case 4: return gn_fwd_kernel<4>;
+    case 8: return gn_fwd_kernel<8>;
+    case 16: return gn_fwd_kernel<16>;
+    case 32: return gn_fwd_kernel<32>;
+    case 64: return gn_fwd_kernel<64>;
+    default: return gn_fwd_kernel<128>;
+  }
+}
+
+gn_bwd_t pick_gn_bwd(int np) {
+  switch (np) {
+    case 2: return gn_bwd_kernel<2>;
+    case 4: return gn_bwd_kernel<4>;
+    case 8: return gn_bwd_kernel<8>;
+    case 16: return gn_bwd_kernel<16>;
+    case 32: return gn_bwd_kernel<32>;
+    case 64: return gn_bwd_kernel<64>;
+    default: return gn_bwd_kernel<128>;
+  }
 }
 
 int launch(kern_t k, unsigned grid, unsigned block, hipStream_t st, const ScanArgs& a) {
@@ -1027,11 +1382,20 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   a.incl = (uint64_t*)(ws + l.off_incl);
   a.T = T;
   a.D = D;
+  a.N = (int)N;
   a.batch = (int)batch;
   a.bc_dt = bc_dtype;
   a.n_dtiles = l.n_dtiles;
   a.n_tiles = l.n_tiles;
   a.K = l.K;
+  if (N > 1) {
+    const int y_dt = out_f32 ? (int)NAJU_DTYPE_F32 : x_dtype;
+    hipLaunchKernelGGL(pick_gn_fwd(np_of(N)), dim3((unsigned)l.n_tiles), dim3(64 * kGnW), 0, st, a, x_dtype,
+                       gate_dtype, y_dt);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+    return NAJU_OK;
+  }
   const int64_t wgs = (int64_t)l.K * l.n_tiles;
   if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
     return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
@@ -1097,26 +1461,36 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   a.partD = dD ? (float*)(ws + l.off_partD) : nullptr;
   a.T = T;
   a.D = D;
+  a.N = (int)N;
   a.batch = (int)batch;
   a.bc_dt = bc_dtype;
   a.n_dtiles = l.n_dtiles;
   a.n_tiles = l.n_tiles;
   a.K = l.K;
-  const int64_t wgs = (int64_t)l.K * l.n_tiles;
-  if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
-    return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
-                l.n_tiles);
-  a.tag = next_tag();
-  kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, true);
-  rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
-  if (rc) return rc;
+  if (N > 1) {
+    const int du_dt = out_f32 ? (int)NAJU_DTYPE_F32 : x_dtype;
+    const int dg_dt = out_f32 ? (int)NAJU_DTYPE_F32 : gate_dtype;
+    hipLaunchKernelGGL(pick_gn_bwd(np_of(N)), dim3((unsigned)l.n_tiles), dim3(64 * kGnW), 0, st, a, x_dtype,
+                       gate_dtype, du_dt, dg_dt);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  } else {
+    const int64_t wgs = (int64_t)l.K * l.n_tiles;
+    if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
+      return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
+                  l.n_tiles);
+    a.tag = next_tag();
+    kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, true);
+    rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
+    if (rc) return rc;
+  }
   if (dB || dC || dD) {
     const int64_t btn = batch * T * N;
     const int n_bc = (dB || dC) ? (int)((btn + 1023) / 1024 < 256 ? (btn + 1023) / 1024 : 256) : 0;
     const int n_d = dD ? (int)((D + 63) / 64) : 0;
     hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
-                       btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD, batch * (int64_t)l.K, D,
-                       dD);
+                       btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD,
+                       batch * (int64_t)(N == 1 ? l.K : 1), D, dD);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;

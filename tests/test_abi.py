@@ -49,6 +49,9 @@ def test_size_queries():
     assert n > 0 and n % (8 * 1024) == 0 and n <= 8 * 1024 * 4096
     ws = L.naju_scan_workspace_bytes(8, 4096, 1024, 1, BF16, BF16, BF16)
     assert ws > 0 and ws % 256 == 0
+    # general N: one float per (b, 32-row sub-chunk, d, n)
+    n64 = L.naju_scan_ckpt_elems(8, 4096, 1024, 64, BF16, F32, BF16)
+    assert n64 == 8 * (4096 // 32) * 1024 * 64
     # invalid requests report 0 / -1 and set the message
     assert L.naju_scan_workspace_bytes(8, 4096, 1024, 0, BF16, BF16, BF16) == 0
     assert b"N" in L.naju_scan_last_error()
@@ -80,7 +83,7 @@ def _bwd(L, **kw):
     (dict(x=BF16, g=F16), _lib.ERR_UNSUPPORTED, "gate"),
     (dict(x=F32, g=BF16), _lib.ERR_UNSUPPORTED, "gate"),
     (dict(x=BF16, g=BF16, bc=F16), _lib.ERR_UNSUPPORTED, "B/C"),
-    (dict(N=3), _lib.ERR_UNSUPPORTED, "N"),
+    (dict(N=129), _lib.ERR_UNSUPPORTED, "N"),
     (dict(u=None), _lib.ERR_INVALID, "null"),
     (dict(y=None), _lib.ERR_INVALID, "null"),
     (dict(ws=None), _lib.ERR_WORKSPACE, "workspace"),
