@@ -831,11 +831,74 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Loads a [kGnCK][kGnDT] tile of one [batch,T,D] stream (rows t0.., channels
-// d0..) as float; out-of-range entries take `fill`.
-__device__ __forceinline__ float gn_ld(const ScanArgs& a, const void* p, int dt, int b, int64_t t, int64_t d,
-                                      float fill) {
-  return (t < a.T && d < a.D) ? ld_any(p, dt, ((int64_t)b * a.T + t) * a.D + d) : fill;
+constexpr int kGnThreads = 64 * kGnW;
+constexpr int kGnE = kGnCK * kGnDT / kGnThreads;  // tile elements per thread
+
+// This thread's kGnE elements (element k = e*kGnThreads + tid is row k/kGnDT,
+// channel k%kGnDT) of a [kGnCK][kGnDT] tile of one [batch,T,D] stream
+// starting at row t0, channel dbase. Rows past T and channels past D read a
+// clamped in-bounds element, which the caller replaces. The dtype switch is
+// outside the element loop, so the loads issue back to back.
+__device__ __forceinline__ void gn_ld_tile(const ScanArgs& a, const void* p, int dt, int b, int64_t t0,
+                                           int64_t dbase, float (&v)[kGnE]) {
+  int64_t idx[kGnE];
+#pragma unroll
+  for (int e = 0; e < kGnE; ++e) {
+    const int k = e * kGnThreads + (int)threadIdx.x;
+    const int64_t t = t0 + k / kGnDT, d = dbase + k % kGnDT;
+    idx[e] = ((int64_t)b * a.T + (t < a.T ? t : a.T - 1)) * a.D + (d < a.D ? d : a.D - 1);
+  }
+  if (dt == NAJU_DTYPE_F32) {
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) v[e] = ((const float*)p)[idx[e]];
+  } else if (dt == NAJU_DTYPE_BF16) {
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) v[e] = (float)((const bf16_t*)p)[idx[e]];
+  } else {
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) v[e] = (float)((const f16_t*)p)[idx[e]];
+  }
+}
+
+// The same for a [kGnCK][NP] tile of B or C ([batch,T,N]); entries past T or
+// N are replaced by the caller.
+template <int NP, int EB>
+__device__ __forceinline__ void gn_ld_bc(const ScanArgs& a, const void* p, int b, int64_t t0, float (&v)[EB]) {
+  int64_t idx[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) {
+    const int k = e * kGnThreads + (int)threadIdx.x;
+    const int64_t t = t0 + k / NP;
+    const int n = k % NP;
+    idx[e] = ((int64_t)b * a.T + (t < a.T ? t : a.T - 1)) * a.N + (n < a.N ? n : a.N - 1);
+  }
+  if (a.bc_dt == NAJU_DTYPE_F32) {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) v[e] = ((const float*)p)[idx[e]];
+  } else if (a.bc_dt == NAJU_DTYPE_BF16) {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) v[e] = (float)((const bf16_t*)p)[idx[e]];
+  } else {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) v[e] = (float)((const f16_t*)p)[idx[e]];
+  }
+}
+
+// Writes a prefetched B/C tile into LDS, zero where the row is past T or the
+// state index past N.
+template <int NP, int EB>
+__device__ __forceinline__ void gn_st_bc(const ScanArgs& a, int64_t t0, const float (&vb)[EB],
+                                         const float (&vc)[EB], float (&sB)[kGnCK][NP], float (&sC)[kGnCK][NP]) {
+#pragma unroll
+  for (int e = 0; e < EB; ++e) {
+    const int k = e * kGnThreads + (int)threadIdx.x;
+    if (k < kGnCK * NP) {
+      const int r = k / NP, n = k % NP;
+      const bool ok = t0 + r < a.T && n < a.N;
+      sB[r][n] = ok ? vb[e] : 0.f;
+      sC[r][n] = ok ? vc[e] : 0.f;
+    }
+  }
 }
 
 template <int NP>
@@ -867,26 +930,36 @@ __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int
       x[q][s2] = (a.h0 && n < N && d < D) ? a.h0[((int64_t)b * D + d) * N + n] : 0.f;
     }
   }
+  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
+  float vu[kGnE], vf[kGnE], vi[kGnE], vb[EB], vc[EB];
+  gn_ld_tile(a, a.u, x_dt, b, 0, dbase, vu);
+  gn_ld_tile(a, a.fl, g_dt, b, 0, dbase, vf);
+  gn_ld_tile(a, a.il, g_dt, b, 0, dbase, vi);
+  gn_ld_bc<NP, EB>(a, a.Bm, b, 0, vb);
+  gn_ld_bc<NP, EB>(a, a.Cm, b, 0, vc);
   for (int sc = 0; sc < KC; ++sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     __syncthreads();  // the previous sub-chunk's tiles are consumed
-    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
-      const int r = e / kGnDT, c = e - r * kGnDT;
-      const int64_t t = t0 + r, d = dbase + c;
-      const bool ok = t < T && d < D;
-      const float u = gn_ld(a, a.u, x_dt, b, t, d, 0.f);
-      s_f[r][c] = ok ? sigm(gn_ld(a, a.fl, g_dt, b, t, d, 0.f)) : 1.f;
-      s_iu[r][c] = ok ? sigm(gn_ld(a, a.il, g_dt, b, t, d, 0.f)) * u : 0.f;
-      s_du[r][c] = (d < D) ? a.Dsk[d] * u : 0.f;
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) {
+      const int k = e * kGnThreads + (int)threadIdx.x;
+      const int r = k / kGnDT, c = k % kGnDT;
+      const int64_t d = dbase + c;
+      const bool ok = t0 + r < T && d < D;
+      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
+      s_iu[r][c] = ok ? sigm(vi[e]) * vu[e] : 0.f;
+      s_du[r][c] = ok ? a.Dsk[d] * vu[e] : 0.f;
     }
-    for (int e = threadIdx.x; e < kGnCK * NP; e += 64 * kGnW) {
-      const int r = e / NP, n = e - r * NP;
-      const int64_t t = t0 + r;
-      const bool ok = t < T && n < N;
-      s_B[r][n] = ok ? ld_any(a.Bm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
-      s_C[r][n] = ok ? ld_any(a.Cm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
-    }
+    gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
     __syncthreads();
+    if (sc + 1 < KC) {  // prefetch the next sub-chunk while this one is scanned
+      const int64_t t1 = t0 + kGnCK;
+      gn_ld_tile(a, a.u, x_dt, b, t1, dbase, vu);
+      gn_ld_tile(a, a.fl, g_dt, b, t1, dbase, vf);
+      gn_ld_tile(a, a.il, g_dt, b, t1, dbase, vi);
+      gn_ld_bc<NP, EB>(a, a.Bm, b, t1, vb);
+      gn_ld_bc<NP, EB>(a, a.Cm, b, t1, vc);
+    }
     const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
@@ -901,17 +974,28 @@ __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int
           if (n < N && d < D) a.ckpt[(((int64_t)b * KC + sc) * D + d) * N + n] = x[q][s2];
         }
       }
-      for (int r = 0; r < rows; ++r) {
-        const float f = s_f[r][c], iu = s_iu[r][c];
-        float acc = 0.f;
+      // the recurrence runs row by row; the sums over n of all rows are
+      // formed afterwards, so their shuffle chains interleave
+      float p[kGnCK];
 #pragma unroll
-        for (int s2 = 0; s2 < S; ++s2) {
-          const int n = nl + 64 * s2;
-          x[q][s2] = fmaf(f, x[q][s2], iu * s_B[r][n]);
-          acc = fmaf(s_C[r][n], x[q][s2], acc);
+      for (int r = 0; r < kGnCK; ++r) {
+        p[r] = 0.f;
+        if (r < rows) {
+          const float f = s_f[r][c], iu = s_iu[r][c];
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) {
+            const int n = nl + 64 * s2;
+            x[q][s2] = fmaf(f, x[q][s2], iu * s_B[r][n]);
+            p[r] = fmaf(s_C[r][n], x[q][s2], p[r]);
+          }
         }
-        acc = group_sum<LG>(acc);
-        if (nl == 0) s_y[r][c] = acc + s_du[r][c];
+      }
+#pragma unroll
+      for (int r = 0; r < kGnCK; ++r) p[r] = group_sum<LG>(p[r]);
+      if (nl == 0) {
+#pragma unroll
+        for (int r = 0; r < kGnCK; ++r)
+          if (r < rows) s_y[r][c] = p[r] + s_du[r][c];
       }
     }
     __syncthreads();
@@ -966,27 +1050,38 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = 0.f;
   }
+  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
+  // At NP = 128 the registers of a prefetched tile would spill: that case
+  // loads each sub-chunk's tiles just before staging them instead.
+  constexpr bool kPrefetch = NP <= 64;
+  float vu[kGnE], vf[kGnE], vi[kGnE], vg[kGnE], vb[EB], vc[EB];
+  auto load_tiles = [&](int64_t tl) {
+    gn_ld_tile(a, a.u, x_dt, b, tl, dbase, vu);
+    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
+    gn_ld_tile(a, a.il, g_dt, b, tl, dbase, vi);
+    gn_ld_tile(a, a.dy, x_dt, b, tl, dbase, vg);
+    gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
+    gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
+  };
+  if (kPrefetch) load_tiles((int64_t)(KC - 1) * kGnCK);
   for (int sc = KC - 1; sc >= 0; --sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+    if (!kPrefetch) load_tiles(t0);
     __syncthreads();  // the previous sub-chunk's tiles are consumed
-    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
-      const int r = e / kGnDT, c = e - r * kGnDT;
-      const int64_t t = t0 + r, d = dbase + c;
-      const bool ok = t < T && d < D;
-      s_f[r][c] = ok ? sigm(gn_ld(a, a.fl, g_dt, b, t, d, 0.f)) : 1.f;
-      s_i[r][c] = ok ? sigm(gn_ld(a, a.il, g_dt, b, t, d, 0.f)) : 0.f;
-      s_u[r][c] = gn_ld(a, a.u, x_dt, b, t, d, 0.f);
-      s_dy[r][c] = gn_ld(a, a.dy, x_dt, b, t, d, 0.f);
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) {
+      const int k = e * kGnThreads + (int)threadIdx.x;
+      const int r = k / kGnDT, c = k % kGnDT;
+      const bool ok = t0 + r < T && dbase + c < D;
+      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
+      s_i[r][c] = ok ? sigm(vi[e]) : 0.f;
+      s_u[r][c] = ok ? vu[e] : 0.f;
+      s_dy[r][c] = ok ? vg[e] : 0.f;
     }
-    for (int e = threadIdx.x; e < kGnCK * NP; e += 64 * kGnW) {
-      const int r = e / NP, n = e - r * NP;
-      const int64_t t = t0 + r;
-      const bool ok = t < T && n < N;
-      s_B[r][n] = ok ? ld_any(a.Bm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
-      s_C[r][n] = ok ? ld_any(a.Cm, a.bc_dt, ((int64_t)b * T + t) * N + n) : 0.f;
-    }
+    gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
     __syncthreads();
+    if (kPrefetch && sc > 0) load_tiles(t0 - kGnCK);  // next (earlier) sub-chunk, while this one runs
     float accB[kGnCK][S], accC[kGnCK][S];
 #pragma unroll
     for (int r = 0; r < kGnCK; ++r)
@@ -1020,29 +1115,40 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
           for (int s2 = 0; s2 < S; ++s2) hist[r][s2] = xs[s2];
         }
       }
+      // adjoint recurrence row by row (reverse); the sums over n of all rows
+      // are formed afterwards so that their shuffle chains interleave
+      float pf[kGnCK], pw[kGnCK];
 #pragma unroll
       for (int r = kGnCK - 1; r >= 0; --r) {
+        pf[r] = pw[r] = 0.f;
         if (r < rows) {
-          const float f = s_f[r][c], ig = s_i[r][c], uu = s_u[r][c], gy = s_dy[r][c];
-          const float iu = ig * uu;
-          float sf = 0.f, sw = 0.f;
+          const float f = s_f[r][c], iu = s_i[r][c] * s_u[r][c], gy = s_dy[r][c];
 #pragma unroll
           for (int s2 = 0; s2 < S; ++s2) {
             const int n = nl + 64 * s2;
             const float xprev = r > 0 ? hist[r - 1][s2] : x0[s2];
             const float xb = fmaf(gy, s_C[r][n], gc[q][s2]);
-            sf = fmaf(xb, xprev, sf);
-            sw = fmaf(xb, s_B[r][n], sw);
+            pf[r] = fmaf(xb, xprev, pf[r]);
+            pw[r] = fmaf(xb, s_B[r][n], pw[r]);
             accB[r][s2] = fmaf(xb, iu, accB[r][s2]);
             accC[r][s2] = fmaf(gy, hist[r][s2], accC[r][s2]);
             gc[q][s2] = f * xb;
           }
-          sf = group_sum<LG>(sf);
-          sw = group_sum<LG>(sw);
-          if (nl == 0) {
-            s_o0[r][c] = fmaf(ig, sw, Dv * gy);            // du
-            s_o1[r][c] = fmaf(-f, f, f) * sf;              // dfl
-            s_o2[r][c] = fmaf(-ig, ig, ig) * (sw * uu);    // dil
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kGnCK; ++r) {
+        pf[r] = group_sum<LG>(pf[r]);
+        pw[r] = group_sum<LG>(pw[r]);
+      }
+      if (nl == 0) {
+#pragma unroll
+        for (int r = 0; r < kGnCK; ++r) {
+          if (r < rows) {
+            const float f = s_f[r][c], ig = s_i[r][c], uu = s_u[r][c], gy = s_dy[r][c];
+            s_o0[r][c] = fmaf(ig, pw[r], Dv * gy);            // du
+            s_o1[r][c] = fmaf(-f, f, f) * pf[r];              // dfl
+            s_o2[r][c] = fmaf(-ig, ig, ig) * (pw[r] * uu);    // dil
             dDs[q] = fmaf(gy, uu, dDs[q]);
           }
         }
