@@ -1265,7 +1265,7 @@ size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 #define NAJU_F_W 4
 #endif
 #ifndef NAJU_F_P
-#define NAJU_F_P 4
+#define NAJU_F_P 1
 #endif
 #ifndef NAJU_B_V
 #define NAJU_B_V 2
@@ -1277,7 +1277,7 @@ size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 #define NAJU_B_W 8
 #endif
 #ifndef NAJU_B_P
-#define NAJU_B_P 2
+#define NAJU_B_P 1
 #endif
 constexpr int kFV = NAJU_F_V, kFR = NAJU_F_R, kFW = NAJU_F_W, kFP = NAJU_F_P;
 constexpr int kBV = NAJU_B_V, kBR = NAJU_B_R, kBW = NAJU_B_W, kBP = NAJU_B_P;
