@@ -189,6 +189,8 @@ struct ScanArgs {
   int n_dtiles;
   int n_tiles;
   int K;
+  int ck_rows;  // N = 1 forward: rows per checkpoint interval (the backward's chunk length)
+  int Kc;       // N = 1 forward: number of checkpoint intervals
   uint32_t tag;  // this launch's tag (nonzero, new for every launch)
 };
 
@@ -472,11 +474,6 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
       st_word(my_incl + j * 64, fmaf(Fw[j], sin[j], Zw[j]), tag);
       s_in[j * 64 + lane] = sin[j];
     }
-    if (a.ckpt) {
-#pragma unroll
-      for (int j = 0; j < V; ++j)
-        if (dok[j]) a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] = sin[j];
-    }
     if (a.hT && k == a.K - 1) {
 #pragma unroll
       for (int j = 0; j < V; ++j)
@@ -492,6 +489,12 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
   for (int w = 0; w < wv; ++w)
 #pragma unroll
     for (int j = 0; j < V; ++j) s[j] = fmaf(s_F[w][j * 64 + lane], s[j], s_Z[w][j * 64 + lane]);
+  // the state entering a checkpoint interval of the backward pass
+  if (a.ckpt && t0 % a.ck_rows == 0 && (FULL || t0 < T)) {
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      if (dok[j]) a.ckpt[((int64_t)b * a.Kc + t0 / a.ck_rows) * D + d0 + j] = s[j];
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -1253,8 +1256,9 @@ size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 
 // Tile geometry of the N = 1 kernels, per direction: V channels per lane,
 // R rows per wave, W waves per workgroup (chunk L = W*R rows), P look-back
-// slots polled per wave and round (window W*P chunks). Both directions use
-// the same chunk length, which fixes the checkpoint layout.
+// slots polled per wave and round (window W*P chunks). The checkpoint holds
+// the state entering every backward chunk, so its layout follows the
+// backward chunk length.
 #ifndef NAJU_F_V
 #define NAJU_F_V 2
 #endif
@@ -1274,15 +1278,18 @@ size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 #define NAJU_B_R 8
 #endif
 #ifndef NAJU_B_W
-#define NAJU_B_W 8
+#define NAJU_B_W 4
 #endif
 #ifndef NAJU_B_P
 #define NAJU_B_P 1
 #endif
 constexpr int kFV = NAJU_F_V, kFR = NAJU_F_R, kFW = NAJU_F_W, kFP = NAJU_F_P;
 constexpr int kBV = NAJU_B_V, kBR = NAJU_B_R, kBW = NAJU_B_W, kBP = NAJU_B_P;
-constexpr int kChunk = kFR * kFW;
-static_assert(kBR * kBW == kChunk, "forward and backward chunk lengths must match");
+constexpr int kFChunk = kFR * kFW;
+constexpr int kBChunk = kBR * kBW;
+// The forward writes the state entering every backward chunk: at the start
+// of a forward wave's rows.
+static_assert(kFChunk % kBChunk == 0 && kBChunk % kFR == 0, "backward chunks must tile forward chunks by waves");
 
 int n1_vec_width(bool bwd) { return bwd ? kBV : kFV; }
 
@@ -1301,7 +1308,7 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   if (N == 1) {
     l.V = n1_vec_width(bwd);
     l.CH = 64 * l.V;
-    l.L = kChunk;
+    l.L = bwd ? kBChunk : kFChunk;
   } else {  // general N: 64-channel tiles walking T, checkpoint every kGnCK rows
     l.V = 1;
     l.CH = kGnDT;
@@ -1432,7 +1439,8 @@ const char* naju_scan_last_error(void) { return g_err; }
 int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
                              int bc_dtype) {
   if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return -1;
-  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false);
+  // N = 1: one state per backward chunk; N > 1: per forward sub-chunk
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, N == 1);
   return batch * (int64_t)l.K * D * N;
 }
 
@@ -1507,6 +1515,8 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
     return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                 l.n_tiles);
   a.tag = next_tag();
+  a.ck_rows = kBChunk;
+  a.Kc = (int)((T + kBChunk - 1) / kBChunk);
   kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, false);
   return launch(k, (unsigned)wgs, 64 * kFW, st, a);
 }
