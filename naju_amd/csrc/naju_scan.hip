@@ -177,7 +177,12 @@ struct ScanArgs {
   float* dh0;
   float* partB;  // [n_dtiles][batch][T][N]
   float* partC;
-  float* partD;  // [batch][K][D]
+  float* partD;  // N = 1: [batch][K][D]; N > 1: [batch][nseg][D]
+  float* segF;   // N > 1, per time segment: [batch][nseg][D] decay over the segment
+  float* segZ;   // [batch][nseg][D][N] the segment's state map from a zero state
+  float* seg0;   // [batch][nseg][D][N] the state (adjoint carry) entering each segment
+  int nseg;      // N > 1: time segments (one workgroup each per channel tile)
+  int seg_sc;    // N > 1: sub-chunks per time segment
   uint32_t* hdr;
   uint64_t* agg;   // [K][n_tiles][2][CH]
   uint64_t* incl;  // [K][n_tiles][CH]
@@ -904,6 +909,228 @@ __device__ __forceinline__ void gn_st_bc(const ScanArgs& a, int64_t t0, const fl
   }
 }
 
+// Writes one prefetched [kGnCK][NP] tile of B or C into LDS (zeros outside).
+template <int NP, int EB>
+__device__ __forceinline__ void gn_st_one(const ScanArgs& a, int64_t t0, const float (&v)[EB], float (&sv)[kGnCK][NP]) {
+#pragma unroll
+  for (int e = 0; e < EB; ++e) {
+    const int k = e * kGnThreads + (int)threadIdx.x;
+    if (k < kGnCK * NP) {
+      const int r = k / NP, n = k % NP;
+      sv[r][n] = (t0 + r < a.T && n < a.N) ? v[e] : 0.f;
+    }
+  }
+}
+
+// Time segments. With nseg > 1 the sub-chunks of T are split into nseg
+// segments of seg_sc sub-chunks, each scanned by its own workgroup per
+// channel tile (grid = n_tiles * segments, tile = blockIdx % n_tiles). The
+// state entering a segment comes from three steps: every segment's map from
+// a zero state (gn_fwd_map_kernel: decay F and state Z per channel), a carry
+// pass over the segments (gn_seg_carry_kernel), then the full scan from the
+// carried state. The backward mirrors this with the adjoint carry.
+
+// Forward map of segment blockIdx / n_tiles (segments 0 .. nseg-2).
+template <int NP>
+__global__ __launch_bounds__(64 * kGnW) void gn_fwd_map_kernel(const ScanArgs a, int x_dt, int g_dt) {
+  constexpr int LG = NP < 64 ? NP : 64;
+  constexpr int S = NP / LG;
+  constexpr int G = 64 / LG;
+  constexpr int NPASS = kGnDT / G;
+  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
+  __shared__ float s_f[kGnCK][kGnDT], s_iu[kGnCK][kGnDT];
+  __shared__ float s_B[kGnCK][NP];
+  const int N = a.N;
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
+  const int64_t T = a.T, D = a.D;
+  const int64_t dbase = (int64_t)dtile * kGnDT;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane / LG, nl = lane - gl * LG;
+  const int KC = (int)((T + kGnCK - 1) / kGnCK);
+  const int sc0 = seg * a.seg_sc;
+  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
+
+  float x[PPW][S], Fc[PPW];
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    Fc[q] = 1.f;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) x[q][s2] = 0.f;
+  }
+  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
+  float vu[kGnE], vf[kGnE], vi[kGnE], vb[EB];
+  auto load_tiles = [&](int64_t tl) {
+    gn_ld_tile(a, a.u, x_dt, b, tl, dbase, vu);
+    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
+    gn_ld_tile(a, a.il, g_dt, b, tl, dbase, vi);
+    gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
+  };
+  load_tiles((int64_t)sc0 * kGnCK);
+  for (int sc = sc0; sc < sc1; ++sc) {
+    const int64_t t0 = (int64_t)sc * kGnCK;
+    __syncthreads();  // the previous sub-chunk's tiles are consumed
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) {
+      const int k = e * kGnThreads + (int)threadIdx.x;
+      const int r = k / kGnDT, c = k % kGnDT;
+      const bool ok = t0 + r < T && dbase + c < D;
+      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
+      s_iu[r][c] = ok ? sigm(vi[e]) * vu[e] : 0.f;
+    }
+    gn_st_one<NP, EB>(a, t0, vb, s_B);
+    __syncthreads();
+    if (sc + 1 < sc1) load_tiles(t0 + kGnCK);
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const int pass = wv + q * kGnW;
+      if (pass >= NPASS) break;
+      const int c = pass * G + gl;
+#pragma unroll
+      for (int r = 0; r < kGnCK; ++r) {
+        if (r < rows) {
+          const float f = s_f[r][c], iu = s_iu[r][c];
+          Fc[q] *= f;
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) x[q][s2] = fmaf(f, x[q][s2], iu * s_B[r][nl + 64 * s2]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    const int pass = wv + q * kGnW;
+    if (pass >= NPASS) break;
+    const int64_t d = dbase + (int64_t)pass * G + gl;
+    if (d >= D) continue;
+    const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) {
+      const int n = nl + 64 * s2;
+      if (n < N) a.segZ[o * N + n] = x[q][s2];
+    }
+    if (nl == 0) a.segF[o] = Fc[q];
+  }
+}
+
+// Adjoint map of segment blockIdx / n_tiles + 1 (segments 1 .. nseg-1): the
+// carry leaving the segment's first row towards the past, from a zero carry
+// entering its last row (segZ), and the product of its gates (segF).
+template <int NP>
+__global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a, int x_dt, int g_dt) {
+  constexpr int LG = NP < 64 ? NP : 64;
+  constexpr int S = NP / LG;
+  constexpr int G = 64 / LG;
+  constexpr int NPASS = kGnDT / G;
+  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
+  __shared__ float s_f[kGnCK][kGnDT], s_dy[kGnCK][kGnDT];
+  __shared__ float s_C[kGnCK][NP];
+  const int N = a.N;
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles) + 1;
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
+  const int64_t T = a.T, D = a.D;
+  const int64_t dbase = (int64_t)dtile * kGnDT;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane / LG, nl = lane - gl * LG;
+  const int KC = (int)((T + kGnCK - 1) / kGnCK);
+  const int sc0 = seg * a.seg_sc;
+  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
+
+  float gc[PPW][S], Ac[PPW];
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    Ac[q] = 1.f;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = 0.f;
+  }
+  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
+  float vf[kGnE], vg[kGnE], vc[EB];
+  auto load_tiles = [&](int64_t tl) {
+    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
+    gn_ld_tile(a, a.dy, x_dt, b, tl, dbase, vg);
+    gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
+  };
+  load_tiles((int64_t)(sc1 - 1) * kGnCK);
+  for (int sc = sc1 - 1; sc >= sc0; --sc) {
+    const int64_t t0 = (int64_t)sc * kGnCK;
+    __syncthreads();  // the previous sub-chunk's tiles are consumed
+#pragma unroll
+    for (int e = 0; e < kGnE; ++e) {
+      const int k = e * kGnThreads + (int)threadIdx.x;
+      const int r = k / kGnDT, c = k % kGnDT;
+      const bool ok = t0 + r < T && dbase + c < D;
+      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
+      s_dy[r][c] = ok ? vg[e] : 0.f;
+    }
+    gn_st_one<NP, EB>(a, t0, vc, s_C);
+    __syncthreads();
+    if (sc > sc0) load_tiles(t0 - kGnCK);
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const int pass = wv + q * kGnW;
+      if (pass >= NPASS) break;
+      const int c = pass * G + gl;
+#pragma unroll
+      for (int r = kGnCK - 1; r >= 0; --r) {
+        if (r < rows) {
+          const float f = s_f[r][c], gy = s_dy[r][c];
+          Ac[q] *= f;
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = f * fmaf(gy, s_C[r][nl + 64 * s2], gc[q][s2]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    const int pass = wv + q * kGnW;
+    if (pass >= NPASS) break;
+    const int64_t d = dbase + (int64_t)pass * G + gl;
+    if (d >= D) continue;
+    const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) {
+      const int n = nl + 64 * s2;
+      if (n < N) a.segZ[o * N + n] = gc[q][s2];
+    }
+    if (nl == 0) a.segF[o] = Ac[q];
+  }
+}
+
+// Carry over the time segments, one thread per (b, d, n): the state entering
+// each segment (dir = +1, from h0) or the adjoint carry entering it from the
+// future (dir = -1, from zero), into seg0.
+__global__ void gn_seg_carry_kernel(const ScanArgs a, int dir) {
+  const int64_t DN = a.D * (int64_t)a.N;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.batch * DN) return;
+  const int64_t b = i / DN, dn = i - b * DN, d = dn / a.N;
+  const int ns = a.nseg;
+  if (dir > 0) {
+    float x = a.h0 ? a.h0[i] : 0.f;
+    for (int sg = 0; sg < ns; ++sg) {
+      const int64_t o = (b * ns + sg) * a.D + d;
+      a.seg0[o * a.N + (dn - d * a.N)] = x;
+      if (sg + 1 < ns) x = fmaf(a.segF[o], x, a.segZ[o * a.N + (dn - d * a.N)]);
+    }
+  } else {
+    float g = 0.f;
+    for (int sg = ns - 1; sg >= 0; --sg) {
+      const int64_t o = (b * ns + sg) * a.D + d;
+      a.seg0[o * a.N + (dn - d * a.N)] = g;
+      if (sg > 0) g = fmaf(a.segF[o], g, a.segZ[o * a.N + (dn - d * a.N)]);
+    }
+  }
+}
+
 template <int NP>
 __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int x_dt, int g_dt, int y_dt) {
   constexpr int LG = NP < 64 ? NP : 64;
@@ -914,15 +1141,21 @@ __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int
   __shared__ float s_f[kGnCK][kGnDT], s_iu[kGnCK][kGnDT], s_du[kGnCK][kGnDT], s_y[kGnCK][kGnDT];
   __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP];
   const int N = a.N;
-  const int b = blockIdx.x / a.n_dtiles;
-  const int dtile = blockIdx.x - b * a.n_dtiles;
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t dbase = (int64_t)dtile * kGnDT;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gl = lane / LG, nl = lane - gl * LG;
   const int KC = (int)((T + kGnCK - 1) / kGnCK);
+  const int sc0 = seg * a.seg_sc;
+  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
 
+  // state entering the segment: h0, or the carried state
+  const float* xin = a.nseg > 1 ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N : (a.h0 ? a.h0 + (int64_t)b * D * N : nullptr);
   float x[PPW][S];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
@@ -930,17 +1163,20 @@ __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) {
       const int n = nl + 64 * s2;
-      x[q][s2] = (a.h0 && n < N && d < D) ? a.h0[((int64_t)b * D + d) * N + n] : 0.f;
+      x[q][s2] = (xin && n < N && d < D) ? xin[d * N + n] : 0.f;
     }
   }
   constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
   float vu[kGnE], vf[kGnE], vi[kGnE], vb[EB], vc[EB];
-  gn_ld_tile(a, a.u, x_dt, b, 0, dbase, vu);
-  gn_ld_tile(a, a.fl, g_dt, b, 0, dbase, vf);
-  gn_ld_tile(a, a.il, g_dt, b, 0, dbase, vi);
-  gn_ld_bc<NP, EB>(a, a.Bm, b, 0, vb);
-  gn_ld_bc<NP, EB>(a, a.Cm, b, 0, vc);
-  for (int sc = 0; sc < KC; ++sc) {
+  {
+    const int64_t tl = (int64_t)sc0 * kGnCK;
+    gn_ld_tile(a, a.u, x_dt, b, tl, dbase, vu);
+    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
+    gn_ld_tile(a, a.il, g_dt, b, tl, dbase, vi);
+    gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
+    gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
+  }
+  for (int sc = sc0; sc < sc1; ++sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     __syncthreads();  // the previous sub-chunk's tiles are consumed
 #pragma unroll
@@ -955,7 +1191,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int
     }
     gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
     __syncthreads();
-    if (sc + 1 < KC) {  // prefetch the next sub-chunk while this one is scanned
+    if (sc + 1 < sc1) {  // prefetch the next sub-chunk while this one is scanned
       const int64_t t1 = t0 + kGnCK;
       gn_ld_tile(a, a.u, x_dt, b, t1, dbase, vu);
       gn_ld_tile(a, a.fl, g_dt, b, t1, dbase, vf);
@@ -1008,7 +1244,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int
       if (t < T && d < D) st_any(a.y, y_dt, ((int64_t)b * T + t) * D + d, s_y[r][c]);
     }
   }
-  if (a.hT) {
+  if (a.hT && seg == a.nseg - 1) {
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       const int pass = wv + q * kGnW;
@@ -1035,8 +1271,10 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   __shared__ float s_o0[kGnCK][kGnDT], s_o1[kGnCK][kGnDT], s_o2[kGnCK][kGnDT];
   __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP], s_pB[kGnCK][NP], s_pC[kGnCK][NP];
   const int N = a.N;
-  const int b = blockIdx.x / a.n_dtiles;
-  const int dtile = blockIdx.x - b * a.n_dtiles;
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t dbase = (int64_t)dtile * kGnDT;
   const int lane = threadIdx.x & 63;
@@ -1044,14 +1282,23 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   const int gl = lane / LG, nl = lane - gl * LG;
   const int KC = (int)((T + kGnCK - 1) / kGnCK);
   const int64_t btn = (int64_t)a.batch * T * N;
+  const int sc0 = seg * a.seg_sc;
+  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
 
-  float gc[PPW][S];  // adjoint carry f_{t+1} x̄_{t+1} per channel pass
+  // adjoint carry f_{t+1} x̄_{t+1} per channel pass: zero past the end of T,
+  // else the carry entering the segment from the future
+  const float* gin = a.nseg > 1 ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N : nullptr;
+  float gc[PPW][S];
   float dDs[PPW];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
     dDs[q] = 0.f;
+    const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
 #pragma unroll
-    for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = 0.f;
+    for (int s2 = 0; s2 < S; ++s2) {
+      const int n = nl + 64 * s2;
+      gc[q][s2] = (gin && n < N && d < D) ? gin[d * N + n] : 0.f;
+    }
   }
   constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
   // At NP = 128 the registers of a prefetched tile would spill: that case
@@ -1066,8 +1313,8 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
     gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
   };
-  if (kPrefetch) load_tiles((int64_t)(KC - 1) * kGnCK);
-  for (int sc = KC - 1; sc >= 0; --sc) {
+  if (kPrefetch) load_tiles((int64_t)(sc1 - 1) * kGnCK);
+  for (int sc = sc1 - 1; sc >= sc0; --sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
     if (!kPrefetch) load_tiles(t0);
@@ -1084,7 +1331,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     }
     gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
     __syncthreads();
-    if (kPrefetch && sc > 0) load_tiles(t0 - kGnCK);  // next (earlier) sub-chunk, while this one runs
+    if (kPrefetch && sc > sc0) load_tiles(t0 - kGnCK);  // next (earlier) sub-chunk, while this one runs
     float accB[kGnCK][S], accC[kGnCK][S];
 #pragma unroll
     for (int r = 0; r < kGnCK; ++r)
@@ -1208,14 +1455,14 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     if (pass >= NPASS) break;
     const int64_t d = dbase + (int64_t)pass * G + gl;
     if (d >= D) continue;
-    if (a.dh0) {
+    if (a.dh0 && seg == 0) {
 #pragma unroll
       for (int s2 = 0; s2 < S; ++s2) {
         const int n = nl + 64 * s2;
         if (n < N) a.dh0[((int64_t)b * D + d) * N + n] = gc[q][s2];
       }
     }
-    if (a.partD && nl == 0) a.partD[(int64_t)b * D + d] = dDs[q];
+    if (a.partD && nl == 0) a.partD[((int64_t)b * a.nseg + seg) * D + d] = dDs[q];
   }
 }
 
@@ -1295,8 +1542,13 @@ int n1_vec_width(bool bwd) { return bwd ? kBV : kFV; }
 
 struct Layout {
   int V, CH, L, K, n_dtiles, n_tiles;
-  size_t off_agg, off_incl, off_partB, off_partC, off_partD, total;
+  int nseg, seg_sc;  // N > 1: time segments
+  size_t off_agg, off_incl, off_partB, off_partC, off_partD, off_segF, off_segZ, off_seg0, total;
 };
+
+// N > 1: enough time segments that about kGnTargetWgs workgroups run per
+// launch (each segment keeps at least one sub-chunk).
+constexpr int kGnTargetWgs = 1024;
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1317,6 +1569,15 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.K = (int)((T + l.L - 1) / l.L);
   l.n_dtiles = (int)((D + l.CH - 1) / l.CH);
   l.n_tiles = (int)(batch * l.n_dtiles);
+  l.nseg = 1;
+  l.seg_sc = l.K;
+  if (N > 1 && l.n_tiles > 0 && l.K > 0) {
+    int64_t want = (kGnTargetWgs + l.n_tiles - 1) / l.n_tiles;
+    if (want > l.K) want = l.K;
+    if (want < 1) want = 1;
+    l.seg_sc = (int)((l.K + want - 1) / want);
+    l.nseg = (l.K + l.seg_sc - 1) / l.seg_sc;
+  }
   const size_t units = N == 1 ? (size_t)l.K * l.n_tiles : 0;
   l.off_agg = off;
   off = align_up(off + units * 2 * l.CH * sizeof(uint64_t));
@@ -1327,7 +1588,14 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.off_partC = off;
   off = align_up(off + (size_t)l.n_dtiles * batch * T * N * sizeof(float));
   l.off_partD = off;
-  off = align_up(off + (size_t)batch * (N == 1 ? l.K : 1) * D * sizeof(float));
+  off = align_up(off + (size_t)batch * (N == 1 ? l.K : l.nseg) * D * sizeof(float));
+  const size_t seg_units = l.nseg > 1 ? (size_t)batch * l.nseg * D : 0;
+  l.off_segF = off;
+  off = align_up(off + seg_units * sizeof(float));
+  l.off_segZ = off;
+  off = align_up(off + seg_units * N * sizeof(float));
+  l.off_seg0 = off;
+  off = align_up(off + seg_units * N * sizeof(float));
   l.total = off;
   return l;
 }
@@ -1414,6 +1682,33 @@ gn_bwd_t pick_gn_bwd(int np) {
     case 64: return gn_bwd_kernel<64>;
     default: return gn_bwd_kernel<128>;
   }
+}
+
+typedef void (*gn_map_t)(ScanArgs, int, int);
+
+gn_map_t pick_gn_map(int np, bool bwd) {
+  switch (np) {
+    case 2: return bwd ? gn_bwd_map_kernel<2> : gn_fwd_map_kernel<2>;
+    case 4: return bwd ? gn_bwd_map_kernel<4> : gn_fwd_map_kernel<4>;
+    case 8: return bwd ? gn_bwd_map_kernel<8> : gn_fwd_map_kernel<8>;
+    case 16: return bwd ? gn_bwd_map_kernel<16> : gn_fwd_map_kernel<16>;
+    case 32: return bwd ? gn_bwd_map_kernel<32> : gn_fwd_map_kernel<32>;
+    case 64: return bwd ? gn_bwd_map_kernel<64> : gn_fwd_map_kernel<64>;
+    default: return bwd ? gn_bwd_map_kernel<128> : gn_fwd_map_kernel<128>;
+  }
+}
+
+// N > 1 with time segments: the segment maps and the carry pass that give
+// every segment its entering state (dir +1) or adjoint carry (dir -1).
+int gn_segments(const ScanArgs& a, const Layout& l, int x_dt, int g_dt, bool bwd, hipStream_t st) {
+  if (l.nseg <= 1) return NAJU_OK;
+  const unsigned grid = (unsigned)((int64_t)l.n_tiles * (l.nseg - 1));
+  hipLaunchKernelGGL(pick_gn_map(np_of(a.N), bwd), dim3(grid), dim3(64 * kGnW), 0, st, a, x_dt, g_dt);
+  const int64_t n = (int64_t)a.batch * a.D * a.N;
+  hipLaunchKernelGGL(gn_seg_carry_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, bwd ? -1 : 1);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
 }
 
 int launch(kern_t k, unsigned grid, unsigned block, hipStream_t st, const ScanArgs& a) {
@@ -1504,8 +1799,16 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   a.K = l.K;
   if (N > 1) {
     const int y_dt = out_f32 ? (int)NAJU_DTYPE_F32 : x_dtype;
-    hipLaunchKernelGGL(pick_gn_fwd(np_of(N)), dim3((unsigned)l.n_tiles), dim3(64 * kGnW), 0, st, a, x_dtype,
-                       gate_dtype, y_dt);
+    a.nseg = l.nseg;
+    a.seg_sc = l.seg_sc;
+    a.segF = (float*)(ws + l.off_segF);
+    a.segZ = (float*)(ws + l.off_segZ);
+    a.seg0 = (float*)(ws + l.off_seg0);
+    if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+    rc = gn_segments(a, l, x_dtype, gate_dtype, false, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(pick_gn_fwd(np_of(N)), dim3((unsigned)((int64_t)l.n_tiles * l.nseg)), dim3(64 * kGnW), 0, st,
+                       a, x_dtype, gate_dtype, y_dt);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
     return NAJU_OK;
@@ -1586,8 +1889,16 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   if (N > 1) {
     const int du_dt = out_f32 ? (int)NAJU_DTYPE_F32 : x_dtype;
     const int dg_dt = out_f32 ? (int)NAJU_DTYPE_F32 : gate_dtype;
-    hipLaunchKernelGGL(pick_gn_bwd(np_of(N)), dim3((unsigned)l.n_tiles), dim3(64 * kGnW), 0, st, a, x_dtype,
-                       gate_dtype, du_dt, dg_dt);
+    a.nseg = l.nseg;
+    a.seg_sc = l.seg_sc;
+    a.segF = (float*)(ws + l.off_segF);
+    a.segZ = (float*)(ws + l.off_segZ);
+    a.seg0 = (float*)(ws + l.off_seg0);
+    if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+    rc = gn_segments(a, l, x_dtype, gate_dtype, true, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(pick_gn_bwd(np_of(N)), dim3((unsigned)((int64_t)l.n_tiles * l.nseg)), dim3(64 * kGnW), 0, st,
+                       a, x_dtype, gate_dtype, du_dt, dg_dt);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   } else {
@@ -1606,7 +1917,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     const int n_d = dD ? (int)((D + 63) / 64) : 0;
     hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
                        btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD,
-                       batch * (int64_t)(N == 1 ? l.K : 1), D, dD);
+                       batch * (int64_t)(N == 1 ? l.K : l.nseg), D, dD);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;
