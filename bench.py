@@ -27,6 +27,7 @@ if _ROOT not in sys.path:
     sys.path.insert(0, _ROOT)
 
 HBM_PEAK_GBS = 8000.0
+VALU_PEAK_TFLOPS = 157.3 / 2  # fp32 FMA without packed-FP32 instructions
 METRIC = "fwd+bwd scan GB/s (% of HBM peak) at B8 L4096 D1024; LM tokens/s"
 
 
@@ -166,6 +167,18 @@ def main():
             "traffic": _traffic(args.config, N),
         },
     }
+    if N > 1:
+        # General N is compute-bound: the recurrence, readout and adjoint are
+        # about 19N flop per element (5N forward, 14N backward), fp32 FMA on
+        # the VALU. Packed-FP32 ops are disabled in this build, so the peak is
+        # half of MI355X's 157.3 TFLOP/s vector fp32.
+        E = Bsz * T * D
+        fl_bwd = 14.0 * N * E
+        ach = fl_bwd / (avg_bwd * 1e-3) / 1e12
+        out["roofline_compute"] = {"kernel": "naju_scan_bwd call", "bound": "valu", "achieved": round(ach, 2),
+                                   "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": round(ach / VALU_PEAK_TFLOPS, 4),
+                                   "fwd_achieved": round(5.0 * N * E / (avg_fwd * 1e-3) / 1e12, 2)}
     if args.flush:
         scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         tf = []
