@@ -870,12 +870,12 @@ __device__ __forceinline__ void gn_ld_tile(const ScanArgs& a, const void* p, int
 
 // The same for a [kGnCK][NP] tile of B or C ([batch,T,N]); entries past T or
 // N are replaced by the caller.
-template <int NP, int EB>
+template <int NP, int EB, int NT = kGnThreads>
 __device__ __forceinline__ void gn_ld_bc(const ScanArgs& a, const void* p, int b, int64_t t0, float (&v)[EB]) {
   int64_t idx[EB];
 #pragma unroll
   for (int e = 0; e < EB; ++e) {
-    const int k = e * kGnThreads + (int)threadIdx.x;
+    const int k = e * NT + (int)threadIdx.x;
     const int64_t t = t0 + k / NP;
     const int n = k % NP;
     idx[e] = ((int64_t)b * a.T + (t < a.T ? t : a.T - 1)) * a.N + (n < a.N ? n : a.N - 1);
@@ -1102,6 +1102,177 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a,
       if (n < N) a.segZ[o * N + n] = gc[q][s2];
     }
     if (nl == 0) a.segF[o] = Ac[q];
+  }
+}
+
+// ----------------------------------------------- general N forward, lanes over d
+//
+// The forward of N > 1 runs with one channel per lane and its NP states in
+// VGPRs (NP = N rounded up to a power of two; states n >= N see B = C = 0 and
+// stay 0). A wave owns 64 consecutive channels of one batch row, a workgroup
+// kGcW waves, for one time segment. B_t and C_t rows of a kGnCK-row sub-chunk
+// are staged in LDS (converted to f32) and read back as broadcasts, so a row
+// costs 2 FMA + 1 multiply per state and no cross-lane sums. Per-lane inputs
+// are loaded in groups of kGcRG rows, the next group while the current one
+// is scanned. MAP: the segment's map from a zero state (decay F and state Z
+// per channel) for the carry pass; otherwise the scan itself from the
+// segment's entering state, with y, the checkpoint and hT.
+constexpr int kGcW = 4;            // waves per workgroup
+constexpr int kGcCH = 64 * kGcW;   // channels per workgroup
+constexpr int kGcRG = 8;           // rows per input group
+
+// The lane's channel's values of rows t0 .. t0+kGcRG-1 (clamped in bounds).
+__device__ __forceinline__ void gc_ld_rows(const void* p, int dt, int64_t rowbase, int64_t t0, int64_t T, int64_t D,
+                                           int64_t d, float (&v)[kGcRG]) {
+  int64_t idx[kGcRG];
+#pragma unroll
+  for (int r = 0; r < kGcRG; ++r) idx[r] = (rowbase + (t0 + r < T ? t0 + r : T - 1)) * D + d;
+  if (dt == NAJU_DTYPE_F32) {
+#pragma unroll
+    for (int r = 0; r < kGcRG; ++r) v[r] = ((const float*)p)[idx[r]];
+  } else if (dt == NAJU_DTYPE_BF16) {
+#pragma unroll
+    for (int r = 0; r < kGcRG; ++r) v[r] = (float)((const bf16_t*)p)[idx[r]];
+  } else {
+#pragma unroll
+    for (int r = 0; r < kGcRG; ++r) v[r] = (float)((const f16_t*)p)[idx[r]];
+  }
+}
+
+template <int NP, bool MAP>
+__global__ __launch_bounds__(64 * kGcW) void gc_fwd_kernel(const ScanArgs a, int x_dt, int g_dt, int y_dt) {
+  constexpr int EB = (kGnCK * NP + 64 * kGcW - 1) / (64 * kGcW);
+  __shared__ float s_B[kGnCK][NP];
+  __shared__ float s_C[MAP ? 1 : kGnCK][NP];
+  const int N = a.N;
+  const int64_t T = a.T, D = a.D;
+  const int ndt = (int)((D + kGcCH - 1) / kGcCH);
+  const int ntl = a.batch * ndt;
+  const int tile = (int)(blockIdx.x % (uint32_t)ntl);
+  const int seg = (int)(blockIdx.x / (uint32_t)ntl);
+  const int b = tile / ndt;
+  const int dtile = tile - b * ndt;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t d = (int64_t)dtile * kGcCH + wv * 64 + lane;
+  const bool dok = d < D;
+  const int64_t dc = dok ? d : D - 1;  // clamped channel for loads
+  const int KC = (int)((T + kGnCK - 1) / kGnCK);
+  const int sc0 = seg * a.seg_sc;
+  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
+  const int64_t rowbase = (int64_t)b * T;
+  const int64_t t_beg = (int64_t)sc0 * kGnCK;
+  const int64_t t_end = (int64_t)sc1 * kGnCK < T ? (int64_t)sc1 * kGnCK : T;
+
+  float x[NP];
+  {
+    const float* xin = MAP ? nullptr
+                           : (a.nseg > 1 ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N
+                                         : (a.h0 ? a.h0 + (int64_t)b * D * N : nullptr));
+#pragma unroll
+    for (int n = 0; n < NP; ++n) x[n] = (xin && dok && n < N) ? xin[dc * N + n] : 0.f;
+  }
+  float Fd = 1.f;
+  const float Dv = MAP ? 0.f : a.Dsk[dc];
+
+  float gu[kGcRG], gf[kGcRG], gi[kGcRG];  // the next input group
+  gc_ld_rows(a.u, x_dt, rowbase, t_beg, T, D, dc, gu);
+  gc_ld_rows(a.fl, g_dt, rowbase, t_beg, T, D, dc, gf);
+  gc_ld_rows(a.il, g_dt, rowbase, t_beg, T, D, dc, gi);
+  for (int sc = sc0; sc < sc1; ++sc) {
+    const int64_t t0 = (int64_t)sc * kGnCK;
+    __syncthreads();  // the previous sub-chunk's B/C rows are consumed
+    {
+      // stage B (and C) rows of the sub-chunk, f32, zero outside [0,T) x [0,N)
+      float vb[EB], vc[EB];
+      gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Bm, b, t0, vb);
+      if (!MAP) gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Cm, b, t0, vc);
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int k = e * 64 * kGcW + (int)threadIdx.x;
+        if (k < kGnCK * NP) {
+          const int r = k / NP, n = k % NP;
+          const bool ok = t0 + r < T && n < N;
+          s_B[r][n] = ok ? vb[e] : 0.f;
+          if (!MAP) s_C[MAP ? 0 : r][n] = ok ? vc[e] : 0.f;
+        }
+      }
+    }
+    __syncthreads();
+    if (!MAP && a.ckpt && dok) {
+      float* ck = a.ckpt + (((int64_t)b * KC + sc) * D + d) * N;
+#pragma unroll
+      for (int n = 0; n < NP; ++n)
+        if (n < N) ck[n] = x[n];
+    }
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+#pragma unroll 1
+    for (int r0 = 0; r0 < rows; r0 += kGcRG) {
+      float cu[kGcRG], cf[kGcRG], ci[kGcRG];
+#pragma unroll
+      for (int r = 0; r < kGcRG; ++r) {
+        cu[r] = gu[r];
+        cf[r] = gf[r];
+        ci[r] = gi[r];
+      }
+      const int64_t tn = t0 + r0 + kGcRG;
+      if (tn < t_end) {
+        gc_ld_rows(a.u, x_dt, rowbase, tn, T, D, dc, gu);
+        gc_ld_rows(a.fl, g_dt, rowbase, tn, T, D, dc, gf);
+        gc_ld_rows(a.il, g_dt, rowbase, tn, T, D, dc, gi);
+      }
+      float yv[kGcRG];
+#pragma unroll
+      for (int r = 0; r < kGcRG; ++r) {
+        yv[r] = 0.f;
+        if (r0 + r < rows) {
+          const float f = sigm(cf[r]);
+          const float w = sigm(ci[r]) * cu[r];
+          const int rr = r0 + r;
+          if (MAP) {
+            Fd *= f;
+#pragma unroll
+            for (int n = 0; n < NP; ++n) x[n] = fmaf(f, x[n], w * s_B[rr][n]);
+          } else {
+            float y4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int n = 0; n < NP; ++n) {
+              x[n] = fmaf(f, x[n], w * s_B[rr][n]);
+              y4[n & 3] = fmaf(s_C[MAP ? 0 : rr][n], x[n], y4[n & 3]);
+            }
+            yv[r] = fmaf(Dv, cu[r], (y4[0] + y4[1]) + (y4[2] + y4[3]));
+          }
+        }
+      }
+      if (!MAP && dok) {
+        const int64_t o = (rowbase + t0 + r0) * D + d;
+        if (y_dt == NAJU_DTYPE_F32) {
+#pragma unroll
+          for (int r = 0; r < kGcRG; ++r)
+            if (r0 + r < rows) ((float*)a.y)[o + (int64_t)r * D] = yv[r];
+        } else if (y_dt == NAJU_DTYPE_BF16) {
+#pragma unroll
+          for (int r = 0; r < kGcRG; ++r)
+            if (r0 + r < rows) ((bf16_t*)a.y)[o + (int64_t)r * D] = (bf16_t)yv[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < kGcRG; ++r)
+            if (r0 + r < rows) ((f16_t*)a.y)[o + (int64_t)r * D] = (f16_t)yv[r];
+        }
+      }
+    }
+  }
+  if (!dok) return;
+  if (MAP) {
+    const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
+#pragma unroll
+    for (int n = 0; n < NP; ++n)
+      if (n < N) a.segZ[o * N + n] = x[n];
+    a.segF[o] = Fd;
+  } else if (a.hT && seg == a.nseg - 1) {
+#pragma unroll
+    for (int n = 0; n < NP; ++n)
+      if (n < N) a.hT[((int64_t)b * D + d) * N + n] = x[n];
   }
 }
 
@@ -1549,6 +1720,7 @@ struct Layout {
 // N > 1: enough time segments that about kGnTargetWgs workgroups run per
 // launch (each segment keeps at least one sub-chunk).
 constexpr int kGnTargetWgs = 1024;
+constexpr int kGcTargetWaves = 2048;
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1572,7 +1744,11 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.nseg = 1;
   l.seg_sc = l.K;
   if (N > 1 && l.n_tiles > 0 && l.K > 0) {
-    int64_t want = (kGnTargetWgs + l.n_tiles - 1) / l.n_tiles;
+    // forward (lanes over channels): about kGcTargetWaves waves; backward
+    // (8-wave workgroups over 64 channels): about kGnTargetWgs workgroups
+    const int64_t per_seg = bwd ? l.n_tiles : batch * ((D + 63) / 64);
+    const int64_t target = bwd ? kGnTargetWgs : kGcTargetWaves;
+    int64_t want = (target + per_seg - 1) / per_seg;
     if (want > l.K) want = l.K;
     if (want < 1) want = 1;
     l.seg_sc = (int)((l.K + want - 1) / want);
@@ -1684,6 +1860,21 @@ gn_bwd_t pick_gn_bwd(int np) {
   }
 }
 
+// Workgroups per time segment of the general-N forward.
+int64_t gc_tiles(int64_t batch, int64_t D) { return batch * ((D + kGcCH - 1) / kGcCH); }
+
+gn_fwd_t pick_gc_fwd(int np, bool map) {
+  switch (np) {
+    case 2: return map ? gc_fwd_kernel<2, true> : gc_fwd_kernel<2, false>;
+    case 4: return map ? gc_fwd_kernel<4, true> : gc_fwd_kernel<4, false>;
+    case 8: return map ? gc_fwd_kernel<8, true> : gc_fwd_kernel<8, false>;
+    case 16: return map ? gc_fwd_kernel<16, true> : gc_fwd_kernel<16, false>;
+    case 32: return map ? gc_fwd_kernel<32, true> : gc_fwd_kernel<32, false>;
+    case 64: return map ? gc_fwd_kernel<64, true> : gc_fwd_kernel<64, false>;
+    default: return map ? gc_fwd_kernel<128, true> : gc_fwd_kernel<128, false>;
+  }
+}
+
 typedef void (*gn_map_t)(ScanArgs, int, int);
 
 gn_map_t pick_gn_map(int np, bool bwd) {
@@ -1702,8 +1893,13 @@ gn_map_t pick_gn_map(int np, bool bwd) {
 // every segment its entering state (dir +1) or adjoint carry (dir -1).
 int gn_segments(const ScanArgs& a, const Layout& l, int x_dt, int g_dt, bool bwd, hipStream_t st) {
   if (l.nseg <= 1) return NAJU_OK;
-  const unsigned grid = (unsigned)((int64_t)l.n_tiles * (l.nseg - 1));
-  hipLaunchKernelGGL(pick_gn_map(np_of(a.N), bwd), dim3(grid), dim3(64 * kGnW), 0, st, a, x_dt, g_dt);
+  if (bwd) {
+    const unsigned grid = (unsigned)((int64_t)l.n_tiles * (l.nseg - 1));
+    hipLaunchKernelGGL(pick_gn_map(np_of(a.N), true), dim3(grid), dim3(64 * kGnW), 0, st, a, x_dt, g_dt);
+  } else {
+    const unsigned grid = (unsigned)(gc_tiles(a.batch, a.D) * (l.nseg - 1));
+    hipLaunchKernelGGL(pick_gc_fwd(np_of(a.N), true), dim3(grid), dim3(64 * kGcW), 0, st, a, x_dt, g_dt, 0);
+  }
   const int64_t n = (int64_t)a.batch * a.D * a.N;
   hipLaunchKernelGGL(gn_seg_carry_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, bwd ? -1 : 1);
   const hipError_t e = hipGetLastError();
@@ -1804,11 +2000,11 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
     a.segF = (float*)(ws + l.off_segF);
     a.segZ = (float*)(ws + l.off_segZ);
     a.seg0 = (float*)(ws + l.off_seg0);
-    if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+    if (gc_tiles(batch, D) * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
     rc = gn_segments(a, l, x_dtype, gate_dtype, false, st);
     if (rc) return rc;
-    hipLaunchKernelGGL(pick_gn_fwd(np_of(N)), dim3((unsigned)((int64_t)l.n_tiles * l.nseg)), dim3(64 * kGnW), 0, st,
-                       a, x_dtype, gate_dtype, y_dt);
+    hipLaunchKernelGGL(pick_gc_fwd(np_of(N), false), dim3((unsigned)(gc_tiles(batch, D) * l.nseg)), dim3(64 * kGcW),
+                       0, st, a, x_dtype, gate_dtype, y_dt);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
     return NAJU_OK;
