@@ -839,6 +839,30 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Sums over aligned groups of LG lanes of the M entries of v, by a
+// transposing butterfly: at each step a lane keeps half of its entries and
+// trades the other half with its partner, so the M sums cost M-1 lane
+// exchanges instead of M*log2(LG). Afterwards lane l of a group holds the
+// sums of entries [l*M/LG, (l+1)*M/LG) in v[0 .. M/LG). Fixed order, so the
+// sums are run-to-run identical.
+template <int LG, int K, int M>
+__device__ __forceinline__ void tr_reduce_step(float (&v)[M], int lane) {
+  if constexpr (LG > 1) {
+    constexpr int m = LG / 2;
+    const bool hi = (lane & m) != 0;
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j) {
+      const float lo_v = v[j], hi_v = v[j + K / 2];
+      v[j] = (hi ? hi_v : lo_v) + __shfl_xor(hi ? lo_v : hi_v, m, 64);
+    }
+    tr_reduce_step<m, K / 2, M>(v, lane);
+  }
+}
+template <int LG, int M>
+__device__ __forceinline__ void tr_reduce(float (&v)[M], int lane) {
+  tr_reduce_step<LG, M, M>(v, lane);
+}
+
 constexpr int kGnThreads = 64 * kGnW;
 constexpr int kGnE = kGnCK * kGnDT / kGnThreads;  // tile elements per thread
 
@@ -1438,8 +1462,10 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   constexpr int G = 64 / LG;
   constexpr int NPASS = kGnDT / G;
   constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
-  __shared__ float s_f[kGnCK][kGnDT], s_i[kGnCK][kGnDT], s_u[kGnCK][kGnDT], s_dy[kGnCK][kGnDT];
-  __shared__ float s_o0[kGnCK][kGnDT], s_o1[kGnCK][kGnDT], s_o2[kGnCK][kGnDT];
+  // rows padded to kGnDT + 1 words: the output lanes read and write one row
+  // each, at the same channel, without bank conflicts
+  __shared__ float s_f[kGnCK][kGnDT + 1], s_i[kGnCK][kGnDT + 1], s_u[kGnCK][kGnDT + 1], s_dy[kGnCK][kGnDT + 1];
+  __shared__ float s_o0[kGnCK][kGnDT + 1], s_o1[kGnCK][kGnDT + 1], s_o2[kGnCK][kGnDT + 1];
   __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP], s_pB[kGnCK][NP], s_pC[kGnCK][NP];
   const int N = a.N;
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
@@ -1536,12 +1562,12 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
           for (int s2 = 0; s2 < S; ++s2) hist[r][s2] = xs[s2];
         }
       }
-      // adjoint recurrence row by row (reverse); the sums over n of all rows
-      // are formed afterwards so that their shuffle chains interleave
-      float pf[kGnCK], pw[kGnCK];
+      // adjoint recurrence row by row (reverse), with this lane's terms of
+      // v[r] = sum_n x̄_t x_{t-1} (dfl) and v[kGnCK + r] = sum_n x̄_t B_t (dws)
+      float v[2 * kGnCK];
 #pragma unroll
       for (int r = kGnCK - 1; r >= 0; --r) {
-        pf[r] = pw[r] = 0.f;
+        v[r] = v[kGnCK + r] = 0.f;
         if (r < rows) {
           const float f = s_f[r][c], iu = s_i[r][c] * s_u[r][c], gy = s_dy[r][c];
 #pragma unroll
@@ -1549,27 +1575,31 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
             const int n = nl + 64 * s2;
             const float xprev = r > 0 ? hist[r - 1][s2] : x0[s2];
             const float xb = fmaf(gy, s_C[r][n], gc[q][s2]);
-            pf[r] = fmaf(xb, xprev, pf[r]);
-            pw[r] = fmaf(xb, s_B[r][n], pw[r]);
+            v[r] = fmaf(xb, xprev, v[r]);
+            v[kGnCK + r] = fmaf(xb, s_B[r][n], v[kGnCK + r]);
             accB[r][s2] = fmaf(xb, iu, accB[r][s2]);
             accC[r][s2] = fmaf(gy, hist[r][s2], accC[r][s2]);
             gc[q][s2] = f * xb;
           }
         }
       }
+      // sums over the channel group's lanes; lane l < LG/2 of the group then
+      // owns rows [l*K2, l*K2 + K2): its dfl sums are in v, the dws sums come
+      // from lane l + LG/2
+      constexpr int K2 = 2 * kGnCK / LG;
+      tr_reduce<LG, 2 * kGnCK>(v, lane);
+      float vw[K2];
 #pragma unroll
-      for (int r = 0; r < kGnCK; ++r) {
-        pf[r] = group_sum<LG>(pf[r]);
-        pw[r] = group_sum<LG>(pw[r]);
-      }
-      if (nl == 0) {
+      for (int j = 0; j < K2; ++j) vw[j] = __shfl_xor(v[j], LG / 2, 64);
+      if (nl < LG / 2) {
 #pragma unroll
-        for (int r = 0; r < kGnCK; ++r) {
+        for (int j = 0; j < K2; ++j) {
+          const int r = nl * K2 + j;
           if (r < rows) {
             const float f = s_f[r][c], ig = s_i[r][c], uu = s_u[r][c], gy = s_dy[r][c];
-            s_o0[r][c] = fmaf(ig, pw[r], Dv * gy);            // du
-            s_o1[r][c] = fmaf(-f, f, f) * pf[r];              // dfl
-            s_o2[r][c] = fmaf(-ig, ig, ig) * (pw[r] * uu);    // dil
+            s_o0[r][c] = fmaf(ig, vw[j], Dv * gy);            // du
+            s_o1[r][c] = fmaf(-f, f, f) * v[j];               // dfl
+            s_o2[r][c] = fmaf(-ig, ig, ig) * (vw[j] * uu);    // dil
             dDs[q] = fmaf(gy, uu, dDs[q]);
           }
         }
@@ -1633,7 +1663,8 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
         if (n < N) a.dh0[((int64_t)b * D + d) * N + n] = gc[q][s2];
       }
     }
-    if (a.partD && nl == 0) a.partD[((int64_t)b * a.nseg + seg) * D + d] = dDs[q];
+    const float dd = group_sum<LG>(dDs[q]);
+    if (a.partD && nl == 0) a.partD[((int64_t)b * a.nseg + seg) * D + d] = dd;
   }
 }
 
