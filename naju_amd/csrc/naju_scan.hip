@@ -132,6 +132,32 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Wave-wide sums of the M entries of v (M a power of two, M <= 64): a
+// transposing butterfly (each lane keeps half of its entries and trades the
+// other half with its partner, masks 32, 16, ...) until one entry is left,
+// then a plain butterfly over the remaining lane bits. Afterwards lane l
+// holds the sum of entry l / (64 / M) in v[0]. Fixed order.
+template <int MASK, int K, int M>
+__device__ __forceinline__ void wave_sums_step(float (&v)[M], int lane) {
+  if constexpr (K > 1) {
+    const bool hi = (lane & MASK) != 0;
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j) {
+      const float lo_v = v[j], hi_v = v[j + K / 2];
+      v[j] = (hi ? hi_v : lo_v) + __shfl_xor(hi ? lo_v : hi_v, MASK, 64);
+    }
+    wave_sums_step<MASK / 2, K / 2, M>(v, lane);
+  } else {
+#pragma unroll
+    for (int m = MASK; m >= 1; m >>= 1) v[0] += __shfl_xor(v[0], m, 64);
+  }
+}
+template <int M>
+__device__ __forceinline__ void wave_sums(float (&v)[M], int lane) {
+  static_assert(M >= 1 && M <= 64 && (M & (M - 1)) == 0, "M must be a power of two <= 64");
+  wave_sums_step<32, M, M>(v, lane);
+}
+
 // Tagged words of the look-back: {value bits, tag} in one 64-bit atomic.
 __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -659,56 +685,58 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
 #pragma unroll
     for (int j = 0; j < V; ++j) g[j] = fmaf(s_F[w][j * 64 + lane], g[j], s_Zb[w][j * 64 + lane]);
 
-  // forward states x_{t-1} of every row (x_{t0-1} = s)
-  float xp[R][V];
+  // forward states x_t of every row (x_{t0-1} = s0)
+  float xs[R][V], s0[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) s0[j] = s[j];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      xp[r][j] = s[j];
       s[j] = fmaf(xf[r][j], s[j], xi[r][j] * Bt[r] * xu[r][j]);
+      xs[r][j] = s[j];
     }
 
   // reverse sweep: gradients (naju/cuda/naju_cuda.cu:116-140 restated);
   // f(1-f) and i(1-i) as fma(-f, f, f), exactly 0 at f in {0, 1}.
-  float pB[R], pC[R], dDs[V];
+  // pq[r] / pq[R + r]: this lane's terms of the dB / dC sums of row r
+  float pq[2 * R], dDs[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) dDs[j] = 0.f;
 #pragma unroll
   for (int r = R - 1; r >= 0; --r) {
-    pB[r] = 0.f;
-    pC[r] = 0.f;
+    pq[r] = 0.f;
+    pq[R + r] = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const float f = xf[r][j], ig = xi[r][j], x = xu[r][j], gy = xg[r][j];
+      const float xprev = r > 0 ? xs[r - 1][j] : s0[j];
       const float xb = fmaf(gy, Ct[r], g[j]);
       const float iu = ig * x;
-      const float xt = fmaf(f, xp[r][j], iu * Bt[r]);
       const float dws = xb * Bt[r];
-      pB[r] = fmaf(xb, iu, pB[r]);
-      pC[r] = fmaf(gy, xt, pC[r]);
+      pq[r] = fmaf(xb, iu, pq[r]);
+      pq[R + r] = fmaf(gy, xs[r][j], pq[R + r]);
       dDs[j] = fmaf(gy, x, dDs[j]);
       g[j] = f * xb;
-      xf[r][j] = fmaf(-f, f, f) * (xb * xp[r][j]);  // dfl
-      xi[r][j] = fmaf(-ig, ig, ig) * (dws * x);     // dil
-      xu[r][j] = fmaf(ig, dws, Dv[j] * gy);         // du
+      xf[r][j] = fmaf(-f, f, f) * (xb * xprev);  // dfl
+      xi[r][j] = fmaf(-ig, ig, ig) * (dws * x);  // dil
+      xu[r][j] = fmaf(ig, dws, Dv[j] * gy);      // du
     }
   }
   if (a.du) st_rows<TDU, V, R, M, !FULL>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
   if (a.dfl) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
   if (a.dil) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
   if (a.partB || a.partC) {
-    // partial sums over this tile's channels, stored [dtile][b*T + t]
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float sb = wave_sum(pB[r]);
-      const float sc = wave_sum(pC[r]);
-      const int64_t t = t0 + r;
-      if (lane == 0 && (FULL || t < T)) {
-        const int64_t o = (int64_t)dtile * a.batch * T + (int64_t)b * T + t;
-        if (a.partB) a.partB[o] = sb;
-        if (a.partC) a.partC[o] = sc;
-      }
+    // partial sums over this tile's channels, stored [dtile][b*T + t]: after
+    // the wave-wide sums, lane l holds entry l / (64 / 2R) of pq
+    wave_sums<2 * R>(pq, lane);
+    constexpr int Q = 64 / (2 * R);
+    const int i = lane / Q;
+    const int r = i < R ? i : i - R;
+    const int64_t t = t0 + r;
+    if (lane % Q == 0 && (FULL || t < T)) {
+      float* dst = i < R ? a.partB : a.partC;
+      if (dst) dst[(int64_t)dtile * a.batch * T + (int64_t)b * T + t] = pq[0];
     }
   }
   if (a.partD) {
@@ -1203,14 +1231,14 @@ __global__ __launch_bounds__(64 * kGcW) void gc_fwd_kernel(const ScanArgs a, int
   gc_ld_rows(a.u, x_dt, rowbase, t_beg, T, D, dc, gu);
   gc_ld_rows(a.fl, g_dt, rowbase, t_beg, T, D, dc, gf);
   gc_ld_rows(a.il, g_dt, rowbase, t_beg, T, D, dc, gi);
+  float vb[EB], vc[EB];  // B (and C) rows of the next sub-chunk
+  gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Bm, b, t_beg, vb);
+  if (!MAP) gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Cm, b, t_beg, vc);
   for (int sc = sc0; sc < sc1; ++sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     __syncthreads();  // the previous sub-chunk's B/C rows are consumed
     {
       // stage B (and C) rows of the sub-chunk, f32, zero outside [0,T) x [0,N)
-      float vb[EB], vc[EB];
-      gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Bm, b, t0, vb);
-      if (!MAP) gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Cm, b, t0, vc);
 #pragma unroll
       for (int e = 0; e < EB; ++e) {
         const int k = e * 64 * kGcW + (int)threadIdx.x;
@@ -1223,6 +1251,10 @@ __global__ __launch_bounds__(64 * kGcW) void gc_fwd_kernel(const ScanArgs a, int
       }
     }
     __syncthreads();
+    if (sc + 1 < sc1) {
+      gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Bm, b, t0 + kGnCK, vb);
+      if (!MAP) gn_ld_bc<NP, EB, 64 * kGcW>(a, a.Cm, b, t0 + kGnCK, vc);
+    }
     if (!MAP && a.ckpt && dok) {
       float* ck = a.ckpt + (((int64_t)b * KC + sc) * D + d) * N;
 #pragma unroll
@@ -1511,6 +1543,21 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
   };
   if (kPrefetch) load_tiles((int64_t)(sc1 - 1) * kGnCK);
+  // checkpointed states entering a sub-chunk, for every channel pass of this
+  // wave, loaded one sub-chunk ahead
+  float ckn[PPW][S];
+  auto load_ckpt = [&](int sck) {
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+        const int n = nl + 64 * s2;
+        ckn[q][s2] = (n < N && d < D && wv + q * kGnW < NPASS) ? a.ckpt[(((int64_t)b * KC + sck) * D + d) * N + n] : 0.f;
+      }
+    }
+  };
+  load_ckpt(sc1 - 1);
   for (int sc = sc1 - 1; sc >= sc0; --sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
@@ -1529,6 +1576,12 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
     __syncthreads();
     if (kPrefetch && sc > sc0) load_tiles(t0 - kGnCK);  // next (earlier) sub-chunk, while this one runs
+    float ckc[PPW][S];
+#pragma unroll
+    for (int q = 0; q < PPW; ++q)
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) ckc[q][s2] = ckn[q][s2];
+    if (sc > sc0) load_ckpt(sc - 1);
     float accB[kGnCK][S], accC[kGnCK][S];
 #pragma unroll
     for (int r = 0; r < kGnCK; ++r)
@@ -1543,10 +1596,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
       const float Dv = d < D ? a.Dsk[d] : 0.f;
       float x0[S], hist[kGnCK][S];
 #pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) {
-        const int n = nl + 64 * s2;
-        x0[s2] = (n < N && d < D) ? a.ckpt[(((int64_t)b * KC + sc) * D + d) * N + n] : 0.f;
-      }
+      for (int s2 = 0; s2 < S; ++s2) x0[s2] = ckc[q][s2];
       {
         float xs[S];
 #pragma unroll
