@@ -976,98 +976,12 @@ __device__ __forceinline__ void gn_st_one(const ScanArgs& a, int64_t t0, const f
 
 // Time segments. With nseg > 1 the sub-chunks of T are split into nseg
 // segments of seg_sc sub-chunks, each scanned by its own workgroup per
-// channel tile (grid = n_tiles * segments, tile = blockIdx % n_tiles). The
-// state entering a segment comes from three steps: every segment's map from
-// a zero state (gn_fwd_map_kernel: decay F and state Z per channel), a carry
+// channel tile (grid = tiles * segments, tile = blockIdx % tiles). The state
+// entering a segment comes from three steps: every segment's map from a zero
+// state (gc_fwd_kernel<NP, true>: decay F and state Z per channel), a carry
 // pass over the segments (gn_seg_carry_kernel), then the full scan from the
-// carried state. The backward mirrors this with the adjoint carry.
-
-// Forward map of segment blockIdx / n_tiles (segments 0 .. nseg-2).
-template <int NP>
-__global__ __launch_bounds__(64 * kGnW) void gn_fwd_map_kernel(const ScanArgs a, int x_dt, int g_dt) {
-  constexpr int LG = NP < 64 ? NP : 64;
-  constexpr int S = NP / LG;
-  constexpr int G = 64 / LG;
-  constexpr int NPASS = kGnDT / G;
-  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
-  __shared__ float s_f[kGnCK][kGnDT], s_iu[kGnCK][kGnDT];
-  __shared__ float s_B[kGnCK][NP];
-  const int N = a.N;
-  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
-  const int b = tile / a.n_dtiles;
-  const int dtile = tile - b * a.n_dtiles;
-  const int64_t T = a.T, D = a.D;
-  const int64_t dbase = (int64_t)dtile * kGnDT;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gl = lane / LG, nl = lane - gl * LG;
-  const int KC = (int)((T + kGnCK - 1) / kGnCK);
-  const int sc0 = seg * a.seg_sc;
-  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
-
-  float x[PPW][S], Fc[PPW];
-#pragma unroll
-  for (int q = 0; q < PPW; ++q) {
-    Fc[q] = 1.f;
-#pragma unroll
-    for (int s2 = 0; s2 < S; ++s2) x[q][s2] = 0.f;
-  }
-  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
-  float vu[kGnE], vf[kGnE], vi[kGnE], vb[EB];
-  auto load_tiles = [&](int64_t tl) {
-    gn_ld_tile(a, a.u, x_dt, b, tl, dbase, vu);
-    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
-    gn_ld_tile(a, a.il, g_dt, b, tl, dbase, vi);
-    gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
-  };
-  load_tiles((int64_t)sc0 * kGnCK);
-  for (int sc = sc0; sc < sc1; ++sc) {
-    const int64_t t0 = (int64_t)sc * kGnCK;
-    __syncthreads();  // the previous sub-chunk's tiles are consumed
-#pragma unroll
-    for (int e = 0; e < kGnE; ++e) {
-      const int k = e * kGnThreads + (int)threadIdx.x;
-      const int r = k / kGnDT, c = k % kGnDT;
-      const bool ok = t0 + r < T && dbase + c < D;
-      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
-      s_iu[r][c] = ok ? sigm(vi[e]) * vu[e] : 0.f;
-    }
-    gn_st_one<NP, EB>(a, t0, vb, s_B);
-    __syncthreads();
-    if (sc + 1 < sc1) load_tiles(t0 + kGnCK);
-    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
-#pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      const int pass = wv + q * kGnW;
-      if (pass >= NPASS) break;
-      const int c = pass * G + gl;
-#pragma unroll
-      for (int r = 0; r < kGnCK; ++r) {
-        if (r < rows) {
-          const float f = s_f[r][c], iu = s_iu[r][c];
-          Fc[q] *= f;
-#pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) x[q][s2] = fmaf(f, x[q][s2], iu * s_B[r][nl + 64 * s2]);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < PPW; ++q) {
-    const int pass = wv + q * kGnW;
-    if (pass >= NPASS) break;
-    const int64_t d = dbase + (int64_t)pass * G + gl;
-    if (d >= D) continue;
-    const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
-#pragma unroll
-    for (int s2 = 0; s2 < S; ++s2) {
-      const int n = nl + 64 * s2;
-      if (n < N) a.segZ[o * N + n] = x[q][s2];
-    }
-    if (nl == 0) a.segF[o] = Fc[q];
-  }
-}
+// carried state. The backward mirrors this with the adjoint carry
+// (gn_bwd_map_kernel, the carry in reverse, gn_bwd_kernel).
 
 // Adjoint map of segment blockIdx / n_tiles + 1 (segments 1 .. nseg-1): the
 // carry leaving the segment's first row towards the past, from a zero carry
@@ -1358,133 +1272,6 @@ __global__ void gn_seg_carry_kernel(const ScanArgs a, int dir) {
   }
 }
 
-template <int NP>
-__global__ __launch_bounds__(64 * kGnW) void gn_fwd_kernel(const ScanArgs a, int x_dt, int g_dt, int y_dt) {
-  constexpr int LG = NP < 64 ? NP : 64;
-  constexpr int S = NP / LG;
-  constexpr int G = 64 / LG;
-  constexpr int NPASS = kGnDT / G;
-  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
-  __shared__ float s_f[kGnCK][kGnDT], s_iu[kGnCK][kGnDT], s_du[kGnCK][kGnDT], s_y[kGnCK][kGnDT];
-  __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP];
-  const int N = a.N;
-  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
-  const int b = tile / a.n_dtiles;
-  const int dtile = tile - b * a.n_dtiles;
-  const int64_t T = a.T, D = a.D;
-  const int64_t dbase = (int64_t)dtile * kGnDT;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gl = lane / LG, nl = lane - gl * LG;
-  const int KC = (int)((T + kGnCK - 1) / kGnCK);
-  const int sc0 = seg * a.seg_sc;
-  const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
-
-  // state entering the segment: h0, or the carried state
-  const float* xin = a.nseg > 1 ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N : (a.h0 ? a.h0 + (int64_t)b * D * N : nullptr);
-  float x[PPW][S];
-#pragma unroll
-  for (int q = 0; q < PPW; ++q) {
-    const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
-#pragma unroll
-    for (int s2 = 0; s2 < S; ++s2) {
-      const int n = nl + 64 * s2;
-      x[q][s2] = (xin && n < N && d < D) ? xin[d * N + n] : 0.f;
-    }
-  }
-  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
-  float vu[kGnE], vf[kGnE], vi[kGnE], vb[EB], vc[EB];
-  {
-    const int64_t tl = (int64_t)sc0 * kGnCK;
-    gn_ld_tile(a, a.u, x_dt, b, tl, dbase, vu);
-    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
-    gn_ld_tile(a, a.il, g_dt, b, tl, dbase, vi);
-    gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
-    gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
-  }
-  for (int sc = sc0; sc < sc1; ++sc) {
-    const int64_t t0 = (int64_t)sc * kGnCK;
-    __syncthreads();  // the previous sub-chunk's tiles are consumed
-#pragma unroll
-    for (int e = 0; e < kGnE; ++e) {
-      const int k = e * kGnThreads + (int)threadIdx.x;
-      const int r = k / kGnDT, c = k % kGnDT;
-      const int64_t d = dbase + c;
-      const bool ok = t0 + r < T && d < D;
-      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
-      s_iu[r][c] = ok ? sigm(vi[e]) * vu[e] : 0.f;
-      s_du[r][c] = ok ? a.Dsk[d] * vu[e] : 0.f;
-    }
-    gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
-    __syncthreads();
-    if (sc + 1 < sc1) {  // prefetch the next sub-chunk while this one is scanned
-      const int64_t t1 = t0 + kGnCK;
-      gn_ld_tile(a, a.u, x_dt, b, t1, dbase, vu);
-      gn_ld_tile(a, a.fl, g_dt, b, t1, dbase, vf);
-      gn_ld_tile(a, a.il, g_dt, b, t1, dbase, vi);
-      gn_ld_bc<NP, EB>(a, a.Bm, b, t1, vb);
-      gn_ld_bc<NP, EB>(a, a.Cm, b, t1, vc);
-    }
-    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
-#pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      const int pass = wv + q * kGnW;
-      if (pass >= NPASS) break;
-      const int c = pass * G + gl;
-      const int64_t d = dbase + c;
-      if (a.ckpt) {
-#pragma unroll
-        for (int s2 = 0; s2 < S; ++s2) {
-          const int n = nl + 64 * s2;
-          if (n < N && d < D) a.ckpt[(((int64_t)b * KC + sc) * D + d) * N + n] = x[q][s2];
-        }
-      }
-      // the recurrence runs row by row; the sums over n of all rows are
-      // formed afterwards, so their shuffle chains interleave
-      float p[kGnCK];
-#pragma unroll
-      for (int r = 0; r < kGnCK; ++r) {
-        p[r] = 0.f;
-        if (r < rows) {
-          const float f = s_f[r][c], iu = s_iu[r][c];
-#pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) {
-            const int n = nl + 64 * s2;
-            x[q][s2] = fmaf(f, x[q][s2], iu * s_B[r][n]);
-            p[r] = fmaf(s_C[r][n], x[q][s2], p[r]);
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < kGnCK; ++r) p[r] = group_sum<LG>(p[r]);
-      if (nl == 0) {
-#pragma unroll
-        for (int r = 0; r < kGnCK; ++r)
-          if (r < rows) s_y[r][c] = p[r] + s_du[r][c];
-      }
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
-      const int r = e / kGnDT, c = e - r * kGnDT;
-      const int64_t t = t0 + r, d = dbase + c;
-      if (t < T && d < D) st_any(a.y, y_dt, ((int64_t)b * T + t) * D + d, s_y[r][c]);
-    }
-  }
-  if (a.hT && seg == a.nseg - 1) {
-#pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      const int pass = wv + q * kGnW;
-      if (pass >= NPASS) break;
-      const int64_t d = dbase + (int64_t)pass * G + gl;
-#pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) {
-        const int n = nl + 64 * s2;
-        if (n < N && d < D) a.hT[((int64_t)b * D + d) * N + n] = x[q][s2];
-      }
-    }
-  }
-}
 
 template <int NP>
 __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int x_dt, int g_dt, int du_dt,
@@ -1917,17 +1704,6 @@ int np_of(int64_t N) {
   return np;
 }
 
-gn_fwd_t pick_gn_fwd(int np) {
-  switch (np) {
-    case 2: return gn_fwd_kernel<2>;
-    case 4: return gn_fwd_kernel<4>;
-    case 8: return gn_fwd_kernel<8>;
-    case 16: return gn_fwd_kernel<16>;
-    case 32: return gn_fwd_kernel<32>;
-    case 64: return gn_fwd_kernel<64>;
-    default: return gn_fwd_kernel<128>;
-  }
-}
 
 gn_bwd_t pick_gn_bwd(int np) {
   switch (np) {
@@ -1958,15 +1734,15 @@ gn_fwd_t pick_gc_fwd(int np, bool map) {
 
 typedef void (*gn_map_t)(ScanArgs, int, int);
 
-gn_map_t pick_gn_map(int np, bool bwd) {
+gn_map_t pick_gn_bwd_map(int np) {
   switch (np) {
-    case 2: return bwd ? gn_bwd_map_kernel<2> : gn_fwd_map_kernel<2>;
-    case 4: return bwd ? gn_bwd_map_kernel<4> : gn_fwd_map_kernel<4>;
-    case 8: return bwd ? gn_bwd_map_kernel<8> : gn_fwd_map_kernel<8>;
-    case 16: return bwd ? gn_bwd_map_kernel<16> : gn_fwd_map_kernel<16>;
-    case 32: return bwd ? gn_bwd_map_kernel<32> : gn_fwd_map_kernel<32>;
-    case 64: return bwd ? gn_bwd_map_kernel<64> : gn_fwd_map_kernel<64>;
-    default: return bwd ? gn_bwd_map_kernel<128> : gn_fwd_map_kernel<128>;
+    case 2: return gn_bwd_map_kernel<2>;
+    case 4: return gn_bwd_map_kernel<4>;
+    case 8: return gn_bwd_map_kernel<8>;
+    case 16: return gn_bwd_map_kernel<16>;
+    case 32: return gn_bwd_map_kernel<32>;
+    case 64: return gn_bwd_map_kernel<64>;
+    default: return gn_bwd_map_kernel<128>;
   }
 }
 
@@ -1976,7 +1752,7 @@ int gn_segments(const ScanArgs& a, const Layout& l, int x_dt, int g_dt, bool bwd
   if (l.nseg <= 1) return NAJU_OK;
   if (bwd) {
     const unsigned grid = (unsigned)((int64_t)l.n_tiles * (l.nseg - 1));
-    hipLaunchKernelGGL(pick_gn_map(np_of(a.N), true), dim3(grid), dim3(64 * kGnW), 0, st, a, x_dt, g_dt);
+    hipLaunchKernelGGL(pick_gn_bwd_map(np_of(a.N)), dim3(grid), dim3(64 * kGnW), 0, st, a, x_dt, g_dt);
   } else {
     const unsigned grid = (unsigned)(gc_tiles(a.batch, a.D) * (l.nseg - 1));
     hipLaunchKernelGGL(pick_gc_fwd(np_of(a.N), true), dim3(grid), dim3(64 * kGcW), 0, st, a, x_dt, g_dt, 0);
