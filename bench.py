@@ -41,7 +41,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c1-c4: the scan itself; c5: the LM training step (tokens/s)")
     ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flush", action="store_true",
@@ -53,6 +54,10 @@ def main():
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
+
+    if args.config == "c5":
+        _bench_lm(args)
+        return
 
     import ctypes
     import torch
@@ -196,6 +201,61 @@ def main():
         out["flushed_GBs"] = round(bytes_step / (med(tf) * 1e-3) / 1e9, 1)
         del scratch
     out["cpu_baseline"] = None if args.no_cpu else _cpu_baseline(args.config, N)
+    print(json.dumps(out), flush=True)
+
+
+def _bench_lm(args):
+    """one training step of the Naju LM (12 layers,
+    d_model 768, vocab 50257, N = 64) on a batch of 8 x 2048 uniformly random
+    token ids: bf16 autocast forward, cross-entropy, backward, gradient
+    clipping at 1.0 and an AdamW step, with every mixer's scan on the HIP
+    kernels. value = tokens per second."""
+    import torch
+    from naju_amd.mixer import NajuLM, build_optimizer
+    dev = torch.device("cuda", 0)
+    V, d_model, n_layers, T, Bsz = 50257, 768, 12, 2048, 8
+    torch.manual_seed(0)
+    model = NajuLM(V, d_model=d_model, n_layers=n_layers, dropout=0.1, scan_backend="hip").to(dev)
+    opt = build_optimizer(model, lr=1e-3, weight_decay=0.1)
+    ids = torch.randint(0, V, (Bsz, T + 1), device=dev)
+    x, y = ids[:, :-1].contiguous(), ids[:, 1:].contiguous()
+    n_params = sum(p.numel() for p in model.parameters())
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = model(x)
+            loss = torch.nn.functional.cross_entropy(logits.float().view(-1, V), y.view(-1))
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    K = args.steps
+    t0 = time.perf_counter()
+    for _ in range(K):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / K
+    tokens = Bsz * T
+    tflops = 6.0 * n_params * tokens / dt / 1e12
+    out = {
+        "metric": METRIC, "value": round(tokens / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 autocast (scan in f32 state)",
+        "data": "synthetic (uniform random token ids; random init)",
+        "config": {"workload": "naju LM training step c5: 12 layers, d_model 768, vocab 50257, N=64, "
+                               "batch 8 x seq 2048, AdamW + clip 1.0",
+                   "parameters": n_params, "parallelism": "single GPU"},
+        "loss_last": round(float(loss), 4),
+        "roofline": {"kernel": "whole training step (6 x parameters x tokens)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
     print(json.dumps(out), flush=True)
 
 

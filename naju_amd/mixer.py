@@ -1,0 +1,176 @@
+"""Naju mixer, residual block and causal LM on top of the MI355X scan.
+
+A restatement of the reference's model code (naju/mixer.py:51-144,
+naju/lm.py:13-33, naju/optim.py:30-52) over this package's scan dispatch, so
+the mixer and the LM training step run with the HIP
+scan where the reference package is absent. Module and parameter names, shapes
+and initialisation follow the reference, so state dicts load in either
+direction with ``strict=True``.
+
+One layer, with u the residual stream and h the content branch:
+
+    [x, z]   = in_proj(u)                          d_model -> 2 d_inner
+    h        = SiLU(causal depthwise conv_k(x) + conv bias)
+    [B, C]   = x_proj(h)                           d_inner -> 2 N
+    f_logit  = f_proj(h) [/ sqrt(d_inner)] + causal dwconv_k(h) + f_bias   (f_bias init +5)
+    i_logit  = i_proj(h) [/ sqrt(d_inner)] + causal dwconv_k(h) + i_bias   (i_bias init -2)
+    cx       = scan(h, f_logit, i_logit, B, C, D=0) / sqrt(N)
+    out      = out_proj((cx + D * h) * SiLU(z))    (D init 0.01)
+
+The bracketed 1/sqrt(d_inner) applies with ``gate_reparam``, whose weights
+start scaled up by sqrt(d_inner) (same forward at init) and whose optimizer
+half is ``build_optimizer``. ``gate_rank`` factors the gate projections as
+two linear maps. The scan runs through ``naju_amd.scan.naju_scan`` with the
+mixer's ``scan_backend`` (default: ``NAJU_SCAN_BACKEND``, else the HIP
+kernels).
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
+
+from naju_amd.scan import naju_scan
+
+
+class RMSNorm(nn.Module):
+    """weight * x / sqrt(mean(x^2) + eps) over the last axis."""
+
+    def __init__(self, d, eps=1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d))
+
+    def forward(self, x):
+        return self.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
+
+
+def _causal_dwconv(x, conv):
+    """Depthwise causal convolution of x [B, T, C] along T with the weights of
+    `conv` (an nn.Conv1d with groups = C): output t sees inputs t-k+1 .. t."""
+    k = conv.weight.shape[-1]
+    xt = F.pad(x.transpose(1, 2), (k - 1, 0))
+    return F.conv1d(xt, conv.weight, conv.bias, groups=conv.groups).transpose(1, 2)
+
+
+class NajuMixer(nn.Module):
+    def __init__(self, d_model, d_state=64, d_conv=4, expand=2, gate_conv_kernel=4,
+                 forget_bias_init=5.0, input_bias_init=-2.0, d_init=0.01,
+                 gate_rank=None, gate_reparam=False, scan_backend=None):
+        super().__init__()
+        if gate_reparam and gate_rank:
+            raise ValueError("gate_reparam is incompatible with gate_rank "
+                             "(the rescale targets the full-rank projections)")
+        di = expand * d_model
+        self.d_model, self.d_state, self.d_inner = d_model, d_state, di
+        self.gate_rank = gate_rank
+        self.gate_reparam = bool(gate_reparam)
+        self.scan_backend = scan_backend
+        self._cx_scale = 1.0 / math.sqrt(d_state)
+
+        self.in_proj = nn.Linear(d_model, 2 * di, bias=False)
+        # the convolutions pad inside _causal_dwconv; the modules hold weights
+        self.conv1d = nn.Conv1d(di, di, kernel_size=d_conv, groups=di, bias=True)
+        self.x_proj = nn.Linear(di, 2 * d_state, bias=False)
+        self.out_proj = nn.Linear(di, d_model, bias=False)
+        self.D = nn.Parameter(torch.full((di,), float(d_init)))
+        self.register_buffer("D_zero", torch.zeros(di), persistent=False)
+
+        self.f_proj = self._gate_proj()
+        self.f_conv = nn.Conv1d(di, di, kernel_size=gate_conv_kernel, groups=di, bias=False)
+        self.f_bias = nn.Parameter(torch.full((di,), float(forget_bias_init)))
+        self.i_proj = self._gate_proj()
+        self.i_conv = nn.Conv1d(di, di, kernel_size=gate_conv_kernel, groups=di, bias=False)
+        self.i_bias = nn.Parameter(torch.full((di,), float(input_bias_init)))
+        if self.gate_reparam:
+            with torch.no_grad():
+                self.f_proj.weight.mul_(math.sqrt(di))
+                self.i_proj.weight.mul_(math.sqrt(di))
+
+    def _gate_proj(self):
+        di = self.d_inner
+        if self.gate_rank:
+            return nn.Sequential(nn.Linear(di, self.gate_rank, bias=False),
+                                 nn.Linear(self.gate_rank, di, bias=False))
+        return nn.Linear(di, di, bias=False)
+
+    def _gate_logit(self, h, proj, conv, bias):
+        p = proj(h)
+        if self.gate_reparam:
+            p = p / math.sqrt(self.d_inner)
+        return p + _causal_dwconv(h, conv) + bias
+
+    def forward(self, u):
+        x, z = self.in_proj(u).chunk(2, dim=-1)
+        h = F.silu(_causal_dwconv(x, self.conv1d))
+        Bm, Cm = self.x_proj(h).split(self.d_state, dim=-1)
+        f_logit = self._gate_logit(h, self.f_proj, self.f_conv, self.f_bias)
+        i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)
+        # the scan reads out the state only; the D skip is applied here
+        cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
+        y = (cx * self._cx_scale + self.D * h) * F.silu(z)
+        return self.out_proj(y)
+
+
+class NajuBlock(nn.Module):
+    """Pre-norm residual block u + Dropout(Mixer(RMSNorm(u)))."""
+
+    def __init__(self, d_model, dropout=0.1, use_ckpt=False, **mixer_kw):
+        super().__init__()
+        self.norm = RMSNorm(d_model)
+        self.mixer = NajuMixer(d_model, **mixer_kw)
+        self.drop = nn.Dropout(dropout)
+        self.use_ckpt = use_ckpt
+
+    def _branch(self, u):
+        return self.drop(self.mixer(self.norm(u)))
+
+    def forward(self, u):
+        if self.use_ckpt and torch.is_grad_enabled():
+            return u + checkpoint(self._branch, u, use_reentrant=False)
+        return u + self._branch(u)
+
+
+class NajuLM(nn.Module):
+    """Embedding, n_layers NajuBlocks, final RMSNorm, LM head (tied to the
+    embedding by default); embedding and head start N(0, 0.02)."""
+
+    def __init__(self, vocab_size, d_model=256, n_layers=6, dropout=0.1,
+                 tie_weights=True, use_ckpt=False, **mixer_kw):
+        super().__init__()
+        self.embed = nn.Embedding(vocab_size, d_model)
+        self.blocks = nn.ModuleList(
+            NajuBlock(d_model, dropout=dropout, use_ckpt=use_ckpt, **mixer_kw) for _ in range(n_layers))
+        self.norm = RMSNorm(d_model)
+        self.head = nn.Linear(d_model, vocab_size, bias=False)
+        nn.init.normal_(self.embed.weight, std=0.02)
+        nn.init.normal_(self.head.weight, std=0.02)
+        if tie_weights:
+            self.head.weight = self.embed.weight
+
+    def forward(self, ids):
+        x = self.embed(ids)
+        for blk in self.blocks:
+            x = blk(x)
+        return self.head(self.norm(x))
+
+
+def build_optimizer(model, lr, weight_decay=0.1):
+    """AdamW; with gate_reparam mixers, their f_proj / i_proj weights get
+    lr * sqrt(d_inner), weight_decay / sqrt(d_inner) and eps 1e-8 / sqrt(d_inner)
+    (reference naju/optim.py:30-52)."""
+    mixers = [m for m in model.modules() if isinstance(m, NajuMixer) and m.gate_reparam]
+    if not mixers:
+        return torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay)
+    widths = {m.d_inner for m in mixers}
+    if len(widths) != 1:
+        raise ValueError(f"mixed d_inner across gate_reparam mixers: {widths}")
+    mult = math.sqrt(widths.pop())
+    gate = {id(p) for m in mixers for p in (m.f_proj.weight, m.i_proj.weight)}
+    rest = [p for p in model.parameters() if id(p) not in gate]
+    gate_params = [p for p in model.parameters() if id(p) in gate]
+    return torch.optim.AdamW(
+        [{"params": rest},
+         {"params": gate_params, "lr": lr * mult, "weight_decay": weight_decay / mult, "eps": 1e-8 / mult}],
+        lr=lr, weight_decay=weight_decay)
