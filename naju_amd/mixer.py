@@ -48,10 +48,26 @@ class RMSNorm(nn.Module):
 
 def _causal_dwconv(x, conv):
     """Depthwise causal convolution of x [B, T, C] along T with the weights of
-    `conv` (an nn.Conv1d with groups = C): output t sees inputs t-k+1 .. t."""
-    k = conv.weight.shape[-1]
-    xt = F.pad(x.transpose(1, 2), (k - 1, 0))
-    return F.conv1d(xt, conv.weight, conv.bias, groups=conv.groups).transpose(1, 2)
+    `conv` (an nn.Conv1d with groups = C): output t sees inputs t-k+1 .. t,
+
+        y[:, t] = bias + sum_j w[:, j] * x[:, t - (k-1) + j].
+
+    Computed as k shifted multiply-adds in the [B, T, C] layout (no
+    transposes), in float32. Under autocast the result takes the autocast
+    dtype, as the library convolution would."""
+    w = conv.weight[:, 0, :].float()  # [C, k]
+    k = w.shape[1]
+    T = x.shape[1]
+    xp = F.pad(x, (0, 0, k - 1, 0))
+    y = xp[:, k - 1:].float() * w[:, k - 1]
+    for j in range(k - 1):
+        y = torch.addcmul(y, xp[:, j:j + T].float(), w[:, j])
+    if conv.bias is not None:
+        y = y + conv.bias.float()
+    dev = x.device.type
+    if torch.is_autocast_enabled(dev):
+        return y.to(torch.get_autocast_dtype(dev))
+    return y.to(x.dtype)
 
 
 class NajuMixer(nn.Module):
