@@ -1,0 +1,62 @@
+/*
+ * naju_mixer.h -- C ABI of the MI355X (gfx950) kernels around the Naju scan
+ * inside the mixer: the depthwise causal convolutions of the content branch
+ * and of the gate logits (reference /root/reference/naju/mixer.py:75-76,
+ * 97-99, 106-110, 115).
+ *
+ *   y[b,t,c] = act( add[b,t,c] + bias[c] + sum_{j<K} w[c,j] * x[b, t-(K-1)+j, c] )
+ *
+ * with x taken as 0 before t = 0 (causal), act = identity or SiLU, and add and
+ * bias optional (NULL). This is one nn.Conv1d(C, C, K, groups=C,
+ * padding=K-1) followed by the slice [..., :T] (mixer.py:115 for the content
+ * branch, with SiLU; mixer.py:106-110 for a gate logit, where add is the gate
+ * projection and bias the gate bias).
+ *
+ * Layouts: add, y, dy, dx : [batch, T, C] row-major (C fastest);
+ *          x : [batch, T, C] with C fastest and x_ld >= C elements between
+ *              consecutive timesteps (x_ld = C when contiguous; 2C for one half
+ *              of the in_proj output [x, z] without a copy);
+ *          w, dw : [C, K] float32 (the Conv1d weight [C, 1, K]);
+ *          bias, dbias : [C] float32.
+ * dtype codes are those of naju_scan.h (F32, BF16, F16). Arithmetic is
+ * float32. Every call is asynchronous on `stream`, allocates nothing and never
+ * synchronises the host; errors are reported as in naju_scan.h, with the
+ * message in naju_mixer_last_error().
+ */
+#ifndef NAJU_MIXER_H
+#define NAJU_MIXER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call of this thread ("" after a success). */
+const char* naju_mixer_last_error(void);
+
+/* Forward: y = act(add + bias + causal_dwconv(x, w)). act: 0 = identity,
+ * 1 = SiLU (then add must be NULL). K <= 8. Replaces the Conv1d calls of
+ * naju/mixer.py:109 and :115 (plus the bias add of :110). */
+int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, void* y,
+                    int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype, int add_dtype, int y_dtype,
+                    void* stream);
+
+/* Bytes of workspace naju_dwconv_bwd needs (per-block partial sums of dw and
+ * dbias); no zero-fill needed. */
+size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K);
+
+/* Backward of naju_dwconv_fwd with add = NULL (the gradient of add is dy
+ * itself): dx, dw and dbias (each nullable to skip it) from dy. With act = 1
+ * the pre-activation is recomputed from x. Deterministic (fixed-order
+ * sums). The autograd of the reference's Conv1d + slice. */
+int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
+                    float* dw, float* dbias, int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype,
+                    int dy_dtype, int dx_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NAJU_MIXER_H */

@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI declared in include/naju_scan.h.
+"""ctypes binding of the C ABI declared in include/naju_scan.h and
+include/naju_mixer.h.
 
 The library is naju_amd/libnaju_scan.so (built by naju_amd/build.py). Nothing
 here falls back to another implementation: if the library is missing or a
@@ -20,6 +21,10 @@ EXPORTED = (
     "naju_scan_fwd",
     "naju_scan_bwd",
     "naju_scan_workspace_status",
+    "naju_mixer_last_error",
+    "naju_dwconv_fwd",
+    "naju_dwconv_workspace_bytes",
+    "naju_dwconv_bwd",
 )
 
 _lib = None
@@ -62,6 +67,16 @@ def lib():
     L.naju_scan_bwd.restype = I
     L.naju_scan_workspace_status.argtypes = [P, P, ctypes.POINTER(ctypes.c_uint32)]
     L.naju_scan_workspace_status.restype = I
+    L.naju_mixer_last_error.argtypes = []
+    L.naju_mixer_last_error.restype = ctypes.c_char_p
+    # x, x_ld, w, bias, add, y, batch, T, C, K, act, x_dt, add_dt, y_dt, stream
+    L.naju_dwconv_fwd.argtypes = [P, I64] + [P] * 4 + [I64] * 3 + [I] * 5 + [P]
+    L.naju_dwconv_fwd.restype = I
+    L.naju_dwconv_workspace_bytes.argtypes = [I64] * 3 + [I]
+    L.naju_dwconv_workspace_bytes.restype = SZ
+    # x, x_ld, w, bias, dy, dx, dw, dbias, batch, T, C, K, act, x_dt, dy_dt, dx_dt, ws, ws_bytes, stream
+    L.naju_dwconv_bwd.argtypes = [P, I64] + [P] * 6 + [I64] * 3 + [I] * 5 + [P, SZ, P]
+    L.naju_dwconv_bwd.restype = I
     _lib = L
     return _lib
 
@@ -69,4 +84,11 @@ def lib():
 def check(rc):
     if rc != OK:
         raise NajuScanError(rc, lib().naju_scan_last_error().decode(errors="replace"))
+    return rc
+
+
+def check_mixer(rc):
+    """check() for the calls of include/naju_mixer.h."""
+    if rc != OK:
+        raise NajuScanError(rc, lib().naju_mixer_last_error().decode(errors="replace"))
     return rc

@@ -10,12 +10,12 @@ import sys
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_PKG)
 LIB_PATH = os.path.join(_PKG, "libnaju_scan.so")
-SOURCES = [os.path.join(_PKG, "csrc", "naju_scan.hip")]
+SOURCES = [os.path.join(_PKG, "csrc", n) for n in ("naju_scan.hip", "naju_mixer.hip")]
 
 # Packed-FP32 VALU ops are disabled for all device code: only plain fp32
 # arithmetic is emitted.
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + os.path.join(_ROOT, "include"),
 ]
@@ -28,20 +28,43 @@ def hipcc():
     return "hipcc"
 
 
-def build(verbose=False):
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + SOURCES + ["-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+def _finish(cmd, proc, verbose):
+    out, err = proc.communicate()
     # hipcc's host pass warns that it does not know the packed-fp32 feature.
-    err = "\n".join(ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    err = "\n".join(ln for ln in err.splitlines() if "packed-fp32-ops" not in ln)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
+
+
+def build(verbose=False):
+    """Compile every HIP source (in parallel, one object each) and link them
+    into LIB_PATH. Always recompiles."""
+    objs = [LIB_PATH + "." + os.path.basename(src) + ".o" for src in SOURCES]
+    jobs = []
+    for src, obj in zip(SOURCES, objs):
+        cmd = [hipcc()] + HIPCC_FLAGS + ["-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        jobs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    try:
+        for cmd, proc in jobs:
+            _finish(cmd, proc, verbose)
+        tmp = LIB_PATH + ".tmp"
+        cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", tmp]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        _finish(cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True), verbose)
+        os.replace(tmp, LIB_PATH)
+    finally:
+        for cmd, proc in jobs:
+            if proc.poll() is None:
+                proc.kill()
+                proc.wait()
+        for obj in objs:
+            if os.path.exists(obj):
+                os.remove(obj)
     return LIB_PATH
 
 

@@ -1,0 +1,122 @@
+"""Depthwise causal convolutions of the mixer on the HIP kernels of
+include/naju_mixer.h.
+
+``dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None)``
+
+    y[:, t] = act(add[:, t] + bias + sum_j w[:, j] * x[:, t - (k-1) + j])
+
+for x [B, T, C] (C contiguous; a row stride above C is taken as it is, so one
+half of a chunked projection needs no copy), weight [C, 1, k] or [C, k]
+(nn.Conv1d with groups = C), bias [C]. ``silu`` applies SiLU to the result
+(then ``add`` must be None). Differentiable in x, weight, bias and add; the
+backward is deterministic. This is the reference's Conv1d(groups=C,
+padding=k-1) + slice (naju/mixer.py:108-110, 115) in the [B, T, C] layout the
+scan uses, with float32 arithmetic and one rounding at the output.
+
+CUDA tensors only: there is no other implementation behind this function,
+and a missing library raises.
+"""
+import torch
+
+from naju_amd import _lib
+
+_DT = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16}
+
+
+class _Workspace:
+    """Per-(device, stream) scratch for the backward's partial sums, grown on
+    demand (the kernels overwrite every byte they later read)."""
+
+    def __init__(self):
+        self._bufs = {}
+
+    def get(self, device, stream, nbytes):
+        key = (device.index, stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_WS = _Workspace()
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _rows(x):
+    """(x, row stride in elements) with C contiguous and [B, T] collapsible."""
+    B, T, C = x.shape
+    if x.stride(2) != 1 or x.stride(0) != T * x.stride(1) or x.stride(1) < C:
+        x = x.contiguous()
+    return x, x.stride(1)
+
+
+class _DwConv(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, bias, add, silu, out_dtype):
+        B, T, C = x.shape
+        K = w.shape[1]
+        x, ldx = _rows(x)
+        y = torch.empty((B, T, C), dtype=out_dtype, device=x.device)
+        L = _lib.lib()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check_mixer(L.naju_dwconv_fwd(
+            _ptr(x), ldx, _ptr(w), _ptr(bias), _ptr(add), _ptr(y), B, T, C, K, int(silu), _DT[x.dtype],
+            _DT[add.dtype] if add is not None else 0, _DT[out_dtype], stream))
+        ctx.save_for_backward(x, w, bias)
+        ctx.silu = silu
+        ctx.add_dtype = None if add is None else add.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, bias = ctx.saved_tensors
+        B, T, C = x.shape
+        K = w.shape[1]
+        if dy.dtype not in _DT:
+            dy = dy.float()
+        dy = dy.contiguous()
+        need_x, need_w, need_b, need_add = ctx.needs_input_grad[:4]
+        dx = torch.empty((B, T, C), dtype=x.dtype, device=x.device) if need_x else None
+        dw = torch.empty((C, K), dtype=torch.float32, device=x.device) if need_w else None
+        db = torch.empty((C,), dtype=torch.float32, device=x.device) if (need_b and bias is not None) else None
+        if dx is not None or dw is not None or db is not None:
+            L = _lib.lib()
+            stream = torch.cuda.current_stream(x.device).cuda_stream
+            nbytes = L.naju_dwconv_workspace_bytes(B, T, C, K)
+            ws = _WS.get(x.device, stream, nbytes)
+            _lib.check_mixer(L.naju_dwconv_bwd(
+                _ptr(x), x.stride(1), _ptr(w), _ptr(bias), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), B, T, C, K,
+                int(ctx.silu), _DT[x.dtype], _DT[dy.dtype], _DT[x.dtype], _ptr(ws), ws.numel(), stream))
+        dadd = dy.to(ctx.add_dtype) if (need_add and ctx.add_dtype is not None) else None
+        return dx, dw, db, dadd, None, None
+
+
+def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
+    if not x.is_cuda:
+        raise RuntimeError("naju_amd.dwconv runs on the HIP kernels only: x must be a CUDA tensor")
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, T, C], got {tuple(x.shape)}")
+    C = x.shape[2]
+    w = weight.reshape(C, -1)
+    if w.dtype != torch.float32:
+        w = w.float()
+    w = w.contiguous()
+    if bias is not None:
+        bias = bias.float().contiguous()
+    if silu and add is not None:
+        raise ValueError("add is not supported together with silu")
+    if add is not None:
+        if add.shape != x.shape:
+            raise ValueError(f"add must have x's shape {tuple(x.shape)}, got {tuple(add.shape)}")
+        if add.dtype not in _DT:
+            add = add.float()
+        add = add.contiguous()
+    if x.dtype not in _DT:
+        x = x.float()
+    if out_dtype is None:
+        out_dtype = x.dtype
+    return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype)

@@ -31,6 +31,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
+from naju_amd.dwconv import dwconv
 from naju_amd.scan import naju_scan
 
 
@@ -46,15 +47,21 @@ class RMSNorm(nn.Module):
         return self.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
 
 
+def _out_dtype(x):
+    dev = x.device.type
+    return torch.get_autocast_dtype(dev) if torch.is_autocast_enabled(dev) else x.dtype
+
+
 def _causal_dwconv(x, conv):
     """Depthwise causal convolution of x [B, T, C] along T with the weights of
     `conv` (an nn.Conv1d with groups = C): output t sees inputs t-k+1 .. t,
 
         y[:, t] = bias + sum_j w[:, j] * x[:, t - (k-1) + j].
 
-    Computed as k shifted multiply-adds in the [B, T, C] layout (no
-    transposes), in float32. Under autocast the result takes the autocast
-    dtype, as the library convolution would."""
+    The formulation for CPU tensors: k shifted multiply-adds in the [B, T, C]
+    layout, in float32. Under autocast the result takes the autocast dtype, as
+    the library convolution would. CUDA tensors take the fused HIP kernels of
+    naju_amd.dwconv instead (NajuMixer._content and _gate_logit)."""
     w = conv.weight[:, 0, :].float()  # [C, k]
     k = w.shape[1]
     T = x.shape[1]
@@ -64,10 +71,7 @@ def _causal_dwconv(x, conv):
         y = torch.addcmul(y, xp[:, j:j + T].float(), w[:, j])
     if conv.bias is not None:
         y = y + conv.bias.float()
-    dev = x.device.type
-    if torch.is_autocast_enabled(dev):
-        return y.to(torch.get_autocast_dtype(dev))
-    return y.to(x.dtype)
+    return y.to(_out_dtype(x))
 
 
 class NajuMixer(nn.Module):
@@ -115,11 +119,21 @@ class NajuMixer(nn.Module):
         p = proj(h)
         if self.gate_reparam:
             p = p / math.sqrt(self.d_inner)
+        if h.is_cuda:
+            # one kernel: projection + conv + bias, in the dtype the sum
+            # promotes to (float32 under autocast: the bias is float32)
+            return dwconv(h, conv.weight, bias, add=p,
+                          out_dtype=torch.promote_types(_out_dtype(h), bias.dtype))
         return p + _causal_dwconv(h, conv) + bias
+
+    def _content(self, x):
+        if x.is_cuda:
+            return dwconv(x, self.conv1d.weight, self.conv1d.bias, silu=True, out_dtype=_out_dtype(x))
+        return F.silu(_causal_dwconv(x, self.conv1d))
 
     def forward(self, u):
         x, z = self.in_proj(u).chunk(2, dim=-1)
-        h = F.silu(_causal_dwconv(x, self.conv1d))
+        h = self._content(x)
         Bm, Cm = self.x_proj(h).split(self.d_state, dim=-1)
         f_logit = self._gate_logit(h, self.f_proj, self.f_conv, self.f_bias)
         i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)

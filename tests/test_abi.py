@@ -15,22 +15,24 @@ import torch
 from naju_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "naju_scan.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("naju_scan.h", "naju_mixer.h")]
 F32, BF16, F16 = 0, 1, 2
 
 
 def header_functions():
-    txt = open(HEADER).read()
-    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return sorted(set(re.findall(r"\b(naju_scan_\w+)\s*\(", txt)))
+    names = set()
+    for h in HEADERS:
+        txt = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer)_\w+)\s*\(", txt))
+    return sorted(names)
 
 
 def test_library_exports_every_header_symbol():
     lib = _lib.lib()
     names = header_functions()
-    assert len(names) >= 7
+    assert len(names) >= 11
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in include/naju_scan.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     assert set(names) == set(_lib.EXPORTED)
     assert lib.naju_scan_version() >= 1
 
@@ -189,3 +191,48 @@ def test_build_flags_disable_packed_fp32():
     flags = " ".join(build.HIPCC_FLAGS)
     assert "--offload-arch=gfx950" in flags
     assert "-target-feature -Xclang -packed-fp32-ops" in flags
+
+
+# --- include/naju_mixer.h: host-side checks of the depthwise conv calls ----
+
+def _dw_fwd(L, K=4, act=0, x_ld=16, add=None, C=16, batch=2, T=8, dts=(F32, F32, F32)):
+    fake = 0x1000  # never dereferenced: every case here returns before a launch
+    return L.naju_dwconv_fwd(fake, x_ld, fake, None, add, fake, batch, T, C, K, act, dts[0], dts[1], dts[2], None)
+
+
+def test_dwconv_host_checks():
+    L = _lib.lib()
+    assert _dw_fwd(L, K=9) == _lib.ERR_UNSUPPORTED and b"K" in L.naju_mixer_last_error()
+    assert _dw_fwd(L, K=0) == _lib.ERR_UNSUPPORTED
+    assert _dw_fwd(L, x_ld=15) == _lib.ERR_INVALID and b"x_ld" in L.naju_mixer_last_error()
+    assert _dw_fwd(L, act=2) == _lib.ERR_INVALID
+    assert _dw_fwd(L, act=1, add=0x2000) == _lib.ERR_UNSUPPORTED
+    assert _dw_fwd(L, dts=(F32, F32, 7)) == _lib.ERR_INVALID
+    assert _dw_fwd(L, batch=-1) == _lib.ERR_INVALID
+    # empty shapes return before any launch
+    assert _dw_fwd(L, batch=0) == _lib.OK and L.naju_mixer_last_error() == b""
+    assert _dw_fwd(L, T=0) == _lib.OK
+    # null required pointer
+    assert L.naju_dwconv_fwd(None, 16, 0x1000, None, None, 0x1000, 2, 8, 16, 4, 0, F32, F32, F32, None) \
+        == _lib.ERR_INVALID
+
+
+def test_dwconv_workspace_size_and_check():
+    L = _lib.lib()
+    # one partial row of (K dw + 1 dbias) floats per channel per 64-row block per batch row
+    assert L.naju_dwconv_workspace_bytes(8, 2048, 1536, 4) >= 8 * 32 * 1536 * 5 * 4
+    assert L.naju_dwconv_workspace_bytes(1, 65, 8, 4) >= 2 * 8 * 5 * 4
+    assert L.naju_dwconv_workspace_bytes(1, 8, 8, 9) == 0
+    fake = 0x1000
+    rc = L.naju_dwconv_bwd(fake, 16, fake, None, fake, fake, fake, None, 2, 8, 16, 4, 0, F32, F32, F32,
+                           None, 0, None)
+    assert rc == _lib.ERR_WORKSPACE and b"workspace" in L.naju_mixer_last_error()
+    # dx only: no sums, no workspace needed -- but it would launch, so check only the no-op case
+    assert L.naju_dwconv_bwd(fake, 16, fake, None, fake, fake, None, None, 0, 8, 16, 4, 0, F32, F32, F32,
+                             None, 0, None) == _lib.OK
+
+
+def test_dwconv_python_rejects_cpu_tensors():
+    from naju_amd.dwconv import dwconv
+    with pytest.raises(RuntimeError, match="CUDA"):
+        dwconv(torch.zeros(1, 4, 4), torch.zeros(4, 1, 4))

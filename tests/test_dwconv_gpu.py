@@ -1,0 +1,139 @@
+"""GPU parity of the depthwise causal convolution kernels (include/naju_mixer.h,
+naju_amd/dwconv.py) against the reference's formulation: nn.functional.conv1d
+with groups = C, padding k-1 and the slice [..., :T] on the [B, C, T]
+transpose (naju/mixer.py:108-110, 115), evaluated on the CPU in float64 with
+autograd for the gradients."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from naju_amd.dwconv import dwconv
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(x, w, bias, add, silu):
+    """float64 CPU reference of y = act(add + bias + causal_dwconv(x))."""
+    T, C = x.shape[1], x.shape[2]
+    K = w.shape[-1]
+    y = F.conv1d(x.transpose(1, 2), w.view(C, 1, K), bias, padding=K - 1, groups=C)[..., :T].transpose(1, 2)
+    if add is not None:
+        y = y + add
+    return F.silu(y) if silu else y
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _run(dev, B, T, C, K, silu, has_bias, has_add, x_dtype, out_dtype, strided=False, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    xs = torch.randn(B, T, 2 * C if strided else C, generator=g)
+    w = torch.randn(C, 1, K, generator=g) / K
+    bias = torch.randn(C, generator=g) if has_bias else None
+    add = torch.randn(B, T, C, generator=g) if has_add else None
+    dy = torch.randn(B, T, C, generator=g)
+    # quantise the inputs to the dtype the kernel reads, so the reference sees the same values
+    xs = xs.to(x_dtype)
+    if add is not None:
+        add = add.to(x_dtype)
+
+    # reference (float64, CPU)
+    xr = xs.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    br = bias.double().requires_grad_(True) if bias is not None else None
+    ar = add.double().requires_grad_(True) if add is not None else None
+    yr = _ref(xr[..., :C], wr, br, ar, silu)
+    yr.backward(dy.double())
+
+    # HIP
+    xg = xs.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    bg = bias.to(dev).requires_grad_(True) if bias is not None else None
+    ag = add.to(dev).requires_grad_(True) if add is not None else None
+    xin = xg[..., :C] if strided else xg
+    if strided:
+        assert xin.stride(1) == 2 * C  # the view goes to the kernel without a copy
+    y = dwconv(xin, wg, bg, add=ag, silu=silu, out_dtype=out_dtype)
+    assert y.dtype == out_dtype and y.shape == (B, T, C)
+    y.backward(dy.to(dev).to(out_dtype))
+    res = {"y": (y, yr), "dx": (xg.grad, xr.grad), "dw": (wg.grad, wr.grad)}
+    if bias is not None:
+        res["db"] = (bg.grad, br.grad)
+    if add is not None:
+        res["dadd"] = (ag.grad, ar.grad)
+    return res
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("silu", [False, True])
+def test_dwconv_fp32_matches_conv1d(gpu, K, silu):
+    res = _run(gpu, B=2, T=150, C=72, K=K, silu=silu, has_bias=True, has_add=not silu,
+               x_dtype=torch.float32, out_dtype=torch.float32)
+    for name, (a, b) in res.items():
+        assert _rel(a, b) < 1e-5, (name, _rel(a, b))
+
+
+@pytest.mark.parametrize("T", [1, 3, 63, 64, 65, 129])
+def test_dwconv_ragged_lengths(gpu, T):
+    """T below K, at and around the 64-row block boundary."""
+    for silu in (False, True):
+        res = _run(gpu, B=3, T=T, C=40, K=4, silu=silu, has_bias=True, has_add=False,
+                   x_dtype=torch.float32, out_dtype=torch.float32, seed=T)
+        for name, (a, b) in res.items():
+            assert _rel(a, b) < 1e-5, (T, silu, name, _rel(a, b))
+
+
+def test_dwconv_strided_input_no_bias(gpu):
+    """x as the first half of a [B, T, 2C] projection, as in the mixer."""
+    res = _run(gpu, B=2, T=100, C=300, K=4, silu=True, has_bias=False, has_add=False,
+               x_dtype=torch.float32, out_dtype=torch.float32, strided=True)
+    for name, (a, b) in res.items():
+        assert _rel(a, b) < 1e-5, (name, _rel(a, b))
+
+
+@pytest.mark.parametrize("silu,out", [(True, torch.bfloat16), (False, torch.float32)])
+def test_dwconv_bf16_inputs(gpu, silu, out):
+    """bf16 reads, float32 arithmetic, one rounding at a bf16 output."""
+    res = _run(gpu, B=2, T=200, C=264, K=4, silu=silu, has_bias=True, has_add=not silu,
+               x_dtype=torch.bfloat16, out_dtype=out, strided=silu)
+    for name, (a, b) in res.items():
+        tol = 2e-3 if name in ("dw", "db") else 8e-3  # bf16 outputs carry one rounding (2^-9 relative)
+        assert _rel(a, b) < tol, (name, _rel(a, b))
+
+
+def test_dwconv_mixer_shape_and_determinism(gpu):
+    """The C5 mixer's shape (d_inner 1536, T 2048, k 4): float64 agreement of
+    the long dw / dbias sums, and bit-identical repeats."""
+    dev = gpu
+    B, T, C, K = 2, 2048, 1536, 4
+    torch.manual_seed(5)
+    x = torch.randn(B, T, C, device=dev, dtype=torch.bfloat16)
+    w = (torch.randn(C, 1, K, device=dev) / K).requires_grad_(True)
+    b = torch.randn(C, device=dev).requires_grad_(True)
+    dy = torch.randn(B, T, C, device=dev, dtype=torch.bfloat16)
+    grads = []
+    for _ in range(2):
+        w.grad = b.grad = None
+        y = dwconv(x, w, b, silu=True, out_dtype=torch.bfloat16)
+        y.backward(dy)
+        grads.append((y.clone(), w.grad.clone(), b.grad.clone()))
+    for a, c in zip(grads[0], grads[1]):
+        assert torch.equal(a, c)
+    wr = w.detach().cpu().double().requires_grad_(True)
+    br = b.detach().cpu().double().requires_grad_(True)
+    yr = _ref(x.cpu().double(), wr, br, None, True)
+    yr.backward(dy.cpu().double())
+    assert _rel(grads[0][1], wr.grad) < 1e-5
+    assert _rel(grads[0][2], br.grad) < 1e-5
+    assert _rel(grads[0][0], yr) < 8e-3
+
+
+def test_dwconv_empty_batch_zero_grads(gpu):
+    w = torch.randn(8, 1, 3, device=gpu, requires_grad=True)
+    b = torch.randn(8, device=gpu, requires_grad=True)
+    x = torch.zeros(0, 5, 8, device=gpu, requires_grad=True)
+    y = dwconv(x, w, b)
+    y.sum().backward()
+    assert torch.equal(w.grad, torch.zeros_like(w)) and torch.equal(b.grad, torch.zeros_like(b))
