@@ -1273,6 +1273,98 @@ __global__ void gn_seg_carry_kernel(const ScanArgs a, int dir) {
 }
 
 
+// ------------------------------------------------- general N backward kernel
+//
+// One workgroup per (batch row, 64-channel tile, time segment), 8 waves.
+// Lanes run over the state index n (LG = min(NP, 64) lanes per channel, S
+// states per lane, G channels per wave instruction). A wave walks its
+// channel passes one after another; per kGnCK-row sub-chunk (the checkpoint
+// interval, walked from the last to the first) and per 16-row half (the later
+// half first) it
+//   1. recomputes the forward states of the half's rows from the checkpoint
+//      (the earlier half's rows first, unstored, when it is the later half),
+//   2. runs the adjoint x̄_t = C_t dy_t + g, g <- f_t x̄_t backwards over
+//      the rows, with this lane's terms of sum_n x̄_t x_{t-1} (dfl) and
+//      sum_n x̄_t B_t (dws), and of the dB / dC sums over the channels,
+//   3. reduces the dfl / dws terms over the channel's lanes every 8 rows with
+//      a transposing butterfly made of DPP and lane-swap moves, and writes
+//      du, dfl, dil over the consumed inputs in LDS.
+// The inputs of a sub-chunk are staged in LDS transposed, as [channel][row]
+// and [n][row], so one 16-byte read yields four rows of a channel (or of a
+// state) and a row costs a quarter of an LDS instruction per stream. Rows
+// past T and channels past D are staged as the neutral step (f = 1, i = u =
+// dy = 0, B = C = 0), so the loops carry no row guards; the stores skip them.
+constexpr int kGnH = 16;          // rows per adjoint half
+constexpr int kGnRG = 8;          // rows per reduction group
+constexpr int kGnRP = kGnCK + 4;  // LDS row pitch (floats) of the transposed tiles
+
+// Lane exchange for the butterfly steps below: the value of the partner lane
+// that differs in bit log2(m) (and, for m = 8 / 4, in the lower bits too:
+// row_mirror pairs i with 15 - i, row_half_mirror i with 7 - i).
+template <int m>
+__device__ __forceinline__ float dpp_partner(float x) {
+  constexpr int ctrl = m == 8 ? 0x140 : m == 4 ? 0x141 : m == 2 ? 0x4E : 0xB1;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
+}
+
+// (lo, hi) -> lanes with bit log2(m) clear get lo + partner's lo, lanes with
+// it set get hi + partner's hi, m = 32 or 16 (one lane-swap instruction).
+template <int m>
+__device__ __forceinline__ float swap_sum(float lo, float hi) {
+  if constexpr (m == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// Transposing butterfly over aligned groups of LG lanes of the M entries of
+// v (the same scheme as tr_reduce, with DPP and lane-swap exchanges). On
+// return, lane l of a group holds the group sums of entries
+// [l*M/LG, (l+1)*M/LG) in v[0 ..) when M >= LG, else entry l / (LG/M) in
+// v[0]. Fixed order: run-to-run identical.
+template <int LG, int K, int M>
+__device__ __forceinline__ void trd_step(float (&v)[M], int lane) {
+  if constexpr (LG > 1) {
+    constexpr int m = LG / 2;
+    if constexpr (K >= 2) {
+      constexpr int h = K / 2;
+      if constexpr (m >= 16) {
+#pragma unroll
+        for (int j = 0; j < h; ++j) v[j] = swap_sum<m>(v[j], v[j + h]);
+      } else {
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int j = 0; j < h; ++j) {
+          const float keep = hi ? v[j + h] : v[j], send = hi ? v[j] : v[j + h];
+          v[j] = keep + dpp_partner<m>(send);
+        }
+      }
+      trd_step<m, h, M>(v, lane);
+    } else {
+      if constexpr (m >= 16)
+        v[0] = swap_sum<m>(v[0], v[0]);
+      else
+        v[0] += dpp_partner<m>(v[0]);
+      trd_step<m, 1, M>(v, lane);
+    }
+  }
+}
+
+// Value of lane l ^ m for the lanes with bit log2(m) clear.
+template <int m>
+__device__ __forceinline__ float from_upper(float x) {
+  if constexpr (m == 32) {
+    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+  } else if constexpr (m == 16) {
+    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+  } else {
+    return __shfl_xor(x, m, 64);
+  }
+}
+
 template <int NP>
 __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int x_dt, int g_dt, int du_dt,
                                                            int dg_dt) {
@@ -1281,11 +1373,18 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   constexpr int G = 64 / LG;
   constexpr int NPASS = kGnDT / G;
   constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
-  // rows padded to kGnDT + 1 words: the output lanes read and write one row
-  // each, at the same channel, without bank conflicts
-  __shared__ float s_f[kGnCK][kGnDT + 1], s_i[kGnCK][kGnDT + 1], s_u[kGnCK][kGnDT + 1], s_dy[kGnCK][kGnDT + 1];
-  __shared__ float s_o0[kGnCK][kGnDT + 1], s_o1[kGnCK][kGnDT + 1], s_o2[kGnCK][kGnDT + 1];
-  __shared__ float s_B[kGnCK][NP], s_C[kGnCK][NP], s_pB[kGnCK][NP], s_pC[kGnCK][NP];
+  static_assert(kGnCK == 4 * kGnW && kGnCK == 2 * kGnH && kGnH == 2 * kGnRG, "tile shape");
+  // B / C staging: thread -> state n = tid % NP, rows [rb*EB, rb*EB + EB)
+  constexpr int EB = kGnCK * NP >= kGnThreads ? kGnCK * NP / kGnThreads : 1;
+  constexpr int BCT = kGnCK * NP / EB;  // threads that stage B / C
+  // one object per tile family, so a lane addresses all of them from one
+  // base register plus immediate offsets: [0] f, [1] i, [2] u, [3] dy
+  // ([channel][row]); [0] B, [1] C ([n][row])
+  __shared__ __align__(16) float s_x[4][kGnDT][kGnRP];
+  __shared__ __align__(16) float s_bc[2][NP][kGnRP];
+  __shared__ float s_pB[kGnCK][NP], s_pC[kGnCK][NP];
+  __shared__ float s_dD[kGnW][kGnDT];
+  __shared__ float s_Dsk[kGnDT];
   const int N = a.N;
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
   const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
@@ -1293,22 +1392,30 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t dbase = (int64_t)dtile * kGnDT;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = (int)threadIdx.x;
+  if (tid < kGnDT) s_Dsk[tid] = dbase + tid < D ? a.Dsk[dbase + tid] : 0.f;  // read after the first barrier
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gl = lane / LG, nl = lane - gl * LG;
   const int KC = (int)((T + kGnCK - 1) / kGnCK);
   const int64_t btn = (int64_t)a.batch * T * N;
   const int sc0 = seg * a.seg_sc;
   const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
+  // staging roles: channel lane, rows 4*wv .. 4*wv+3; B / C state bn, rows
+  // bn_r0 .. bn_r0+EB-1
+  const int64_t dl = dbase + lane;
+  const bool dl_ok = dl < D;
+  const uint32_t lane_c = (uint32_t)(dl_ok ? dl : D - 1) - (uint32_t)dbase;  // clamped channel offset
+  const int bn = tid % NP, bn_r0 = (tid / NP) * EB;
+  const bool bn_act = tid < BCT;
+  const int bnc = bn < N ? bn : N - 1;
 
   // adjoint carry f_{t+1} x̄_{t+1} per channel pass: zero past the end of T,
   // else the carry entering the segment from the future
   const float* gin = a.nseg > 1 ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N : nullptr;
   float gc[PPW][S];
-  float dDs[PPW];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
-    dDs[q] = 0.f;
     const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) {
@@ -1316,175 +1423,318 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
       gc[q][s2] = (gin && n < N && d < D) ? gin[d * N + n] : 0.f;
     }
   }
-  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
-  // At NP = 128 the registers of a prefetched tile would spill: that case
-  // loads each sub-chunk's tiles just before staging them instead.
-  constexpr bool kPrefetch = NP <= 64;
-  float vu[kGnE], vf[kGnE], vi[kGnE], vg[kGnE], vb[EB], vc[EB];
-  auto load_tiles = [&](int64_t tl) {
-    gn_ld_tile(a, a.u, x_dt, b, tl, dbase, vu);
-    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
-    gn_ld_tile(a, a.il, g_dt, b, tl, dbase, vi);
-    gn_ld_tile(a, a.dy, x_dt, b, tl, dbase, vg);
-    gn_ld_bc<NP, EB>(a, a.Bm, b, tl, vb);
-    gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
-  };
-  if (kPrefetch) load_tiles((int64_t)(sc1 - 1) * kGnCK);
-  // checkpointed states entering a sub-chunk, for every channel pass of this
-  // wave, loaded one sub-chunk ahead
-  float ckn[PPW][S];
-  auto load_ckpt = [&](int sck) {
-#pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
-#pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) {
-        const int n = nl + 64 * s2;
-        ckn[q][s2] = (n < N && d < D && wv + q * kGnW < NPASS) ? a.ckpt[(((int64_t)b * KC + sck) * D + d) * N + n] : 0.f;
-      }
-    }
-  };
-  load_ckpt(sc1 - 1);
+  float dDacc = 0.f;
+
   for (int sc = sc1 - 1; sc >= sc0; --sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
-    if (!kPrefetch) load_tiles(t0);
-    __syncthreads();  // the previous sub-chunk's tiles are consumed
+    // this sub-chunk's inputs and checkpointed states
+    // Global addresses are a uniform 64-bit base (this sub-chunk's first
+    // row) plus a 32-bit per-lane element offset (clamped in bounds), so a
+    // stream costs one address register per lane.
+    const int64_t xrow0 = ((int64_t)b * T + t0) * D + dbase;  // [B,T,D] element of (t0, dbase)
+    const int64_t brow0 = ((int64_t)b * T + t0) * N;          // [B,T,N] element of (t0, 0)
+    float vu[4], vf[4], vi[4], vg[4], vb[EB], vc[EB];
+    {
+      uint32_t xo[4];
 #pragma unroll
-    for (int e = 0; e < kGnE; ++e) {
-      const int k = e * kGnThreads + (int)threadIdx.x;
-      const int r = k / kGnDT, c = k % kGnDT;
-      const bool ok = t0 + r < T && dbase + c < D;
-      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
-      s_i[r][c] = ok ? sigm(vi[e]) : 0.f;
-      s_u[r][c] = ok ? vu[e] : 0.f;
-      s_dy[r][c] = ok ? vg[e] : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        const int rr = 4 * wv + e < rows ? 4 * wv + e : rows - 1;
+        xo[e] = (uint32_t)rr * (uint32_t)D + lane_c;
+      }
+      auto ld4 = [&](const void* p, int dt, float (&o)[4]) {
+        if (dt == NAJU_DTYPE_F32) {
+          const char* q = (const char*)((const float*)p + xrow0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = *(const float*)(q + xo[e] * 4u);
+        } else if (dt == NAJU_DTYPE_BF16) {
+          const char* q = (const char*)((const bf16_t*)p + xrow0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = (float)*(const bf16_t*)(q + xo[e] * 2u);
+        } else {
+          const char* q = (const char*)((const f16_t*)p + xrow0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = (float)*(const f16_t*)(q + xo[e] * 2u);
+        }
+      };
+      ld4(a.u, x_dt, vu);
+      ld4(a.fl, g_dt, vf);
+      ld4(a.il, g_dt, vi);
+      ld4(a.dy, x_dt, vg);
+      uint32_t bo[EB];
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int rr = bn_r0 + e < rows ? bn_r0 + e : rows - 1;
+        bo[e] = (uint32_t)rr * (uint32_t)N + (uint32_t)bnc;
+      }
+      if (bn_act) {
+        if (a.bc_dt == NAJU_DTYPE_F32) {
+          const char* qb = (const char*)((const float*)a.Bm + brow0);
+          const char* qc = (const char*)((const float*)a.Cm + brow0);
+#pragma unroll
+          for (int e = 0; e < EB; ++e) vb[e] = *(const float*)(qb + bo[e] * 4u), vc[e] = *(const float*)(qc + bo[e] * 4u);
+        } else if (a.bc_dt == NAJU_DTYPE_BF16) {
+          const char* qb = (const char*)((const bf16_t*)a.Bm + brow0);
+          const char* qc = (const char*)((const bf16_t*)a.Cm + brow0);
+#pragma unroll
+          for (int e = 0; e < EB; ++e)
+            vb[e] = (float)*(const bf16_t*)(qb + bo[e] * 2u), vc[e] = (float)*(const bf16_t*)(qc + bo[e] * 2u);
+        } else {
+          const char* qb = (const char*)((const f16_t*)a.Bm + brow0);
+          const char* qc = (const char*)((const f16_t*)a.Cm + brow0);
+#pragma unroll
+          for (int e = 0; e < EB; ++e)
+            vb[e] = (float)*(const f16_t*)(qb + bo[e] * 2u), vc[e] = (float)*(const f16_t*)(qc + bo[e] * 2u);
+        }
+      }
     }
-    gn_st_bc<NP, EB>(a, t0, vb, vc, s_B, s_C);
+    float x0[PPW][S];
+    {
+      const float* ck = a.ckpt + (((int64_t)b * KC + sc) * D + dbase) * N;
+#pragma unroll
+      for (int q = 0; q < PPW; ++q) {
+        const int cq = (wv + q * kGnW) * G;  // first channel of the pass (uniform)
+        const float* ckq = ck + (int64_t)cq * N;
+#pragma unroll
+        for (int s2 = 0; s2 < S; ++s2) {
+          const int n = nl + 64 * s2;
+          const bool ok = n < N && dbase + cq + gl < D && wv + q * kGnW < NPASS;
+          x0[q][s2] = ok ? *(const float*)((const char*)ckq + ((uint32_t)gl * (uint32_t)N + (uint32_t)n) * 4u) : 0.f;
+        }
+      }
+    }
+    __syncthreads();  // the previous sub-chunk's LDS tiles are stored
+    {
+      float4 F, I, U, Y;
+      float* pF = &F.x;
+      float* pI = &I.x;
+      float* pU = &U.x;
+      float* pY = &Y.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = dl_ok && t0 + 4 * wv + e < T;
+        pF[e] = ok ? sigm(vf[e]) : 1.f;
+        pI[e] = ok ? sigm(vi[e]) : 0.f;
+        pU[e] = ok ? vu[e] : 0.f;
+        pY[e] = ok ? vg[e] : 0.f;
+        dDacc = fmaf(pY[e], pU[e], dDacc);
+      }
+      *(float4*)&s_x[0][lane][4 * wv] = F;
+      *(float4*)&s_x[1][lane][4 * wv] = I;
+      *(float4*)&s_x[2][lane][4 * wv] = U;
+      *(float4*)&s_x[3][lane][4 * wv] = Y;
+      if (bn_act) {
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+          const bool ok = t0 + bn_r0 + e < T && bn < N;
+          s_bc[0][bn][bn_r0 + e] = ok ? vb[e] : 0.f;
+          s_bc[1][bn][bn_r0 + e] = ok ? vc[e] : 0.f;
+        }
+      }
+    }
     __syncthreads();
-    if (kPrefetch && sc > sc0) load_tiles(t0 - kGnCK);  // next (earlier) sub-chunk, while this one runs
-    float ckc[PPW][S];
+
+    for (int h = 1; h >= 0; --h) {
+      const int hr0 = h * kGnH;
+      if (hr0 >= rows) continue;  // uniform over the workgroup
+      float accB[kGnH][S], accC[kGnH][S];
 #pragma unroll
-    for (int q = 0; q < PPW; ++q)
+      for (int r = 0; r < kGnH; ++r)
 #pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) ckc[q][s2] = ckn[q][s2];
-    if (sc > sc0) load_ckpt(sc - 1);
-    float accB[kGnCK][S], accC[kGnCK][S];
+        for (int s2 = 0; s2 < S; ++s2) accB[r][s2] = accC[r][s2] = 0.f;
 #pragma unroll
-    for (int r = 0; r < kGnCK; ++r)
-#pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) accB[r][s2] = accC[r][s2] = 0.f;
-#pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      const int pass = wv + q * kGnW;
-      if (pass >= NPASS) break;
-      const int c = pass * G + gl;
-      const int64_t d = dbase + c;
-      const float Dv = d < D ? a.Dsk[d] : 0.f;
-      float x0[S], hist[kGnCK][S];
-#pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) x0[s2] = ckc[q][s2];
-      {
+      for (int q = 0; q < PPW; ++q) {
+        const int pass = wv + q * kGnW;
+        if (pass >= NPASS) break;
+        // passes are independent: keep the scheduler from interleaving them
+        // (their live registers would add up)
+        __builtin_amdgcn_sched_barrier(0);
+        const int c = pass * G + gl;
         float xs[S];
 #pragma unroll
-        for (int s2 = 0; s2 < S; ++s2) xs[s2] = x0[s2];
+        for (int s2 = 0; s2 < S; ++s2) xs[s2] = x0[q][s2];
+        // forward states: rows [0, hr0) unstored, then the half's rows
+        for (int r4 = 0; r4 < hr0; r4 += 4) {
+          const float4 f4 = *(const float4*)&s_x[0][c][r4], i4 = *(const float4*)&s_x[1][c][r4];
+          const float4 u4 = *(const float4*)&s_x[2][c][r4];
+          float4 B4[S];
 #pragma unroll
-        for (int r = 0; r < kGnCK; ++r) {
-          if (r < rows) {
-            const float f = s_f[r][c], iu = s_i[r][c] * s_u[r][c];
+          for (int s2 = 0; s2 < S; ++s2) B4[s2] = *(const float4*)&s_bc[0][nl + 64 * s2][r4];
+          const float* pf = &f4.x;
+          const float* pi = &i4.x;
+          const float* pu = &u4.x;
 #pragma unroll
-            for (int s2 = 0; s2 < S; ++s2) xs[s2] = fmaf(f, xs[s2], iu * s_B[r][nl + 64 * s2]);
+          for (int e = 0; e < 4; ++e) {
+            const float iu = pi[e] * pu[e];
+#pragma unroll
+            for (int s2 = 0; s2 < S; ++s2) xs[s2] = fmaf(pf[e], xs[s2], iu * (&B4[s2].x)[e]);
           }
+        }
+        float xin[S], hist[kGnH][S];
 #pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) hist[r][s2] = xs[s2];
+        for (int s2 = 0; s2 < S; ++s2) xin[s2] = xs[s2];
+        // The LDS reads of each 4-row block are issued right before the
+        // block (scheduling fences): hoisting all of a half's reads would
+        // hold 16 rows of operands in registers at once.
+#pragma unroll
+        for (int r4 = 0; r4 < kGnH; r4 += 4) {
+          __builtin_amdgcn_sched_barrier(0);
+          const int r = hr0 + r4;
+          const float4 f4 = *(const float4*)&s_x[0][c][r], i4 = *(const float4*)&s_x[1][c][r];
+          const float4 u4 = *(const float4*)&s_x[2][c][r];
+          float4 B4[S];
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) B4[s2] = *(const float4*)&s_bc[0][nl + 64 * s2][r];
+          const float* pf = &f4.x;
+          const float* pi = &i4.x;
+          const float* pu = &u4.x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float iu = pi[e] * pu[e];
+#pragma unroll
+            for (int s2 = 0; s2 < S; ++s2) {
+              xs[s2] = fmaf(pf[e], xs[s2], iu * (&B4[s2].x)[e]);
+              hist[r4 + e][s2] = xs[s2];
+            }
+          }
+        }
+        // adjoint over the half's rows, last first, reduced every kGnRG rows.
+        // The memory clobber makes it read its operands from LDS again
+        // instead of keeping the recompute's 16 rows of them in registers.
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int grp = kGnH / kGnRG - 1; grp >= 0; --grp) {
+          float v[2 * kGnRG];  // [0, kGnRG): dfl terms, [kGnRG, 2 kGnRG): dws terms
+#pragma unroll
+          for (int r4 = kGnRG - 4; r4 >= 0; r4 -= 4) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int lr = grp * kGnRG + r4;  // local row of the half
+            const int r = hr0 + lr;
+            const float4 f4 = *(const float4*)&s_x[0][c][r], i4 = *(const float4*)&s_x[1][c][r];
+            const float4 u4 = *(const float4*)&s_x[2][c][r], y4 = *(const float4*)&s_x[3][c][r];
+            float4 B4[S], C4[S];
+#pragma unroll
+            for (int s2 = 0; s2 < S; ++s2) {
+              B4[s2] = *(const float4*)&s_bc[0][nl + 64 * s2][r];
+              C4[s2] = *(const float4*)&s_bc[1][nl + 64 * s2][r];
+            }
+            const float* pf = &f4.x;
+            const float* pi = &i4.x;
+            const float* pu = &u4.x;
+            const float* py = &y4.x;
+#pragma unroll
+            for (int e = 3; e >= 0; --e) {
+              const int j = r4 + e;  // row within the group
+              const float iu = pi[e] * pu[e], gy = py[e];
+              float tf = 0.f, tw = 0.f;
+#pragma unroll
+              for (int s2 = 0; s2 < S; ++s2) {
+                const float xprev = lr + e > 0 ? hist[lr + e - 1][s2] : xin[s2];
+                const float xb = fmaf(gy, (&C4[s2].x)[e], gc[q][s2]);
+                tf = fmaf(xb, xprev, tf);
+                tw = fmaf(xb, (&B4[s2].x)[e], tw);
+                accB[lr + e][s2] = fmaf(xb, iu, accB[lr + e][s2]);
+                accC[lr + e][s2] = fmaf(gy, hist[lr + e][s2], accC[lr + e][s2]);
+                // keep the updates here: sunk to the end of the pass they
+                // would hold every row's operands in registers
+                asm volatile("" : "+v"(accB[lr + e][s2]), "+v"(accC[lr + e][s2]));
+                gc[q][s2] = pf[e] * xb;
+              }
+              v[j] = tf;
+              v[kGnRG + j] = tw;
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          trd_step<LG, 2 * kGnRG, 2 * kGnRG>(v, lane);
+          // lanes holding dfl sums (the lower half of the group) take the
+          // matching dws sums from the upper half and write the outputs over
+          // the consumed f, i, u of their rows
+          constexpr int KF = 2 * kGnRG >= LG ? 2 * kGnRG / LG : 1;
+          constexpr int SPREAD = 2 * kGnRG >= LG ? 1 : LG / (2 * kGnRG);
+          float vw[KF];
+#pragma unroll
+          for (int j = 0; j < KF; ++j) vw[j] = from_upper<LG / 2>(v[j]);
+          if (nl < LG / 2 && nl % SPREAD == 0) {
+            const int e0 = (nl / SPREAD) * KF;
+#pragma unroll
+            for (int j = 0; j < KF; ++j) {
+              const int r = hr0 + grp * kGnRG + e0 + j;
+              const float f = s_x[0][c][r], ig = s_x[1][c][r], uu = s_x[2][c][r], gy = s_x[3][c][r];
+              s_x[1][c][r] = fmaf(ig, vw[j], s_Dsk[c] * gy);     // du
+              s_x[0][c][r] = fmaf(-f, f, f) * v[j];              // dfl
+              s_x[2][c][r] = fmaf(-ig, ig, ig) * (vw[j] * uu);   // dil
+            }
+          }
         }
       }
-      // adjoint recurrence row by row (reverse), with this lane's terms of
-      // v[r] = sum_n x̄_t x_{t-1} (dfl) and v[kGnCK + r] = sum_n x̄_t B_t (dws)
-      float v[2 * kGnCK];
+      // dB / dC partials of the half's rows: over the channel groups of this
+      // wave, then over the waves in wave order
+      if constexpr (G > 1) {
 #pragma unroll
-      for (int r = kGnCK - 1; r >= 0; --r) {
-        v[r] = v[kGnCK + r] = 0.f;
-        if (r < rows) {
-          const float f = s_f[r][c], iu = s_i[r][c] * s_u[r][c], gy = s_dy[r][c];
+        for (int r = 0; r < kGnH; ++r)
 #pragma unroll
           for (int s2 = 0; s2 < S; ++s2) {
-            const int n = nl + 64 * s2;
-            const float xprev = r > 0 ? hist[r - 1][s2] : x0[s2];
-            const float xb = fmaf(gy, s_C[r][n], gc[q][s2]);
-            v[r] = fmaf(xb, xprev, v[r]);
-            v[kGnCK + r] = fmaf(xb, s_B[r][n], v[kGnCK + r]);
-            accB[r][s2] = fmaf(xb, iu, accB[r][s2]);
-            accC[r][s2] = fmaf(gy, hist[r][s2], accC[r][s2]);
-            gc[q][s2] = f * xb;
+#pragma unroll
+            for (int m = 32; m >= LG; m >>= 1) {
+              accB[r][s2] += __shfl_xor(accB[r][s2], m, 64);
+              accC[r][s2] += __shfl_xor(accC[r][s2], m, 64);
+            }
           }
-        }
       }
-      // sums over the channel group's lanes; lane l < LG/2 of the group then
-      // owns rows [l*K2, l*K2 + K2): its dfl sums are in v, the dws sums come
-      // from lane l + LG/2
-      constexpr int K2 = 2 * kGnCK / LG;
-      tr_reduce<LG, 2 * kGnCK>(v, lane);
-      float vw[K2];
+      for (int w = 0; w < kGnW; ++w) {
+        if (wv == w && gl == 0) {
 #pragma unroll
-      for (int j = 0; j < K2; ++j) vw[j] = __shfl_xor(v[j], LG / 2, 64);
-      if (nl < LG / 2) {
+          for (int r = 0; r < kGnH; ++r)
 #pragma unroll
-        for (int j = 0; j < K2; ++j) {
-          const int r = nl * K2 + j;
-          if (r < rows) {
-            const float f = s_f[r][c], ig = s_i[r][c], uu = s_u[r][c], gy = s_dy[r][c];
-            s_o0[r][c] = fmaf(ig, vw[j], Dv * gy);            // du
-            s_o1[r][c] = fmaf(-f, f, f) * v[j];               // dfl
-            s_o2[r][c] = fmaf(-ig, ig, ig) * (vw[j] * uu);    // dil
-            dDs[q] = fmaf(gy, uu, dDs[q]);
-          }
+            for (int s2 = 0; s2 < S; ++s2) {
+              const int n = nl + 64 * s2;
+              s_pB[hr0 + r][n] = (w == 0 ? 0.f : s_pB[hr0 + r][n]) + accB[r][s2];
+              s_pC[hr0 + r][n] = (w == 0 ? 0.f : s_pC[hr0 + r][n]) + accC[r][s2];
+            }
+        }
+        __syncthreads();
+      }
+    }
+    // stores: dB / dC partials, then du / dfl / dil (channel lane, rows
+    // 4*wv .. 4*wv+3, one 16-byte LDS read per stream)
+    {
+      float* pB = a.partB ? a.partB + (int64_t)dtile * btn + brow0 : nullptr;
+      float* pC = a.partC ? a.partC + (int64_t)dtile * btn + brow0 : nullptr;
+      for (int e = tid; e < kGnCK * NP; e += kGnThreads) {
+        const int r = e / NP, n = e - r * NP;
+        if (r < rows && n < N) {
+          const uint32_t o = ((uint32_t)r * (uint32_t)N + (uint32_t)n) * 4u;
+          if (pB) *(float*)((char*)pB + o) = s_pB[r][n];
+          if (pC) *(float*)((char*)pC + o) = s_pC[r][n];
         }
       }
     }
-    // dB/dC partials: sum over the channel groups of this wave, then over the
-    // waves in wave order.
+    if (dl_ok) {
+      const float4 o0 = *(const float4*)&s_x[1][lane][4 * wv];
+      const float4 o1 = *(const float4*)&s_x[0][lane][4 * wv];
+      const float4 o2 = *(const float4*)&s_x[2][lane][4 * wv];
+      auto st4 = [&](void* p, int dt, const float4& v) {
+        if (!p) return;
 #pragma unroll
-    for (int r = 0; r < kGnCK; ++r)
-#pragma unroll
-      for (int s2 = 0; s2 < S; ++s2) {
-#pragma unroll
-        for (int m = 32; m >= LG; m >>= 1) {
-          accB[r][s2] += __shfl_xor(accB[r][s2], m, 64);
-          accC[r][s2] += __shfl_xor(accC[r][s2], m, 64);
-        }
-      }
-    for (int w = 0; w < kGnW; ++w) {
-      if (wv == w && gl == 0) {
-#pragma unroll
-        for (int r = 0; r < kGnCK; ++r)
-#pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) {
-            const int n = nl + 64 * s2;
-            s_pB[r][n] = (w == 0 ? 0.f : s_pB[r][n]) + accB[r][s2];
-            s_pC[r][n] = (w == 0 ? 0.f : s_pC[r][n]) + accC[r][s2];
+        for (int e = 0; e < 4; ++e) {
+          if (4 * wv + e < rows) {
+            uint32_t o = (uint32_t)(4 * wv + e) * (uint32_t)D + (uint32_t)lane;
+            // computed here: addresses hoisted to the top of the sub-chunk
+            // would occupy registers through the whole scan
+            asm volatile("" : "+v"(o));
+            const float x = (&v.x)[e];
+            if (dt == NAJU_DTYPE_F32)
+              *(float*)((char*)((float*)p + xrow0) + o * 4u) = x;
+            else if (dt == NAJU_DTYPE_BF16)
+              *(bf16_t*)((char*)((bf16_t*)p + xrow0) + o * 2u) = (bf16_t)x;
+            else
+              *(f16_t*)((char*)((f16_t*)p + xrow0) + o * 2u) = (f16_t)x;
           }
-      }
-      __syncthreads();
-    }
-    for (int e = threadIdx.x; e < kGnCK * NP; e += 64 * kGnW) {
-      const int r = e / NP, n = e - r * NP;
-      const int64_t t = t0 + r;
-      if (t < T && n < N) {
-        const int64_t i = ((int64_t)b * T + t) * N + n;
-        if (a.partB) a.partB[(int64_t)dtile * btn + i] = s_pB[r][n];
-        if (a.partC) a.partC[(int64_t)dtile * btn + i] = s_pC[r][n];
-      }
-    }
-    for (int e = threadIdx.x; e < kGnCK * kGnDT; e += 64 * kGnW) {
-      const int r = e / kGnDT, c = e - r * kGnDT;
-      const int64_t t = t0 + r, d = dbase + c;
-      if (t < T && d < D) {
-        const int64_t o = ((int64_t)b * T + t) * D + d;
-        if (a.du) st_any(a.du, du_dt, o, s_o0[r][c]);
-        if (a.dfl) st_any(a.dfl, dg_dt, o, s_o1[r][c]);
-        if (a.dil) st_any(a.dil, dg_dt, o, s_o2[r][c]);
-      }
+        }
+      };
+      st4(a.du, du_dt, o0);
+      st4(a.dfl, dg_dt, o1);
+      st4(a.dil, dg_dt, o2);
     }
   }
 #pragma unroll
@@ -1500,8 +1750,15 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
         if (n < N) a.dh0[((int64_t)b * D + d) * N + n] = gc[q][s2];
       }
     }
-    const float dd = group_sum<LG>(dDs[q]);
-    if (a.partD && nl == 0) a.partD[((int64_t)b * a.nseg + seg) * D + d] = dd;
+  }
+  // dD = sum dy * u over this segment's rows, in wave order
+  s_dD[wv][lane] = dDacc;
+  __syncthreads();
+  if (tid < kGnDT && dbase + tid < D && a.partD) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGnW; ++w) s += s_dD[w][tid];
+    a.partD[((int64_t)b * a.nseg + seg) * D + dbase + tid] = s;
   }
 }
 
