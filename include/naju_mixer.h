@@ -2,7 +2,8 @@
  * naju_mixer.h -- C ABI of the MI355X (gfx950) kernels around the Naju scan
  * inside the mixer: the depthwise causal convolutions of the content branch
  * and of the gate logits (reference /root/reference/naju/mixer.py:75-76,
- * 97-99, 106-110, 115).
+ * 97-99, 106-110, 115), and the readout epilogue after the scan
+ * (mixer.py:123-124).
  *
  *   y[b,t,c] = act( add[b,t,c] + bias[c] + sum_{j<K} w[c,j] * x[b, t-(K-1)+j, c] )
  *
@@ -54,6 +55,28 @@ size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K);
 int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
                     float* dw, float* dbias, int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype,
                     int dy_dtype, int dx_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Readout epilogue of the mixer (naju/mixer.py:123-124), one pass:
+ *
+ *   y[r,c] = (cx[r,c] * scale + Dv[c] * h[r,c]) * SiLU(z[r,c])
+ *
+ * over rows r < n_rows (= batch * T) and channels c < C. cx, h, y are
+ * [n_rows, C] contiguous; z has z_ld >= C elements between rows (the second
+ * half of the in_proj output [x, z] goes in without a copy); Dv is [C] f32. */
+int naju_readout_fwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
+                     void* y, int64_t n_rows, int64_t C, int cx_dtype, int h_dtype, int z_dtype, int y_dtype,
+                     void* stream);
+
+/* Bytes of workspace naju_readout_bwd needs for the dD partial sums. */
+size_t naju_readout_workspace_bytes(int64_t n_rows, int64_t C);
+
+/* Backward of naju_readout_fwd: dcx, dh, dz (each [n_rows, C] contiguous,
+ * in the given dtypes) and dD [C] f32 (summed over rows in a fixed order),
+ * each nullable to skip it. */
+int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
+                     const void* dy, void* dcx, void* dh, void* dz, float* dD, int64_t n_rows, int64_t C,
+                     int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype, int dz_dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

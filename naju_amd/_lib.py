@@ -25,6 +25,9 @@ EXPORTED = (
     "naju_dwconv_fwd",
     "naju_dwconv_workspace_bytes",
     "naju_dwconv_bwd",
+    "naju_readout_fwd",
+    "naju_readout_workspace_bytes",
+    "naju_readout_bwd",
 )
 
 _lib = None
@@ -77,6 +80,15 @@ def lib():
     # x, x_ld, w, bias, dy, dx, dw, dbias, batch, T, C, K, act, x_dt, dy_dt, dx_dt, ws, ws_bytes, stream
     L.naju_dwconv_bwd.argtypes = [P, I64] + [P] * 6 + [I64] * 3 + [I] * 5 + [P, SZ, P]
     L.naju_dwconv_bwd.restype = I
+    F = ctypes.c_float
+    # cx, h, z, z_ld, Dv, scale, y, n_rows, C, cx_dt, h_dt, z_dt, y_dt, stream
+    L.naju_readout_fwd.argtypes = [P, P, P, I64, P, F, P, I64, I64] + [I] * 4 + [P]
+    L.naju_readout_fwd.restype = I
+    L.naju_readout_workspace_bytes.argtypes = [I64, I64]
+    L.naju_readout_workspace_bytes.restype = SZ
+    # cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz, dD, n_rows, C, 7 dtypes, ws, ws_bytes, stream
+    L.naju_readout_bwd.argtypes = [P, P, P, I64, P, F] + [P] * 5 + [I64, I64] + [I] * 7 + [P, SZ, P]
+    L.naju_readout_bwd.restype = I
     _lib = L
     return _lib
 

@@ -166,6 +166,61 @@ __global__ void dwconv_fold_kernel(const float* part, int64_t nblk, int64_t C, i
   }
 }
 
+// ---------------------------------------------------------- readout epilogue
+//
+// y = (cx * scale + Dv * h) * SiLU(z), one thread per channel over a block of
+// kRows rows (grid: channel blocks x row blocks). The backward writes dcx,
+// dh, dz and a per-row-block partial of dD = sum_r dy * SiLU(z) * h, folded
+// in block order by dwconv_fold_kernel (K = 0).
+__global__ __launch_bounds__(kThreads) void readout_fwd_kernel(const void* cx, const void* h, const void* z,
+                                                              int64_t z_ld, const float* Dv, float scale, void* y,
+                                                              int64_t n_rows, int64_t C, int cx_dt, int h_dt,
+                                                              int z_dt, int y_dt) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kRows;
+  const int64_t r1 = r0 + kRows < n_rows ? r0 + kRows : n_rows;
+  const float dv = Dv[c];
+#pragma unroll 4
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t o = r * C + c;
+    const float zz = ldv(z, z_dt, r * z_ld + c);
+    const float a = fmaf(ldv(cx, cx_dt, o), scale, dv * ldv(h, h_dt, o));
+    stv(y, y_dt, o, a * silu(zz));
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, const void* h, const void* z,
+                                                              int64_t z_ld, const float* Dv, float scale,
+                                                              const void* dy, void* dcx, void* dh, void* dz,
+                                                              float* part, int64_t n_rows, int64_t C, int cx_dt,
+                                                              int h_dt, int z_dt, int dy_dt, int dcx_dt, int dh_dt,
+                                                              int dz_dt) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kRows;
+  const int64_t r1 = r0 + kRows < n_rows ? r0 + kRows : n_rows;
+  const float dv = Dv[c];
+  float dd = 0.f;
+#pragma unroll 4
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t o = r * C + c;
+    const float zz = ldv(z, z_dt, r * z_ld + c);
+    const float hh = ldv(h, h_dt, o);
+    const float g = ldv(dy, dy_dt, o);
+    const float sg = 1.f / (1.f + __expf(-zz));
+    const float gs = g * (zz * sg);  // dy * SiLU(z)
+    if (dcx) stv(dcx, dcx_dt, o, gs * scale);
+    if (dh) stv(dh, dh_dt, o, gs * dv);
+    dd = fmaf(gs, hh, dd);
+    if (dz) {
+      const float a = fmaf(ldv(cx, cx_dt, o), scale, dv * hh);
+      stv(dz, dz_dt, o, g * a * sg * fmaf(zz, 1.f - sg, 1.f));
+    }
+  }
+  if (part) part[(int64_t)blockIdx.y * C + c] = dd;
+}
+
 thread_local char g_err[256] = "";
 
 int fail(int code, const char* fmt, ...) {
@@ -183,7 +238,8 @@ int check(int64_t batch, int64_t T, int64_t C, int K, int act, int64_t x_ld) {
   if (x_ld < C) return fail(NAJU_ERR_INVALID, "x_ld (%lld) must be >= C (%lld)", (long long)x_ld, (long long)C);
   if (K < 1 || K > kMaxK) return fail(NAJU_ERR_UNSUPPORTED, "kernel size K must be in [1, %d], got %d", kMaxK, K);
   if (act != 0 && act != 1) return fail(NAJU_ERR_INVALID, "act must be 0 (identity) or 1 (SiLU)");
-  if (batch > 65535 || T > (1ll << 31) || C > (1ll << 30)) return fail(NAJU_ERR_UNSUPPORTED, "shape too large");
+  if (batch > 65535 || (T + kRows - 1) / kRows > 65535 || C > (1ll << 30))
+    return fail(NAJU_ERR_UNSUPPORTED, "shape too large (batch <= 65535, T <= %d)", 65535 * kRows);
   return NAJU_OK;
 }
 
@@ -293,6 +349,73 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
     hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part,
                        batch * n_tblocks(T), C, K, dw, dbias);
   }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+int naju_readout_fwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
+                     void* y, int64_t n_rows, int64_t C, int cx_dtype, int h_dtype, int z_dtype, int y_dtype,
+                     void* stream) {
+  g_err[0] = 0;
+  if (n_rows < 0 || C < 0) return fail(NAJU_ERR_INVALID, "negative shape");
+  if (z_ld < C) return fail(NAJU_ERR_INVALID, "z_ld (%lld) must be >= C (%lld)", (long long)z_ld, (long long)C);
+  if (!dt_ok(cx_dtype) || !dt_ok(h_dtype) || !dt_ok(z_dtype) || !dt_ok(y_dtype))
+    return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if ((n_rows + kRows - 1) / kRows > 65535 || C > (1ll << 30))
+    return fail(NAJU_ERR_UNSUPPORTED, "shape too large (at most %d rows)", 65535 * kRows);
+  if (n_rows == 0 || C == 0) return NAJU_OK;
+  if (!cx || !h || !z || !Dv || !y) return fail(NAJU_ERR_INVALID, "null pointer (cx, h, z, Dv and y are required)");
+  const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)((n_rows + kRows - 1) / kRows));
+  hipLaunchKernelGGL(readout_fwd_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, cx, h, z, z_ld, Dv, scale, y,
+                     n_rows, C, cx_dtype, h_dtype, z_dtype, y_dtype);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+size_t naju_readout_workspace_bytes(int64_t n_rows, int64_t C) {
+  if (n_rows < 0 || C < 0) return 0;
+  return (size_t)((n_rows + kRows - 1) / kRows) * C * sizeof(float) + 256;
+}
+
+int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
+                     const void* dy, void* dcx, void* dh, void* dz, float* dD, int64_t n_rows, int64_t C,
+                     int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype, int dz_dtype,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (n_rows < 0 || C < 0) return fail(NAJU_ERR_INVALID, "negative shape");
+  if (z_ld < C) return fail(NAJU_ERR_INVALID, "z_ld (%lld) must be >= C (%lld)", (long long)z_ld, (long long)C);
+  if (!dt_ok(cx_dtype) || !dt_ok(h_dtype) || !dt_ok(z_dtype) || !dt_ok(dy_dtype) || !dt_ok(dcx_dtype) ||
+      !dt_ok(dh_dtype) || !dt_ok(dz_dtype))
+    return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if ((n_rows + kRows - 1) / kRows > 65535 || C > (1ll << 30))
+    return fail(NAJU_ERR_UNSUPPORTED, "shape too large (at most %d rows)", 65535 * kRows);
+  hipStream_t st = (hipStream_t)stream;
+  if (C == 0) return NAJU_OK;
+  const int64_t nblk = (n_rows + kRows - 1) / kRows;
+  if (n_rows == 0) {
+    if (dD) {
+      hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, st, nullptr,
+                         (int64_t)0, C, 0, nullptr, dD);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+    }
+    return NAJU_OK;
+  }
+  if (!h || !z || !Dv || !dy) return fail(NAJU_ERR_INVALID, "null pointer (h, z, Dv and dy are required)");
+  if (dz && !cx) return fail(NAJU_ERR_INVALID, "cx is required for dz");
+  const size_t need = naju_readout_workspace_bytes(n_rows, C);
+  if (dD && (!workspace || workspace_bytes < need))
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  float* part = dD ? (float*)workspace : nullptr;
+  const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)nblk);
+  hipLaunchKernelGGL(readout_bwd_kernel, grid, dim3(kThreads), 0, st, cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz,
+                     part, n_rows, C, cx_dtype, h_dtype, z_dtype, dy_dtype, dcx_dtype, dh_dtype, dz_dtype);
+  if (dD)
+    hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, st, part, nblk, C, 0,
+                       nullptr, dD);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return NAJU_OK;

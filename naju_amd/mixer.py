@@ -32,6 +32,7 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from naju_amd.dwconv import dwconv
+from naju_amd.readout import readout
 from naju_amd.scan import naju_scan
 
 
@@ -139,7 +140,12 @@ class NajuMixer(nn.Module):
         i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)
         # the scan reads out the state only; the D skip is applied here
         cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
-        y = (cx * self._cx_scale + self.D * h) * F.silu(z)
+        if h.is_cuda:
+            # one kernel each way; the output takes the autocast dtype the
+            # out_proj GEMM consumes
+            y = readout(cx, h, z, self.D, self._cx_scale, out_dtype=_out_dtype(h))
+        else:
+            y = (cx * self._cx_scale + self.D * h) * F.silu(z)
         return self.out_proj(y)
 
 

@@ -23,14 +23,14 @@ def header_functions():
     names = set()
     for h in HEADERS:
         txt = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer)_\w+)\s*\(", txt))
+        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer|readout)_\w+)\s*\(", txt))
     return sorted(names)
 
 
 def test_library_exports_every_header_symbol():
     lib = _lib.lib()
     names = header_functions()
-    assert len(names) >= 11
+    assert len(names) >= 14
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     assert set(names) == set(_lib.EXPORTED)
@@ -236,3 +236,30 @@ def test_dwconv_python_rejects_cpu_tensors():
     from naju_amd.dwconv import dwconv
     with pytest.raises(RuntimeError, match="CUDA"):
         dwconv(torch.zeros(1, 4, 4), torch.zeros(4, 1, 4))
+
+
+def test_readout_host_checks():
+    L = _lib.lib()
+    fake = 0x1000
+    def fwd(z_ld=16, dts=(F32, F32, F32, F32), rows=4, C=16, y=fake):
+        return L.naju_readout_fwd(fake, fake, fake, z_ld, fake, 0.125, y, rows, C, *dts, None)
+    assert fwd(z_ld=15) == _lib.ERR_INVALID and b"z_ld" in L.naju_mixer_last_error()
+    assert fwd(dts=(F32, F32, 9, F32)) == _lib.ERR_INVALID
+    assert fwd(rows=-1) == _lib.ERR_INVALID
+    assert fwd(rows=64 * 65535 + 1) == _lib.ERR_UNSUPPORTED
+    assert fwd(y=None) == _lib.ERR_INVALID
+    assert fwd(rows=0) == _lib.OK and L.naju_mixer_last_error() == b""
+    assert L.naju_readout_workspace_bytes(16384, 1536) >= 256 * 1536 * 4
+    rc = L.naju_readout_bwd(fake, fake, fake, 16, fake, 0.125, fake, None, None, None, fake, 4, 16,
+                            *([F32] * 7), None, 0, None)
+    assert rc == _lib.ERR_WORKSPACE
+    rc = L.naju_readout_bwd(None, fake, fake, 16, fake, 0.125, fake, None, None, fake, None, 4, 16,
+                            *([F32] * 7), None, 0, None)
+    assert rc == _lib.ERR_INVALID and b"cx" in L.naju_mixer_last_error()
+
+
+def test_readout_python_rejects_cpu_tensors():
+    from naju_amd.readout import readout
+    x = torch.zeros(1, 2, 4)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        readout(x, x, x, torch.zeros(4), 0.5)

@@ -63,7 +63,7 @@ def test_lm_bf16_autocast_hip_matches_oracle(gpu):
             logits = m(ids)
             loss = torch.nn.functional.cross_entropy(logits[:, :-1].float().reshape(-1, V), ids[:, 1:].reshape(-1))
         loss.backward()
-        losses.append(float(loss))
+        losses.append(float(loss.detach()))
     assert abs(losses[0] - losses[1]) < 1e-3 * abs(losses[1])
     for (n, pa), pb in zip(ma.named_parameters(), mb.parameters()):
         assert _rel(pa.grad, pb.grad) < 3e-2, n
@@ -86,5 +86,5 @@ def test_lm_train_step_reduces_loss(gpu):
         loss.backward()
         torch.nn.utils.clip_grad_norm_(lm.parameters(), 1.0)
         opt.step()
-        first = float(loss) if first is None else first
+        first = float(loss.detach()) if first is None else first
     assert float(loss) < first - 0.1
