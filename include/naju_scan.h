@@ -21,10 +21,18 @@
  * covers f_logit, i_logit, dfl and dil; the bc dtype covers B, C, dB and dC.
  * Supported: u in {F32, BF16, F16}; gate and bc each either F32 or equal to
  * the u dtype. Arithmetic and the state are float32 throughout.
- * out_f32 = 0: every output has its input's dtype (y and du: u dtype; dfl,
- * dil: gate dtype; dB, dC: bc dtype). out_f32 = 1: y, du, dfl, dil, dB and dC
- * are all float32 (bf16 storage rounding alone is up to 2^-8 relative, so
- * this is the form in which the kernels' own accuracy is measured).
+ * flags (bit set, 0 = defaults):
+ *   NAJU_FLAG_OUT_F32 (1): y, du, dfl, dil, dB and dC are all float32 instead
+ *     of their inputs' dtypes (y and du: u dtype; dfl, dil: gate dtype; dB,
+ *     dC: bc dtype). bf16 storage rounding alone is up to 2^-8 relative, so
+ *     this is the form in which the kernels' own accuracy is measured.
+ *   NAJU_FLAG_DETERMINISTIC (2): run-to-run bitwise identical results. At
+ *     N = 1 each chunk then takes its carry from its immediate predecessor's
+ *     inclusive carry only (a fixed composition order; the carries travel
+ *     along the chunks one hop at a time, which is slower). Without it, a
+ *     chunk composes whichever predecessors' maps are ready first, so N = 1
+ *     results repeat to float32 rounding only. N > 1 is always bitwise
+ *     deterministic.
  *
  * Workspace: naju_scan_workspace_bytes() bytes of device memory that MUST be
  * zero-filled once before its first use; every call leaves it reusable
@@ -49,6 +57,9 @@ extern "C" {
 #define NAJU_DTYPE_F32 0
 #define NAJU_DTYPE_BF16 1
 #define NAJU_DTYPE_F16 2
+
+#define NAJU_FLAG_OUT_F32 1
+#define NAJU_FLAG_DETERMINISTIC 2
 
 #define NAJU_OK 0
 #define NAJU_ERR_INVALID -1     /* bad pointer, shape or dtype code        */
@@ -81,7 +92,7 @@ size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D,
  * (naju/chunk_affine_triton.py:257-288) and naju_fwd / naju_fwd_chunked
  * (naju/cuda/naju_cuda.cu:241-259, :211-238).
  *   h0   : optional initial state (NULL = zeros, the reference behaviour)
- *   y    : output, u dtype (float32 when out_f32)
+ *   y    : output, u dtype (float32 with NAJU_FLAG_OUT_F32)
  *   ckpt : optional (NULL under no_grad); state checkpoint for the backward
  *   hT   : optional final state x_{T-1}
  */
@@ -89,7 +100,7 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit,
                   const void* B, const void* C, const float* D_skip,
                   const float* h0, void* y, float* ckpt, float* hT,
                   int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, int out_f32, void* workspace,
+                  int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream);
 
 /* Fused backward scan. Replaces naju_bwd (naju/cuda/naju_cuda.cu:261-286),
@@ -107,7 +118,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   const float* ckpt, const void* dy, void* du, void* dfl,
                   void* dil, void* dB, void* dC, float* dD, float* dh0,
                   int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, int out_f32, void* workspace,
+                  int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream);
 
 /* Reads the workspace's device-side status word (synchronises `stream`).

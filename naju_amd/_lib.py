@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnaju_sca
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = 0, -1, -2, -3, -4
+FLAG_OUT_F32, FLAG_DETERMINISTIC = 1, 2
 
 EXPORTED = (
     "naju_scan_version",
@@ -60,11 +61,11 @@ def lib():
     L.naju_scan_ckpt_elems.restype = I64
     L.naju_scan_workspace_bytes.argtypes = [I64] * 4 + [I] * 3
     L.naju_scan_workspace_bytes.restype = SZ
-    # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, out_f32, ws, ws_bytes,
+    # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, flags, ws, ws_bytes,
     # stream
     L.naju_scan_fwd.argtypes = [P] * 10 + [I64] * 4 + [I] * 4 + [P, SZ, P]
     L.naju_scan_fwd.restype = I
-    # u, fl, il, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N, dts, out_f32, ws,
+    # u, fl, il, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N, dts, flags, ws,
     # ws_bytes, stream
     L.naju_scan_bwd.argtypes = [P] * 15 + [I64] * 4 + [I] * 4 + [P, SZ, P]
     L.naju_scan_bwd.restype = I

@@ -223,6 +223,7 @@ struct ScanArgs {
   int ck_rows;  // N = 1 forward: rows per checkpoint interval (the backward's chunk length)
   int Kc;       // N = 1 forward: number of checkpoint intervals
   uint32_t tag;  // this launch's tag (nonzero, new for every launch)
+  int strict;    // N = 1: take carries from the immediate predecessor's inclusive carry only
 };
 
 // Workgroup blockIdx.x serves tile blockIdx.x % n_tiles; the chunk comes from
@@ -336,7 +337,9 @@ __device__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, 
           done = 1;
           break;
         }
-        if (st != 1) break;
+        // strict: never compose aggregates, wait for the predecessor's
+        // inclusive carry (a fixed composition order)
+        if (st != 1 || a.strict) break;
 #pragma unroll
         for (int j = 0; j < V; ++j) {
           aZ[j] = fmaf(aF[j], sh.Z[slot][j * 64 + lane], aZ[j]);
@@ -2059,11 +2062,13 @@ size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D, int64_t N,
 
 int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                   const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch, int64_t T,
-                  int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int out_f32, void* workspace,
+                  int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
+  if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC)) return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || D == 0) return NAJU_OK;
   if (T == 0) {
@@ -2128,6 +2133,7 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
     return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                 l.n_tiles);
   a.tag = next_tag();
+  a.strict = (flags & NAJU_FLAG_DETERMINISTIC) != 0;
   a.ck_rows = kBChunk;
   a.Kc = (int)((T + kBChunk - 1) / kBChunk);
   kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, false);
@@ -2137,11 +2143,13 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
 int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                   const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil, void* dB,
                   void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, int out_f32, void* workspace, size_t workspace_bytes,
+                  int gate_dtype, int bc_dtype, int flags, void* workspace, size_t workspace_bytes,
                   void* stream) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
+  if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC)) return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || T == 0 || D == 0) {
     // Gradients of an empty scan: the reductions over the empty axes are 0.
@@ -2217,6 +2225,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
       return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                   l.n_tiles);
     a.tag = next_tag();
+    a.strict = (flags & NAJU_FLAG_DETERMINISTIC) != 0;
     kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, true);
     rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
     if (rc) return rc;

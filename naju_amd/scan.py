@@ -58,6 +58,13 @@ class _Workspace:
 _WS = _Workspace()
 
 
+def _flags():
+    """NAJU_FLAG_DETERMINISTIC when torch's deterministic mode is on
+    (torch.use_deterministic_algorithms(True)): bitwise repeatable N = 1
+    carries, at a cost in speed."""
+    return _lib.FLAG_DETERMINISTIC if torch.are_deterministic_algorithms_enabled() else 0
+
+
 def _stream_handle(device):
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -126,7 +133,7 @@ class NajuScanHip(torch.autograd.Function):
         y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
         _lib.check(L.naju_scan_fwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
-            _ptr(y), _ptr(ckpt), None, Bsz, T, D, N, *dts, 0, ws.data_ptr(), ws.numel(), stream))
+            _ptr(y), _ptr(ckpt), None, Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
         if need_grad:
             ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
             ctx.meta = (Bsz, T, D, N, dts, h0 is not None,
@@ -154,7 +161,7 @@ class NajuScanHip(torch.autograd.Function):
         _lib.check(L.naju_scan_bwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
             _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
-            Bsz, T, D, N, *dts, 0, ws.data_ptr(), ws.numel(), stream))
+            Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
         grads = [du, dfl, dil, dB, dC, dD]
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
         return (*grads, dh0)

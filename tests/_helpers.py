@@ -100,9 +100,10 @@ def check_all(y, grads, ref_y, ref_g, skip=()):
 _DTC = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
 
-def run_abi(ins, device, out_f32=True):
+def run_abi(ins, device, out_f32=True, deterministic=False):
     """Forward + backward through the C ABI directly (naju_scan_fwd/_bwd), with
-    every output in float32 when out_f32. Returns (y, grads) like run_hip."""
+    every output in float32 when out_f32 and fixed-order carries when
+    deterministic. Returns (y, grads) like run_hip."""
     from naju_amd import _lib
     L = _lib.lib()
     t = {k: (v.to(device).contiguous() if v is not None else None) for k, v in ins.items()}
@@ -114,6 +115,7 @@ def run_abi(ins, device, out_f32=True):
     N = Bm.shape[-1]
     dts = (_DTC[u.dtype], _DTC[fl.dtype], _DTC[Bm.dtype])
     od = lambda x: torch.float32 if out_f32 else x.dtype  # noqa: E731
+    flags = (_lib.FLAG_OUT_F32 if out_f32 else 0) | (_lib.FLAG_DETERMINISTIC if deterministic else 0)
     y = torch.empty(u.shape, dtype=od(u), device=device)
     ck = torch.empty(max(1, L.naju_scan_ckpt_elems(Bsz, T, D, N, *dts)), dtype=torch.float32, device=device)
     nb = L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)
@@ -121,7 +123,7 @@ def run_abi(ins, device, out_f32=True):
     st = torch.cuda.current_stream(device).cuda_stream
     p = lambda x: None if x is None else x.data_ptr()  # noqa: E731
     _lib.check(L.naju_scan_fwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(h0), p(y), p(ck), None,
-                               Bsz, T, D, N, *dts, int(out_f32), p(ws), ws.numel(), st))
+                               Bsz, T, D, N, *dts, flags, p(ws), ws.numel(), st))
     g = {"du": torch.empty(u.shape, dtype=od(u), device=device),
          "dfl": torch.empty(u.shape, dtype=od(fl), device=device),
          "dil": torch.empty(u.shape, dtype=od(il), device=device),
@@ -132,6 +134,6 @@ def run_abi(ins, device, out_f32=True):
         g["dh0"] = torch.empty(h0.shape, dtype=torch.float32, device=device)
     _lib.check(L.naju_scan_bwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(ck), p(dy), p(g["du"]),
                                p(g["dfl"]), p(g["dil"]), p(g["dB"]), p(g["dC"]), p(g["dD"]), p(g.get("dh0")),
-                               Bsz, T, D, N, *dts, int(out_f32), p(ws), ws.numel(), st))
+                               Bsz, T, D, N, *dts, flags, p(ws), ws.numel(), st))
     torch.cuda.synchronize()
     return y, g

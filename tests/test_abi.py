@@ -263,3 +263,10 @@ def test_readout_python_rejects_cpu_tensors():
     x = torch.zeros(1, 2, 4)
     with pytest.raises(RuntimeError, match="CUDA"):
         readout(x, x, x, torch.zeros(4), 0.5)
+
+
+def test_unknown_flag_bits_rejected():
+    L = _lib.lib()
+    fake = 0x1000
+    rc = L.naju_scan_fwd(*([fake] * 6), None, fake, fake, None, 2, 8, 16, 1, F32, F32, F32, 4, fake, 1 << 30, None)
+    assert rc == _lib.ERR_INVALID and b"flag" in L.naju_scan_last_error()

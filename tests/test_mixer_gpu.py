@@ -87,4 +87,4 @@ def test_lm_train_step_reduces_loss(gpu):
         torch.nn.utils.clip_grad_norm_(lm.parameters(), 1.0)
         opt.step()
         first = float(loss.detach()) if first is None else first
-    assert float(loss) < first - 0.1
+    assert float(loss.detach()) < first - 0.1

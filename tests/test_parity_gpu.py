@@ -110,6 +110,41 @@ def test_long_sequence_near_one(gpu):
     check_all(y, g, ry, rg)
 
 
+@pytest.mark.parametrize("shape", [(4, 700, 320), (2, 4096, 1024)])
+def test_deterministic_flag_bitwise(gpu, shape):
+    """NAJU_FLAG_DETERMINISTIC: every chunk takes its carry from its immediate
+    predecessor, so repeated runs are bitwise identical (including the full
+    C2 sequence length with 64 forward / 128 backward chunks), and the
+    results still match the oracle."""
+    B, T, D = shape
+    ins = rand_inputs(B, T, D, 1, seed=17, dtype=torch.bfloat16)
+    y1, g1 = run_abi(ins, gpu, out_f32=True, deterministic=True)
+    y2, g2 = run_abi(ins, gpu, out_f32=True, deterministic=True)
+    assert torch.equal(y1, y2)
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
+    if T <= 1024:
+        ry, rg = oracle_all(ins)
+        check_all(y1.cpu(), {k: v.cpu() for k, v in g1.items()}, ry, rg)
+
+
+def test_torch_deterministic_mode_selects_flag(gpu):
+    """torch.use_deterministic_algorithms(True) makes the Python backend pass
+    NAJU_FLAG_DETERMINISTIC: two autograd runs agree bitwise."""
+    ins = rand_inputs(2, 1500, 256, 1, seed=19, dtype=torch.bfloat16)
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True)
+    try:
+        y1, g1 = run_hip(ins, gpu)
+        y2, g2 = run_hip(ins, gpu)
+    finally:
+        torch.use_deterministic_algorithms(prev)
+    assert torch.equal(y1, y2)
+    for k in g1:
+        if g1[k] is not None:
+            assert torch.equal(g1[k], g2[k]), k
+
+
 def test_repeatable_and_workspace_reusable(gpu):
     """Two identical runs agree to float32 rounding. (Chunk carries are
     composed in the order the decoupled look-back meets its predecessors,
