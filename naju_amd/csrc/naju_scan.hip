@@ -988,7 +988,13 @@ __device__ __forceinline__ void gn_st_one(const ScanArgs& a, int64_t t0, const f
 
 // Adjoint map of segment blockIdx / n_tiles + 1 (segments 1 .. nseg-1): the
 // carry leaving the segment's first row towards the past, from a zero carry
-// entering its last row (segZ), and the product of its gates (segF).
+// entering its last row (segZ), and the product of its gates (segF). Lanes
+// over n as in gn_bwd_kernel; each sub-chunk's f, dy and C are staged in LDS
+// transposed ([channel][row], [n][row]) so a 16-byte read yields four rows,
+// with the next sub-chunk's loads in flight while this one is walked. Rows
+// past T are staged as f = 1, dy = 0 and change nothing.
+constexpr int kGmRP = kGnCK + 4;  // LDS row pitch of the transposed tiles
+
 template <int NP>
 __global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a, int x_dt, int g_dt) {
   constexpr int LG = NP < 64 ? NP : 64;
@@ -996,8 +1002,11 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a,
   constexpr int G = 64 / LG;
   constexpr int NPASS = kGnDT / G;
   constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
-  __shared__ float s_f[kGnCK][kGnDT], s_dy[kGnCK][kGnDT];
-  __shared__ float s_C[kGnCK][NP];
+  constexpr int EB = kGnCK * NP >= kGnThreads ? kGnCK * NP / kGnThreads : 1;
+  constexpr int BCT = kGnCK * NP / EB;
+  static_assert(kGnCK == 4 * kGnW, "tile shape");
+  __shared__ __align__(16) float s_x[2][kGnDT][kGmRP];  // [0] f, [1] dy
+  __shared__ __align__(16) float s_c[NP][kGmRP];
   const int N = a.N;
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
   const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles) + 1;
@@ -1005,12 +1014,19 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a,
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
   const int64_t dbase = (int64_t)dtile * kGnDT;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gl = lane / LG, nl = lane - gl * LG;
   const int KC = (int)((T + kGnCK - 1) / kGnCK);
   const int sc0 = seg * a.seg_sc;
   const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
+  const int64_t dl = dbase + lane;
+  const bool dl_ok = dl < D;
+  const uint32_t lane_c = (uint32_t)(dl_ok ? dl : D - 1) - (uint32_t)dbase;
+  const int bn = tid % NP, bn_r0 = (tid / NP) * EB;
+  const bool bn_act = tid < BCT;
+  const int bnc = bn < N ? bn : N - 1;
 
   float gc[PPW][S], Ac[PPW];
 #pragma unroll
@@ -1019,41 +1035,97 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a,
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = 0.f;
   }
-  constexpr int EB = (kGnCK * NP + kGnThreads - 1) / kGnThreads;
-  float vf[kGnE], vg[kGnE], vc[EB];
-  auto load_tiles = [&](int64_t tl) {
-    gn_ld_tile(a, a.fl, g_dt, b, tl, dbase, vf);
-    gn_ld_tile(a, a.dy, x_dt, b, tl, dbase, vg);
-    gn_ld_bc<NP, EB>(a, a.Cm, b, tl, vc);
+  float vf[4], vg[4], vc[EB];
+  // this thread's rows 4*wv .. 4*wv+3 of channel lane (f, dy) and rows
+  // bn_r0 .. of state bn (C) of the sub-chunk at t0 (rows clamped in bounds)
+  auto load = [&](int64_t t0) {
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+    const int64_t xrow0 = ((int64_t)b * T + t0) * D + dbase;
+    uint32_t xo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = 4 * wv + e < rows ? 4 * wv + e : rows - 1;
+      xo[e] = (uint32_t)rr * (uint32_t)D + lane_c;
+    }
+    auto ld4 = [&](const void* p, int dt, float (&o)[4]) {
+      if (dt == NAJU_DTYPE_F32) {
+        const char* q = (const char*)((const float*)p + xrow0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = *(const float*)(q + xo[e] * 4u);
+      } else if (dt == NAJU_DTYPE_BF16) {
+        const char* q = (const char*)((const bf16_t*)p + xrow0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (float)*(const bf16_t*)(q + xo[e] * 2u);
+      } else {
+        const char* q = (const char*)((const f16_t*)p + xrow0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (float)*(const f16_t*)(q + xo[e] * 2u);
+      }
+    };
+    ld4(a.fl, g_dt, vf);
+    ld4(a.dy, x_dt, vg);
+    if (bn_act) {
+      const int64_t brow0 = ((int64_t)b * T + t0) * N;
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int rr = bn_r0 + e < rows ? bn_r0 + e : rows - 1;
+        const uint32_t o = (uint32_t)rr * (uint32_t)N + (uint32_t)bnc;
+        if (a.bc_dt == NAJU_DTYPE_F32)
+          vc[e] = *(const float*)((const char*)((const float*)a.Cm + brow0) + o * 4u);
+        else if (a.bc_dt == NAJU_DTYPE_BF16)
+          vc[e] = (float)*(const bf16_t*)((const char*)((const bf16_t*)a.Cm + brow0) + o * 2u);
+        else
+          vc[e] = (float)*(const f16_t*)((const char*)((const f16_t*)a.Cm + brow0) + o * 2u);
+      }
+    }
   };
-  load_tiles((int64_t)(sc1 - 1) * kGnCK);
+  load((int64_t)(sc1 - 1) * kGnCK);
   for (int sc = sc1 - 1; sc >= sc0; --sc) {
     const int64_t t0 = (int64_t)sc * kGnCK;
     __syncthreads();  // the previous sub-chunk's tiles are consumed
+    {
+      float4 F4, Y4;
+      float* pF = &F4.x;
+      float* pY = &Y4.x;
 #pragma unroll
-    for (int e = 0; e < kGnE; ++e) {
-      const int k = e * kGnThreads + (int)threadIdx.x;
-      const int r = k / kGnDT, c = k % kGnDT;
-      const bool ok = t0 + r < T && dbase + c < D;
-      s_f[r][c] = ok ? sigm(vf[e]) : 1.f;
-      s_dy[r][c] = ok ? vg[e] : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = dl_ok && t0 + 4 * wv + e < T;
+        pF[e] = ok ? sigm(vf[e]) : 1.f;
+        pY[e] = ok ? vg[e] : 0.f;
+      }
+      *(float4*)&s_x[0][lane][4 * wv] = F4;
+      *(float4*)&s_x[1][lane][4 * wv] = Y4;
+      if (bn_act) {
+#pragma unroll
+        for (int e = 0; e < EB; ++e) s_c[bn][bn_r0 + e] = (t0 + bn_r0 + e < T && bn < N) ? vc[e] : 0.f;
+      }
     }
-    gn_st_one<NP, EB>(a, t0, vc, s_C);
     __syncthreads();
-    if (sc > sc0) load_tiles(t0 - kGnCK);
-    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+    if (sc > sc0) load(t0 - kGnCK);  // next (earlier) sub-chunk, while this one runs
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       const int pass = wv + q * kGnW;
-      if (pass >= NPASS) break;
+      // only when some waves have fewer passes: a branch here would let the
+      // LDS reads of later passes be hoisted above it
+      if constexpr (NPASS % kGnW != 0) {
+        if (pass >= NPASS) break;
+      }
       const int c = pass * G + gl;
 #pragma unroll
-      for (int r = kGnCK - 1; r >= 0; --r) {
-        if (r < rows) {
-          const float f = s_f[r][c], gy = s_dy[r][c];
+      for (int r4 = kGnCK - 4; r4 >= 0; r4 -= 4) {
+        // reads issued per block: hoisted across the unrolled passes and
+        // blocks they would need hundreds of registers
+        __builtin_amdgcn_sched_barrier(0);
+        const float4 f4 = *(const float4*)&s_x[0][c][r4], y4 = *(const float4*)&s_x[1][c][r4];
+        float4 C4[S];
+#pragma unroll
+        for (int s2 = 0; s2 < S; ++s2) C4[s2] = *(const float4*)&s_c[nl + 64 * s2][r4];
+#pragma unroll
+        for (int e = 3; e >= 0; --e) {
+          const float f = (&f4.x)[e], gy = (&y4.x)[e];
           Ac[q] *= f;
 #pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = f * fmaf(gy, s_C[r][nl + 64 * s2], gc[q][s2]);
+          for (int s2 = 0; s2 < S; ++s2) gc[q][s2] = f * fmaf(gy, (&C4[s2].x)[e], gc[q][s2]);
         }
       }
     }
@@ -1548,7 +1620,9 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
 #pragma unroll
       for (int q = 0; q < PPW; ++q) {
         const int pass = wv + q * kGnW;
-        if (pass >= NPASS) break;
+        if constexpr (NPASS % kGnW != 0) {
+          if (pass >= NPASS) break;
+        }
         // passes are independent: keep the scheduler from interleaving them
         // (their live registers would add up)
         __builtin_amdgcn_sched_barrier(0);
