@@ -1008,10 +1008,12 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_map_kernel(const ScanArgs a,
   __shared__ __align__(16) float s_x[2][kGnDT][kGmRP];  // [0] f, [1] dy
   __shared__ __align__(16) float s_c[NP][kGmRP];
   const int N = a.N;
-  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles) + 1;
-  const int b = tile / a.n_dtiles;
-  const int dtile = tile - b * a.n_dtiles;
+  const int mdt = (int)((a.D + kGnDT - 1) / kGnDT);  // this kernel's channel tiles
+  const int mtiles = a.batch * mdt;
+  const int tile = (int)(blockIdx.x % (uint32_t)mtiles);
+  const int seg = (int)(blockIdx.x / (uint32_t)mtiles) + 1;
+  const int b = tile / mdt;
+  const int dtile = tile - b * mdt;
   const int64_t T = a.T, D = a.D;
   const int64_t dbase = (int64_t)dtile * kGnDT;
   const int tid = (int)threadIdx.x;
@@ -1440,35 +1442,37 @@ __device__ __forceinline__ float from_upper(float x) {
   }
 }
 
-template <int NP>
-__global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int x_dt, int g_dt, int du_dt,
+template <int NP, int DT, int W>
+__global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_dt, int g_dt, int du_dt,
                                                            int dg_dt) {
   constexpr int LG = NP < 64 ? NP : 64;
   constexpr int S = NP / LG;
   constexpr int G = 64 / LG;
-  constexpr int NPASS = kGnDT / G;
-  constexpr int PPW = (NPASS + kGnW - 1) / kGnW;
-  static_assert(kGnCK == 4 * kGnW && kGnCK == 2 * kGnH && kGnH == 2 * kGnRG, "tile shape");
+  constexpr int TH = 64 * W;         // threads
+  constexpr int RGS = TH / DT;        // staging row groups of 4 rows
+  constexpr int NPASS = DT / G;
+  constexpr int PPW = (NPASS + W - 1) / W;
+  static_assert(RGS * 4 == kGnCK && kGnCK == 2 * kGnH && kGnH == 2 * kGnRG, "tile shape");
   // B / C staging: thread -> state n = tid % NP, rows [rb*EB, rb*EB + EB)
-  constexpr int EB = kGnCK * NP >= kGnThreads ? kGnCK * NP / kGnThreads : 1;
+  constexpr int EB = kGnCK * NP >= TH ? kGnCK * NP / TH : 1;
   constexpr int BCT = kGnCK * NP / EB;  // threads that stage B / C
   // one object per tile family, so a lane addresses all of them from one
   // base register plus immediate offsets: [0] f, [1] i, [2] u, [3] dy
   // ([channel][row]); [0] B, [1] C ([n][row])
-  __shared__ __align__(16) float s_x[4][kGnDT][kGnRP];
+  __shared__ __align__(16) float s_x[4][DT][kGnRP];
   __shared__ __align__(16) float s_bc[2][NP][kGnRP];
   __shared__ float s_pB[kGnCK][NP], s_pC[kGnCK][NP];
-  __shared__ float s_dD[kGnW][kGnDT];
-  __shared__ float s_Dsk[kGnDT];
+  __shared__ float s_dD[RGS][DT];
+  __shared__ float s_Dsk[DT];
   const int N = a.N;
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
   const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles);
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
-  const int64_t dbase = (int64_t)dtile * kGnDT;
+  const int64_t dbase = (int64_t)dtile * DT;
   const int tid = (int)threadIdx.x;
-  if (tid < kGnDT) s_Dsk[tid] = dbase + tid < D ? a.Dsk[dbase + tid] : 0.f;  // read after the first barrier
+  if (tid < DT) s_Dsk[tid] = dbase + tid < D ? a.Dsk[dbase + tid] : 0.f;  // read after the first barrier
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gl = lane / LG, nl = lane - gl * LG;
@@ -1476,9 +1480,10 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   const int64_t btn = (int64_t)a.batch * T * N;
   const int sc0 = seg * a.seg_sc;
   const int sc1 = sc0 + a.seg_sc < KC ? sc0 + a.seg_sc : KC;
-  // staging roles: channel lane, rows 4*wv .. 4*wv+3; B / C state bn, rows
+  // staging roles: channel sch, rows 4*srg .. 4*srg+3; B / C state bn, rows
   // bn_r0 .. bn_r0+EB-1
-  const int64_t dl = dbase + lane;
+  const int sch = tid % DT, srg = tid / DT;
+  const int64_t dl = dbase + sch;
   const bool dl_ok = dl < D;
   const uint32_t lane_c = (uint32_t)(dl_ok ? dl : D - 1) - (uint32_t)dbase;  // clamped channel offset
   const int bn = tid % NP, bn_r0 = (tid / NP) * EB;
@@ -1491,7 +1496,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   float gc[PPW][S];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
-    const int64_t d = dbase + (int64_t)(wv + q * kGnW) * G + gl;
+    const int64_t d = dbase + (int64_t)(wv + q * W) * G + gl;
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) {
       const int n = nl + 64 * s2;
@@ -1514,7 +1519,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
       uint32_t xo[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int rr = 4 * wv + e < rows ? 4 * wv + e : rows - 1;
+        const int rr = 4 * srg + e < rows ? 4 * srg + e : rows - 1;
         xo[e] = (uint32_t)rr * (uint32_t)D + lane_c;
       }
       auto ld4 = [&](const void* p, int dt, float (&o)[4]) {
@@ -1568,12 +1573,12 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
       const float* ck = a.ckpt + (((int64_t)b * KC + sc) * D + dbase) * N;
 #pragma unroll
       for (int q = 0; q < PPW; ++q) {
-        const int cq = (wv + q * kGnW) * G;  // first channel of the pass (uniform)
+        const int cq = (wv + q * W) * G;  // first channel of the pass (uniform)
         const float* ckq = ck + (int64_t)cq * N;
 #pragma unroll
         for (int s2 = 0; s2 < S; ++s2) {
           const int n = nl + 64 * s2;
-          const bool ok = n < N && dbase + cq + gl < D && wv + q * kGnW < NPASS;
+          const bool ok = n < N && dbase + cq + gl < D && wv + q * W < NPASS;
           x0[q][s2] = ok ? *(const float*)((const char*)ckq + ((uint32_t)gl * (uint32_t)N + (uint32_t)n) * 4u) : 0.f;
         }
       }
@@ -1587,17 +1592,17 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
       float* pY = &Y.x;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const bool ok = dl_ok && t0 + 4 * wv + e < T;
+        const bool ok = dl_ok && t0 + 4 * srg + e < T;
         pF[e] = ok ? sigm(vf[e]) : 1.f;
         pI[e] = ok ? sigm(vi[e]) : 0.f;
         pU[e] = ok ? vu[e] : 0.f;
         pY[e] = ok ? vg[e] : 0.f;
         dDacc = fmaf(pY[e], pU[e], dDacc);
       }
-      *(float4*)&s_x[0][lane][4 * wv] = F;
-      *(float4*)&s_x[1][lane][4 * wv] = I;
-      *(float4*)&s_x[2][lane][4 * wv] = U;
-      *(float4*)&s_x[3][lane][4 * wv] = Y;
+      *(float4*)&s_x[0][sch][4 * srg] = F;
+      *(float4*)&s_x[1][sch][4 * srg] = I;
+      *(float4*)&s_x[2][sch][4 * srg] = U;
+      *(float4*)&s_x[3][sch][4 * srg] = Y;
       if (bn_act) {
 #pragma unroll
         for (int e = 0; e < EB; ++e) {
@@ -1619,8 +1624,8 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
         for (int s2 = 0; s2 < S; ++s2) accB[r][s2] = accC[r][s2] = 0.f;
 #pragma unroll
       for (int q = 0; q < PPW; ++q) {
-        const int pass = wv + q * kGnW;
-        if constexpr (NPASS % kGnW != 0) {
+        const int pass = wv + q * W;
+        if constexpr (NPASS % W != 0) {
           if (pass >= NPASS) break;
         }
         // passes are independent: keep the scheduler from interleaving them
@@ -1758,7 +1763,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
             }
           }
       }
-      for (int w = 0; w < kGnW; ++w) {
+      for (int w = 0; w < W; ++w) {
         if (wv == w && gl == 0) {
 #pragma unroll
           for (int r = 0; r < kGnH; ++r)
@@ -1777,7 +1782,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     {
       float* pB = a.partB ? a.partB + (int64_t)dtile * btn + brow0 : nullptr;
       float* pC = a.partC ? a.partC + (int64_t)dtile * btn + brow0 : nullptr;
-      for (int e = tid; e < kGnCK * NP; e += kGnThreads) {
+      for (int e = tid; e < kGnCK * NP; e += TH) {
         const int r = e / NP, n = e - r * NP;
         if (r < rows && n < N) {
           const uint32_t o = ((uint32_t)r * (uint32_t)N + (uint32_t)n) * 4u;
@@ -1787,15 +1792,15 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
       }
     }
     if (dl_ok) {
-      const float4 o0 = *(const float4*)&s_x[1][lane][4 * wv];
-      const float4 o1 = *(const float4*)&s_x[0][lane][4 * wv];
-      const float4 o2 = *(const float4*)&s_x[2][lane][4 * wv];
+      const float4 o0 = *(const float4*)&s_x[1][sch][4 * srg];
+      const float4 o1 = *(const float4*)&s_x[0][sch][4 * srg];
+      const float4 o2 = *(const float4*)&s_x[2][sch][4 * srg];
       auto st4 = [&](void* p, int dt, const float4& v) {
         if (!p) return;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (4 * wv + e < rows) {
-            uint32_t o = (uint32_t)(4 * wv + e) * (uint32_t)D + (uint32_t)lane;
+          if (4 * srg + e < rows) {
+            uint32_t o = (uint32_t)(4 * srg + e) * (uint32_t)D + (uint32_t)sch;
             // computed here: addresses hoisted to the top of the sub-chunk
             // would occupy registers through the whole scan
             asm volatile("" : "+v"(o));
@@ -1816,7 +1821,7 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
   }
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
-    const int pass = wv + q * kGnW;
+    const int pass = wv + q * W;
     if (pass >= NPASS) break;
     const int64_t d = dbase + (int64_t)pass * G + gl;
     if (d >= D) continue;
@@ -1829,12 +1834,12 @@ __global__ __launch_bounds__(64 * kGnW) void gn_bwd_kernel(const ScanArgs a, int
     }
   }
   // dD = sum dy * u over this segment's rows, in wave order
-  s_dD[wv][lane] = dDacc;
+  s_dD[srg][sch] = dDacc;
   __syncthreads();
-  if (tid < kGnDT && dbase + tid < D && a.partD) {
+  if (tid < DT && dbase + tid < D && a.partD) {
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kGnW; ++w) s += s_dD[w][tid];
+    for (int w = 0; w < RGS; ++w) s += s_dD[w][tid];
     a.partD[((int64_t)b * a.nseg + seg) * D + dbase + tid] = s;
   }
 }
@@ -1921,10 +1926,16 @@ struct Layout {
 
 // N > 1: enough time segments that about kGnTargetWgs workgroups run per
 // launch (each segment keeps at least one sub-chunk).
-constexpr int kGnTargetWgs = 1024;
+#ifndef NAJU_GN_TARGET_WGS
+#define NAJU_GN_TARGET_WGS 1536  // two rounds of three 4-wave workgroups per CU
+#endif
+constexpr int kGnTargetWgs = NAJU_GN_TARGET_WGS;
 constexpr int kGcTargetWaves = 2048;
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int np_of(int64_t N);
+int gn_bwd_dt(int np);
 
 Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd) {
   Layout l{};
@@ -1935,9 +1946,9 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
     l.V = n1_vec_width(bwd);
     l.CH = 64 * l.V;
     l.L = bwd ? kBChunk : kFChunk;
-  } else {  // general N: 64-channel tiles walking T, checkpoint every kGnCK rows
+  } else {  // general N: channel tiles walking T, checkpoint every kGnCK rows
     l.V = 1;
-    l.CH = kGnDT;
+    l.CH = bwd ? gn_bwd_dt(np_of(N)) : kGnDT;  // the backward kernel's tiles (dB/dC partials)
     l.L = kGnCK;
   }
   l.K = (int)((T + l.L - 1) / l.L);
@@ -1949,7 +1960,8 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
     // forward (lanes over channels): about kGcTargetWaves waves; backward
     // (8-wave workgroups over 64 channels): about kGnTargetWgs workgroups
     const int64_t per_seg = bwd ? l.n_tiles : batch * ((D + 63) / 64);
-    const int64_t target = bwd ? kGnTargetWgs : kGcTargetWaves;
+    // (the 8-wave NP = 128 backward runs one workgroup per CU: 1024)
+    const int64_t target = bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
     int64_t want = (target + per_seg - 1) / per_seg;
     if (want > l.K) want = l.K;
     if (want < 1) want = 1;
@@ -2039,15 +2051,21 @@ int np_of(int64_t N) {
 }
 
 
+// Backward workgroup shape per NP: 32 channels in 4 waves (three workgroups
+// fit a CU: 149 VGPRs, 54 KB of LDS) up to NP = 64; 64 channels in 8 waves
+// at NP = 128, whose B/C tiles would not leave room for three.
+int gn_bwd_dt(int np) { return np <= 64 ? 32 : 64; }
+int gn_bwd_waves(int np) { return np <= 64 ? 4 : 8; }
+
 gn_bwd_t pick_gn_bwd(int np) {
   switch (np) {
-    case 2: return gn_bwd_kernel<2>;
-    case 4: return gn_bwd_kernel<4>;
-    case 8: return gn_bwd_kernel<8>;
-    case 16: return gn_bwd_kernel<16>;
-    case 32: return gn_bwd_kernel<32>;
-    case 64: return gn_bwd_kernel<64>;
-    default: return gn_bwd_kernel<128>;
+    case 2: return gn_bwd_kernel<2, 32, 4>;
+    case 4: return gn_bwd_kernel<4, 32, 4>;
+    case 8: return gn_bwd_kernel<8, 32, 4>;
+    case 16: return gn_bwd_kernel<16, 32, 4>;
+    case 32: return gn_bwd_kernel<32, 32, 4>;
+    case 64: return gn_bwd_kernel<64, 32, 4>;
+    default: return gn_bwd_kernel<128, 64, 8>;
   }
 }
 
@@ -2085,7 +2103,8 @@ gn_map_t pick_gn_bwd_map(int np) {
 int gn_segments(const ScanArgs& a, const Layout& l, int x_dt, int g_dt, bool bwd, hipStream_t st) {
   if (l.nseg <= 1) return NAJU_OK;
   if (bwd) {
-    const unsigned grid = (unsigned)((int64_t)l.n_tiles * (l.nseg - 1));
+    // the map kernel tiles channels by kGnDT, independently of the main kernel
+    const unsigned grid = (unsigned)((int64_t)a.batch * ((a.D + kGnDT - 1) / kGnDT) * (l.nseg - 1));
     hipLaunchKernelGGL(pick_gn_bwd_map(np_of(a.N)), dim3(grid), dim3(64 * kGnW), 0, st, a, x_dt, g_dt);
   } else {
     const unsigned grid = (unsigned)(gc_tiles(a.batch, a.D) * (l.nseg - 1));
@@ -2289,7 +2308,8 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
     rc = gn_segments(a, l, x_dtype, gate_dtype, true, st);
     if (rc) return rc;
-    hipLaunchKernelGGL(pick_gn_bwd(np_of(N)), dim3((unsigned)((int64_t)l.n_tiles * l.nseg)), dim3(64 * kGnW), 0, st,
+    hipLaunchKernelGGL(pick_gn_bwd(np_of(N)), dim3((unsigned)((int64_t)l.n_tiles * l.nseg)),
+                       dim3(64 * gn_bwd_waves(np_of(N))), 0, st,
                        a, x_dtype, gate_dtype, du_dt, dg_dt);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
