@@ -12,12 +12,15 @@
 // as it is. The backward walks its block in reverse with a window of the
 // next K-1 output gradients, recomputing the pre-activation from x when the
 // activation is SiLU, and writes per-block partial sums of dw and dbias that
-// a second kernel folds in block order (deterministic).
+// a second kernel folds in a fixed order (deterministic).
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+
+#include <initializer_list>
+#include <type_traits>
 
 #include "naju_mixer.h"
 #include "naju_scan.h"
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void dwconv_fwd_kernel(const void* x, int
     for (int j = 0; j < K - 1; ++j) acc = fmaf(wr[j], xw[j], acc);
 #pragma unroll
     for (int j = 0; j + 1 < K - 1; ++j) xw[j] = xw[j + 1];
-    if (K > 1) xw[K - 2] = xt;
+    if constexpr (K > 1) xw[K - 2] = xt;
     if (add) acc += ldv(add, add_dt, base + t * C);
     stv(y, y_dt, base + t * C, SILU ? silu(acc) : acc);
   }
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int
     // shift the windows down by one row
 #pragma unroll
     for (int j = K - 2; j > 0; --j) gz[j] = gz[j - 1];
-    if (K > 1) gz[0] = dz;
+    if constexpr (K > 1) gz[0] = dz;
 #pragma unroll
     for (int j = K - 1; j > 0; --j) xv[j] = xv[j - 1];
     const int64_t tn = t - K;  // x[(t-1) - (K-1)]
@@ -151,27 +154,12 @@ __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int
   }
 }
 
-// dw[c, j] / dbias[c] = sum over the partials of all blocks, in block order.
-__global__ void dwconv_fold_kernel(const float* part, int64_t nblk, int64_t C, int K, float* dw, float* dbias) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // c * (K+1) + j
-  if (i >= C * (K + 1)) return;
-  float s = 0.f;
-#pragma unroll 8
-  for (int64_t q = 0; q < nblk; ++q) s += part[q * C * (K + 1) + i];
-  const int64_t c = i / (K + 1), j = i - c * (K + 1);
-  if (j < K) {
-    if (dw) dw[c * K + j] = s;
-  } else if (dbias) {
-    dbias[c] = s;
-  }
-}
-
 // ---------------------------------------------------------- readout epilogue
 //
 // y = (cx * scale + Dv * h) * SiLU(z), one thread per channel over a block of
 // kRows rows (grid: channel blocks x row blocks). The backward writes dcx,
 // dh, dz and a per-row-block partial of dD = sum_r dy * SiLU(z) * h, folded
-// in block order by dwconv_fold_kernel (K = 0).
+// in a fixed order by fold_cols_kernel (K = 0).
 __global__ __launch_bounds__(kThreads) void readout_fwd_kernel(const void* cx, const void* h, const void* z,
                                                               int64_t z_ld, const float* Dv, float scale, void* y,
                                                               int64_t n_rows, int64_t C, int cx_dt, int h_dt,
@@ -220,6 +208,305 @@ __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, c
   }
   if (part) part[(int64_t)blockIdx.y * C + c] = dd;
 }
+
+// ------------------------------------------------ vector fast paths (K = 4)
+//
+// The same operations with 8 channels per thread and 16-byte accesses (one
+// wave moves 1 KB per load instruction instead of 128 B), kVRows rows per
+// thread with all row loads issued together, one wave per block. Used when
+// C and the row strides are multiples of 8 and the pointers 16-byte
+// aligned; the scalar kernels above serve every other case.
+constexpr int kVec = 8;
+constexpr int kVRows = 16;
+
+template <typename T>
+__device__ __forceinline__ void ld8(const T* p, float (&o)[kVec]) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  const v8 v = *(const v8*)p;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) o[j] = (float)v[j];
+}
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const float (&x)[kVec]) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  v8 v;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) v[j] = (T)x[j];
+  *(v8*)p = v;
+}
+__device__ __forceinline__ void ld8f(const float* p, float (&o)[kVec]) {
+  const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+  o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
+}
+
+// grid: (ceil(C / (64 * kVec)), ceil(T / kVRows), batch), 64 threads. A
+// thread walks its rows in order with the last K-1 inputs in registers.
+template <typename TX, typename TY, bool SILU, bool ADD>
+__global__ __launch_bounds__(64) void dwconv4_fwd_vec(const TX* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ w, const float* __restrict__ bias,
+                                                      const TX* __restrict__ add, TY* __restrict__ y, int64_t T,
+                                                      int64_t C) {
+  constexpr int K = 4;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  if (c0 >= C) return;
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kVRows;
+  const int64_t t1 = t0 + kVRows < T ? t0 + kVRows : T;
+  float wr[kVec][K], bc[kVec];
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const float4 q = *(const float4*)(w + (c0 + j) * K);
+    wr[j][0] = q.x, wr[j][1] = q.y, wr[j][2] = q.z, wr[j][3] = q.w;
+  }
+  if (bias) {
+    ld8f(bias + c0, bc);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) bc[j] = 0.f;
+  }
+  const TX* xb = x + b * T * ldx + c0;
+  float xw[K - 1][kVec];  // rows t-3, t-2, t-1 entering row t
+#pragma unroll
+  for (int r = 0; r < K - 1; ++r) {
+    const int64_t t = t0 - (K - 1) + r;
+    if (t >= 0) {
+      ld8(xb + t * ldx, xw[r]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) xw[r][j] = 0.f;
+    }
+  }
+#pragma unroll 4
+  for (int64_t t = t0; t < t1; ++t) {
+    float xt[kVec], acc[kVec];
+    ld8(xb + t * ldx, xt);
+    const int64_t o = (b * T + t) * C + c0;
+    float ad[kVec];
+    if (ADD) ld8(add + o, ad);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      float a = fmaf(wr[j][K - 1], xt[j], bc[j]);
+#pragma unroll
+      for (int k = 0; k < K - 1; ++k) a = fmaf(wr[j][k], xw[k][j], a);
+      if (ADD) a += ad[j];
+      acc[j] = SILU ? silu(a) : a;
+      xw[0][j] = xw[1][j];
+      xw[1][j] = xw[2][j];
+      xw[2][j] = xt[j];
+    }
+    st8(y + o, acc);
+  }
+}
+
+// Backward of dwconv4_fwd_vec without add (the reverse walk of
+// dwconv_bwd_kernel with 8 channels per thread); part [batch * nTB][C][K+1].
+template <typename TX, typename TDY, bool SILU>
+__global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ w, const float* __restrict__ bias,
+                                                      const TDY* __restrict__ dy, TX* __restrict__ dx,
+                                                      float* __restrict__ part, int64_t T, int64_t C) {
+  constexpr int K = 4;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  if (c0 >= C) return;
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kVRows;
+  const int64_t t1 = t0 + kVRows < T ? t0 + kVRows : T;
+  float wr[kVec][K], bc[kVec];
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const float4 q = *(const float4*)(w + (c0 + j) * K);
+    wr[j][0] = q.x, wr[j][1] = q.y, wr[j][2] = q.z, wr[j][3] = q.w;
+  }
+  if (bias) {
+    ld8f(bias + c0, bc);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) bc[j] = 0.f;
+  }
+  const TX* xb = x + b * T * ldx + c0;
+  const int64_t tstart = (t1 - 1 + (K - 1)) < (T - 1) ? (t1 - 1 + (K - 1)) : (T - 1);
+  // windows entering row t: gz[k] = dz[t+1+k] (k < K-1), xv[k] = x[t-(K-1)+k]
+  float gz[K - 1][kVec], xv[K][kVec];
+#pragma unroll
+  for (int k = 0; k < K - 1; ++k)
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) gz[k][j] = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int64_t t = tstart - (K - 1) + k;
+    if (t >= 0) {
+      ld8(xb + t * ldx, xv[k]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) xv[k][j] = 0.f;
+    }
+  }
+  float dw[kVec][K], db[kVec];
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    db[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) dw[j][k] = 0.f;
+  }
+#pragma unroll 2
+  for (int64_t t = tstart; t >= t0; --t) {
+    float dz[kVec], xn[kVec];
+    ld8(dy + (b * T + t) * C + c0, dz);
+    const int64_t tn = t - K;  // the row entering the x window next
+    if (tn >= 0 && t - 1 >= t0) {
+      ld8(xb + tn * ldx, xn);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) xn[j] = 0.f;
+    }
+    if (SILU) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        float z = bc[j];
+#pragma unroll
+        for (int k = 0; k < K; ++k) z = fmaf(wr[j][k], xv[k][j], z);
+        const float sg = 1.f / (1.f + __expf(-z));
+        dz[j] *= sg * fmaf(z, 1.f - sg, 1.f);
+      }
+    }
+    if (t < t1) {
+      float g[kVec];
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        float a = wr[j][K - 1] * dz[j];
+#pragma unroll
+        for (int k = 0; k < K - 1; ++k) a = fmaf(wr[j][k], gz[K - 2 - k][j], a);
+        g[j] = a;
+#pragma unroll
+        for (int k = 0; k < K; ++k) dw[j][k] = fmaf(dz[j], xv[k][j], dw[j][k]);
+        db[j] += dz[j];
+      }
+      if (dx) st8(dx + (b * T + t) * C + c0, g);
+    }
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      gz[2][j] = gz[1][j];
+      gz[1][j] = gz[0][j];
+      gz[0][j] = dz[j];
+      xv[3][j] = xv[2][j];
+      xv[2][j] = xv[1][j];
+      xv[1][j] = xv[0][j];
+      xv[0][j] = xn[j];
+    }
+  }
+  if (part) {
+    float* pp = part + (((int64_t)b * gridDim.y + blockIdx.y) * C + c0) * (K + 1);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) pp[j * (K + 1) + k] = dw[j][k];
+      pp[j * (K + 1) + K] = db[j];
+    }
+  }
+}
+
+// grid: (ceil(C / (64 * kVec)), ceil(n_rows / kVRows)), 64 threads
+template <typename T>
+__global__ __launch_bounds__(64) void readout_fwd_vec(const T* __restrict__ cx, const T* __restrict__ h,
+                                                      const T* __restrict__ z, int64_t z_ld,
+                                                      const float* __restrict__ Dv, float scale, T* __restrict__ y,
+                                                      int64_t n_rows, int64_t C) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  if (c0 >= C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kVRows;
+  float dv[kVec];
+  ld8f(Dv + c0, dv);
+#pragma unroll
+  for (int r = 0; r < kVRows; ++r) {
+    const int64_t row = r0 + r;
+    if (row >= n_rows) break;
+    float a[kVec], hh[kVec], zz[kVec];
+    ld8(cx + row * C + c0, a);
+    ld8(h + row * C + c0, hh);
+    ld8(z + row * z_ld + c0, zz);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) a[j] = fmaf(a[j], scale, dv[j] * hh[j]) * silu(zz[j]);
+    st8(y + row * C + c0, a);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, const T* __restrict__ h,
+                                                      const T* __restrict__ z, int64_t z_ld,
+                                                      const float* __restrict__ Dv, float scale,
+                                                      const T* __restrict__ dy, T* __restrict__ dcx,
+                                                      T* __restrict__ dh, T* __restrict__ dz,
+                                                      float* __restrict__ part, int64_t n_rows, int64_t C) {
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  if (c0 >= C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kVRows;
+  float dv[kVec], dd[kVec];
+  ld8f(Dv + c0, dv);
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) dd[j] = 0.f;
+#pragma unroll
+  for (int r = 0; r < kVRows; ++r) {
+    const int64_t row = r0 + r;
+    if (row >= n_rows) break;
+    float cc[kVec], hh[kVec], zz[kVec], g[kVec];
+    ld8(cx + row * C + c0, cc);
+    ld8(h + row * C + c0, hh);
+    ld8(z + row * z_ld + c0, zz);
+    ld8(dy + row * C + c0, g);
+    float o0[kVec], o1[kVec], o2[kVec];
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const float sg = 1.f / (1.f + __expf(-zz[j]));
+      const float gs = g[j] * (zz[j] * sg);
+      o0[j] = gs * scale;
+      o1[j] = gs * dv[j];
+      dd[j] = fmaf(gs, hh[j], dd[j]);
+      const float a = fmaf(cc[j], scale, dv[j] * hh[j]);
+      o2[j] = g[j] * a * sg * fmaf(zz[j], 1.f - sg, 1.f);
+    }
+    if (dcx) st8(dcx + row * C + c0, o0);
+    if (dh) st8(dh + row * C + c0, o1);
+    if (dz) st8(dz + row * C + c0, o2);
+  }
+  if (part) {
+    float* pp = part + (int64_t)blockIdx.y * C + c0;
+    *(float4*)pp = make_float4(dd[0], dd[1], dd[2], dd[3]);
+    *(float4*)(pp + 4) = make_float4(dd[4], dd[5], dd[6], dd[7]);
+  }
+}
+
+// out[i] (i < ncol) = sum over q < nblk of part[q * ncol + i], in a fixed
+// order: each of 16 waves sums every 16th block of a 64-column slice, then
+// wave 0 adds the 16 partial sums in wave order. The dw / dbias columns of
+// the conv partials ([C][K+1]) go to dw (j < K) and dbias (j == K); with
+// K = 0 every column is a dbias (the readout's dD).
+__global__ __launch_bounds__(1024) void fold_cols_kernel(const float* __restrict__ part, int64_t nblk, int64_t C,
+                                                         int K, float* __restrict__ dw, float* __restrict__ dbias) {
+  __shared__ float s[16][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t ncol = C * (K + 1);
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  float acc = 0.f;
+  if (i < ncol) {
+#pragma unroll 4
+    for (int64_t q = wv; q < nblk; q += 16) acc += part[q * ncol + i];
+  }
+  s[wv][lane] = acc;
+  __syncthreads();
+  if (wv == 0 && i < ncol) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) t += s[w][lane];
+    const int64_t c = i / (K + 1), j = i - c * (K + 1);
+    if (j < K) {
+      if (dw) dw[c * K + j] = t;
+    } else if (dbias) {
+      dbias[c] = t;
+    }
+  }
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 thread_local char g_err[256] = "";
 
@@ -283,6 +570,73 @@ bwd_t pick_bwd(int K, bool silu) {
 
 int64_t n_tblocks(int64_t T) { return (T + kRows - 1) / kRows; }
 
+typedef void (*dwf_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, int64_t);
+typedef void (*dwb_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, float*, int64_t,
+                          int64_t);
+
+template <typename TX>
+dwf_vec_t dwf_vec_for(int y_dt, bool silu, bool add) {
+  if (y_dt == NAJU_DTYPE_F32) {
+    if (silu) return (dwf_vec_t)dwconv4_fwd_vec<TX, float, true, false>;
+    return add ? (dwf_vec_t)dwconv4_fwd_vec<TX, float, false, true> : (dwf_vec_t)dwconv4_fwd_vec<TX, float, false, false>;
+  }
+  if (silu) return (dwf_vec_t)dwconv4_fwd_vec<TX, TX, true, false>;
+  return add ? (dwf_vec_t)dwconv4_fwd_vec<TX, TX, false, true> : (dwf_vec_t)dwconv4_fwd_vec<TX, TX, false, false>;
+}
+
+// The K = 4 vector kernel for these arguments, or nullptr (scalar path):
+// x and add in one dtype, y in that dtype or float32, C and x_ld multiples
+// of 8, 16-byte aligned pointers, T / kVRows blocks within the grid limit.
+dwf_vec_t pick_fwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, void* y,
+                       int64_t T, int64_t C, int K, int act, int x_dt, int add_dt, int y_dt) {
+  if (K != 4 || C % kVec || x_ld % kVec || (T + kVRows - 1) / kVRows > 65535) return nullptr;
+  if (!al16(x) || !al16(w) || !al16(y) || (bias && !al16(bias)) || (add && !al16(add))) return nullptr;
+  if (add && add_dt != x_dt) return nullptr;
+  if (y_dt != x_dt && y_dt != NAJU_DTYPE_F32) return nullptr;
+  const bool silu = act == 1, has_add = add != nullptr;
+  if (x_dt == NAJU_DTYPE_BF16) return dwf_vec_for<bf16_t>(y_dt, silu, has_add);
+  if (x_dt == NAJU_DTYPE_F16) return dwf_vec_for<f16_t>(y_dt, silu, has_add);
+  return dwf_vec_for<float>(y_dt, silu, has_add);
+}
+
+template <typename TX>
+dwb_vec_t dwb_vec_for(int dy_dt, bool silu) {
+  if (dy_dt == NAJU_DTYPE_F32 && !std::is_same<TX, float>::value)
+    return silu ? (dwb_vec_t)dwconv4_bwd_vec<TX, float, true> : (dwb_vec_t)dwconv4_bwd_vec<TX, float, false>;
+  return silu ? (dwb_vec_t)dwconv4_bwd_vec<TX, TX, true> : (dwb_vec_t)dwconv4_bwd_vec<TX, TX, false>;
+}
+
+dwb_vec_t pick_bwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
+                       int64_t T, int64_t C, int K, int act, int x_dt, int dy_dt, int dx_dt) {
+  if (K != 4 || C % kVec || x_ld % kVec || (T + kVRows - 1) / kVRows > 65535) return nullptr;
+  if (!al16(x) || !al16(w) || !al16(dy) || (bias && !al16(bias)) || (dx && !al16(dx))) return nullptr;
+  if (dx_dt != x_dt || (dy_dt != x_dt && dy_dt != NAJU_DTYPE_F32)) return nullptr;
+  if (x_dt == NAJU_DTYPE_BF16) return dwb_vec_for<bf16_t>(dy_dt, act == 1);
+  if (x_dt == NAJU_DTYPE_F16) return dwb_vec_for<f16_t>(dy_dt, act == 1);
+  return dwb_vec_for<float>(dy_dt, act == 1);
+}
+
+// Readout vector path: every [n_rows, C] stream in one dtype.
+bool readout_vec_ok(int64_t n_rows, int64_t C, int64_t z_ld, std::initializer_list<const void*> ptrs,
+                    std::initializer_list<int> dts) {
+  if (C % kVec || z_ld % kVec || (n_rows + kVRows - 1) / kVRows > 65535) return false;
+  for (const void* p : ptrs)
+    if (p && !al16(p)) return false;
+  int first = -1;
+  for (int d : dts) {
+    if (first < 0) first = d;
+    if (d != first) return false;
+  }
+  return true;
+}
+
+int launch_fold(const float* part, int64_t nblk, int64_t C, int K, float* dw, float* dbias, hipStream_t st) {
+  const int64_t ncol = C * (K + 1);
+  hipLaunchKernelGGL(fold_cols_kernel, dim3((unsigned)((ncol + 63) / 64)), dim3(1024), 0, st, part, nblk, C, K, dw,
+                     dbias);
+  return hipGetLastError() == hipSuccess ? NAJU_OK : fail(NAJU_ERR_LAUNCH, "fold launch failed");
+}
+
 }  // namespace
 
 extern "C" {
@@ -300,9 +654,15 @@ int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (act == 1 && add) return fail(NAJU_ERR_UNSUPPORTED, "add must be NULL with act = SiLU");
   if (batch == 0 || T == 0 || C == 0) return NAJU_OK;
   if (!x || !w || !y) return fail(NAJU_ERR_INVALID, "null pointer (x, w and y are required)");
-  const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
-  hipLaunchKernelGGL(pick_fwd(K, act == 1), grid, dim3(kThreads), 0, (hipStream_t)stream, x, x_ld, w, bias, add, y,
-                     T, C, x_dtype, add_dtype, y_dtype);
+  if (dwf_vec_t kv = pick_fwd_vec(x, x_ld, w, bias, add, y, T, C, K, act, x_dtype, add_dtype, y_dtype)) {
+    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)((T + kVRows - 1) / kVRows),
+                    (unsigned)batch);
+    hipLaunchKernelGGL(kv, grid, dim3(64), 0, (hipStream_t)stream, x, x_ld, w, bias, add, y, T, C);
+  } else {
+    const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
+    hipLaunchKernelGGL(pick_fwd(K, act == 1), grid, dim3(kThreads), 0, (hipStream_t)stream, x, x_ld, w, bias, add,
+                       y, T, C, x_dtype, add_dtype, y_dtype);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return NAJU_OK;
@@ -310,7 +670,7 @@ int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bi
 
 size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K) {
   if (check(batch, T, C, K, 0, C) != NAJU_OK) return 0;
-  return (size_t)batch * n_tblocks(T) * C * (K + 1) * sizeof(float) + 256;
+  return (size_t)batch * ((T + kVRows - 1) / kVRows) * C * (K + 1) * sizeof(float) + 256;
 }
 
 int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
@@ -325,13 +685,7 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (batch == 0 || T == 0) {
     // empty sums: the fold over zero blocks writes the zeros (a kernel, not a
     // memset, so that the call can be captured into a graph)
-    if (dw || dbias) {
-      const int64_t n = C * (K + 1);
-      hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, nullptr,
-                         (int64_t)0, C, K, dw, dbias);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
-    }
+    if (dw || dbias) return launch_fold(nullptr, 0, C, K, dw, dbias, st);
     return NAJU_OK;
   }
   if (!x || !w || !dy) return fail(NAJU_ERR_INVALID, "null pointer (x, w and dy are required)");
@@ -340,17 +694,22 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (sums && (!workspace || workspace_bytes < need))
     return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
                 workspace ? workspace_bytes : (size_t)0);
-  const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
   float* part = sums ? (float*)workspace : nullptr;
-  hipLaunchKernelGGL(pick_bwd(K, act == 1), grid, dim3(kThreads), 0, st, x, x_ld, w, bias, dy, dx, part, T, C,
-                     x_dtype, dy_dtype, dx_dtype);
-  if (sums) {
-    const int64_t n = C * (K + 1);
-    hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part,
-                       batch * n_tblocks(T), C, K, dw, dbias);
+  int64_t nblk;
+  if (dwb_vec_t kv = pick_bwd_vec(x, x_ld, w, bias, dy, dx, T, C, K, act, x_dtype, dy_dtype, dx_dtype)) {
+    const int64_t ntb = (T + kVRows - 1) / kVRows;
+    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)ntb, (unsigned)batch);
+    hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, part, T, C);
+    nblk = batch * ntb;
+  } else {
+    const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
+    hipLaunchKernelGGL(pick_bwd(K, act == 1), grid, dim3(kThreads), 0, st, x, x_ld, w, bias, dy, dx, part, T, C,
+                       x_dtype, dy_dtype, dx_dtype);
+    nblk = batch * n_tblocks(T);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  if (sums) return launch_fold(part, nblk, C, K, dw, dbias, st);
   return NAJU_OK;
 }
 
@@ -366,9 +725,23 @@ int naju_readout_fwd(const void* cx, const void* h, const void* z, int64_t z_ld,
     return fail(NAJU_ERR_UNSUPPORTED, "shape too large (at most %d rows)", 65535 * kRows);
   if (n_rows == 0 || C == 0) return NAJU_OK;
   if (!cx || !h || !z || !Dv || !y) return fail(NAJU_ERR_INVALID, "null pointer (cx, h, z, Dv and y are required)");
-  const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)((n_rows + kRows - 1) / kRows));
-  hipLaunchKernelGGL(readout_fwd_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, cx, h, z, z_ld, Dv, scale, y,
-                     n_rows, C, cx_dtype, h_dtype, z_dtype, y_dtype);
+  if (readout_vec_ok(n_rows, C, z_ld, {cx, h, z, Dv, y}, {cx_dtype, h_dtype, z_dtype, y_dtype})) {
+    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)((n_rows + kVRows - 1) / kVRows));
+    hipStream_t st = (hipStream_t)stream;
+    if (cx_dtype == NAJU_DTYPE_BF16)
+      hipLaunchKernelGGL(readout_fwd_vec<bf16_t>, grid, dim3(64), 0, st, (const bf16_t*)cx, (const bf16_t*)h,
+                         (const bf16_t*)z, z_ld, Dv, scale, (bf16_t*)y, n_rows, C);
+    else if (cx_dtype == NAJU_DTYPE_F16)
+      hipLaunchKernelGGL(readout_fwd_vec<f16_t>, grid, dim3(64), 0, st, (const f16_t*)cx, (const f16_t*)h,
+                         (const f16_t*)z, z_ld, Dv, scale, (f16_t*)y, n_rows, C);
+    else
+      hipLaunchKernelGGL(readout_fwd_vec<float>, grid, dim3(64), 0, st, (const float*)cx, (const float*)h,
+                         (const float*)z, z_ld, Dv, scale, (float*)y, n_rows, C);
+  } else {
+    const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)((n_rows + kRows - 1) / kRows));
+    hipLaunchKernelGGL(readout_fwd_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, cx, h, z, z_ld, Dv, scale,
+                       y, n_rows, C, cx_dtype, h_dtype, z_dtype, y_dtype);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return NAJU_OK;
@@ -376,7 +749,7 @@ int naju_readout_fwd(const void* cx, const void* h, const void* z, int64_t z_ld,
 
 size_t naju_readout_workspace_bytes(int64_t n_rows, int64_t C) {
   if (n_rows < 0 || C < 0) return 0;
-  return (size_t)((n_rows + kRows - 1) / kRows) * C * sizeof(float) + 256;
+  return (size_t)((n_rows + kVRows - 1) / kVRows) * C * sizeof(float) + 256;
 }
 
 int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
@@ -393,14 +766,8 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
     return fail(NAJU_ERR_UNSUPPORTED, "shape too large (at most %d rows)", 65535 * kRows);
   hipStream_t st = (hipStream_t)stream;
   if (C == 0) return NAJU_OK;
-  const int64_t nblk = (n_rows + kRows - 1) / kRows;
   if (n_rows == 0) {
-    if (dD) {
-      hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, st, nullptr,
-                         (int64_t)0, C, 0, nullptr, dD);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
-    }
+    if (dD) return launch_fold(nullptr, 0, C, 0, nullptr, dD, st);
     return NAJU_OK;
   }
   if (!h || !z || !Dv || !dy) return fail(NAJU_ERR_INVALID, "null pointer (h, z, Dv and dy are required)");
@@ -410,14 +777,33 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
     return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
                 workspace ? workspace_bytes : (size_t)0);
   float* part = dD ? (float*)workspace : nullptr;
-  const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)nblk);
-  hipLaunchKernelGGL(readout_bwd_kernel, grid, dim3(kThreads), 0, st, cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz,
-                     part, n_rows, C, cx_dtype, h_dtype, z_dtype, dy_dtype, dcx_dtype, dh_dtype, dz_dtype);
-  if (dD)
-    hipLaunchKernelGGL(dwconv_fold_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, st, part, nblk, C, 0,
-                       nullptr, dD);
+  int64_t nblk;
+  if (readout_vec_ok(n_rows, C, z_ld, {cx, h, z, Dv, dy, dcx, dh, dz},
+                     {h_dtype, z_dtype, dy_dtype, cx ? cx_dtype : h_dtype, dcx ? dcx_dtype : h_dtype,
+                      dh ? dh_dtype : h_dtype, dz ? dz_dtype : h_dtype})) {
+    nblk = (n_rows + kVRows - 1) / kVRows;
+    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)nblk);
+    if (h_dtype == NAJU_DTYPE_BF16)
+      hipLaunchKernelGGL(readout_bwd_vec<bf16_t>, grid, dim3(64), 0, st, (const bf16_t*)cx, (const bf16_t*)h,
+                         (const bf16_t*)z, z_ld, Dv, scale, (const bf16_t*)dy, (bf16_t*)dcx, (bf16_t*)dh, (bf16_t*)dz,
+                         part, n_rows, C);
+    else if (h_dtype == NAJU_DTYPE_F16)
+      hipLaunchKernelGGL(readout_bwd_vec<f16_t>, grid, dim3(64), 0, st, (const f16_t*)cx, (const f16_t*)h,
+                         (const f16_t*)z, z_ld, Dv, scale, (const f16_t*)dy, (f16_t*)dcx, (f16_t*)dh, (f16_t*)dz,
+                         part, n_rows, C);
+    else
+      hipLaunchKernelGGL(readout_bwd_vec<float>, grid, dim3(64), 0, st, (const float*)cx, (const float*)h,
+                         (const float*)z, z_ld, Dv, scale, (const float*)dy, (float*)dcx, (float*)dh, (float*)dz,
+                         part, n_rows, C);
+  } else {
+    nblk = (n_rows + kRows - 1) / kRows;
+    const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)nblk);
+    hipLaunchKernelGGL(readout_bwd_kernel, grid, dim3(kThreads), 0, st, cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz,
+                       part, n_rows, C, cx_dtype, h_dtype, z_dtype, dy_dtype, dcx_dtype, dh_dtype, dz_dtype);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  if (dD) return launch_fold(part, nblk, C, 0, nullptr, dD, st);
   return NAJU_OK;
 }
 
