@@ -207,11 +207,13 @@ def main():
 def _bench_lm(args):
     """one training step of the Naju LM (12 layers,
     d_model 768, vocab 50257, N = 64) on a batch of 8 x 2048 uniformly random
-    token ids: bf16 autocast forward, cross-entropy, backward, gradient
+    token ids: bf16 autocast forward, cross-entropy (the fused HIP kernels of
+    naju_amd.xent on the bf16 logits), backward, gradient
     clipping at 1.0 and an AdamW step, with every mixer's scan on the HIP
     kernels. value = tokens per second."""
     import torch
     from naju_amd.mixer import NajuLM, build_optimizer
+    from naju_amd.xent import cross_entropy
     dev = torch.device("cuda", 0)
     V, d_model, n_layers, T, Bsz = 50257, 768, 12, 2048, 8
     torch.manual_seed(0)
@@ -224,7 +226,7 @@ def _bench_lm(args):
     def step():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             logits = model(x)
-            loss = torch.nn.functional.cross_entropy(logits.float().view(-1, V), y.view(-1))
+            loss = cross_entropy(logits.view(-1, V), y.view(-1))
         opt.zero_grad(set_to_none=True)
         loss.backward()
         torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)

@@ -1,5 +1,5 @@
-"""ctypes binding of the C ABI declared in include/naju_scan.h and
-include/naju_mixer.h.
+"""ctypes binding of the C ABI declared in include/naju_scan.h,
+include/naju_mixer.h and include/naju_loss.h.
 
 The library is naju_amd/libnaju_scan.so (built by naju_amd/build.py). Nothing
 here falls back to another implementation: if the library is missing or a
@@ -29,6 +29,10 @@ EXPORTED = (
     "naju_readout_fwd",
     "naju_readout_workspace_bytes",
     "naju_readout_bwd",
+    "naju_loss_last_error",
+    "naju_xent_workspace_bytes",
+    "naju_xent_fwd",
+    "naju_xent_bwd",
 )
 
 _lib = None
@@ -90,6 +94,16 @@ def lib():
     # cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz, dD, n_rows, C, 7 dtypes, ws, ws_bytes, stream
     L.naju_readout_bwd.argtypes = [P, P, P, I64, P, F] + [P] * 5 + [I64, I64] + [I] * 7 + [P, SZ, P]
     L.naju_readout_bwd.restype = I
+    L.naju_loss_last_error.argtypes = []
+    L.naju_loss_last_error.restype = ctypes.c_char_p
+    L.naju_xent_workspace_bytes.argtypes = [I64]
+    L.naju_xent_workspace_bytes.restype = SZ
+    # x, x_ld, target, n_rows, n_cols, x_dt, ignore_index, lse, loss, scale, ws, ws_bytes, stream
+    L.naju_xent_fwd.argtypes = [P, I64, P, I64, I64, I, I64, P, P, P, P, SZ, P]
+    L.naju_xent_fwd.restype = I
+    # x, x_ld, target, n_rows, n_cols, x_dt, ignore_index, lse, scale, dloss, dx, dx_ld, dx_dt, stream
+    L.naju_xent_bwd.argtypes = [P, I64, P, I64, I64, I, I64, P, P, P, P, I64, I, P]
+    L.naju_xent_bwd.restype = I
     _lib = L
     return _lib
 
@@ -104,4 +118,11 @@ def check_mixer(rc):
     """check() for the calls of include/naju_mixer.h."""
     if rc != OK:
         raise NajuScanError(rc, lib().naju_mixer_last_error().decode(errors="replace"))
+    return rc
+
+
+def check_loss(rc):
+    """check() for the calls of include/naju_loss.h."""
+    if rc != OK:
+        raise NajuScanError(rc, lib().naju_loss_last_error().decode(errors="replace"))
     return rc

@@ -1,0 +1,359 @@
+// naju_loss.hip -- cross-entropy of the Naju LM training step on MI355X
+// (gfx950), behind the C ABI of include/naju_loss.h.
+//
+// The reference computes nn.functional.cross_entropy on the logits under bf16
+// autocast (/root/reference/evals/lm/train.py:74): torch upcasts the bf16
+// logits to a float32 copy, runs log_softmax (one read, one float32 write),
+// nll_loss, and in the backward the softmax gradient in float32 plus a cast
+// back to bf16 -- about five passes over an n_rows x V tensor that is 1.6 GB
+// in bf16 at the LM configuration (16384 x 50257). Here the forward is one
+// read of the logits in their own dtype (an online max / sum-of-exponentials
+// per row, then a fixed-order mean), and the backward one read plus one write
+// in the logits' dtype, with the loss gradient taken from device memory.
+//
+// One workgroup per row: lanes stream 16-byte vectors (8 bf16 / 4 fp32) of
+// the row, with the row's unaligned head and tail (rows of an odd width start
+// at any 2-byte boundary) handled element by element.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "naju_loss.h"
+#include "naju_scan.h"
+
+namespace {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kUnroll = 4;  // 16-byte vectors per lane in flight
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T>
+__device__ __forceinline__ float tof(T v) {
+  return (float)v;
+}
+template <typename T>
+__device__ __forceinline__ T fromf(float v) {
+  return (T)v;
+}
+
+__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// (m, s): the running maximum and sum_i exp(v_i - m) of a set of values.
+// Empty sets are (-inf, 0). Merging is symmetric in its two operands.
+__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * exp2_((m - mn) * kLog2e) + s2 * exp2_((m2 - mn) * kLog2e);
+  m = mn;
+}
+
+template <int N>
+__device__ __forceinline__ void ms_add(float& m, float& s, const float (&v)[N]) {
+  float mm = v[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) mm = fmaxf(mm, v[i]);
+  const float mn = fmaxf(m, mm);
+  if (mn == -INFINITY) return;
+  float acc = s * exp2_((m - mn) * kLog2e);
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc += exp2_((v[i] - mn) * kLog2e);
+  s = acc;
+  m = mn;
+}
+
+// Elements of a row before its first 16-byte boundary (at most n).
+template <typename T>
+__device__ __forceinline__ int64_t head_elems(const T* p, int64_t n) {
+  constexpr int E = 16 / sizeof(T);
+  const int mis = (int)(((uintptr_t)p & 15) / sizeof(T));
+  const int64_t h = (E - mis) % E;
+  return h < n ? h : n;
+}
+
+// grid: n_rows workgroups of kThreads.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void xent_fwd_kernel(const T* __restrict__ x, int64_t ld,
+                                                            const int64_t* __restrict__ target, int64_t n_cols,
+                                                            int64_t ignore, float* __restrict__ lse,
+                                                            float* __restrict__ row_loss,
+                                                            float* __restrict__ row_valid) {
+  constexpr int E = 16 / sizeof(T);
+  typedef T vec_t __attribute__((ext_vector_type(E)));
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T* p = x + r * ld;
+  const int64_t head = head_elems(p, n_cols);
+  const int64_t nvec = (n_cols - head) / E;
+  const int64_t tail0 = head + nvec * E;
+
+  float m = -INFINITY, s = 0.f;
+  if (tid < head) {
+    const float v[1] = {tof(p[tid])};
+    ms_add(m, s, v);
+  }
+  if (tail0 + tid < n_cols) {
+    const float v[1] = {tof(p[tail0 + tid])};
+    ms_add(m, s, v);
+  }
+  const vec_t* q = reinterpret_cast<const vec_t*>(p + head);
+  int64_t i = tid;
+  for (; i + (kUnroll - 1) * kThreads < nvec; i += kUnroll * kThreads) {
+    vec_t a[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) a[u] = q[i + u * kThreads];
+    float v[kUnroll * E];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[u * E + e] = tof(a[u][e]);
+    ms_add(m, s, v);
+  }
+  for (; i < nvec; i += kThreads) {
+    const vec_t a = q[i];
+    float v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = tof(a[e]);
+    ms_add(m, s, v);
+  }
+
+  // workgroup-wide merge: butterfly within each wave, then the waves in order
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ms_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+  __shared__ float sm[kWaves], ss[kWaves];
+  const int lane = tid & 63, wv = tid >> 6;
+  if (lane == 0) {
+    sm[wv] = m;
+    ss[wv] = s;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float M = sm[0], S = ss[0];
+    for (int w = 1; w < kWaves; ++w) ms_merge(M, S, sm[w], ss[w]);
+    const float l = M + logf(S);
+    lse[r] = l;
+    const int64_t t = target[r];
+    float loss = 0.f, valid = 0.f;
+    if (t != ignore) {
+      valid = 1.f;
+      loss = (t >= 0 && t < n_cols) ? l - tof(p[t]) : __builtin_nanf("");
+    }
+    row_loss[r] = loss;
+    row_valid[r] = valid;
+  }
+}
+
+// One workgroup: loss = sum(row_loss) / sum(row_valid), scale = 1 / count,
+// summed in float64 in a fixed order.
+__global__ __launch_bounds__(1024) void xent_mean_kernel(const float* __restrict__ row_loss,
+                                                         const float* __restrict__ row_valid, int64_t n,
+                                                         float* __restrict__ loss, float* __restrict__ scale) {
+  __shared__ double sa[1024], sc[1024];
+  const int t = threadIdx.x;
+  double a = 0.0, c = 0.0;
+  for (int64_t i = t; i < n; i += 1024) {
+    a += row_loss[i];
+    c += row_valid[i];
+  }
+  sa[t] = a;
+  sc[t] = c;
+  __syncthreads();
+  for (int w = 512; w >= 1; w >>= 1) {
+    if (t < w) {
+      sa[t] += sa[t + w];
+      sc[t] += sc[t + w];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    loss[0] = (float)(sa[0] / sc[0]);  // 0 / 0 = NaN when no row is valid
+    scale[0] = sc[0] > 0.0 ? (float)(1.0 / sc[0]) : 0.f;
+  }
+}
+
+// grid: n_rows workgroups of kThreads.
+// dx[c] = g * (exp(x[c] - lse) - [c == t]), g = dloss * scale (0 if ignored).
+template <typename T, typename TD>
+__global__ __launch_bounds__(kThreads) void xent_bwd_kernel(const T* __restrict__ x, int64_t ld,
+                                                            const int64_t* __restrict__ target, int64_t n_cols,
+                                                            int64_t ignore, const float* __restrict__ lse,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ dloss, TD* __restrict__ dx,
+                                                            int64_t dld) {
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T* p = x + r * ld;
+  TD* d = dx + r * dld;
+  const int64_t t = target[r];
+  if (t == ignore) {
+    for (int64_t c = tid; c < n_cols; c += kThreads) d[c] = fromf<TD>(0.f);
+    return;
+  }
+  const float g = (t >= 0 && t < n_cols) ? dloss[0] * scale[0] : __builtin_nanf("");
+  const float l = lse[r];
+  auto grad = [&](float v, int64_t c) {
+    const float e = exp2_((v - l) * kLog2e) * g;
+    return c == t ? e - g : e;
+  };
+
+  constexpr int E = 16 / sizeof(T);
+  const int64_t head = head_elems(p, n_cols);
+  const bool vec = sizeof(T) == sizeof(TD) && head == head_elems(reinterpret_cast<const T*>(d), n_cols);
+  if (!vec) {
+    for (int64_t c = tid; c < n_cols; c += kThreads) d[c] = fromf<TD>(grad(tof(p[c]), c));
+    return;
+  }
+  typedef T vec_t __attribute__((ext_vector_type(E)));
+  typedef TD dvec_t __attribute__((ext_vector_type(E)));
+  const int64_t nvec = (n_cols - head) / E;
+  const int64_t tail0 = head + nvec * E;
+  if (tid < head) d[tid] = fromf<TD>(grad(tof(p[tid]), tid));
+  if (tail0 + tid < n_cols) d[tail0 + tid] = fromf<TD>(grad(tof(p[tail0 + tid]), tail0 + tid));
+  const vec_t* q = reinterpret_cast<const vec_t*>(p + head);
+  dvec_t* o = reinterpret_cast<dvec_t*>(d + head);
+  int64_t i = tid;
+  for (; i + (kUnroll - 1) * kThreads < nvec; i += kUnroll * kThreads) {
+    vec_t a[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) a[u] = q[i + u * kThreads];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t c0 = head + (i + u * kThreads) * E;
+      dvec_t w;
+#pragma unroll
+      for (int e = 0; e < E; ++e) w[e] = fromf<TD>(grad(tof(a[u][e]), c0 + e));
+      o[i + u * kThreads] = w;
+    }
+  }
+  for (; i < nvec; i += kThreads) {
+    const vec_t a = q[i];
+    const int64_t c0 = head + i * E;
+    dvec_t w;
+#pragma unroll
+    for (int e = 0; e < E; ++e) w[e] = fromf<TD>(grad(tof(a[e]), c0 + e));
+    o[i] = w;
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+thread_local char g_err[256] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool dt_ok(int dt) { return dt == NAJU_DTYPE_F32 || dt == NAJU_DTYPE_BF16 || dt == NAJU_DTYPE_F16; }
+
+size_t ws_bytes(int64_t n_rows) { return n_rows < 0 ? 0 : (size_t)n_rows * 2 * sizeof(float) + 256; }
+
+int check_shape(int64_t x_ld, int64_t n_rows, int64_t n_cols, int x_dtype) {
+  if (n_rows < 0 || n_cols < 0) return fail(NAJU_ERR_INVALID, "negative shape");
+  if (x_ld < n_cols) return fail(NAJU_ERR_INVALID, "x_ld (%lld) must be >= n_cols (%lld)", (long long)x_ld,
+                                 (long long)n_cols);
+  if (!dt_ok(x_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (n_rows > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "at most 2^31-1 rows");
+  return NAJU_OK;
+}
+
+int launched() {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+template <typename T>
+void launch_fwd(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
+                float* lse, float* rl, float* rv, hipStream_t st) {
+  xent_fwd_kernel<T><<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse, rl,
+                                                                      rv);
+}
+
+template <typename T, typename TD>
+void launch_bwd(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
+                const float* lse, const float* scale, const float* dloss, void* dx, int64_t dld, hipStream_t st) {
+  xent_bwd_kernel<T, TD><<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse,
+                                                                          scale, dloss, (TD*)dx, dld);
+}
+
+template <typename T>
+void launch_bwd_dt(int dx_dt, const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols,
+                   int64_t ignore, const float* lse, const float* scale, const float* dloss, void* dx, int64_t dld,
+                   hipStream_t st) {
+  if (dx_dt == NAJU_DTYPE_F32)
+    launch_bwd<T, float>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, st);
+  else if (dx_dt == NAJU_DTYPE_BF16)
+    launch_bwd<T, bf16_t>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, st);
+  else
+    launch_bwd<T, f16_t>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* naju_loss_last_error(void) { return g_err; }
+
+size_t naju_xent_workspace_bytes(int64_t n_rows) { return ws_bytes(n_rows); }
+
+int naju_xent_fwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols, int x_dtype,
+                  int64_t ignore_index, float* lse, float* loss, float* scale, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_shape(x_ld, n_rows, n_cols, x_dtype);
+  if (rc) return rc;
+  if (!loss || !scale) return fail(NAJU_ERR_INVALID, "null pointer (loss and scale are required)");
+  if (n_rows > 0 && (!x || !target || !lse)) return fail(NAJU_ERR_INVALID, "null pointer (x, target and lse)");
+  if (n_rows > 0 && n_cols == 0) return fail(NAJU_ERR_INVALID, "n_cols must be positive when there are rows");
+  if (!workspace || workspace_bytes < ws_bytes(n_rows))
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed", ws_bytes(n_rows));
+  hipStream_t st = (hipStream_t)stream;
+  float* rl = (float*)workspace;
+  float* rv = rl + n_rows;
+  if (n_rows > 0) {
+    if (x_dtype == NAJU_DTYPE_F32)
+      launch_fwd<float>(x, x_ld, target, n_rows, n_cols, ignore_index, lse, rl, rv, st);
+    else if (x_dtype == NAJU_DTYPE_BF16)
+      launch_fwd<bf16_t>(x, x_ld, target, n_rows, n_cols, ignore_index, lse, rl, rv, st);
+    else
+      launch_fwd<f16_t>(x, x_ld, target, n_rows, n_cols, ignore_index, lse, rl, rv, st);
+    if ((rc = launched())) return rc;
+  }
+  xent_mean_kernel<<<1, 1024, 0, st>>>(rl, rv, n_rows, loss, scale);
+  return launched();
+}
+
+int naju_xent_bwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols, int x_dtype,
+                  int64_t ignore_index, const float* lse, const float* scale, const float* dloss, void* dx,
+                  int64_t dx_ld, int dx_dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check_shape(x_ld, n_rows, n_cols, x_dtype);
+  if (rc) return rc;
+  if (dx_ld < n_cols) return fail(NAJU_ERR_INVALID, "dx_ld (%lld) must be >= n_cols (%lld)", (long long)dx_ld,
+                                  (long long)n_cols);
+  if (!dt_ok(dx_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (n_rows == 0 || n_cols == 0) return NAJU_OK;
+  if (!x || !target || !lse || !scale || !dloss || !dx)
+    return fail(NAJU_ERR_INVALID, "null pointer (x, target, lse, scale, dloss and dx are required)");
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == NAJU_DTYPE_F32)
+    launch_bwd_dt<float>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld, st);
+  else if (x_dtype == NAJU_DTYPE_BF16)
+    launch_bwd_dt<bf16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld,
+                          st);
+  else
+    launch_bwd_dt<f16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld, st);
+  return launched();
+}
+
+}  // extern "C"

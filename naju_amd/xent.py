@@ -1,0 +1,92 @@
+"""Cross-entropy of the LM training step on the HIP kernels of
+include/naju_loss.h.
+
+``cross_entropy(logits, target, ignore_index=-100)``
+
+    mean over rows r with target[r] != ignore_index of
+        logsumexp(logits[r]) - logits[r, target[r]]
+
+for logits [rows, V] (a row stride above V is taken as it is) and int64
+targets [rows]: the reference's ``nn.functional.cross_entropy(logits.reshape(
+-1, V), y.reshape(-1))`` under bf16 autocast (evals/lm/train.py:74), which
+evaluates it in float32 on the upcast logits. Here the logits are read in
+their own dtype (no float32 copy) and the arithmetic is float32; the gradient
+comes back in the logits' dtype, as autocast's cast would return it. The
+loss is float32 and deterministic. A target outside [0, V) that is not
+ignore_index gives a NaN loss instead of a device assertion.
+
+CUDA tensors only: there is no other implementation behind this function,
+and a missing library raises.
+"""
+import torch
+
+from naju_amd import _lib
+
+_DT = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16}
+
+
+class _Workspace:
+    """Per-(device, stream) scratch for the per-row losses, grown on demand
+    (the forward overwrites every byte it later reads)."""
+
+    def __init__(self):
+        self._bufs = {}
+
+    def get(self, device, stream, nbytes):
+        key = (device.index, stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_WS = _Workspace()
+
+
+class _CrossEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, target, ignore_index):
+        rows, cols = x.shape
+        dev = x.device
+        lse = torch.empty(rows, dtype=torch.float32, device=dev)
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        scale = torch.empty((), dtype=torch.float32, device=dev)
+        L = _lib.lib()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        nbytes = L.naju_xent_workspace_bytes(rows)
+        ws = _WS.get(dev, stream, nbytes)
+        _lib.check_loss(L.naju_xent_fwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype],
+                                        ignore_index, lse.data_ptr(), loss.data_ptr(), scale.data_ptr(),
+                                        ws.data_ptr(), ws.numel(), stream))
+        ctx.save_for_backward(x, target, lse, scale)
+        ctx.ignore_index = ignore_index
+        return loss
+
+    @staticmethod
+    def backward(ctx, dloss):
+        x, target, lse, scale = ctx.saved_tensors
+        rows, cols = x.shape
+        dloss = dloss.detach().float().contiguous()
+        dx = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+        L = _lib.lib()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check_loss(L.naju_xent_bwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype],
+                                        ctx.ignore_index, lse.data_ptr(), scale.data_ptr(), dloss.data_ptr(),
+                                        dx.data_ptr(), dx.stride(0), _DT[x.dtype], stream))
+        return dx, None, None
+
+
+def cross_entropy(logits, target, ignore_index=-100):
+    if not logits.is_cuda:
+        raise RuntimeError("naju_amd.cross_entropy runs on the HIP kernels only: logits must be a CUDA tensor")
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [rows, classes], got {tuple(logits.shape)}")
+    if target.shape != logits.shape[:1]:
+        raise ValueError(f"target must be [{logits.shape[0]}], got {tuple(target.shape)}")
+    if logits.dtype not in _DT:
+        logits = logits.float()
+    if logits.stride(1) != 1 or logits.stride(0) < logits.shape[1]:
+        logits = logits.contiguous()
+    target = target.to(device=logits.device, dtype=torch.int64).contiguous()
+    return _CrossEntropy.apply(logits, target, int(ignore_index))

@@ -15,7 +15,7 @@ import torch
 from naju_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("naju_scan.h", "naju_mixer.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("naju_scan.h", "naju_mixer.h", "naju_loss.h")]
 F32, BF16, F16 = 0, 1, 2
 
 
@@ -23,14 +23,14 @@ def header_functions():
     names = set()
     for h in HEADERS:
         txt = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer|readout)_\w+)\s*\(", txt))
+        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer|readout|loss|xent)_\w+)\s*\(", txt))
     return sorted(names)
 
 
 def test_library_exports_every_header_symbol():
     lib = _lib.lib()
     names = header_functions()
-    assert len(names) >= 14
+    assert len(names) >= 18
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     assert set(names) == set(_lib.EXPORTED)
@@ -256,6 +256,35 @@ def test_readout_host_checks():
     rc = L.naju_readout_bwd(None, fake, fake, 16, fake, 0.125, fake, None, None, fake, None, 4, 16,
                             *([F32] * 7), None, 0, None)
     assert rc == _lib.ERR_INVALID and b"cx" in L.naju_mixer_last_error()
+
+
+def test_xent_host_checks():
+    L = _lib.lib()
+    fake = 0x1000
+    ws_need = L.naju_xent_workspace_bytes(16)
+    assert ws_need >= 16 * 8
+    def fwd(ld=32, rows=16, cols=32, dt=F32, loss=fake, ws=fake, ws_bytes=ws_need):
+        return L.naju_xent_fwd(fake, ld, fake, rows, cols, dt, -100, fake, loss, fake, ws, ws_bytes, None)
+    assert fwd(ld=31) == _lib.ERR_INVALID and b"x_ld" in L.naju_loss_last_error()
+    assert fwd(dt=7) == _lib.ERR_INVALID
+    assert fwd(rows=-1) == _lib.ERR_INVALID
+    assert fwd(rows=1 << 31) == _lib.ERR_UNSUPPORTED
+    assert fwd(loss=None) == _lib.ERR_INVALID
+    assert fwd(cols=0, ld=0) == _lib.ERR_INVALID and b"n_cols" in L.naju_loss_last_error()
+    assert fwd(ws_bytes=ws_need - 1) == _lib.ERR_WORKSPACE
+    assert fwd(ws=None) == _lib.ERR_WORKSPACE
+    def bwd(dx_ld=32, rows=16, cols=32, dx_dt=BF16, dloss=fake):
+        return L.naju_xent_bwd(fake, 32, fake, rows, cols, F32, -100, fake, fake, dloss, fake, dx_ld, dx_dt, None)
+    assert bwd(dx_ld=31) == _lib.ERR_INVALID and b"dx_ld" in L.naju_loss_last_error()
+    assert bwd(dx_dt=5) == _lib.ERR_INVALID
+    assert bwd(dloss=None) == _lib.ERR_INVALID and b"dloss" in L.naju_loss_last_error()
+    assert bwd(rows=0) == _lib.OK and L.naju_loss_last_error() == b""
+
+
+def test_xent_python_rejects_cpu_tensors():
+    from naju_amd.xent import cross_entropy
+    with pytest.raises(RuntimeError, match="CUDA"):
+        cross_entropy(torch.zeros(2, 5), torch.zeros(2, dtype=torch.int64))
 
 
 def test_readout_python_rejects_cpu_tensors():
