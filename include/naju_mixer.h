@@ -2,8 +2,8 @@
  * naju_mixer.h -- C ABI of the MI355X (gfx950) kernels around the Naju scan
  * inside the mixer: the depthwise causal convolutions of the content branch
  * and of the gate logits (reference /root/reference/naju/mixer.py:75-76,
- * 97-99, 106-110, 115), and the readout epilogue after the scan
- * (mixer.py:123-124).
+ * 97-99, 106-110, 115), the readout epilogue after the scan
+ * (mixer.py:123-124), and the blocks' RMSNorm (mixer.py:51-58).
  *
  *   y[b,t,c] = act( add[b,t,c] + bias[c] + sum_{j<K} w[c,j] * x[b, t-(K-1)+j, c] )
  *
@@ -77,6 +77,28 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
                      const void* dy, void* dcx, void* dh, void* dz, float* dD, int64_t n_rows, int64_t C,
                      int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype, int dz_dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* RMSNorm of the residual blocks and of the LM's final norm
+ * (naju/mixer.py:51-58):
+ *
+ *   y[r,c] = (w[c] * x[r,c]) * rstd[r],  rstd[r] = 1 / sqrt(mean_c x[r,c]^2 + eps)
+ *
+ * x, y [n_rows, d] contiguous, w [d] f32, rstd [n_rows] f32 (saved for the
+ * backward). y may take another dtype than x: under autocast the consumer is
+ * a bf16 GEMM, and writing y in bf16 gives it the same values as the cast
+ * autocast would make. Served: x f32 or bf16, d a multiple of 4 up to 4096,
+ * 16-byte aligned pointers; anything else returns NAJU_ERR_UNSUPPORTED. */
+int naju_rmsnorm_fwd(const void* x, const float* w, float eps, void* y, float* rstd, int64_t n_rows, int64_t d,
+                     int x_dtype, int y_dtype, void* stream);
+
+/* Bytes of workspace naju_rmsnorm_bwd needs for the dw partial sums. */
+size_t naju_rmsnorm_workspace_bytes(int64_t n_rows, int64_t d);
+
+/* Backward of naju_rmsnorm_fwd: dx [n_rows, d] in x's dtype and dw [d] f32
+ * (summed over rows in a fixed order; nullable to skip it) from dy. */
+int naju_rmsnorm_bwd(const void* x, const float* w, const float* rstd, const void* dy, void* dx, float* dw,
+                     int64_t n_rows, int64_t d, int x_dtype, int dy_dtype, int dx_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,9 @@ EXPORTED = (
     "naju_readout_fwd",
     "naju_readout_workspace_bytes",
     "naju_readout_bwd",
+    "naju_rmsnorm_fwd",
+    "naju_rmsnorm_workspace_bytes",
+    "naju_rmsnorm_bwd",
     "naju_loss_last_error",
     "naju_xent_workspace_bytes",
     "naju_xent_fwd",
@@ -94,6 +97,14 @@ def lib():
     # cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz, dD, n_rows, C, 7 dtypes, ws, ws_bytes, stream
     L.naju_readout_bwd.argtypes = [P, P, P, I64, P, F] + [P] * 5 + [I64, I64] + [I] * 7 + [P, SZ, P]
     L.naju_readout_bwd.restype = I
+    # x, w, eps, y, rstd, n_rows, d, x_dt, y_dt, stream
+    L.naju_rmsnorm_fwd.argtypes = [P, P, F, P, P, I64, I64, I, I, P]
+    L.naju_rmsnorm_fwd.restype = I
+    L.naju_rmsnorm_workspace_bytes.argtypes = [I64, I64]
+    L.naju_rmsnorm_workspace_bytes.restype = SZ
+    # x, w, rstd, dy, dx, dw, n_rows, d, x_dt, dy_dt, dx_dt, ws, ws_bytes, stream
+    L.naju_rmsnorm_bwd.argtypes = [P] * 6 + [I64, I64, I, I, I, P, SZ, P]
+    L.naju_rmsnorm_bwd.restype = I
     L.naju_loss_last_error.argtypes = []
     L.naju_loss_last_error.restype = ctypes.c_char_p
     L.naju_xent_workspace_bytes.argtypes = [I64]

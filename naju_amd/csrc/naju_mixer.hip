@@ -637,6 +637,277 @@ int launch_fold(const float* part, int64_t nblk, int64_t C, int K, float* dw, fl
   return hipGetLastError() == hipSuccess ? NAJU_OK : fail(NAJU_ERR_LAUNCH, "fold launch failed");
 }
 
+
+// ------------------------------------------------------------------ RMSNorm
+//
+//   y[r,c] = (w[c] * x[r,c]) * rstd[r],  rstd[r] = 1 / sqrt(mean_c x[r,c]^2 + eps)
+//
+// (reference RMSNorm, /root/reference/naju/mixer.py:51-58, same order of the
+// two products). One wave per row: lane l holds the columns 4(l + 64g) ..
+// +3 for g < G (G * 256 >= d), so the row is read once into registers and
+// written once; each wave does RPW rows with all their loads issued first.
+// The backward,
+//   dx = rstd * (w * dy) - x * rstd^3 * sum_c(w * dy * x) / d,
+//   dw = sum_r (dy * rstd) * x,
+// keeps each wave's dw terms in registers, adds the waves of a workgroup in
+// order and leaves one row of partial sums per workgroup, which
+// fold_cols_kernel adds in workgroup order (deterministic).
+constexpr int kNormWaves = 4;
+
+template <typename T>
+__device__ __forceinline__ void ld4(const T* p, float (&o)[4]) {
+  typedef T v_t __attribute__((ext_vector_type(4)));
+  const v_t v = *reinterpret_cast<const v_t*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (float)v[e];
+}
+template <typename T>
+__device__ __forceinline__ void st4(T* p, const float (&o)[4]) {
+  typedef T v_t __attribute__((ext_vector_type(4)));
+  v_t v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (T)o[e];
+  *reinterpret_cast<v_t*>(p) = v;
+}
+
+__device__ __forceinline__ float wave_allsum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <int G>
+constexpr int norm_rpw() {
+  return G <= 4 ? 4 : (G <= 8 ? 2 : 1);
+}
+
+// grid: ceil(n_rows / (kNormWaves * RPW)) workgroups of 64 * kNormWaves.
+template <typename TX, typename TY, int G>
+__global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_fwd_vec(const TX* __restrict__ x,
+                                                                   const float* __restrict__ w, float eps,
+                                                                   TY* __restrict__ y, float* __restrict__ rstd,
+                                                                   int64_t n_rows, int64_t d) {
+  constexpr int RPW = norm_rpw<G>();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t r0 = ((int64_t)blockIdx.x * kNormWaves + wv) * RPW;
+  float wr[G][4], xv[RPW][G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t c = ((int64_t)g * 64 + lane) * 4;
+    if (c < d) {
+      ld4(w + c, wr[g]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wr[g][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t c = ((int64_t)g * 64 + lane) * 4;
+      if (r0 + i < n_rows && c < d) {
+        ld4(x + (r0 + i) * d + c, xv[i][g]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[i][g][e] = 0.f;
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int64_t r = r0 + i;
+    float ss = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = fmaf(xv[i][g][e], xv[i][g][e], ss);
+    const float rs = rsqrtf(wave_allsum(ss) / (float)d + eps);
+    if (r >= n_rows) continue;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t c = ((int64_t)g * 64 + lane) * 4;
+      if (c < d) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (wr[g][e] * xv[i][g][e]) * rs;
+        st4(y + r * d + c, o);
+      }
+    }
+    if (lane == 0) rstd[r] = rs;
+  }
+}
+
+template <typename TX, typename TDY, int G>
+__global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_vec(const TX* __restrict__ x,
+                                                                   const float* __restrict__ w,
+                                                                   const float* __restrict__ rstd,
+                                                                   const TDY* __restrict__ dy, TX* __restrict__ dx,
+                                                                   float* __restrict__ part, int64_t n_rows,
+                                                                   int64_t d) {
+  constexpr int RPW = norm_rpw<G>();
+  __shared__ float s_acc[kNormWaves][G * 256];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t r0 = ((int64_t)blockIdx.x * kNormWaves + wv) * RPW;
+  float wr[G][4], acc[G][4], xv[RPW][G][4], gv[RPW][G][4], rs[RPW];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t c = ((int64_t)g * 64 + lane) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
+    if (c < d) {
+      ld4(w + c, wr[g]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wr[g][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const bool rv = r0 + i < n_rows;
+    rs[i] = rv ? rstd[r0 + i] : 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t c = ((int64_t)g * 64 + lane) * 4;
+      if (rv && c < d) {
+        ld4(x + (r0 + i) * d + c, xv[i][g]);
+        ld4(dy + (r0 + i) * d + c, gv[i][g]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[i][g][e] = gv[i][g][e] = 0.f;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int64_t r = r0 + i;
+    float s = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s = fmaf(wr[g][e] * gv[i][g][e], xv[i][g][e], s);
+        acc[g][e] = fmaf(gv[i][g][e] * rs[i], xv[i][g][e], acc[g][e]);
+      }
+    const float k = rs[i] * rs[i] * rs[i] * wave_allsum(s) / (float)d;
+    if (r >= n_rows) continue;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t c = ((int64_t)g * 64 + lane) * 4;
+      if (c < d) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = fmaf(wr[g][e] * gv[i][g][e], rs[i], -xv[i][g][e] * k);
+        st4(dx + r * d + c, o);
+      }
+    }
+  }
+  if (!part) return;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_acc[wv][(g * 64 + lane) * 4 + e] = acc[g][e];
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < d; c += 64 * kNormWaves) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < kNormWaves; ++q) t += s_acc[q][c];
+    part[(int64_t)blockIdx.x * d + c] = t;
+  }
+}
+
+constexpr int kNormGs[] = {1, 2, 3, 4, 8, 16};
+
+int norm_g(int64_t d) {
+  for (int g : kNormGs)
+    if ((int64_t)g * 256 >= d) return g;
+  return 0;
+}
+
+int64_t norm_blocks(int64_t n_rows, int G) {
+  const int64_t per = (int64_t)kNormWaves * (G <= 4 ? 4 : (G <= 8 ? 2 : 1));
+  return (n_rows + per - 1) / per;
+}
+
+template <typename TX, typename TY>
+void norm_fwd_launch(int G, dim3 grid, hipStream_t st, const void* x, const float* w, float eps, void* y, float* rstd,
+                     int64_t n, int64_t d) {
+  const dim3 blk(64 * kNormWaves);
+#define NAJU_NORM_F(GG)                                                                                          \
+  case GG:                                                                                                      \
+    hipLaunchKernelGGL((rmsnorm_fwd_vec<TX, TY, GG>), grid, blk, 0, st, (const TX*)x, w, eps, (TY*)y, rstd, n, d); \
+    break;
+  switch (G) {
+    NAJU_NORM_F(1)
+    NAJU_NORM_F(2)
+    NAJU_NORM_F(3)
+    NAJU_NORM_F(4)
+    NAJU_NORM_F(8)
+    NAJU_NORM_F(16)
+  }
+#undef NAJU_NORM_F
+}
+
+template <typename TX, typename TDY>
+void norm_bwd_launch(int G, dim3 grid, hipStream_t st, const void* x, const float* w, const float* rstd,
+                     const void* dy, void* dx, float* part, int64_t n, int64_t d) {
+  const dim3 blk(64 * kNormWaves);
+#define NAJU_NORM_B(GG)                                                                                          \
+  case GG:                                                                                                      \
+    hipLaunchKernelGGL((rmsnorm_bwd_vec<TX, TDY, GG>), grid, blk, 0, st, (const TX*)x, w, rstd, (const TDY*)dy,  \
+                       (TX*)dx, part, n, d);                                                                     \
+    break;
+  switch (G) {
+    NAJU_NORM_B(1)
+    NAJU_NORM_B(2)
+    NAJU_NORM_B(3)
+    NAJU_NORM_B(4)
+    NAJU_NORM_B(8)
+    NAJU_NORM_B(16)
+  }
+#undef NAJU_NORM_B
+}
+
+template <typename TX>
+bool norm_fwd_dt(int y_dt, int G, dim3 grid, hipStream_t st, const void* x, const float* w, float eps, void* y,
+                 float* rstd, int64_t n, int64_t d) {
+  if (y_dt == NAJU_DTYPE_F32)
+    norm_fwd_launch<TX, float>(G, grid, st, x, w, eps, y, rstd, n, d);
+  else if (y_dt == NAJU_DTYPE_BF16)
+    norm_fwd_launch<TX, bf16_t>(G, grid, st, x, w, eps, y, rstd, n, d);
+  else
+    norm_fwd_launch<TX, f16_t>(G, grid, st, x, w, eps, y, rstd, n, d);
+  return true;
+}
+
+template <typename TX>
+bool norm_bwd_dt(int dy_dt, int G, dim3 grid, hipStream_t st, const void* x, const float* w, const float* rstd,
+                 const void* dy, void* dx, float* part, int64_t n, int64_t d) {
+  if (dy_dt == NAJU_DTYPE_F32)
+    norm_bwd_launch<TX, float>(G, grid, st, x, w, rstd, dy, dx, part, n, d);
+  else if (dy_dt == NAJU_DTYPE_BF16)
+    norm_bwd_launch<TX, bf16_t>(G, grid, st, x, w, rstd, dy, dx, part, n, d);
+  else
+    norm_bwd_launch<TX, f16_t>(G, grid, st, x, w, rstd, dy, dx, part, n, d);
+  return true;
+}
+
+// Host-side checks shared by both directions; 0 or an error code.
+int norm_check(int64_t n_rows, int64_t d, int x_dt, std::initializer_list<int> dts,
+               std::initializer_list<const void*> ptrs) {
+  if (n_rows < 0 || d < 0) return fail(NAJU_ERR_INVALID, "negative shape");
+  if (!dt_ok(x_dt)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  for (int dt : dts)
+    if (!dt_ok(dt)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (x_dt == NAJU_DTYPE_F16) return fail(NAJU_ERR_UNSUPPORTED, "float16 x is not served (float32 or bfloat16)");
+  if (d % 4 != 0 || d > 16 * 256)
+    return fail(NAJU_ERR_UNSUPPORTED, "d must be a multiple of 4 and at most 4096 (got %lld)", (long long)d);
+  if (n_rows > (int64_t)0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "too many rows");
+  for (const void* p : ptrs)
+    if (p && ((uintptr_t)p % 16) != 0)
+      return fail(NAJU_ERR_UNSUPPORTED, "pointers must be 16-byte aligned");
+  return NAJU_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -804,6 +1075,64 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   if (dD) return launch_fold(part, nblk, C, 0, nullptr, dD, st);
+  return NAJU_OK;
+}
+
+
+int naju_rmsnorm_fwd(const void* x, const float* w, float eps, void* y, float* rstd, int64_t n_rows, int64_t d,
+                     int x_dtype, int y_dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = norm_check(n_rows, d, x_dtype, {y_dtype}, {x, w, y, rstd});
+  if (rc) return rc;
+  if (n_rows == 0 || d == 0) return NAJU_OK;
+  if (!x || !w || !y || !rstd) return fail(NAJU_ERR_INVALID, "null pointer (x, w, y and rstd are required)");
+  const int G = norm_g(d);
+  const dim3 grid((unsigned)norm_blocks(n_rows, G));
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == NAJU_DTYPE_F32)
+    norm_fwd_dt<float>(y_dtype, G, grid, st, x, w, eps, y, rstd, n_rows, d);
+  else
+    norm_fwd_dt<bf16_t>(y_dtype, G, grid, st, x, w, eps, y, rstd, n_rows, d);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+size_t naju_rmsnorm_workspace_bytes(int64_t n_rows, int64_t d) {
+  if (n_rows < 0 || d < 0) return 0;
+  const int G = norm_g(d);
+  return (size_t)norm_blocks(n_rows, G ? G : 16) * (size_t)d * sizeof(float) + 256;
+}
+
+int naju_rmsnorm_bwd(const void* x, const float* w, const float* rstd, const void* dy, void* dx, float* dw,
+                     int64_t n_rows, int64_t d, int x_dtype, int dy_dtype, int dx_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = norm_check(n_rows, d, x_dtype, {dy_dtype, dx_dtype}, {x, w, dy, dx, workspace});
+  if (rc) return rc;
+  if (dx_dtype != x_dtype) return fail(NAJU_ERR_UNSUPPORTED, "dx must have x's dtype");
+  if (d == 0) return NAJU_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (n_rows == 0) {
+    if (dw) return launch_fold(nullptr, 0, d, 0, nullptr, dw, st);
+    return NAJU_OK;
+  }
+  if (!x || !w || !rstd || !dy || !dx)
+    return fail(NAJU_ERR_INVALID, "null pointer (x, w, rstd, dy and dx are required)");
+  const size_t need = naju_rmsnorm_workspace_bytes(n_rows, d);
+  if (dw && (!workspace || workspace_bytes < need))
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  const int G = norm_g(d);
+  const int64_t nblk = norm_blocks(n_rows, G);
+  float* part = dw ? (float*)workspace : nullptr;
+  if (x_dtype == NAJU_DTYPE_F32)
+    norm_bwd_dt<float>(dy_dtype, G, dim3((unsigned)nblk), st, x, w, rstd, dy, dx, part, n_rows, d);
+  else
+    norm_bwd_dt<bf16_t>(dy_dtype, G, dim3((unsigned)nblk), st, x, w, rstd, dy, dx, part, n_rows, d);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  if (dw) return launch_fold(part, nblk, d, 0, nullptr, dw, st);
   return NAJU_OK;
 }
 

@@ -33,19 +33,33 @@ from torch.utils.checkpoint import checkpoint
 
 from naju_amd.dwconv import dwconv
 from naju_amd.readout import readout
+from naju_amd.rmsnorm import rms_norm
+from naju_amd.rmsnorm import supported as rmsnorm_supported
 from naju_amd.scan import naju_scan
 
 
 class RMSNorm(nn.Module):
-    """weight * x / sqrt(mean(x^2) + eps) over the last axis."""
+    """weight * x / sqrt(mean(x^2) + eps) over the last axis.
+
+    ``out_dtype`` (default: the promoted dtype of weight and x, as the
+    reference's expression gives) lets a caller whose consumer is an
+    autocast GEMM take y in the autocast dtype directly: the same values the
+    GEMM's own cast would produce, without the float32 copy. CUDA inputs the
+    fused kernels serve (naju_amd.rmsnorm.supported) run on them; others use
+    the reference's expression."""
 
     def __init__(self, d, eps=1e-5):
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(d))
 
-    def forward(self, x):
-        return self.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
+    def forward(self, x, out_dtype=None):
+        if out_dtype is None:
+            out_dtype = torch.promote_types(self.weight.dtype, x.dtype)
+        if rmsnorm_supported(x):
+            return rms_norm(x, self.weight, self.eps, out_dtype)
+        y = self.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
+        return y.to(out_dtype)
 
 
 def _out_dtype(x):
@@ -160,7 +174,8 @@ class NajuBlock(nn.Module):
         self.use_ckpt = use_ckpt
 
     def _branch(self, u):
-        return self.drop(self.mixer(self.norm(u)))
+        # the norm's output feeds in_proj only: take it in that GEMM's dtype
+        return self.drop(self.mixer(self.norm(u, out_dtype=_out_dtype(u))))
 
     def forward(self, u):
         if self.use_ckpt and torch.is_grad_enabled():
@@ -189,7 +204,7 @@ class NajuLM(nn.Module):
         x = self.embed(ids)
         for blk in self.blocks:
             x = blk(x)
-        return self.head(self.norm(x))
+        return self.head(self.norm(x, out_dtype=_out_dtype(x)))
 
 
 def build_optimizer(model, lr, weight_decay=0.1):

@@ -23,14 +23,14 @@ def header_functions():
     names = set()
     for h in HEADERS:
         txt = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer|readout|loss|xent)_\w+)\s*\(", txt))
+        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer|readout|rmsnorm|loss|xent)_\w+)\s*\(", txt))
     return sorted(names)
 
 
 def test_library_exports_every_header_symbol():
     lib = _lib.lib()
     names = header_functions()
-    assert len(names) >= 18
+    assert len(names) >= 21
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     assert set(names) == set(_lib.EXPORTED)
@@ -279,6 +279,37 @@ def test_xent_host_checks():
     assert bwd(dx_dt=5) == _lib.ERR_INVALID
     assert bwd(dloss=None) == _lib.ERR_INVALID and b"dloss" in L.naju_loss_last_error()
     assert bwd(rows=0) == _lib.OK and L.naju_loss_last_error() == b""
+
+
+def test_rmsnorm_host_checks():
+    L = _lib.lib()
+    fake = 0x1000
+    def fwd(d=768, rows=4, x_dt=F32, y_dt=BF16, x=fake, y=fake):
+        return L.naju_rmsnorm_fwd(x, fake, 1e-5, y, fake, rows, d, x_dt, y_dt, None)
+    assert fwd(d=6) == _lib.ERR_UNSUPPORTED and b"multiple of 4" in L.naju_mixer_last_error()
+    assert fwd(d=4100) == _lib.ERR_UNSUPPORTED
+    assert fwd(x_dt=F16) == _lib.ERR_UNSUPPORTED
+    assert fwd(y_dt=9) == _lib.ERR_INVALID
+    assert fwd(rows=-1) == _lib.ERR_INVALID
+    assert fwd(x=fake + 4) == _lib.ERR_UNSUPPORTED and b"aligned" in L.naju_mixer_last_error()
+    assert fwd(y=None) == _lib.ERR_INVALID
+    assert fwd(rows=0) == _lib.OK and L.naju_mixer_last_error() == b""
+    need = L.naju_rmsnorm_workspace_bytes(16384, 768)
+    assert need >= (16384 // 16) * 768 * 4
+    def bwd(dx_dt=F32, ws=fake, ws_bytes=need, dw=fake):
+        return L.naju_rmsnorm_bwd(fake, fake, fake, fake, fake, dw, 16384, 768, F32, BF16, dx_dt, ws, ws_bytes, None)
+    assert bwd(dx_dt=BF16) == _lib.ERR_UNSUPPORTED and b"dx" in L.naju_mixer_last_error()
+    assert bwd(ws_bytes=need - 1) == _lib.ERR_WORKSPACE
+    assert bwd(ws=None) == _lib.ERR_WORKSPACE
+
+
+def test_rmsnorm_module_cpu_uses_reference_expression():
+    from naju_amd.mixer import RMSNorm
+    m = RMSNorm(8)
+    x = torch.randn(3, 8)
+    ref = m.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + m.eps)
+    assert torch.equal(m(x), ref)
+    assert m(x, out_dtype=torch.bfloat16).dtype == torch.bfloat16
 
 
 def test_xent_python_rejects_cpu_tensors():
