@@ -207,13 +207,19 @@ class NajuLM(nn.Module):
         return self.head(self.norm(x, out_dtype=_out_dtype(x)))
 
 
-def build_optimizer(model, lr, weight_decay=0.1):
+def build_optimizer(model, lr, weight_decay=0.1, fused=None):
     """AdamW; with gate_reparam mixers, their f_proj / i_proj weights get
     lr * sqrt(d_inner), weight_decay / sqrt(d_inner) and eps 1e-8 / sqrt(d_inner)
-    (reference naju/optim.py:30-52)."""
+    (reference naju/optim.py:30-52).
+
+    ``fused`` (default: True when every parameter is a CUDA tensor) selects
+    torch's single-kernel AdamW update instead of its multi-kernel foreach
+    one: the same update rule, one read and write of each optimizer tensor."""
+    if fused is None:
+        fused = all(p.is_cuda for p in model.parameters())
     mixers = [m for m in model.modules() if isinstance(m, NajuMixer) and m.gate_reparam]
     if not mixers:
-        return torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay)
+        return torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay, fused=fused)
     widths = {m.d_inner for m in mixers}
     if len(widths) != 1:
         raise ValueError(f"mixed d_inner across gate_reparam mixers: {widths}")
@@ -224,4 +230,4 @@ def build_optimizer(model, lr, weight_decay=0.1):
     return torch.optim.AdamW(
         [{"params": rest},
          {"params": gate_params, "lr": lr * mult, "weight_decay": weight_decay / mult, "eps": 1e-8 / mult}],
-        lr=lr, weight_decay=weight_decay)
+        lr=lr, weight_decay=weight_decay, fused=fused)

@@ -88,3 +88,38 @@ def test_lm_train_step_reduces_loss(gpu):
         opt.step()
         first = float(loss.detach()) if first is None else first
     assert float(loss.detach()) < first - 0.1
+
+
+def test_lm_step_fused_loss_and_optimizer_match_reference_loop(gpu):
+    """The C5 step's pieces: naju_amd.xent.cross_entropy on the bf16 logits
+    and build_optimizer's fused AdamW against the reference loop's
+    cross_entropy on the float32 upcast and torch's foreach AdamW
+    (evals/lm/train.py:70-79), from the same weights and batch."""
+    from naju_amd.mixer import build_optimizer
+    from naju_amd.xent import cross_entropy
+    dev = torch.device("cuda", 0)
+    V = 97
+    torch.manual_seed(5)
+    ma = NajuLM(V, d_model=32, n_layers=2, dropout=0.0, d_state=8, scan_backend="hip").to(dev)
+    mb = NajuLM(V, d_model=32, n_layers=2, dropout=0.0, d_state=8, scan_backend="hip").to(dev)
+    mb.load_state_dict(ma.state_dict())
+    oa = build_optimizer(ma, lr=1e-3)
+    ob = torch.optim.AdamW(mb.parameters(), lr=1e-3, weight_decay=0.1, foreach=True)
+    assert oa.defaults["fused"]
+    ids = torch.randint(0, V, (3, 40), device=dev)
+    for step in range(3):
+        losses = []
+        for m, o, fused in ((ma, oa, True), (mb, ob, False)):
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                logits = m(ids)[:, :-1].reshape(-1, V)
+                tgt = ids[:, 1:].reshape(-1)
+                loss = cross_entropy(logits, tgt) if fused else \
+                    torch.nn.functional.cross_entropy(logits.float(), tgt)
+            o.zero_grad(set_to_none=True)
+            loss.backward()
+            torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
+            o.step()
+            losses.append(float(loss.detach()))
+        assert abs(losses[0] - losses[1]) < 2e-3 * abs(losses[1]), (step, losses)
+    for (n, pa), pb in zip(ma.named_parameters(), mb.parameters()):
+        assert _rel(pa.detach(), pb.detach()) < 1e-3, n
