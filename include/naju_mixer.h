@@ -13,10 +13,12 @@
  * branch, with SiLU; mixer.py:106-110 for a gate logit, where add is the gate
  * projection and bias the gate bias).
  *
- * Layouts: add, y, dy, dx : [batch, T, C] row-major (C fastest);
+ * Layouts: y, dy, dx : [batch, T, C] row-major (C fastest);
  *          x : [batch, T, C] with C fastest and x_ld >= C elements between
  *              consecutive timesteps (x_ld = C when contiguous; 2C for one half
  *              of the in_proj output [x, z] without a copy);
+ *          add : the same with add_ld >= C (one slice of a fused projection
+ *              output goes in without a copy);
  *          w, dw : [C, K] float32 (the Conv1d weight [C, 1, K]);
  *          bias, dbias : [C] float32.
  * dtype codes are those of naju_scan.h (F32, BF16, F16). Arithmetic is
@@ -40,9 +42,9 @@ const char* naju_mixer_last_error(void);
 /* Forward: y = act(add + bias + causal_dwconv(x, w)). act: 0 = identity,
  * 1 = SiLU (then add must be NULL). K <= 8. Replaces the Conv1d calls of
  * naju/mixer.py:109 and :115 (plus the bias add of :110). */
-int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, void* y,
-                    int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype, int add_dtype, int y_dtype,
-                    void* stream);
+int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, int64_t add_ld,
+                    void* y, int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype, int add_dtype,
+                    int y_dtype, void* stream);
 
 /* Bytes of workspace naju_dwconv_bwd needs (per-block partial sums of dw and
  * dbias); no zero-fill needed. */

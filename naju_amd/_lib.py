@@ -80,8 +80,8 @@ def lib():
     L.naju_scan_workspace_status.restype = I
     L.naju_mixer_last_error.argtypes = []
     L.naju_mixer_last_error.restype = ctypes.c_char_p
-    # x, x_ld, w, bias, add, y, batch, T, C, K, act, x_dt, add_dt, y_dt, stream
-    L.naju_dwconv_fwd.argtypes = [P, I64] + [P] * 4 + [I64] * 3 + [I] * 5 + [P]
+    # x, x_ld, w, bias, add, add_ld, y, batch, T, C, K, act, x_dt, add_dt, y_dt, stream
+    L.naju_dwconv_fwd.argtypes = [P, I64] + [P] * 3 + [I64, P] + [I64] * 3 + [I] * 5 + [P]
     L.naju_dwconv_fwd.restype = I
     L.naju_dwconv_workspace_bytes.argtypes = [I64] * 3 + [I]
     L.naju_dwconv_workspace_bytes.restype = SZ

@@ -53,8 +53,9 @@ __device__ __forceinline__ float silu(float z) { return z / (1.f + __expf(-z)); 
 // grid: (ceil(C / kThreads), ceil(T / kRows), batch)
 template <int K, bool SILU>
 __global__ __launch_bounds__(kThreads) void dwconv_fwd_kernel(const void* x, int64_t ldx, const float* w,
-                                                             const float* bias, const void* add, void* y, int64_t T,
-                                                             int64_t C, int x_dt, int add_dt, int y_dt) {
+                                                             const float* bias, const void* add, int64_t ld_add,
+                                                             void* y, int64_t T, int64_t C, int x_dt, int add_dt,
+                                                             int y_dt) {
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (c >= C) return;
   const int64_t b = blockIdx.z;
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void dwconv_fwd_kernel(const void* x, int
 #pragma unroll
     for (int j = 0; j + 1 < K - 1; ++j) xw[j] = xw[j + 1];
     if constexpr (K > 1) xw[K - 2] = xt;
-    if (add) acc += ldv(add, add_dt, base + t * C);
+    if (add) acc += ldv(add, add_dt, (b * T + t) * ld_add + c);
     stv(y, y_dt, base + t * C, SILU ? silu(acc) : acc);
   }
 }
@@ -244,8 +245,8 @@ __device__ __forceinline__ void ld8f(const float* p, float (&o)[kVec]) {
 template <typename TX, typename TY, bool SILU, bool ADD>
 __global__ __launch_bounds__(64) void dwconv4_fwd_vec(const TX* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ w, const float* __restrict__ bias,
-                                                      const TX* __restrict__ add, TY* __restrict__ y, int64_t T,
-                                                      int64_t C) {
+                                                      const TX* __restrict__ add, int64_t ld_add,
+                                                      TY* __restrict__ y, int64_t T, int64_t C) {
   constexpr int K = 4;
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
   if (c0 >= C) return;
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(64) void dwconv4_fwd_vec(const TX* __restrict__ x, 
     ld8(xb + t * ldx, xt);
     const int64_t o = (b * T + t) * C + c0;
     float ad[kVec];
-    if (ADD) ld8(add + o, ad);
+    if (ADD) ld8(add + (b * T + t) * ld_add + c0, ad);
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
       float a = fmaf(wr[j][K - 1], xt[j], bc[j]);
@@ -530,8 +531,8 @@ int check(int64_t batch, int64_t T, int64_t C, int K, int act, int64_t x_ld) {
   return NAJU_OK;
 }
 
-typedef void (*fwd_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, int64_t, int,
-                      int, int);
+typedef void (*fwd_t)(const void*, int64_t, const float*, const float*, const void*, int64_t, void*, int64_t, int64_t,
+                      int, int, int);
 typedef void (*bwd_t)(const void*, int64_t, const float*, const float*, const void*, void*, float*, int64_t, int64_t,
                       int, int, int);
 
@@ -570,7 +571,8 @@ bwd_t pick_bwd(int K, bool silu) {
 
 int64_t n_tblocks(int64_t T) { return (T + kRows - 1) / kRows; }
 
-typedef void (*dwf_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, int64_t);
+typedef void (*dwf_vec_t)(const void*, int64_t, const float*, const float*, const void*, int64_t, void*, int64_t,
+                          int64_t);
 typedef void (*dwb_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, float*, int64_t,
                           int64_t);
 
@@ -585,11 +587,14 @@ dwf_vec_t dwf_vec_for(int y_dt, bool silu, bool add) {
 }
 
 // The K = 4 vector kernel for these arguments, or nullptr (scalar path):
-// x and add in one dtype, y in that dtype or float32, C and x_ld multiples
-// of 8, 16-byte aligned pointers, T / kVRows blocks within the grid limit.
-dwf_vec_t pick_fwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, void* y,
-                       int64_t T, int64_t C, int K, int act, int x_dt, int add_dt, int y_dt) {
-  if (K != 4 || C % kVec || x_ld % kVec || (T + kVRows - 1) / kVRows > 65535) return nullptr;
+// x and add in one dtype, y in that dtype or float32, C, x_ld and add_ld
+// multiples of 8, 16-byte aligned pointers, T / kVRows blocks within the
+// grid limit.
+dwf_vec_t pick_fwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add,
+                       int64_t add_ld, void* y, int64_t T, int64_t C, int K, int act, int x_dt, int add_dt,
+                       int y_dt) {
+  if (K != 4 || C % kVec || x_ld % kVec || (add && add_ld % kVec) || (T + kVRows - 1) / kVRows > 65535)
+    return nullptr;
   if (!al16(x) || !al16(w) || !al16(y) || (bias && !al16(bias)) || (add && !al16(add))) return nullptr;
   if (add && add_dt != x_dt) return nullptr;
   if (y_dt != x_dt && y_dt != NAJU_DTYPE_F32) return nullptr;
@@ -914,25 +919,27 @@ extern "C" {
 
 const char* naju_mixer_last_error(void) { return g_err; }
 
-int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, void* y,
-                    int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype, int add_dtype, int y_dtype,
-                    void* stream) {
+int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add, int64_t add_ld,
+                    void* y, int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype, int add_dtype,
+                    int y_dtype, void* stream) {
   g_err[0] = 0;
   int rc = check(batch, T, C, K, act, x_ld);
   if (rc) return rc;
+  if (add && add_ld < C)
+    return fail(NAJU_ERR_INVALID, "add_ld (%lld) must be >= C (%lld)", (long long)add_ld, (long long)C);
   if (!dt_ok(x_dtype) || !dt_ok(y_dtype) || (add && !dt_ok(add_dtype)))
     return fail(NAJU_ERR_INVALID, "unknown dtype code");
   if (act == 1 && add) return fail(NAJU_ERR_UNSUPPORTED, "add must be NULL with act = SiLU");
   if (batch == 0 || T == 0 || C == 0) return NAJU_OK;
   if (!x || !w || !y) return fail(NAJU_ERR_INVALID, "null pointer (x, w and y are required)");
-  if (dwf_vec_t kv = pick_fwd_vec(x, x_ld, w, bias, add, y, T, C, K, act, x_dtype, add_dtype, y_dtype)) {
+  if (dwf_vec_t kv = pick_fwd_vec(x, x_ld, w, bias, add, add_ld, y, T, C, K, act, x_dtype, add_dtype, y_dtype)) {
     const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)((T + kVRows - 1) / kVRows),
                     (unsigned)batch);
-    hipLaunchKernelGGL(kv, grid, dim3(64), 0, (hipStream_t)stream, x, x_ld, w, bias, add, y, T, C);
+    hipLaunchKernelGGL(kv, grid, dim3(64), 0, (hipStream_t)stream, x, x_ld, w, bias, add, add_ld, y, T, C);
   } else {
     const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
     hipLaunchKernelGGL(pick_fwd(K, act == 1), grid, dim3(kThreads), 0, (hipStream_t)stream, x, x_ld, w, bias, add,
-                       y, T, C, x_dtype, add_dtype, y_dtype);
+                       add_ld, y, T, C, x_dtype, add_dtype, y_dtype);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));

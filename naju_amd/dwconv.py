@@ -5,8 +5,8 @@ include/naju_mixer.h.
 
     y[:, t] = act(add[:, t] + bias + sum_j w[:, j] * x[:, t - (k-1) + j])
 
-for x [B, T, C] (C contiguous; a row stride above C is taken as it is, so one
-half of a chunked projection needs no copy), weight [C, 1, k] or [C, k]
+for x and add [B, T, C] (C contiguous; a row stride above C is taken as it
+is, so one slice of a chunked projection needs no copy), weight [C, 1, k] or [C, k]
 (nn.Conv1d with groups = C), bias [C]. ``silu`` applies SiLU to the result
 (then ``add`` must be None). Differentiable in x, weight, bias and add; the
 backward is deterministic. This is the reference's Conv1d(groups=C,
@@ -63,8 +63,11 @@ class _DwConv(torch.autograd.Function):
         y = torch.empty((B, T, C), dtype=out_dtype, device=x.device)
         L = _lib.lib()
         stream = torch.cuda.current_stream(x.device).cuda_stream
+        ld_add = C
+        if add is not None:
+            add, ld_add = _rows(add)
         _lib.check_mixer(L.naju_dwconv_fwd(
-            _ptr(x), ldx, _ptr(w), _ptr(bias), _ptr(add), _ptr(y), B, T, C, K, int(silu), _DT[x.dtype],
+            _ptr(x), ldx, _ptr(w), _ptr(bias), _ptr(add), ld_add, _ptr(y), B, T, C, K, int(silu), _DT[x.dtype],
             _DT[add.dtype] if add is not None else 0, _DT[out_dtype], stream))
         ctx.save_for_backward(x, w, bias)
         ctx.silu = silu
@@ -114,7 +117,6 @@ def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
             raise ValueError(f"add must have x's shape {tuple(x.shape)}, got {tuple(add.shape)}")
         if add.dtype not in _DT:
             add = add.float()
-        add = add.contiguous()
     if x.dtype not in _DT:
         x = x.float()
     if out_dtype is None:

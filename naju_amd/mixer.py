@@ -130,8 +130,9 @@ class NajuMixer(nn.Module):
                                  nn.Linear(self.gate_rank, di, bias=False))
         return nn.Linear(di, di, bias=False)
 
-    def _gate_logit(self, h, proj, conv, bias):
-        p = proj(h)
+    def _gate_logit(self, h, proj, conv, bias, p=None):
+        if p is None:
+            p = proj(h)
         if self.gate_reparam:
             p = p / math.sqrt(self.d_inner)
         if h.is_cuda:
@@ -149,9 +150,20 @@ class NajuMixer(nn.Module):
     def forward(self, u):
         x, z = self.in_proj(u).chunk(2, dim=-1)
         h = self._content(x)
-        Bm, Cm = self.x_proj(h).split(self.d_state, dim=-1)
-        f_logit = self._gate_logit(h, self.f_proj, self.f_conv, self.f_bias)
-        i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)
+        if h.is_cuda and not self.gate_rank:
+            # f_proj, i_proj and x_proj in one GEMM over h (the same weights:
+            # each output column is the same product), so h's gradient from
+            # the three comes back as one GEMM instead of three plus two adds;
+            # the convolutions read their slices in place
+            di, N = self.d_inner, self.d_state
+            w = torch.cat([self.f_proj.weight, self.i_proj.weight, self.x_proj.weight], 0)
+            p_f, p_i, Bm, Cm = F.linear(h, w).split([di, di, N, N], dim=-1)
+            f_logit = self._gate_logit(h, None, self.f_conv, self.f_bias, p=p_f)
+            i_logit = self._gate_logit(h, None, self.i_conv, self.i_bias, p=p_i)
+        else:
+            Bm, Cm = self.x_proj(h).split(self.d_state, dim=-1)
+            f_logit = self._gate_logit(h, self.f_proj, self.f_conv, self.f_bias)
+            i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)
         # the scan reads out the state only; the D skip is applied here
         cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
         if h.is_cuda:

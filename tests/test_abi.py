@@ -195,9 +195,10 @@ def test_build_flags_disable_packed_fp32():
 
 # --- include/naju_mixer.h: host-side checks of the depthwise conv calls ----
 
-def _dw_fwd(L, K=4, act=0, x_ld=16, add=None, C=16, batch=2, T=8, dts=(F32, F32, F32)):
+def _dw_fwd(L, K=4, act=0, x_ld=16, add=None, add_ld=16, C=16, batch=2, T=8, dts=(F32, F32, F32)):
     fake = 0x1000  # never dereferenced: every case here returns before a launch
-    return L.naju_dwconv_fwd(fake, x_ld, fake, None, add, fake, batch, T, C, K, act, dts[0], dts[1], dts[2], None)
+    return L.naju_dwconv_fwd(fake, x_ld, fake, None, add, add_ld, fake, batch, T, C, K, act, dts[0], dts[1], dts[2],
+                             None)
 
 
 def test_dwconv_host_checks():
@@ -207,13 +208,14 @@ def test_dwconv_host_checks():
     assert _dw_fwd(L, x_ld=15) == _lib.ERR_INVALID and b"x_ld" in L.naju_mixer_last_error()
     assert _dw_fwd(L, act=2) == _lib.ERR_INVALID
     assert _dw_fwd(L, act=1, add=0x2000) == _lib.ERR_UNSUPPORTED
+    assert _dw_fwd(L, add=0x2000, add_ld=15) == _lib.ERR_INVALID and b"add_ld" in L.naju_mixer_last_error()
     assert _dw_fwd(L, dts=(F32, F32, 7)) == _lib.ERR_INVALID
     assert _dw_fwd(L, batch=-1) == _lib.ERR_INVALID
     # empty shapes return before any launch
     assert _dw_fwd(L, batch=0) == _lib.OK and L.naju_mixer_last_error() == b""
     assert _dw_fwd(L, T=0) == _lib.OK
     # null required pointer
-    assert L.naju_dwconv_fwd(None, 16, 0x1000, None, None, 0x1000, 2, 8, 16, 4, 0, F32, F32, F32, None) \
+    assert L.naju_dwconv_fwd(None, 16, 0x1000, None, None, 16, 0x1000, 2, 8, 16, 4, 0, F32, F32, F32, None) \
         == _lib.ERR_INVALID
 
 

@@ -137,3 +137,29 @@ def test_dwconv_empty_batch_zero_grads(gpu):
     y = dwconv(x, w, b)
     y.sum().backward()
     assert torch.equal(w.grad, torch.zeros_like(w)) and torch.equal(b.grad, torch.zeros_like(b))
+
+
+@pytest.mark.parametrize("x_dtype,C", [(torch.float32, 72), (torch.bfloat16, 264), (torch.bfloat16, 100)])
+def test_dwconv_strided_add(gpu, x_dtype, C):
+    """add as one slice of a wider projection output (row stride 3C + 8, as
+    the fused gate projection passes it): read in place, same result as a
+    contiguous add, gradient of the slice = dy."""
+    g = torch.Generator().manual_seed(C)
+    B, T, K = 2, 90, 4
+    x = torch.randn(B, T, C, generator=g).to(x_dtype)
+    w = torch.randn(C, 1, K, generator=g) / K
+    bias = torch.randn(C, generator=g)
+    wide = torch.randn(B, T, 3 * C + 8, generator=g).to(x_dtype)
+    dy = torch.randn(B, T, C, generator=g)
+    wg = wide.to(gpu).requires_grad_(True)
+    add = wg[..., C:2 * C]
+    assert add.stride(1) == 3 * C + 8
+    y = dwconv(x.to(gpu), w.to(gpu), bias.to(gpu), add=add, out_dtype=torch.float32)
+    y.backward(dy.to(gpu))
+    y2 = dwconv(x.to(gpu), w.to(gpu), bias.to(gpu), add=add.detach().contiguous(), out_dtype=torch.float32)
+    assert torch.equal(y.detach(), y2)
+    yr = _ref(x.double(), w.double(), bias.double(), wide[..., C:2 * C].double(), False)
+    assert _rel(y, yr) < 1e-5
+    gr = torch.zeros(B, T, 3 * C + 8, dtype=torch.float64)
+    gr[..., C:2 * C] = dy.to(x_dtype).double()
+    assert _rel(wg.grad, gr) < 1e-6
