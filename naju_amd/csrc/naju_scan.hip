@@ -816,6 +816,47 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
   __shared__ float s_acc[16][64];
   if ((int)blockIdx.x < n_bc_blocks) {
     const int64_t stride = (int64_t)n_bc_blocks * blockDim.x;
+    if (btn % 4 == 0) {
+      // four consecutive entries per thread, the parts of dB and dC loaded
+      // four at a time with 16-byte loads, added in part order (the same
+      // order, so the same sums, as the scalar loop below)
+      const int64_t n4 = btn / 4;
+      const float4* pb = reinterpret_cast<const float4*>(partB);
+      const float4* pc = reinterpret_cast<const float4*>(partC);
+      for (int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < n4; i4 += stride) {
+        float sb[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {0.f, 0.f, 0.f, 0.f};
+        int q = 0;
+        for (; q + 4 <= n_parts; q += 4) {
+          float4 vb[4], vc[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (dB) vb[u] = pb[(int64_t)(q + u) * n4 + i4];
+            if (dC) vc[u] = pc[(int64_t)(q + u) * n4 + i4];
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            sb[0] += vb[u].x, sb[1] += vb[u].y, sb[2] += vb[u].z, sb[3] += vb[u].w;
+            sc[0] += vc[u].x, sc[1] += vc[u].y, sc[2] += vc[u].z, sc[3] += vc[u].w;
+          }
+        }
+        for (; q < n_parts; ++q) {
+          if (dB) {
+            const float4 v = pb[(int64_t)q * n4 + i4];
+            sb[0] += v.x, sb[1] += v.y, sb[2] += v.z, sb[3] += v.w;
+          }
+          if (dC) {
+            const float4 v = pc[(int64_t)q * n4 + i4];
+            sc[0] += v.x, sc[1] += v.y, sc[2] += v.z, sc[3] += v.w;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (dB) st_any(dB, bc_dt, 4 * i4 + e, sb[e]);
+          if (dC) st_any(dC, bc_dt, 4 * i4 + e, sc[e]);
+        }
+      }
+      return;
+    }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
       if (dB) st_any(dB, bc_dt, i, sum_parts(partB, n_parts, btn, i));
       if (dC) st_any(dC, bc_dt, i, sum_parts(partC, n_parts, btn, i));
@@ -2326,7 +2367,10 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   }
   if (dB || dC || dD) {
     const int64_t btn = batch * T * N;
-    const int n_bc = (dB || dC) ? (int)((btn + 1023) / 1024 < 256 ? (btn + 1023) / 1024 : 256) : 0;
+    // enough workgroups for about one pass of the threads over the entries
+    // (four per thread when btn % 4 == 0), at most 1024
+    const int64_t per = btn % 4 == 0 ? 4 * 1024 : 1024;
+    const int n_bc = (dB || dC) ? (int)((btn + per - 1) / per < 1024 ? (btn + per - 1) / per : 1024) : 0;
     const int n_d = dD ? (int)((D + 63) / 64) : 0;
     hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
                        btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD,
