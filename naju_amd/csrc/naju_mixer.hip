@@ -349,14 +349,16 @@ __global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, 
 #pragma unroll
     for (int k = 0; k < K; ++k) dw[j][k] = 0.f;
   }
-#pragma unroll 2
+#pragma unroll 4
   for (int64_t t = tstart; t >= t0; --t) {
     float dz[kVec], xn[kVec];
     ld8(dy + (b * T + t) * C + c0, dz);
-    const int64_t tn = t - K;  // the row entering the x window next
-    if (tn >= 0 && t - 1 >= t0) {
-      ld8(xb + tn * ldx, xn);
-    } else {
+    // the row entering the x window next; loaded from a clamped (in-bounds)
+    // row without a branch, so the loads of later iterations can be issued
+    // early, and zeroed when it lies outside the block's window
+    const int64_t tn = t - K;
+    ld8(xb + (tn >= 0 ? tn : 0) * ldx, xn);
+    if (!(tn >= 0 && t - 1 >= t0)) {
 #pragma unroll
       for (int j = 0; j < kVec; ++j) xn[j] = 0.f;
     }
