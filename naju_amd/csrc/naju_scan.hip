@@ -1636,9 +1636,11 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
         const bool ok = dl_ok && t0 + 4 * srg + e < T;
         pF[e] = ok ? sigm(vf[e]) : 1.f;
         pI[e] = ok ? sigm(vi[e]) : 0.f;
-        pU[e] = ok ? vu[e] : 0.f;
+        // the tile holds w = i*u, the only form the recompute and the
+        // adjoint use (dil is formed from it below)
+        pU[e] = ok ? pI[e] * vu[e] : 0.f;
         pY[e] = ok ? vg[e] : 0.f;
-        dDacc = fmaf(pY[e], pU[e], dDacc);
+        dDacc = fmaf(pY[e], ok ? vu[e] : 0.f, dDacc);
       }
       *(float4*)&s_x[0][sch][4 * srg] = F;
       *(float4*)&s_x[1][sch][4 * srg] = I;
@@ -1678,17 +1680,16 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
         for (int s2 = 0; s2 < S; ++s2) xs[s2] = x0[q][s2];
         // forward states: rows [0, hr0) unstored, then the half's rows
         for (int r4 = 0; r4 < hr0; r4 += 4) {
-          const float4 f4 = *(const float4*)&s_x[0][c][r4], i4 = *(const float4*)&s_x[1][c][r4];
+          const float4 f4 = *(const float4*)&s_x[0][c][r4];
           const float4 u4 = *(const float4*)&s_x[2][c][r4];
           float4 B4[S];
 #pragma unroll
           for (int s2 = 0; s2 < S; ++s2) B4[s2] = *(const float4*)&s_bc[0][nl + 64 * s2][r4];
           const float* pf = &f4.x;
-          const float* pi = &i4.x;
           const float* pu = &u4.x;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float iu = pi[e] * pu[e];
+            const float iu = pu[e];
 #pragma unroll
             for (int s2 = 0; s2 < S; ++s2) xs[s2] = fmaf(pf[e], xs[s2], iu * (&B4[s2].x)[e]);
           }
@@ -1703,17 +1704,16 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
         for (int r4 = 0; r4 < kGnH; r4 += 4) {
           __builtin_amdgcn_sched_barrier(0);
           const int r = hr0 + r4;
-          const float4 f4 = *(const float4*)&s_x[0][c][r], i4 = *(const float4*)&s_x[1][c][r];
+          const float4 f4 = *(const float4*)&s_x[0][c][r];
           const float4 u4 = *(const float4*)&s_x[2][c][r];
           float4 B4[S];
 #pragma unroll
           for (int s2 = 0; s2 < S; ++s2) B4[s2] = *(const float4*)&s_bc[0][nl + 64 * s2][r];
           const float* pf = &f4.x;
-          const float* pi = &i4.x;
           const float* pu = &u4.x;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float iu = pi[e] * pu[e];
+            const float iu = pu[e];
 #pragma unroll
             for (int s2 = 0; s2 < S; ++s2) {
               xs[s2] = fmaf(pf[e], xs[s2], iu * (&B4[s2].x)[e]);
@@ -1733,7 +1733,7 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
             __builtin_amdgcn_sched_barrier(0);
             const int lr = grp * kGnRG + r4;  // local row of the half
             const int r = hr0 + lr;
-            const float4 f4 = *(const float4*)&s_x[0][c][r], i4 = *(const float4*)&s_x[1][c][r];
+            const float4 f4 = *(const float4*)&s_x[0][c][r];
             const float4 u4 = *(const float4*)&s_x[2][c][r], y4 = *(const float4*)&s_x[3][c][r];
             float4 B4[S], C4[S];
 #pragma unroll
@@ -1742,13 +1742,12 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
               C4[s2] = *(const float4*)&s_bc[1][nl + 64 * s2][r];
             }
             const float* pf = &f4.x;
-            const float* pi = &i4.x;
             const float* pu = &u4.x;
             const float* py = &y4.x;
 #pragma unroll
             for (int e = 3; e >= 0; --e) {
               const int j = r4 + e;  // row within the group
-              const float iu = pi[e] * pu[e], gy = py[e];
+              const float iu = pu[e], gy = py[e];
               float tf = 0.f, tw = 0.f;
 #pragma unroll
               for (int s2 = 0; s2 < S; ++s2) {
@@ -1782,10 +1781,10 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
 #pragma unroll
             for (int j = 0; j < KF; ++j) {
               const int r = hr0 + grp * kGnRG + e0 + j;
-              const float f = s_x[0][c][r], ig = s_x[1][c][r], uu = s_x[2][c][r], gy = s_x[3][c][r];
+              const float f = s_x[0][c][r], ig = s_x[1][c][r], w = s_x[2][c][r], gy = s_x[3][c][r];
               s_x[1][c][r] = fmaf(ig, vw[j], s_Dsk[c] * gy);     // du
               s_x[0][c][r] = fmaf(-f, f, f) * v[j];              // dfl
-              s_x[2][c][r] = fmaf(-ig, ig, ig) * (vw[j] * uu);   // dil
+              s_x[2][c][r] = (1.f - ig) * (vw[j] * w);           // dil = i(1-i) u dws
             }
           }
         }
