@@ -1320,12 +1320,19 @@ __global__ __launch_bounds__(64 * kGcW) void gc_fwd_kernel(const ScanArgs a, int
           if (MAP) {
             Fd *= f;
 #pragma unroll
-            for (int n = 0; n < NP; ++n) x[n] = fmaf(f, x[n], w * s_B[rr][n]);
+            for (int n = 0; n < NP; ++n) {
+              // f*x then + w*B as two in-place updates of x (a multiply and
+              // an accumulating FMA): no temporary per state and no register
+              // move of the loop-carried state
+              x[n] *= f;
+              x[n] = fmaf(w, s_B[rr][n], x[n]);
+            }
           } else {
             float y4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int n = 0; n < NP; ++n) {
-              x[n] = fmaf(f, x[n], w * s_B[rr][n]);
+              x[n] *= f;
+              x[n] = fmaf(w, s_B[rr][n], x[n]);
               y4[n & 3] = fmaf(s_C[MAP ? 0 : rr][n], x[n], y4[n & 3]);
             }
             yv[r] = fmaf(Dv, cu[r], (y4[0] + y4[1]) + (y4[2] + y4[3]));
