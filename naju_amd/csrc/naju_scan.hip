@@ -1698,7 +1698,7 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
           for (int e = 0; e < 4; ++e) {
             const float iu = pu[e];
 #pragma unroll
-            for (int s2 = 0; s2 < S; ++s2) xs[s2] = fmaf(pf[e], xs[s2], iu * (&B4[s2].x)[e]);
+            for (int s2 = 0; s2 < S; ++s2) xs[s2] = fmaf(iu, (&B4[s2].x)[e], xs[s2] * pf[e]);
           }
         }
         float xin[S], hist[kGnH][S];
@@ -1723,7 +1723,7 @@ __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_
             const float iu = pu[e];
 #pragma unroll
             for (int s2 = 0; s2 < S; ++s2) {
-              xs[s2] = fmaf(pf[e], xs[s2], iu * (&B4[s2].x)[e]);
+              xs[s2] = fmaf(iu, (&B4[s2].x)[e], xs[s2] * pf[e]);
               hist[r4 + e][s2] = xs[s2];
             }
           }
