@@ -47,6 +47,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flush", action="store_true",
                     help="also time steps with a 1 GiB cache-flush write before each step")
+    ap.add_argument("--tune-gemms", default=None, metavar="CSV",
+                    help="c5: time the GEMM solutions during the warmup and record them in CSV "
+                         "(default: read naju_amd/tunableop_mi355x_lm.csv)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run 3 plain 512 MiB device copies (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -214,7 +217,15 @@ def _bench_lm(args):
     import torch
     from naju_amd.mixer import NajuLM, build_optimizer
     from naju_amd.xent import cross_entropy
+    from naju_amd import gemm_tuning
     dev = torch.device("cuda", 0)
+    # GEMM solutions: the recorded choice for these shapes (PyTorch
+    # TunableOp), or time them now with --tune-gemms (during the warmup)
+    if args.tune_gemms:
+        gemm_tuning.tune(args.tune_gemms)
+        tuned = args.tune_gemms
+    else:
+        tuned = gemm_tuning.DEFAULT if gemm_tuning.load() else None
     V, d_model, n_layers, T, Bsz = 50257, 768, 12, 2048, 8
     torch.manual_seed(0)
     model = NajuLM(V, d_model=d_model, n_layers=n_layers, dropout=0.1, scan_backend="hip").to(dev)
@@ -251,8 +262,9 @@ def _bench_lm(args):
         "data": "synthetic (uniform random token ids; random init)",
         "config": {"workload": "naju LM training step c5: 12 layers, d_model 768, vocab 50257, N=64, "
                                "batch 8 x seq 2048, AdamW + clip 1.0",
-                   "parameters": n_params, "parallelism": "single GPU"},
-        "loss_last": round(float(loss), 4),
+                   "parameters": n_params, "parallelism": "single GPU",
+                   "gemm_choices": os.path.basename(tuned) if tuned else "library default"},
+        "loss_last": round(float(loss.detach()), 4),
         "roofline": {"kernel": "whole training step (6 x parameters x tokens)", "bound": "mfma",
                      "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4), "traffic": None},
