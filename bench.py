@@ -17,6 +17,7 @@ workload.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--N 1]
 """
 import argparse
+import gc
 import json
 import os
 import sys
@@ -247,6 +248,11 @@ def _bench_lm(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # Python's cyclic collector: a full collection walks every live object and
+    # stalls the launching thread for tens of ms (the GPU queue drains
+    # meanwhile); the objects alive after the warmup are moved out of its way
+    gc.collect()
+    gc.freeze()
     K = args.steps
     t0 = time.perf_counter()
     for _ in range(K):

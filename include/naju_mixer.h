@@ -50,13 +50,17 @@ int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bi
  * dbias); no zero-fill needed. */
 size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K);
 
-/* Backward of naju_dwconv_fwd with add = NULL (the gradient of add is dy
- * itself): dx, dw and dbias (each nullable to skip it) from dy. With act = 1
- * the pre-activation is recomputed from x. Deterministic (fixed-order
- * sums). The autograd of the reference's Conv1d + slice. */
+/* Backward of naju_dwconv_fwd: dx (dx_ld >= C elements between rows), dw
+ * and dbias (each nullable to skip it) from dy. With act = 1 the
+ * pre-activation is recomputed from x. The gradient of add is dy itself;
+ * dadd (act = 0 only, nullable) receives it in dadd_dtype with dadd_ld
+ * elements between rows, so that it lands in place in a wider gradient
+ * buffer (one slice of a fused projection's gradient). Deterministic
+ * (fixed-order sums). The autograd of the reference's Conv1d + slice. */
 int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
-                    float* dw, float* dbias, int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype,
-                    int dy_dtype, int dx_dtype, void* workspace, size_t workspace_bytes, void* stream);
+                    int64_t dx_ld, float* dw, float* dbias, void* dadd, int64_t dadd_ld, int64_t batch, int64_t T,
+                    int64_t C, int K, int act, int x_dtype, int dy_dtype, int dx_dtype, int dadd_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Readout epilogue of the mixer (naju/mixer.py:123-124), one pass:
  *
@@ -72,13 +76,14 @@ int naju_readout_fwd(const void* cx, const void* h, const void* z, int64_t z_ld,
 /* Bytes of workspace naju_readout_bwd needs for the dD partial sums. */
 size_t naju_readout_workspace_bytes(int64_t n_rows, int64_t C);
 
-/* Backward of naju_readout_fwd: dcx, dh, dz (each [n_rows, C] contiguous,
- * in the given dtypes) and dD [C] f32 (summed over rows in a fixed order),
- * each nullable to skip it. */
+/* Backward of naju_readout_fwd: dcx, dh ([n_rows, C] contiguous), dz
+ * (dz_ld >= C elements between rows, so that it can land in place in the
+ * in_proj output's gradient), in the given dtypes, and dD [C] f32 (summed
+ * over rows in a fixed order), each nullable to skip it. */
 int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
-                     const void* dy, void* dcx, void* dh, void* dz, float* dD, int64_t n_rows, int64_t C,
-                     int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype, int dz_dtype,
-                     void* workspace, size_t workspace_bytes, void* stream);
+                     const void* dy, void* dcx, void* dh, void* dz, int64_t dz_ld, float* dD, int64_t n_rows,
+                     int64_t C, int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype,
+                     int dz_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* RMSNorm of the residual blocks and of the LM's final norm
  * (naju/mixer.py:51-58):

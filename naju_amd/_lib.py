@@ -85,8 +85,9 @@ def lib():
     L.naju_dwconv_fwd.restype = I
     L.naju_dwconv_workspace_bytes.argtypes = [I64] * 3 + [I]
     L.naju_dwconv_workspace_bytes.restype = SZ
-    # x, x_ld, w, bias, dy, dx, dw, dbias, batch, T, C, K, act, x_dt, dy_dt, dx_dt, ws, ws_bytes, stream
-    L.naju_dwconv_bwd.argtypes = [P, I64] + [P] * 6 + [I64] * 3 + [I] * 5 + [P, SZ, P]
+    # x, x_ld, w, bias, dy, dx, dx_ld, dw, dbias, dadd, dadd_ld, batch, T, C, K, act, x_dt, dy_dt, dx_dt,
+    # dadd_dt, ws, ws_bytes, stream
+    L.naju_dwconv_bwd.argtypes = [P, I64] + [P] * 4 + [I64] + [P] * 3 + [I64] * 4 + [I] * 6 + [P, SZ, P]
     L.naju_dwconv_bwd.restype = I
     F = ctypes.c_float
     # cx, h, z, z_ld, Dv, scale, y, n_rows, C, cx_dt, h_dt, z_dt, y_dt, stream
@@ -94,8 +95,8 @@ def lib():
     L.naju_readout_fwd.restype = I
     L.naju_readout_workspace_bytes.argtypes = [I64, I64]
     L.naju_readout_workspace_bytes.restype = SZ
-    # cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz, dD, n_rows, C, 7 dtypes, ws, ws_bytes, stream
-    L.naju_readout_bwd.argtypes = [P, P, P, I64, P, F] + [P] * 5 + [I64, I64] + [I] * 7 + [P, SZ, P]
+    # cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz, dz_ld, dD, n_rows, C, 7 dtypes, ws, ws_bytes, stream
+    L.naju_readout_bwd.argtypes = [P, P, P, I64, P, F] + [P] * 4 + [I64, P, I64, I64] + [I] * 7 + [P, SZ, P]
     L.naju_readout_bwd.restype = I
     # x, w, eps, y, rstd, n_rows, d, x_dt, y_dt, stream
     L.naju_rmsnorm_fwd.argtypes = [P, P, F, P, P, I64, I64, I, I, P]

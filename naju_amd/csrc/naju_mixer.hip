@@ -90,8 +90,10 @@ __global__ __launch_bounds__(kThreads) void dwconv_fwd_kernel(const void* x, int
 // grid as the forward. part: [batch * ceil(T / kRows)][C][K + 1] (dw, dbias).
 template <int K, bool SILU>
 __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int64_t ldx, const float* w,
-                                                             const float* bias, const void* dy, void* dx, float* part,
-                                                             int64_t T, int64_t C, int x_dt, int dy_dt, int dx_dt) {
+                                                             const float* bias, const void* dy, void* dx,
+                                                             int64_t ld_dx, void* dadd, int64_t ld_dadd, float* part,
+                                                             int64_t T, int64_t C, int x_dt, int dy_dt, int dx_dt,
+                                                             int dadd_dt) {
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (c >= C) return;
   const int64_t b = blockIdx.z;
@@ -133,7 +135,8 @@ __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int
       float g = wr[K - 1] * dz;
 #pragma unroll
       for (int j = 0; j < K - 1; ++j) g = fmaf(wr[j], gz[K - 2 - j], g);
-      if (dx) stv(dx, dx_dt, base + t * C, g);
+      if (dx) stv(dx, dx_dt, (b * T + t) * ld_dx + c, g);
+      if (dadd) stv(dadd, dadd_dt, (b * T + t) * ld_dadd + c, dz);
 #pragma unroll
       for (int j = 0; j < K; ++j) dw[j] = fmaf(dz, xv[j], dw[j]);
       db += dz;
@@ -182,7 +185,8 @@ __global__ __launch_bounds__(kThreads) void readout_fwd_kernel(const void* cx, c
 __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, const void* h, const void* z,
                                                               int64_t z_ld, const float* Dv, float scale,
                                                               const void* dy, void* dcx, void* dh, void* dz,
-                                                              float* part, int64_t n_rows, int64_t C, int cx_dt,
+                                                              int64_t dz_ld, float* part, int64_t n_rows, int64_t C,
+                                                              int cx_dt,
                                                               int h_dt, int z_dt, int dy_dt, int dcx_dt, int dh_dt,
                                                               int dz_dt) {
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -204,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, c
     dd = fmaf(gs, hh, dd);
     if (dz) {
       const float a = fmaf(ldv(cx, cx_dt, o), scale, dv * hh);
-      stv(dz, dz_dt, o, g * a * sg * fmaf(zz, 1.f - sg, 1.f));
+      stv(dz, dz_dt, r * dz_ld + c, g * a * sg * fmaf(zz, 1.f - sg, 1.f));
     }
   }
   if (part) part[(int64_t)blockIdx.y * C + c] = dd;
@@ -304,7 +308,8 @@ __global__ __launch_bounds__(64) void dwconv4_fwd_vec(const TX* __restrict__ x, 
 template <typename TX, typename TDY, bool SILU>
 __global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ w, const float* __restrict__ bias,
-                                                      const TDY* __restrict__ dy, TX* __restrict__ dx,
+                                                      const TDY* __restrict__ dy, TX* __restrict__ dx, int64_t ld_dx,
+                                                      TX* __restrict__ dadd, int64_t ld_dadd,
                                                       float* __restrict__ part, int64_t T, int64_t C) {
   constexpr int K = 4;
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
@@ -384,7 +389,8 @@ __global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, 
         for (int k = 0; k < K; ++k) dw[j][k] = fmaf(dz[j], xv[k][j], dw[j][k]);
         db[j] += dz[j];
       }
-      if (dx) st8(dx + (b * T + t) * C + c0, g);
+      if (dx) st8(dx + (b * T + t) * ld_dx + c0, g);
+      if (!SILU && dadd) st8(dadd + (b * T + t) * ld_dadd + c0, dz);
     }
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
@@ -438,7 +444,7 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
                                                       const T* __restrict__ z, int64_t z_ld,
                                                       const float* __restrict__ Dv, float scale,
                                                       const T* __restrict__ dy, T* __restrict__ dcx,
-                                                      T* __restrict__ dh, T* __restrict__ dz,
+                                                      T* __restrict__ dh, T* __restrict__ dz, int64_t dz_ld,
                                                       float* __restrict__ part, int64_t n_rows, int64_t C) {
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
   if (c0 >= C) return;
@@ -469,7 +475,7 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
     }
     if (dcx) st8(dcx + row * C + c0, o0);
     if (dh) st8(dh + row * C + c0, o1);
-    if (dz) st8(dz + row * C + c0, o2);
+    if (dz) st8(dz + row * dz_ld + c0, o2);
   }
   if (part) {
     float* pp = part + (int64_t)blockIdx.y * C + c0;
@@ -535,8 +541,8 @@ int check(int64_t batch, int64_t T, int64_t C, int K, int act, int64_t x_ld) {
 
 typedef void (*fwd_t)(const void*, int64_t, const float*, const float*, const void*, int64_t, void*, int64_t, int64_t,
                       int, int, int);
-typedef void (*bwd_t)(const void*, int64_t, const float*, const float*, const void*, void*, float*, int64_t, int64_t,
-                      int, int, int);
+typedef void (*bwd_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, void*, int64_t,
+                      float*, int64_t, int64_t, int, int, int, int);
 
 template <int K>
 fwd_t pick_fwd_k(bool silu) {
@@ -575,7 +581,8 @@ int64_t n_tblocks(int64_t T) { return (T + kRows - 1) / kRows; }
 
 typedef void (*dwf_vec_t)(const void*, int64_t, const float*, const float*, const void*, int64_t, void*, int64_t,
                           int64_t);
-typedef void (*dwb_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, float*, int64_t,
+typedef void (*dwb_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, void*,
+                          int64_t, float*, int64_t,
                           int64_t);
 
 template <typename TX>
@@ -614,10 +621,14 @@ dwb_vec_t dwb_vec_for(int dy_dt, bool silu) {
 }
 
 dwb_vec_t pick_bwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
-                       int64_t T, int64_t C, int K, int act, int x_dt, int dy_dt, int dx_dt) {
-  if (K != 4 || C % kVec || x_ld % kVec || (T + kVRows - 1) / kVRows > 65535) return nullptr;
-  if (!al16(x) || !al16(w) || !al16(dy) || (bias && !al16(bias)) || (dx && !al16(dx))) return nullptr;
-  if (dx_dt != x_dt || (dy_dt != x_dt && dy_dt != NAJU_DTYPE_F32)) return nullptr;
+                       int64_t dx_ld, const void* dadd, int64_t dadd_ld, int64_t T, int64_t C, int K, int act,
+                       int x_dt, int dy_dt, int dx_dt, int dadd_dt) {
+  if (K != 4 || C % kVec || x_ld % kVec || dx_ld % kVec || (dadd && dadd_ld % kVec) ||
+      (T + kVRows - 1) / kVRows > 65535)
+    return nullptr;
+  if (!al16(x) || !al16(w) || !al16(dy) || (bias && !al16(bias)) || (dx && !al16(dx)) || (dadd && !al16(dadd)))
+    return nullptr;
+  if (dx_dt != x_dt || (dadd && dadd_dt != x_dt) || (dy_dt != x_dt && dy_dt != NAJU_DTYPE_F32)) return nullptr;
   if (x_dt == NAJU_DTYPE_BF16) return dwb_vec_for<bf16_t>(dy_dt, act == 1);
   if (x_dt == NAJU_DTYPE_F16) return dwb_vec_for<f16_t>(dy_dt, act == 1);
   return dwb_vec_for<float>(dy_dt, act == 1);
@@ -625,8 +636,8 @@ dwb_vec_t pick_bwd_vec(const void* x, int64_t x_ld, const float* w, const float*
 
 // Readout vector path: every [n_rows, C] stream in one dtype.
 bool readout_vec_ok(int64_t n_rows, int64_t C, int64_t z_ld, std::initializer_list<const void*> ptrs,
-                    std::initializer_list<int> dts) {
-  if (C % kVec || z_ld % kVec || (n_rows + kVRows - 1) / kVRows > 65535) return false;
+                    std::initializer_list<int> dts, int64_t dz_ld = 0) {
+  if (C % kVec || z_ld % kVec || dz_ld % kVec || (n_rows + kVRows - 1) / kVRows > 65535) return false;
   for (const void* p : ptrs)
     if (p && !al16(p)) return false;
   int first = -1;
@@ -954,12 +965,18 @@ size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K) {
 }
 
 int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
-                    float* dw, float* dbias, int64_t batch, int64_t T, int64_t C, int K, int act, int x_dtype,
-                    int dy_dtype, int dx_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+                    int64_t dx_ld, float* dw, float* dbias, void* dadd, int64_t dadd_ld, int64_t batch, int64_t T,
+                    int64_t C, int K, int act, int x_dtype, int dy_dtype, int dx_dtype, int dadd_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check(batch, T, C, K, act, x_ld);
   if (rc) return rc;
-  if (!dt_ok(x_dtype) || !dt_ok(dy_dtype) || !dt_ok(dx_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (!dt_ok(x_dtype) || !dt_ok(dy_dtype) || !dt_ok(dx_dtype) || (dadd && !dt_ok(dadd_dtype)))
+    return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (dx && dx_ld < C) return fail(NAJU_ERR_INVALID, "dx_ld (%lld) must be >= C (%lld)", (long long)dx_ld, (long long)C);
+  if (dadd && dadd_ld < C)
+    return fail(NAJU_ERR_INVALID, "dadd_ld (%lld) must be >= C (%lld)", (long long)dadd_ld, (long long)C);
+  if (dadd && act == 1) return fail(NAJU_ERR_UNSUPPORTED, "dadd must be NULL with act = SiLU");
   hipStream_t st = (hipStream_t)stream;
   if (C == 0) return NAJU_OK;
   if (batch == 0 || T == 0) {
@@ -976,15 +993,16 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
                 workspace ? workspace_bytes : (size_t)0);
   float* part = sums ? (float*)workspace : nullptr;
   int64_t nblk;
-  if (dwb_vec_t kv = pick_bwd_vec(x, x_ld, w, bias, dy, dx, T, C, K, act, x_dtype, dy_dtype, dx_dtype)) {
+  if (dwb_vec_t kv = pick_bwd_vec(x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, T, C, K, act, x_dtype, dy_dtype,
+                                  dx_dtype, dadd_dtype)) {
     const int64_t ntb = (T + kVRows - 1) / kVRows;
     const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)ntb, (unsigned)batch);
-    hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, part, T, C);
+    hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C);
     nblk = batch * ntb;
   } else {
     const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
-    hipLaunchKernelGGL(pick_bwd(K, act == 1), grid, dim3(kThreads), 0, st, x, x_ld, w, bias, dy, dx, part, T, C,
-                       x_dtype, dy_dtype, dx_dtype);
+    hipLaunchKernelGGL(pick_bwd(K, act == 1), grid, dim3(kThreads), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd,
+                       dadd_ld, part, T, C, x_dtype, dy_dtype, dx_dtype, dadd_dtype);
     nblk = batch * n_tblocks(T);
   }
   const hipError_t e = hipGetLastError();
@@ -1033,12 +1051,14 @@ size_t naju_readout_workspace_bytes(int64_t n_rows, int64_t C) {
 }
 
 int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld, const float* Dv, float scale,
-                     const void* dy, void* dcx, void* dh, void* dz, float* dD, int64_t n_rows, int64_t C,
-                     int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype, int dz_dtype,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+                     const void* dy, void* dcx, void* dh, void* dz, int64_t dz_ld, float* dD, int64_t n_rows,
+                     int64_t C, int cx_dtype, int h_dtype, int z_dtype, int dy_dtype, int dcx_dtype, int dh_dtype,
+                     int dz_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   if (n_rows < 0 || C < 0) return fail(NAJU_ERR_INVALID, "negative shape");
   if (z_ld < C) return fail(NAJU_ERR_INVALID, "z_ld (%lld) must be >= C (%lld)", (long long)z_ld, (long long)C);
+  if (dz && dz_ld < C)
+    return fail(NAJU_ERR_INVALID, "dz_ld (%lld) must be >= C (%lld)", (long long)dz_ld, (long long)C);
   if (!dt_ok(cx_dtype) || !dt_ok(h_dtype) || !dt_ok(z_dtype) || !dt_ok(dy_dtype) || !dt_ok(dcx_dtype) ||
       !dt_ok(dh_dtype) || !dt_ok(dz_dtype))
     return fail(NAJU_ERR_INVALID, "unknown dtype code");
@@ -1060,26 +1080,27 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
   int64_t nblk;
   if (readout_vec_ok(n_rows, C, z_ld, {cx, h, z, Dv, dy, dcx, dh, dz},
                      {h_dtype, z_dtype, dy_dtype, cx ? cx_dtype : h_dtype, dcx ? dcx_dtype : h_dtype,
-                      dh ? dh_dtype : h_dtype, dz ? dz_dtype : h_dtype})) {
+                      dh ? dh_dtype : h_dtype, dz ? dz_dtype : h_dtype},
+                     dz ? dz_ld : 0)) {
     nblk = (n_rows + kVRows - 1) / kVRows;
     const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)nblk);
     if (h_dtype == NAJU_DTYPE_BF16)
       hipLaunchKernelGGL(readout_bwd_vec<bf16_t>, grid, dim3(64), 0, st, (const bf16_t*)cx, (const bf16_t*)h,
                          (const bf16_t*)z, z_ld, Dv, scale, (const bf16_t*)dy, (bf16_t*)dcx, (bf16_t*)dh, (bf16_t*)dz,
-                         part, n_rows, C);
+                         dz_ld, part, n_rows, C);
     else if (h_dtype == NAJU_DTYPE_F16)
       hipLaunchKernelGGL(readout_bwd_vec<f16_t>, grid, dim3(64), 0, st, (const f16_t*)cx, (const f16_t*)h,
                          (const f16_t*)z, z_ld, Dv, scale, (const f16_t*)dy, (f16_t*)dcx, (f16_t*)dh, (f16_t*)dz,
-                         part, n_rows, C);
+                         dz_ld, part, n_rows, C);
     else
       hipLaunchKernelGGL(readout_bwd_vec<float>, grid, dim3(64), 0, st, (const float*)cx, (const float*)h,
                          (const float*)z, z_ld, Dv, scale, (const float*)dy, (float*)dcx, (float*)dh, (float*)dz,
-                         part, n_rows, C);
+                         dz_ld, part, n_rows, C);
   } else {
     nblk = (n_rows + kRows - 1) / kRows;
     const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)nblk);
     hipLaunchKernelGGL(readout_bwd_kernel, grid, dim3(kThreads), 0, st, cx, h, z, z_ld, Dv, scale, dy, dcx, dh, dz,
-                       part, n_rows, C, cx_dtype, h_dtype, z_dtype, dy_dtype, dcx_dtype, dh_dtype, dz_dtype);
+                       dz_ld, part, n_rows, C, cx_dtype, h_dtype, z_dtype, dy_dtype, dcx_dtype, dh_dtype, dz_dtype);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));

@@ -19,6 +19,7 @@ and a missing library raises.
 import torch
 
 from naju_amd import _lib
+from naju_amd.gradsink import sink_of
 
 _DT = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16}
 
@@ -56,7 +57,7 @@ def _rows(x):
 
 class _DwConv(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, bias, add, silu, out_dtype):
+    def forward(ctx, x, w, bias, add, silu, out_dtype, x_sink, add_sink):
         B, T, C = x.shape
         K = w.shape[1]
         x, ldx = _rows(x)
@@ -72,6 +73,8 @@ class _DwConv(torch.autograd.Function):
         ctx.save_for_backward(x, w, bias)
         ctx.silu = silu
         ctx.add_dtype = None if add is None else add.dtype
+        # pieces of a gradsink.split(): their gradients go into its buffer
+        ctx.x_sink, ctx.add_sink = x_sink, add_sink
         return y
 
     @staticmethod
@@ -83,19 +86,34 @@ class _DwConv(torch.autograd.Function):
             dy = dy.float()
         dy = dy.contiguous()
         need_x, need_w, need_b, need_add = ctx.needs_input_grad[:4]
-        dx = torch.empty((B, T, C), dtype=x.dtype, device=x.device) if need_x else None
+        dx = None
+        if need_x:
+            if ctx.x_sink is not None:
+                sink, col = ctx.x_sink
+                dx = sink.slice(col, C)
+            else:
+                dx = torch.empty((B, T, C), dtype=x.dtype, device=x.device)
         dw = torch.empty((C, K), dtype=torch.float32, device=x.device) if need_w else None
         db = torch.empty((C,), dtype=torch.float32, device=x.device) if (need_b and bias is not None) else None
-        if dx is not None or dw is not None or db is not None:
+        # the gradient of add is dy: written by the kernel into the sink's
+        # buffer (in add's dtype and row stride), or a cast of dy
+        dadd = None
+        if need_add and ctx.add_dtype is not None and ctx.add_sink is not None and not ctx.silu:
+            sink, col = ctx.add_sink
+            dadd = sink.slice(col, C)
+        if dx is not None or dw is not None or db is not None or dadd is not None:
             L = _lib.lib()
             stream = torch.cuda.current_stream(x.device).cuda_stream
             nbytes = L.naju_dwconv_workspace_bytes(B, T, C, K)
             ws = _WS.get(x.device, stream, nbytes)
             _lib.check_mixer(L.naju_dwconv_bwd(
-                _ptr(x), x.stride(1), _ptr(w), _ptr(bias), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), B, T, C, K,
-                int(ctx.silu), _DT[x.dtype], _DT[dy.dtype], _DT[x.dtype], _ptr(ws), ws.numel(), stream))
-        dadd = dy.to(ctx.add_dtype) if (need_add and ctx.add_dtype is not None) else None
-        return dx, dw, db, dadd, None, None
+                _ptr(x), x.stride(1), _ptr(w), _ptr(bias), _ptr(dy), _ptr(dx), dx.stride(1) if dx is not None else C,
+                _ptr(dw), _ptr(db), _ptr(dadd), dadd.stride(1) if dadd is not None else C, B, T, C, K,
+                int(ctx.silu), _DT[x.dtype], _DT[dy.dtype], _DT[x.dtype],
+                _DT[dadd.dtype] if dadd is not None else 0, _ptr(ws), ws.numel(), stream))
+        if dadd is None and need_add and ctx.add_dtype is not None:
+            dadd = dy.to(ctx.add_dtype)
+        return dx, dw, db, dadd, None, None, None, None
 
 
 def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
@@ -115,10 +133,11 @@ def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
     if add is not None:
         if add.shape != x.shape:
             raise ValueError(f"add must have x's shape {tuple(x.shape)}, got {tuple(add.shape)}")
-        if add.dtype not in _DT:
-            add = add.float()
+    x_sink, add_sink = sink_of(x), sink_of(add)
     if x.dtype not in _DT:
-        x = x.float()
+        x, x_sink = x.float(), None
+    if add is not None and add.dtype not in _DT:
+        add, add_sink = add.float(), None
     if out_dtype is None:
         out_dtype = x.dtype
-    return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype)
+    return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype, x_sink, add_sink)

@@ -1,0 +1,70 @@
+"""Splits whose consumers write their gradients in place.
+
+Autograd's backward of ``t.split(sizes, -1)`` concatenates the pieces'
+gradients into a new tensor of t's shape: one more read and write of t's
+size. ``split(t, sizes)`` returns the same views, tagged with a GradSink.
+A HIP kernel that consumes a piece (the depthwise convolution's x or add,
+the readout's z) asks the sink for that piece's slice of one gradient
+buffer of t's shape and writes its gradient there, with t's row stride.
+The split's backward then returns that buffer itself, copying in only the
+pieces whose gradient arrived in another tensor (a piece that also had
+other consumers, whose gradients autograd summed elsewhere, or one whose
+consumer does not use the sink) and zero-filling pieces without a gradient.
+"""
+import torch
+
+
+class GradSink:
+    """One gradient buffer, allocated at the first request of a backward."""
+
+    def __init__(self, like):
+        self.shape, self.dtype, self.device = like.shape, like.dtype, like.device
+        self.buf = None
+
+    def slice(self, col0, width):
+        if self.buf is None:
+            self.buf = torch.empty(self.shape, dtype=self.dtype, device=self.device)
+        return self.buf[..., col0:col0 + width]
+
+
+class _Split(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, t, sizes, sink):
+        ctx.sizes = sizes
+        ctx.sink = sink
+        return t.split(list(sizes), dim=-1)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        sink, sizes = ctx.sink, ctx.sizes
+        if sink.buf is None:
+            parts = [g if g is not None else torch.zeros(sink.shape[:-1] + (w,), dtype=sink.dtype, device=sink.device)
+                     for g, w in zip(grads, sizes)]
+            return torch.cat(parts, dim=-1), None, None
+        buf = sink.buf
+        sink.buf = None  # a later backward through the same graph allocates anew
+        col = 0
+        for g, w in zip(grads, sizes):
+            dst = buf[..., col:col + w]
+            if g is None:
+                dst.zero_()
+            elif g.data_ptr() != dst.data_ptr() or g.stride() != dst.stride() or g.dtype != dst.dtype:
+                dst.copy_(g)
+            col += w
+        return buf, None, None
+
+
+def split(t, sizes):
+    """t.split(sizes, -1), with the pieces tagged for in-place gradients."""
+    sink = GradSink(t)
+    pieces = _Split.apply(t, tuple(int(w) for w in sizes), sink)
+    col = 0
+    for p, w in zip(pieces, sizes):
+        p._naju_sink = (sink, col)
+        col += int(w)
+    return pieces
+
+
+def sink_of(t):
+    """(sink, first column) of a piece returned by split(), else None."""
+    return getattr(t, "_naju_sink", None) if t is not None else None

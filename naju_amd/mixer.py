@@ -31,6 +31,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
+from naju_amd import gradsink
 from naju_amd.dwconv import dwconv
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
@@ -148,7 +149,13 @@ class NajuMixer(nn.Module):
         return F.silu(_causal_dwconv(x, self.conv1d))
 
     def forward(self, u):
-        x, z = self.in_proj(u).chunk(2, dim=-1)
+        xz = self.in_proj(u)
+        if xz.is_cuda:
+            # x feeds the content convolution and z the readout; both write
+            # their gradients straight into one buffer for in_proj
+            x, z = gradsink.split(xz, [self.d_inner, self.d_inner])
+        else:
+            x, z = xz.chunk(2, dim=-1)
         h = self._content(x)
         if h.is_cuda and not self.gate_rank:
             # f_proj, i_proj and x_proj in one GEMM over h (the same weights:
@@ -157,7 +164,7 @@ class NajuMixer(nn.Module):
             # the convolutions read their slices in place
             di, N = self.d_inner, self.d_state
             w = torch.cat([self.f_proj.weight, self.i_proj.weight, self.x_proj.weight], 0)
-            p_f, p_i, Bm, Cm = F.linear(h, w).split([di, di, N, N], dim=-1)
+            p_f, p_i, Bm, Cm = gradsink.split(F.linear(h, w), [di, di, N, N])
             f_logit = self._gate_logit(h, None, self.f_conv, self.f_bias, p=p_f)
             i_logit = self._gate_logit(h, None, self.i_conv, self.i_bias, p=p_i)
         else:

@@ -15,6 +15,7 @@ import torch
 
 from naju_amd import _lib
 from naju_amd.dwconv import _DT, _WS, _ptr
+from naju_amd.gradsink import sink_of
 
 
 def _rows_of(t):
@@ -27,7 +28,7 @@ def _rows_of(t):
 
 class _Readout(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, cx, h, z, Dv, scale, out_dtype):
+    def forward(ctx, cx, h, z, Dv, scale, out_dtype, z_sink):
         B, T, C = h.shape
         z, z_ld = _rows_of(z)
         y = torch.empty((B, T, C), dtype=out_dtype, device=h.device)
@@ -38,6 +39,7 @@ class _Readout(torch.autograd.Function):
             _DT[cx.dtype], _DT[h.dtype], _DT[z.dtype], _DT[out_dtype], stream))
         ctx.save_for_backward(cx, h, z, Dv)
         ctx.scale = float(scale)
+        ctx.z_sink = z_sink  # z is a piece of a gradsink.split(): dz goes into its buffer
         return y
 
     @staticmethod
@@ -50,7 +52,13 @@ class _Readout(torch.autograd.Function):
         need_cx, need_h, need_z, need_D = ctx.needs_input_grad[:4]
         dcx = torch.empty((B, T, C), dtype=cx.dtype, device=h.device) if need_cx else None
         dh = torch.empty((B, T, C), dtype=h.dtype, device=h.device) if need_h else None
-        dz = torch.empty((B, T, C), dtype=z.dtype, device=h.device) if need_z else None
+        dz = None
+        if need_z:
+            if ctx.z_sink is not None:
+                sink, col = ctx.z_sink
+                dz = sink.slice(col, C)
+            else:
+                dz = torch.empty((B, T, C), dtype=z.dtype, device=h.device)
         dD = torch.empty((C,), dtype=torch.float32, device=h.device) if need_D else None
         if any(t is not None for t in (dcx, dh, dz, dD)):
             L = _lib.lib()
@@ -59,9 +67,10 @@ class _Readout(torch.autograd.Function):
             ws = _WS.get(h.device, stream, nbytes)
             _lib.check_mixer(L.naju_readout_bwd(
                 _ptr(cx), _ptr(h), _ptr(z), z.stride(1), _ptr(Dv), ctx.scale, _ptr(dy), _ptr(dcx), _ptr(dh),
-                _ptr(dz), _ptr(dD), B * T, C, _DT[cx.dtype], _DT[h.dtype], _DT[z.dtype], _DT[dy.dtype],
-                _DT[cx.dtype], _DT[h.dtype], _DT[z.dtype], _ptr(ws), ws.numel(), stream))
-        return dcx, dh, dz, dD, None, None
+                _ptr(dz), dz.stride(1) if dz is not None else C, _ptr(dD), B * T, C, _DT[cx.dtype], _DT[h.dtype],
+                _DT[z.dtype], _DT[dy.dtype], _DT[cx.dtype], _DT[h.dtype], _DT[z.dtype], _ptr(ws), ws.numel(),
+                stream))
+        return dcx, dh, dz, dD, None, None, None
 
 
 def readout(cx, h, z, D, scale, out_dtype=None):
@@ -74,9 +83,10 @@ def readout(cx, h, z, D, scale, out_dtype=None):
         raise ValueError(f"D must be [C] = [{h.shape[2]}], got {tuple(D.shape)}")
     cx = (cx if cx.dtype in _DT else cx.float()).contiguous()
     h = (h if h.dtype in _DT else h.float()).contiguous()
+    z_sink = sink_of(z)
     if z.dtype not in _DT:
-        z = z.float()
+        z, z_sink = z.float(), None
     Dv = D if D.dtype == torch.float32 else D.float()
     if out_dtype is None:
         out_dtype = torch.promote_types(torch.promote_types(cx.dtype, h.dtype), Dv.dtype)
-    return _Readout.apply(cx, h, z, Dv.contiguous(), float(scale), out_dtype)
+    return _Readout.apply(cx, h, z, Dv.contiguous(), float(scale), out_dtype, z_sink)

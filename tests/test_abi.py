@@ -226,12 +226,15 @@ def test_dwconv_workspace_size_and_check():
     assert L.naju_dwconv_workspace_bytes(1, 65, 8, 4) >= 2 * 8 * 5 * 4
     assert L.naju_dwconv_workspace_bytes(1, 8, 8, 9) == 0
     fake = 0x1000
-    rc = L.naju_dwconv_bwd(fake, 16, fake, None, fake, fake, fake, None, 2, 8, 16, 4, 0, F32, F32, F32,
-                           None, 0, None)
-    assert rc == _lib.ERR_WORKSPACE and b"workspace" in L.naju_mixer_last_error()
+    def bwd(dx_ld=16, dw=fake, dadd=None, dadd_ld=16, batch=2, act=0):
+        return L.naju_dwconv_bwd(fake, 16, fake, None, fake, fake, dx_ld, dw, None, dadd, dadd_ld, batch, 8, 16, 4,
+                                 act, F32, F32, F32, BF16, None, 0, None)
+    assert bwd() == _lib.ERR_WORKSPACE and b"workspace" in L.naju_mixer_last_error()
+    assert bwd(dx_ld=15) == _lib.ERR_INVALID and b"dx_ld" in L.naju_mixer_last_error()
+    assert bwd(dadd=fake, dadd_ld=12) == _lib.ERR_INVALID and b"dadd_ld" in L.naju_mixer_last_error()
+    assert bwd(dadd=fake, act=1) == _lib.ERR_UNSUPPORTED
     # dx only: no sums, no workspace needed -- but it would launch, so check only the no-op case
-    assert L.naju_dwconv_bwd(fake, 16, fake, None, fake, fake, None, None, 0, 8, 16, 4, 0, F32, F32, F32,
-                             None, 0, None) == _lib.OK
+    assert bwd(dw=None, batch=0) == _lib.OK
 
 
 def test_dwconv_python_rejects_cpu_tensors():
@@ -252,12 +255,15 @@ def test_readout_host_checks():
     assert fwd(y=None) == _lib.ERR_INVALID
     assert fwd(rows=0) == _lib.OK and L.naju_mixer_last_error() == b""
     assert L.naju_readout_workspace_bytes(16384, 1536) >= 256 * 1536 * 4
-    rc = L.naju_readout_bwd(fake, fake, fake, 16, fake, 0.125, fake, None, None, None, fake, 4, 16,
+    rc = L.naju_readout_bwd(fake, fake, fake, 16, fake, 0.125, fake, None, None, None, 16, fake, 4, 16,
                             *([F32] * 7), None, 0, None)
     assert rc == _lib.ERR_WORKSPACE
-    rc = L.naju_readout_bwd(None, fake, fake, 16, fake, 0.125, fake, None, None, fake, None, 4, 16,
+    rc = L.naju_readout_bwd(None, fake, fake, 16, fake, 0.125, fake, None, None, fake, 16, None, 4, 16,
                             *([F32] * 7), None, 0, None)
     assert rc == _lib.ERR_INVALID and b"cx" in L.naju_mixer_last_error()
+    rc = L.naju_readout_bwd(fake, fake, fake, 16, fake, 0.125, fake, None, None, fake, 8, None, 4, 16,
+                            *([F32] * 7), None, 0, None)
+    assert rc == _lib.ERR_INVALID and b"dz_ld" in L.naju_mixer_last_error()
 
 
 def test_xent_host_checks():

@@ -163,3 +163,36 @@ def test_dwconv_strided_add(gpu, x_dtype, C):
     gr = torch.zeros(B, T, 3 * C + 8, dtype=torch.float64)
     gr[..., C:2 * C] = dy.to(x_dtype).double()
     assert _rel(wg.grad, gr) < 1e-6
+
+
+def test_gradsink_split_matches_plain_split(gpu):
+    """Pieces of gradsink.split() whose consumers write their gradients in
+    place give the same gradient as autograd's split + concatenation, also
+    when a piece has a second consumer (summed gradient: copied in) or none
+    (zero-filled)."""
+    from naju_amd import gradsink
+    from naju_amd.readout import readout
+    torch.manual_seed(9)
+    B, T, C = 2, 40, 32
+    base = torch.randn(B, T, 3 * C + 16, device=gpu).to(torch.bfloat16)
+    cx = torch.randn(B, T, C, device=gpu).to(torch.bfloat16)
+    h = torch.randn(B, T, C, device=gpu).to(torch.bfloat16)
+    w = torch.randn(C, 1, 4, device=gpu) / 4
+    bias = torch.randn(C, device=gpu)
+    D = torch.randn(C, device=gpu)
+    gy = [torch.randn(B, T, C, device=gpu) for _ in range(3)]
+    grads = []
+    for use_sink in (True, False):
+        t = base.clone().requires_grad_(True)
+        if use_sink:
+            x, z, p, q = gradsink.split(t, [C, C, C, 16])
+        else:
+            x, z, p, q = t.split([C, C, C, 16], dim=-1)
+        y0 = dwconv(x, w, bias, silu=True, out_dtype=torch.float32)
+        y1 = readout(cx, h, z, D, 0.5, out_dtype=torch.float32)
+        y2 = dwconv(h, w, bias, add=p, out_dtype=torch.float32)
+        loss = (y0 * gy[0]).sum() + (y1 * gy[1]).sum() + (y2 * gy[2]).sum() + 0.5 * x.float().sum()
+        loss.backward()
+        grads.append(t.grad.clone())
+    assert torch.equal(grads[0], grads[1])
+    assert torch.count_nonzero(grads[0][..., 3 * C:]) == 0
