@@ -1490,6 +1490,165 @@ __device__ __forceinline__ float from_upper(float x) {
   }
 }
 
+// General-N forward with Q = NP/4 lanes per channel, four states per lane,
+// over the whole of T: lane (channel c, quarter q) holds x[n] for
+// n = 4q .. 4q+3. With Q times the lanes per channel of gc_fwd_kernel it
+// needs no time segments (no segment-map pass, no carry pass) once the
+// batch x channel-group grid fills the GPU on its own. Per
+// 32-row sub-chunk the workgroup stages B and C ([row][n]) and the channels'
+// gates f, w = i*u and u ([row][channel]) in LDS, each value computed once;
+// a lane's part of y_t = sum_n C_t[n] x_t[n] is summed over the channel's Q
+// lanes by a transposing butterfly over 8 rows at a time, and y goes back
+// through LDS so that its stores are row-contiguous.
+constexpr int kGqW = 4;   // waves per workgroup
+constexpr int kGqRG = 8;  // rows per reduction group
+
+template <int NP>
+__global__ __launch_bounds__(64 * kGqW) void gq_fwd_kernel(const ScanArgs a, int x_dt, int g_dt, int y_dt) {
+  constexpr int Q = NP / 4;          // lanes per channel
+  constexpr int CPW = 64 / Q;        // channels per wave
+  constexpr int CPB = CPW * kGqW;    // channels per workgroup
+  constexpr int NT = 64 * kGqW;      // threads
+  constexpr int EB = kGnCK * NP / NT;   // B / C values staged per thread
+  constexpr int EG = kGnCK * CPB / NT;  // gate values staged per thread
+  static_assert(Q >= 4 && Q <= 16 && EB >= 1 && EG >= 1, "tile shape");
+  __shared__ __align__(16) float s_B[kGnCK][NP];
+  __shared__ __align__(16) float s_C[kGnCK][NP];
+  __shared__ float s_f[kGnCK][CPB], s_w[kGnCK][CPB], s_u[kGnCK][CPB], s_y[kGnCK][CPB];
+  const int N = a.N;
+  const int64_t T = a.T, D = a.D;
+  const int ndt = (int)((D + CPB - 1) / CPB);
+  const int b = (int)(blockIdx.x / (uint32_t)ndt);
+  const int dtile = (int)(blockIdx.x - (uint32_t)b * (uint32_t)ndt);
+  const int64_t dbase = (int64_t)dtile * CPB;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int cl = wv * CPW + lane / Q;  // this lane's channel within the workgroup
+  const int q = lane % Q;
+  const int64_t d = dbase + cl;
+  const bool dok = d < D;
+  const int64_t rowbase = (int64_t)b * T;
+  const int KC = (int)((T + kGnCK - 1) / kGnCK);
+  const int sc0 = 0, sc1 = KC;
+  const float* xin = a.h0 ? a.h0 + (int64_t)b * D * N : nullptr;
+  float x[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int n = 4 * q + k;
+    x[k] = (xin && dok && n < N) ? xin[d * N + n] : 0.f;
+  }
+  // staging roles for the gates: entry k = e * NT + tid -> (row, channel)
+  // two register sets of staged inputs: sub-chunk sc is loaded while
+  // sc - 2 is computed (a wave's compute of one sub-chunk is shorter than
+  // the load latency)
+  float gu0[EG], gf0[EG], gi0[EG], vb0[EB], vc0[EB];
+  float gu1[EG], gf1[EG], gi1[EG], vb1[EB], vc1[EB];
+  auto load = [&](int64_t t0, float (&gu)[EG], float (&gf)[EG], float (&gi)[EG], float (&vb)[EB],
+                  float (&vc)[EB]) {
+#pragma unroll
+    for (int e = 0; e < EG; ++e) {
+      const int k = e * NT + tid;
+      const int r = k / CPB, c = k % CPB;
+      const int64_t t = t0 + r < T ? t0 + r : T - 1;
+      const int64_t dc = dbase + c < D ? dbase + c : D - 1;
+      const int64_t o = (rowbase + t) * D + dc;
+      gu[e] = ld_any(a.u, x_dt, o);
+      gf[e] = ld_any(a.fl, g_dt, o);
+      gi[e] = ld_any(a.il, g_dt, o);
+    }
+    gn_ld_bc<NP, EB, NT>(a, a.Bm, b, t0, vb);
+    gn_ld_bc<NP, EB, NT>(a, a.Cm, b, t0, vc);
+  };
+  auto body = [&](int sc, float (&gu)[EG], float (&gf)[EG], float (&gi)[EG], float (&vb)[EB], float (&vc)[EB]) {
+    const int64_t t0 = (int64_t)sc * kGnCK;
+    const int rows = (int)((T - t0) < kGnCK ? (T - t0) : kGnCK);
+    __syncthreads();  // the previous sub-chunk's tiles are consumed, its y stored
+#pragma unroll
+    for (int e = 0; e < EG; ++e) {
+      const int k = e * NT + tid;
+      const int r = k / CPB, c = k % CPB;
+      const bool ok = r < rows && dbase + c < D;
+      const float f = sigm(gf[e]);
+      s_f[r][c] = ok ? f : 1.f;
+      s_w[r][c] = ok ? sigm(gi[e]) * gu[e] : 0.f;
+      s_u[r][c] = ok ? gu[e] : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < EB; ++e) {
+      const int k = e * NT + tid;
+      const int r = k / NP, n = k % NP;
+      const bool ok = r < rows && n < N;
+      s_B[r][n] = ok ? vb[e] : 0.f;
+      s_C[r][n] = ok ? vc[e] : 0.f;
+    }
+    __syncthreads();
+    if (sc + 2 < sc1) load(t0 + 2 * kGnCK, gu, gf, gi, vb, vc);  // while this one runs
+    // the state entering this sub-chunk: the backward's checkpoint
+    if (a.ckpt && dok) {
+      float* ck = a.ckpt + (((int64_t)b * KC + sc) * D + d) * N;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (4 * q + k < N) ck[4 * q + k] = x[k];
+    }
+#pragma unroll
+    for (int g = 0; g < kGnCK; g += kGqRG) {
+      float yp[kGqRG];
+#pragma unroll
+      for (int rr = 0; rr < kGqRG; ++rr) {
+        const int r = g + rr;
+        const float f = s_f[r][cl], w = s_w[r][cl];
+        const float4 b4 = *(const float4*)&s_B[r][4 * q];
+        const float4 c4 = *(const float4*)&s_C[r][4 * q];
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          x[k] *= f;
+          x[k] = fmaf(w, (&b4.x)[k], x[k]);
+          acc = fmaf((&c4.x)[k], x[k], acc);
+        }
+        yp[rr] = acc;
+      }
+      // sums over the channel's Q lanes: lane q then holds row q / (Q / 8)
+      // of the group (Q >= 8), or rows 2q, 2q+1 (Q = 4)
+      trd_step<Q, kGqRG, kGqRG>(yp, lane);
+      if constexpr (Q >= kGqRG) {
+        constexpr int SP = Q / kGqRG;
+        if (q % SP == 0) {
+          const int r = g + q / SP;
+          s_y[r][cl] = fmaf(a.Dsk[dok ? d : 0], s_u[r][cl], yp[0]);
+        }
+      } else {
+        constexpr int PER = kGqRG / Q;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int r = g + q * PER + j;
+          s_y[r][cl] = fmaf(a.Dsk[dok ? d : 0], s_u[r][cl], yp[j]);
+        }
+      }
+    }
+    __syncthreads();
+    // y of the sub-chunk, row-contiguous stores
+#pragma unroll
+    for (int e = 0; e < EG; ++e) {
+      const int k = e * NT + tid;
+      const int r = k / CPB, c = k % CPB;
+      if (r < rows && dbase + c < D) st_any(a.y, y_dt, (rowbase + t0 + r) * D + dbase + c, s_y[r][c]);
+    }
+  };
+  load((int64_t)sc0 * kGnCK, gu0, gf0, gi0, vb0, vc0);
+  if (sc0 + 1 < sc1) load((int64_t)(sc0 + 1) * kGnCK, gu1, gf1, gi1, vb1, vc1);
+  for (int sc = sc0; sc < sc1; sc += 2) {
+    body(sc, gu0, gf0, gi0, vb0, vc0);
+    if (sc + 1 < sc1) body(sc + 1, gu1, gf1, gi1, vb1, vc1);
+  }
+  if (a.hT && dok) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (4 * q + k < N) a.hT[((int64_t)b * D + d) * N + 4 * q + k] = x[k];
+  }
+}
+
 template <int NP, int DT, int W>
 __global__ __launch_bounds__(64 * W) void gn_bwd_kernel(const ScanArgs a, int x_dt, int g_dt, int du_dt,
                                                            int dg_dt) {
@@ -1978,10 +2137,16 @@ struct Layout {
 #endif
 constexpr int kGnTargetWgs = NAJU_GN_TARGET_WGS;
 constexpr int kGcTargetWaves = 2048;
+// gq_fwd_kernel serves a forward whose batch x channel-group grid holds at
+// least three 4-wave workgroups per CU (256 CUs); smaller grids take the
+// segmented gc_fwd_kernel, whose time segments supply the parallelism.
+constexpr int kGqMinWgs = 768;
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int np_of(int64_t N);
+bool gq_ok(int64_t N, int64_t batch, int64_t D);
+int gq_channels(int64_t N);
 int gn_bwd_dt(int np);
 
 Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd) {
@@ -2003,7 +2168,7 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.n_tiles = (int)(batch * l.n_dtiles);
   l.nseg = 1;
   l.seg_sc = l.K;
-  if (N > 1 && l.n_tiles > 0 && l.K > 0) {
+  if (N > 1 && l.n_tiles > 0 && l.K > 0 && (bwd || !gq_ok(N, batch, D))) {
     // forward (lanes over channels): about kGcTargetWaves waves; backward
     // (8-wave workgroups over 64 channels): about kGnTargetWgs workgroups
     const int64_t per_seg = bwd ? l.n_tiles : batch * ((D + 63) / 64);
@@ -2118,6 +2283,21 @@ gn_bwd_t pick_gn_bwd(int np) {
 
 // Workgroups per time segment of the general-N forward.
 int64_t gc_tiles(int64_t batch, int64_t D) { return batch * ((D + kGcCH - 1) / kGcCH); }
+
+// The forward without time segments (gq_fwd_kernel): 16 <= NP <= 64 and a
+// grid that fills the GPU.
+int gq_channels(int64_t N) { return 64 / (np_of((int)N) / 4) * kGqW; }
+bool gq_ok(int64_t N, int64_t batch, int64_t D) {
+  const int np = np_of((int)N);
+  return N > 1 && np >= 16 && np <= 64 && batch * ((D + gq_channels(N) - 1) / gq_channels(N)) >= kGqMinWgs;
+}
+gn_fwd_t pick_gq_fwd(int np) {
+  switch (np) {
+    case 16: return gq_fwd_kernel<16>;
+    case 32: return gq_fwd_kernel<32>;
+    default: return gq_fwd_kernel<64>;
+  }
+}
 
 gn_fwd_t pick_gc_fwd(int np, bool map) {
   switch (np) {
@@ -2259,6 +2439,16 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
     a.segF = (float*)(ws + l.off_segF);
     a.segZ = (float*)(ws + l.off_segZ);
     a.seg0 = (float*)(ws + l.off_seg0);
+    if (gq_ok(N, batch, D)) {
+      // one workgroup per (batch row, channel group), over all of T
+      const int64_t grid = batch * ((D + gq_channels(N) - 1) / gq_channels(N));
+      if (grid > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+      hipLaunchKernelGGL(pick_gq_fwd(np_of(N)), dim3((unsigned)grid), dim3(64 * kGqW), 0, st, a, x_dtype, gate_dtype,
+                         y_dt);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+      return NAJU_OK;
+    }
     if (gc_tiles(batch, D) * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
     rc = gn_segments(a, l, x_dtype, gate_dtype, false, st);
     if (rc) return rc;

@@ -123,3 +123,16 @@ def test_full_size_c2_n64_channel_slice(gpu):
     check("dh0", g["dh0"].cpu().numpy()[bb, dd], rg["dh0"], tol_for(torch.float32))
     ref_dD = (ins["dy"].float() * ins["u"].float()).sum((0, 1)).double().cpu().numpy()
     assert np.max(np.abs(g["dD"].double().cpu().numpy() - ref_dD)) <= 1e-4 * max(1.0, np.abs(ref_dD).max())
+
+
+@pytest.mark.parametrize("N,D", [(48, 1536), (32, 3072), (16, 6144)])
+def test_wide_grid_forward_general_n(gpu, N, D):
+    """Batch x channel grids that fill the GPU on their own take the forward
+    with four states per lane and no time segments (the C5 layer is one:
+    8 x 1536 channels at N = 64): ragged T, N below its power-of-two tile,
+    h0, and the mixer's dtypes (bf16 u, B, C; f32 gates)."""
+    ins = rand_inputs(8, 70, D, N, seed=N, dtype=torch.bfloat16, gate_dtype=torch.float32,
+                      bc_dtype=torch.bfloat16, h0_std=0.3)
+    y, g = run_hip(ins, gpu)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
