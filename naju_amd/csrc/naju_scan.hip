@@ -2103,10 +2103,10 @@ size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 #define NAJU_F_P 1
 #endif
 #ifndef NAJU_B_V
-#define NAJU_B_V 2
+#define NAJU_B_V 1
 #endif
 #ifndef NAJU_B_R
-#define NAJU_B_R 8
+#define NAJU_B_R 16
 #endif
 #ifndef NAJU_B_W
 #define NAJU_B_W 4
