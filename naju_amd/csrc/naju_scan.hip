@@ -826,15 +826,16 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
       for (int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < n4; i4 += stride) {
         float sb[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {0.f, 0.f, 0.f, 0.f};
         int q = 0;
-        for (; q + 4 <= n_parts; q += 4) {
-          float4 vb[4], vc[4];
+        // eight parts of each quantity in flight per thread
+        for (; q + 8 <= n_parts; q += 8) {
+          float4 vb[8], vc[8];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < 8; ++u) {
             if (dB) vb[u] = pb[(int64_t)(q + u) * n4 + i4];
             if (dC) vc[u] = pc[(int64_t)(q + u) * n4 + i4];
           }
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < 8; ++u) {
             sb[0] += vb[u].x, sb[1] += vb[u].y, sb[2] += vb[u].z, sb[3] += vb[u].w;
             sc[0] += vc[u].x, sc[1] += vc[u].y, sc[2] += vc[u].z, sc[3] += vc[u].w;
           }
