@@ -223,6 +223,7 @@ __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, c
 // aligned; the scalar kernels above serve every other case.
 constexpr int kVec = 8;
 constexpr int kVRows = 16;
+constexpr int kVRowsB = 32;  // rows per block of the vector conv backward (a longer reverse walk per halo)
 
 template <typename T>
 __device__ __forceinline__ void ld8(const T* p, float (&o)[kVec]) {
@@ -315,8 +316,8 @@ __global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, 
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
   if (c0 >= C) return;
   const int64_t b = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.y * kVRows;
-  const int64_t t1 = t0 + kVRows < T ? t0 + kVRows : T;
+  const int64_t t0 = (int64_t)blockIdx.y * kVRowsB;
+  const int64_t t1 = t0 + kVRowsB < T ? t0 + kVRowsB : T;
   float wr[kVec][K], bc[kVec];
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
@@ -624,7 +625,7 @@ dwb_vec_t pick_bwd_vec(const void* x, int64_t x_ld, const float* w, const float*
                        int64_t dx_ld, const void* dadd, int64_t dadd_ld, int64_t T, int64_t C, int K, int act,
                        int x_dt, int dy_dt, int dx_dt, int dadd_dt) {
   if (K != 4 || C % kVec || x_ld % kVec || dx_ld % kVec || (dadd && dadd_ld % kVec) ||
-      (T + kVRows - 1) / kVRows > 65535)
+      (T + kVRowsB - 1) / kVRowsB > 65535)
     return nullptr;
   if (!al16(x) || !al16(w) || !al16(dy) || (bias && !al16(bias)) || (dx && !al16(dx)) || (dadd && !al16(dadd)))
     return nullptr;
@@ -961,7 +962,9 @@ int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bi
 
 size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K) {
   if (check(batch, T, C, K, 0, C) != NAJU_OK) return 0;
-  return (size_t)batch * ((T + kVRows - 1) / kVRows) * C * (K + 1) * sizeof(float) + 256;
+  // partial rows: one per block of the scalar (kRows) or vector (kVRowsB) backward
+  const int64_t rows = kVRowsB < kRows ? kVRowsB : kRows;
+  return (size_t)batch * ((T + rows - 1) / rows) * C * (K + 1) * sizeof(float) + 256;
 }
 
 int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
@@ -995,7 +998,7 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
   int64_t nblk;
   if (dwb_vec_t kv = pick_bwd_vec(x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, T, C, K, act, x_dtype, dy_dtype,
                                   dx_dtype, dadd_dtype)) {
-    const int64_t ntb = (T + kVRows - 1) / kVRows;
+    const int64_t ntb = (T + kVRowsB - 1) / kVRowsB;
     const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)ntb, (unsigned)batch);
     hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C);
     nblk = batch * ntb;
