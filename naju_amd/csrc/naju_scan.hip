@@ -806,16 +806,61 @@ __device__ __forceinline__ float sum_parts(const float* __restrict__ p, int n_pa
 //     partB/partC[q*btn + i] (consecutive threads read consecutive i);
 //   blocks [n_bc_blocks, ...): dD[d] = sum over the n_rows rows of
 //     partD[row][d], 64 channels per block; wave w of 16 sums rows
-//     w, w+16, ... with four interleaved accumulators, then the 16 wave
-//     sums are added in wave order.
+//     w, w+16, ... (32 loads in flight) with four interleaved
+//     accumulators, then the 16 wave sums are added in wave order.
 __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ partB,
                                                     const float* __restrict__ partC, int n_parts, int64_t btn,
                                                     void* dB, void* dC, int bc_dt, int n_bc_blocks,
                                                     const float* __restrict__ partD, int64_t n_rows, int64_t D,
-                                                    float* __restrict__ dD) {
+                                                    float* __restrict__ dD, int bc_split) {
   __shared__ float s_acc[16][64];
+  __shared__ float4 s_b4[16][64], s_c4[16][64];
   if ((int)blockIdx.x < n_bc_blocks) {
     const int64_t stride = (int64_t)n_bc_blocks * blockDim.x;
+    if (bc_split) {
+      // few entries (btn % 4 == 0): a block takes 64 float4 entries and its
+      // 16 waves split the parts, wave k summing the k-th run of
+      // ceil(n_parts / 16) consecutive parts; the 16 runs are then added in
+      // run order, so far more workgroups share the reads
+      const int j = (int)threadIdx.x & 63, k = (int)threadIdx.x >> 6;
+      const int64_t n4 = btn / 4;
+      const int64_t i4 = (int64_t)blockIdx.x * 64 + j;
+      const int per = (n_parts + 15) / 16;
+      const int q0 = k * per, q1 = q0 + per < n_parts ? q0 + per : n_parts;
+      float4 sb = make_float4(0.f, 0.f, 0.f, 0.f), sc = sb;
+      if (i4 < n4) {
+        const float4* pb = reinterpret_cast<const float4*>(partB);
+        const float4* pc = reinterpret_cast<const float4*>(partC);
+        for (int q = q0; q < q1; ++q) {
+          if (dB) {
+            const float4 v = pb[(int64_t)q * n4 + i4];
+            sb.x += v.x, sb.y += v.y, sb.z += v.z, sb.w += v.w;
+          }
+          if (dC) {
+            const float4 v = pc[(int64_t)q * n4 + i4];
+            sc.x += v.x, sc.y += v.y, sc.z += v.z, sc.w += v.w;
+          }
+        }
+      }
+      s_b4[k][j] = sb;
+      s_c4[k][j] = sc;
+      __syncthreads();
+      if (k == 0 && i4 < n4) {
+        float4 tb = s_b4[0][j], tc = s_c4[0][j];
+#pragma unroll
+        for (int m = 1; m < 16; ++m) {
+          const float4 vb = s_b4[m][j], vc = s_c4[m][j];
+          tb.x += vb.x, tb.y += vb.y, tb.z += vb.z, tb.w += vb.w;
+          tc.x += vc.x, tc.y += vc.y, tc.z += vc.z, tc.w += vc.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (dB) st_any(dB, bc_dt, 4 * i4 + e, (&tb.x)[e]);
+          if (dC) st_any(dC, bc_dt, 4 * i4 + e, (&tc.x)[e]);
+        }
+      }
+      return;
+    }
     if (btn % 4 == 0) {
       // four consecutive entries per thread, the parts of dB and dC loaded
       // four at a time with 16-byte loads, added in part order (the same
@@ -868,10 +913,15 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
   const int64_t d = (int64_t)(blockIdx.x - n_bc_blocks) * 64 + lane;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (d < D) {
+    // 32 rows of a wave in flight per round: at N = 1 a wave's whole share
+    // (512 rows over 16 waves at B = 8, T = 4096) is one memory round trip
     int64_t r = w;
-    for (; r + 48 < n_rows; r += 64) {
+    for (; r + 16 * 31 < n_rows; r += 16 * 32) {
+      float v[32];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] += partD[(r + 16 * u) * D + d];
+      for (int u = 0; u < 32; ++u) v[u] = partD[(r + 16 * u) * D + d];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) acc[u & 3] += v[u];
     }
     for (int u = 0; r < n_rows; r += 16, ++u) acc[u & 3] += partD[r * D + d];
   }
@@ -2566,12 +2616,17 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     const int64_t btn = batch * T * N;
     // enough workgroups for about one pass of the threads over the entries
     // (four per thread when btn % 4 == 0), at most 1024
+    // (when that leaves fewer than 128 workgroups and btn % 4 == 0, 64
+    // entries per workgroup with the parts split over its waves instead)
     const int64_t per = btn % 4 == 0 ? 4 * 1024 : 1024;
-    const int n_bc = (dB || dC) ? (int)((btn + per - 1) / per < 1024 ? (btn + per - 1) / per : 1024) : 0;
+    const int64_t n_plain = (btn + per - 1) / per;
+    const int bc_split = btn % 4 == 0 && n_plain < 128 ? 1 : 0;
+    const int64_t n_bc64 = bc_split ? (btn / 4 + 63) / 64 : (n_plain < 1024 ? n_plain : 1024);
+    const int n_bc = (dB || dC) ? (int)n_bc64 : 0;
     const int n_d = dD ? (int)((D + 63) / 64) : 0;
     hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
                        btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD,
-                       batch * (int64_t)(N == 1 ? l.K : l.nseg), D, dD);
+                       batch * (int64_t)(N == 1 ? l.K : l.nseg), D, dD, bc_split);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;
