@@ -112,6 +112,8 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit,
  *   dh0          [batch,D,N] float32 (gradient of h0)
  * Every gradient pointer may be NULL to skip it. ckpt must come from
  * naju_scan_fwd with the same inputs, shape and dtype codes.
+ * Shape limits beyond the forward's: N > 1 needs D < 2^25
+ * (NAJU_ERR_UNSUPPORTED otherwise).
  */
 int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   const void* B, const void* C, const float* D_skip,

@@ -2530,6 +2530,10 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
   if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC)) return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  // The general-N backward addresses a sub-chunk's [32 rows x channels]
+  // tiles with 32-bit byte offsets from the tile's first element.
+  if (N > 1 && D >= (1ll << 25))
+    return fail(NAJU_ERR_UNSUPPORTED, "the backward at N > 1 needs D < 2^25 channels, got %lld", (long long)D);
   const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || T == 0 || D == 0) {

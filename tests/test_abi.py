@@ -102,6 +102,7 @@ def test_fwd_argument_checks(kw, code, msg):
     (dict(dy=None), _lib.ERR_INVALID, "null"),
     (dict(T=-3), _lib.ERR_INVALID, "negative"),
     (dict(ws=None), _lib.ERR_WORKSPACE, "workspace"),
+    (dict(N=2, D=1 << 25), _lib.ERR_UNSUPPORTED, "2^25"),
 ])
 def test_bwd_argument_checks(kw, code, msg):
     L = _lib.lib()
