@@ -17,6 +17,9 @@
  * (a hipStream_t; NULL = the default stream), allocates nothing and never
  * synchronises the host.
  *
+ * Shape limits: batch, T, D <= 2^30; 1 <= N <= 128; N > 1 needs D < 2^25
+ * (NAJU_ERR_UNSUPPORTED otherwise).
+ *
  * dtype codes: the u-stream dtype covers u, y, dy and du; the gate dtype
  * covers f_logit, i_logit, dfl and dil; the bc dtype covers B, C, dB and dC.
  * Supported: u in {F32, BF16, F16}; gate and bc each either F32 or equal to
@@ -112,8 +115,6 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit,
  *   dh0          [batch,D,N] float32 (gradient of h0)
  * Every gradient pointer may be NULL to skip it. ckpt must come from
  * naju_scan_fwd with the same inputs, shape and dtype codes.
- * Shape limits beyond the forward's: N > 1 needs D < 2^25
- * (NAJU_ERR_UNSUPPORTED otherwise).
  */
 int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   const void* B, const void* C, const float* D_skip,

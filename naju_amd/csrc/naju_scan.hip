@@ -1019,23 +1019,33 @@ __device__ __forceinline__ void gn_ld_tile(const ScanArgs& a, const void* p, int
 // N are replaced by the caller.
 template <int NP, int EB, int NT = kGnThreads>
 __device__ __forceinline__ void gn_ld_bc(const ScanArgs& a, const void* p, int b, int64_t t0, float (&v)[EB]) {
-  int64_t idx[EB];
+  static_assert(NT % NP == 0, "staging rows");
+  // A uniform base (row t0 of batch row b) plus a 32-bit per-lane offset
+  // (at most kGnCK rows x N < 2^12 elements): rows past T are clamped to the
+  // last row, states past N to N - 1.
+  const int64_t tb = t0 < a.T ? t0 : a.T - 1;
+  const int rmax = (int)(a.T - tb < kGnCK ? a.T - tb : kGnCK) - 1;
+  const int64_t row0 = ((int64_t)b * a.T + tb) * a.N;
+  const int n = (int)threadIdx.x % NP;
+  const uint32_t nn = (uint32_t)(n < a.N ? n : a.N - 1);
+  uint32_t off[EB];
 #pragma unroll
   for (int e = 0; e < EB; ++e) {
-    const int k = e * NT + (int)threadIdx.x;
-    const int64_t t = t0 + k / NP;
-    const int n = k % NP;
-    idx[e] = ((int64_t)b * a.T + (t < a.T ? t : a.T - 1)) * a.N + (n < a.N ? n : a.N - 1);
+    const int r = e * (NT / NP) + (int)threadIdx.x / NP;
+    off[e] = (uint32_t)(r < rmax ? r : rmax) * (uint32_t)a.N + nn;
   }
   if (a.bc_dt == NAJU_DTYPE_F32) {
+    const float* q = (const float*)p + row0;
 #pragma unroll
-    for (int e = 0; e < EB; ++e) v[e] = ((const float*)p)[idx[e]];
+    for (int e = 0; e < EB; ++e) v[e] = q[off[e]];
   } else if (a.bc_dt == NAJU_DTYPE_BF16) {
+    const bf16_t* q = (const bf16_t*)p + row0;
 #pragma unroll
-    for (int e = 0; e < EB; ++e) v[e] = (float)((const bf16_t*)p)[idx[e]];
+    for (int e = 0; e < EB; ++e) v[e] = (float)q[off[e]];
   } else {
+    const f16_t* q = (const f16_t*)p + row0;
 #pragma unroll
-    for (int e = 0; e < EB; ++e) v[e] = (float)((const f16_t*)p)[idx[e]];
+    for (int e = 0; e < EB; ++e) v[e] = (float)q[off[e]];
   }
 }
 
@@ -2270,6 +2280,10 @@ int check_common(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g
   if (N > 128) return fail(NAJU_ERR_UNSUPPORTED, "N (d_state) must be <= 128, got %lld", (long long)N);
   if (T > (1ll << 30) || D > (1ll << 30) || batch > (1ll << 30))
     return fail(NAJU_ERR_INVALID, "dimension exceeds 2^30");
+  // The general-N kernels address a sub-chunk's [32 rows x channels] tiles
+  // with 32-bit offsets from the tile's first element.
+  if (N > 1 && D >= (1ll << 25))
+    return fail(NAJU_ERR_UNSUPPORTED, "N > 1 needs D < 2^25 channels, got %lld", (long long)D);
   return NAJU_OK;
 }
 
@@ -2530,10 +2544,6 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
   if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC)) return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
-  // The general-N backward addresses a sub-chunk's [32 rows x channels]
-  // tiles with 32-bit byte offsets from the tile's first element.
-  if (N > 1 && D >= (1ll << 25))
-    return fail(NAJU_ERR_UNSUPPORTED, "the backward at N > 1 needs D < 2^25 channels, got %lld", (long long)D);
   const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || T == 0 || D == 0) {

@@ -90,6 +90,7 @@ def _bwd(L, **kw):
     (dict(y=None), _lib.ERR_INVALID, "null"),
     (dict(ws=None), _lib.ERR_WORKSPACE, "workspace"),
     (dict(ws=256, wsb=16), _lib.ERR_WORKSPACE, "workspace"),
+    (dict(N=2, D=1 << 25), _lib.ERR_UNSUPPORTED, "2^25"),
 ])
 def test_fwd_argument_checks(kw, code, msg):
     L = _lib.lib()
