@@ -118,9 +118,18 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    # the timed region: K steps back to back, nothing else on the stream
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for k in range(K):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / K
+    # per-call durations (the roofline): K more steps with HIP events around
+    # each call, on the stream the kernels run on
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
     for k in range(K):
         ev[k][0].record(stream)
         fwd()
@@ -128,8 +137,6 @@ def main():
         bwd()
         ev[k][2].record(stream)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / K
     t_fwd = sorted(e[0].elapsed_time(e[1]) for e in ev)
     t_bwd = sorted(e[1].elapsed_time(e[2]) for e in ev)
     avg_fwd = sum(t_fwd) / K

@@ -1019,6 +1019,31 @@ __device__ __forceinline__ void gn_ld_tile(const ScanArgs& a, const void* p, int
 // N are replaced by the caller.
 template <int NP, int EB, int NT = kGnThreads>
 __device__ __forceinline__ void gn_ld_bc(const ScanArgs& a, const void* p, int b, int64_t t0, float (&v)[EB]) {
+  int64_t idx[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) {
+    const int k = e * NT + (int)threadIdx.x;
+    const int64_t t = t0 + k / NP;
+    const int n = k % NP;
+    idx[e] = ((int64_t)b * a.T + (t < a.T ? t : a.T - 1)) * a.N + (n < a.N ? n : a.N - 1);
+  }
+  if (a.bc_dt == NAJU_DTYPE_F32) {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) v[e] = ((const float*)p)[idx[e]];
+  } else if (a.bc_dt == NAJU_DTYPE_BF16) {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) v[e] = (float)((const bf16_t*)p)[idx[e]];
+  } else {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) v[e] = (float)((const f16_t*)p)[idx[e]];
+  }
+}
+
+// The same from a uniform tile base plus 32-bit lane offsets (the gq
+// forward's staging; the segmented forward keeps gn_ld_bc, which measured
+// faster there).
+template <int NP, int EB, int NT = kGnThreads>
+__device__ __forceinline__ void gq_ld_bc(const ScanArgs& a, const void* p, int b, int64_t t0, float (&v)[EB]) {
   static_assert(NT % NP == 0, "staging rows");
   // A uniform base (row t0 of batch row b) plus a 32-bit per-lane offset
   // (at most kGnCK rows x N < 2^12 elements): rows past T are clamped to the
@@ -1618,8 +1643,8 @@ __global__ __launch_bounds__(64 * kGqW) void gq_fwd_kernel(const ScanArgs a, int
       gf[e] = ld_any(a.fl, g_dt, o);
       gi[e] = ld_any(a.il, g_dt, o);
     }
-    gn_ld_bc<NP, EB, NT>(a, a.Bm, b, t0, vb);
-    gn_ld_bc<NP, EB, NT>(a, a.Cm, b, t0, vc);
+    gq_ld_bc<NP, EB, NT>(a, a.Bm, b, t0, vb);
+    gq_ld_bc<NP, EB, NT>(a, a.Cm, b, t0, vc);
   };
   auto body = [&](int sc, float (&gu)[EG], float (&gf)[EG], float (&gi)[EG], float (&vb)[EB], float (&vc)[EB]) {
     const int64_t t0 = (int64_t)sc * kGnCK;
