@@ -3,7 +3,7 @@
 A step is one forward (naju_scan_fwd) plus one backward (naju_scan_bwd) of the
 scan over one batch of synthetic input resident in HBM, through the C ABI on
 preallocated buffers (the hot path itself, no autograd bookkeeping). The
-default workload is BASELINE configuration 2: B=8, L=4096, D=1024, bf16
+default workload is benchmark configuration c2 (naju_amd.workloads.CONFIGS): B=8, L=4096, D=1024, bf16
 streams with fp32 state, N=1 (B=C=1), h0 ~ N(0, 0.1^2), dy ~ N(0,1).
 
 value = algorithmic bytes of fwd+bwd per step * K / wall time of K steps
@@ -162,7 +162,7 @@ def main():
         "vs_baseline": None,
         "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[xdt]
         + " streams, f32 state/accum",
-        "data": "synthetic (seeded; BASELINE.json config recipe)",
+        "data": "synthetic (seeded; the c2 gate/input recipe of naju_amd.workloads)",
         "config": {"workload": f"naju scan fwd+bwd {args.config}: B={Bsz} L={T} D={D} N={N}"
                    + (" B=C=1" if N == 1 else " B,C~N(0,1/N)") + (" with h0" if has_h0 else ""),
                    "batch": Bsz, "seq_len": T, "channels": D, "d_state": N,
@@ -216,7 +216,7 @@ def main():
 
 
 def _bench_lm(args):
-    """one training step of the Naju LM (12 layers,
+    """Benchmark configuration c5: one training step of the Naju LM (12 layers,
     d_model 768, vocab 50257, N = 64) on a batch of 8 x 2048 uniformly random
     token ids: bf16 autocast forward, cross-entropy (the fused HIP kernels of
     naju_amd.xent on the bf16 logits), backward, gradient

@@ -2,7 +2,7 @@
 
 A restatement of the reference's model code (naju/mixer.py:51-144,
 naju/lm.py:13-33, naju/optim.py:30-52) over this package's scan dispatch, so
-the mixer and the LM training step run with the HIP
+the mixer and the LM training step (benchmark configuration c5) run with the HIP
 scan where the reference package is absent. Module and parameter names, shapes
 and initialisation follow the reference, so state dicts load in either
 direction with ``strict=True``.

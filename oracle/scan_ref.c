@@ -164,7 +164,7 @@ void naju_oracle_bwd(const float* u, const float* fl, const float* il,
 }
 
 /* Per-channel forward on a subset of channels (for size-independent sliced
- * checks at full BASELINE shapes: y, du, dfl, dil are per-(b,d) independent).
+ * checks at the full benchmark shapes: y, du, dfl, dil are per-(b,d) independent).
  * chans[k] = b*D + d; outputs y_s[k*T + t]. */
 void naju_oracle_fwd_channels(const float* u, const float* fl, const float* il,
                               const float* Bm, const float* Cm,

@@ -46,7 +46,7 @@ def test_missing_library_fails_loudly(monkeypatch):
 
 def test_size_queries():
     L = _lib.lib()
-    # BASELINE config 2 at N=1: ckpt = one float per (b, chunk, d)
+    # benchmark configuration c2 at N=1: ckpt = one float per (b, chunk, d)
     n = L.naju_scan_ckpt_elems(8, 4096, 1024, 1, BF16, BF16, BF16)
     assert n > 0 and n % (8 * 1024) == 0 and n <= 8 * 1024 * 4096
     ws = L.naju_scan_workspace_bytes(8, 4096, 1024, 1, BF16, BF16, BF16)

@@ -232,7 +232,7 @@ def test_empty_time_axis(gpu):
 
 @pytest.mark.parametrize("name", ["c2"])
 def test_full_size_batch_row_slice(gpu, name):
-    """Full BASELINE size on the GPU; batch row 0 checked in full against the
+    """Full benchmark size on the GPU; batch row 0 checked in full against the
     oracle (every output except dD depends only on its own batch row), dD
     checked against sum(dy*u) over the whole batch."""
     from naju_amd.workloads import config_inputs

@@ -1,4 +1,5 @@
-"""GPU parity at the full sizes of BASELINE configs 3 and 4 (N = 1), against
+"""GPU parity at the full sizes of benchmark configurations c3 and c4
+(naju_amd.workloads.CONFIGS, N = 1), against
 the fp64 oracle run over channel slices on the host's cores.
 
 Config 3 (B=1, T=131072, D=2048, fp32, retention near 1): EVERY output is

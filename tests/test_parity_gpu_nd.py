@@ -101,7 +101,7 @@ def test_golden_oracle_n4(gpu):
 
 
 def test_full_size_c2_n64_channel_slice(gpu):
-    """BASELINE config 2 at the mixer's N = 64, full size on the GPU; 24
+    """Benchmark configuration c2 at the mixer's N = 64, full size on the GPU; 24
     channels checked against the per-channel oracle (y, du, dfl, dil, dh0 are
     per-channel), dD against sum(dy*u)."""
     from naju_amd.workloads import config_inputs
