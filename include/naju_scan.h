@@ -43,6 +43,13 @@
  * stream-ordered calls. Calls that overlap in time (different streams) need
  * different workspaces.
  *
+ * HIP graphs: the calls issue kernel launches only (no allocation, memset or
+ * host synchronisation), so they can be recorded by stream capture. At N = 1
+ * a call made while `stream` is capturing also records a one-thread kernel
+ * that advances a device-side epoch in the workspace, and the scan kernels
+ * take their cross-workgroup hand-off tags from it, so each replay is
+ * independent of the previous one (eager calls use host-side tags).
+ *
  * Return codes: 0 on success, a negative NAJU_ERR_* otherwise, with a message
  * in naju_scan_last_error() (thread-local). Argument checks run on the host,
  * before any device work, so they are testable without a GPU.
@@ -124,12 +131,14 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream);
 
-/* Reads the workspace's device-side status word (synchronises `stream`).
+/* Reads the workspace's device-side status word (synchronises `stream`)
+ * and, when it is nonzero, clears it and rewinds the workspace's ticket
+ * counters, so the workspace is usable again.
  * 0 = healthy; 1 = a carry hand-off between workgroups exceeded its
  * bounded wait and the affected outputs were set to NaN; 2 = a ticket
  * counter held a value out of range (a workspace that was not zero-filled
- * before first use), and the affected workgroups did nothing. No counterpart
- * in the reference (its kernels have no cross-workgroup waits). */
+ * before first use), and the affected workgroups wrote NaN outputs. No
+ * counterpart in the reference (its kernels have no cross-workgroup waits). */
 int naju_scan_workspace_status(const void* workspace, void* stream,
                                uint32_t* status);
 

@@ -171,9 +171,11 @@ __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float((
 
 // Workspace header, a fixed-size region that no other part of any layout
 // ever overlaps (so its counters, which must start at zero, are only ever
-// written by the ticket logic below): word 0 is the status word; tile t's
-// ticket counter is word kCtrBase + t*kCtrStride, t < kMaxTiles.
-enum { HDR_STATUS = 0 };
+// written by the ticket logic below): word 0 is the status word; word 1 the
+// device epoch (look-back tags of launches recorded into a HIP graph, see
+// epoch_bump_kernel); tile t's ticket counter is word kCtrBase + t*kCtrStride,
+// t < kMaxTiles.
+enum { HDR_STATUS = 0, HDR_EPOCH = 1 };
 constexpr int kCtrBase = 64;
 constexpr int kCtrStride = 4;
 constexpr int kMaxTiles = 1 << 16;
@@ -222,25 +224,50 @@ struct ScanArgs {
   int K;
   int ck_rows;  // N = 1 forward: rows per checkpoint interval (the backward's chunk length)
   int Kc;       // N = 1 forward: number of checkpoint intervals
-  uint32_t tag;  // this launch's tag (nonzero, new for every launch)
+  // N = 1: this launch's look-back tag. Nonzero: a host tag (odd, new for
+  // every eager launch). Zero: the launch was recorded into a HIP graph, and
+  // the tag comes from the device epoch, which the one-thread
+  // epoch_bump_kernel recorded right before it advances on every replay.
+  uint32_t tag;
   int strict;    // N = 1: take carries from the immediate predecessor's inclusive carry only
 };
+
+// Look-back tag of a launch from the device epoch E: even and nonzero, so it
+// never equals a host tag (odd) or the tag 0 of a zero-filled workspace.
+__device__ __forceinline__ uint32_t epoch_tag(uint32_t e) { return (e & 0x7fffffffu) << 1; }
+
+// Advances the device epoch by one (skipping the values whose tag would be
+// 0). Recorded into a HIP graph before each N = 1 scan launch, so every
+// replay of that launch sees a new tag: look-back words left by an earlier
+// replay carry an older tag and are never taken for fresh ones. Stream order
+// makes the new value visible to the scan launch that follows.
+__global__ void epoch_bump_kernel(uint32_t* hdr) {
+  uint32_t e = hdr[HDR_EPOCH] + 1u;
+  if (epoch_tag(e) == 0u) e += 1u;
+  hdr[HDR_EPOCH] = e;
+}
 
 // Workgroup blockIdx.x serves tile blockIdx.x % n_tiles; the chunk comes from
 // that tile's ticket counter, so a tile's chunks are handed out in the order
 // its workgroups start and every chunk a workgroup waits on is already held
 // by a running workgroup. The workgroup that draws the tile's last ticket
 // rewinds the counter for the next launch (all K tickets are taken by then).
+// Also returns the launch's look-back tag in *s_tag (a.tag, or the device
+// epoch's tag when a.tag is 0: read next to the ticket, in the same round
+// trip; nothing changes the epoch while the launch runs).
 // Returns false (after recording it in the status word) if the counter held
 // a value outside [0, K): a workspace that was not zero-filled. The caller
-// then exits without touching memory.
-__device__ __forceinline__ bool take_ticket(const ScanArgs& a, int tile, uint32_t* s_ticket) {
+// then poisons its blockIdx chunk instead of computing it.
+__device__ __forceinline__ bool take_ticket(const ScanArgs& a, int tile, uint32_t* s_ticket, uint32_t* s_tag) {
   if (threadIdx.x == 0) {
     uint32_t* ctr = a.hdr + kCtrBase + (int64_t)tile * kCtrStride;
+    uint32_t e = 0;
+    if (a.tag == 0u) e = __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t == (uint32_t)a.K - 1) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t >= (uint32_t)a.K) __hip_atomic_store(a.hdr + HDR_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *s_ticket = t;
+    *s_tag = a.tag != 0u ? a.tag : epoch_tag(e);
   }
   __syncthreads();
   return *s_ticket < (uint32_t)a.K;
@@ -410,14 +437,13 @@ __device__ __forceinline__ void ld_scalars(const T* __restrict__ p, int64_t rowb
 // chunk and tile lie wholly inside [0,T) x [0,D) runs the FULL body: no
 // bounds checks, all loads issued back to back; edge workgroups check.
 template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O, bool FULL>
-__device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, int lane, int wv,
-                                            float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V], float (&s_in)[64 * V],
-                                            LookShared<V, W, P>& s_lb) {
+__device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, int lane, int wv, uint32_t tag,
+                                            bool poison, float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
+                                            float (&s_in)[64 * V], LookShared<V, W, P>& s_lb) {
   using TY = std::conditional_t<F32O, float, TU>;  // y dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
   constexpr int M = FULL ? kVecAll : (VEC ? kVecLane : kElem);
-  const uint32_t tag = a.tag;
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
@@ -490,7 +516,11 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
         Zw[j] = fmaf(f, Zw[j], s_Z[w][j * 64 + lane]);
         Fw[j] *= f;
       }
-    if (k > 0) {
+    if (poison) {
+      // no valid ticket: this chunk's outputs become NaN, nothing is published
+#pragma unroll
+      for (int j = 0; j < V; ++j) sin[j] = __builtin_nanf("");
+    } else if (k > 0) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         st_word(my_agg + j * 64, Fw[j], tag);
@@ -501,11 +531,11 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
       for (int j = 0; j < V; ++j) sin[j] = (a.h0 && dok[j]) ? a.h0[(int64_t)b * D + d0 + j] : 0.f;
     }
   }
-  if (k > 0) wg_look_back<V, W, P>(a, s_lb, k, tile, -1, tag, lane, wv, sin);
+  if (k > 0 && !poison) wg_look_back<V, W, P>(a, s_lb, k, tile, -1, tag, lane, wv, sin);
   if (wv == 0) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      st_word(my_incl + j * 64, fmaf(Fw[j], sin[j], Zw[j]), tag);
+      if (!poison) st_word(my_incl + j * 64, fmaf(Fw[j], sin[j], Zw[j]), tag);
       s_in[j * 64 + lane] = sin[j];
     }
     if (a.hT && k == a.K - 1) {
@@ -540,25 +570,28 @@ template <typename TU, typename TG, typename TB, int V, int R, int W, int P, boo
 __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
-  __shared__ uint32_t s_ticket;
+  __shared__ uint32_t s_ticket, s_tag;
   __shared__ float s_F[W][CH];
   __shared__ float s_Z[W][CH];
   __shared__ float s_in[CH];
   __shared__ LookShared<V, W, P> s_lb;
 
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  if (!take_ticket(a, tile, &s_ticket)) return;
-  const int k = (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  // an out-of-range ticket (a workspace that was not zero-filled) poisons
+  // the chunk this workgroup's index names, so no output is left unwritten
+  const bool poison = !take_ticket(a, tile, &s_ticket, &s_tag);
+  const int k = poison ? (int)(blockIdx.x / (uint32_t)a.n_tiles) : (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dtile = tile % a.n_dtiles;
   if constexpr (VEC) {
     if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
-      n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, s_F, s_Z, s_in, s_lb);
+      n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_in, s_lb);
       return;
     }
   }
-  n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, s_F, s_Z, s_in, s_lb);
+  n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_in, s_lb);
 }
 
 // ----------------------------------------------------------- N = 1 backward
@@ -569,8 +602,8 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 // (ticket -> chunk K-1-k), so the look-back walks towards larger t. The
 // forward state entering the chunk comes from the forward's checkpoint.
 template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O, bool FULL>
-__device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, int lane, int wv,
-                                            float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
+__device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, int lane, int wv, uint32_t tag,
+                                            bool poison, float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
                                             float (&s_Zb)[W][64 * V], float (&s_g)[64 * V],
                                             LookShared<V, W, P>& s_lb) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
@@ -578,7 +611,6 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
   constexpr int M = FULL ? kVecAll : (VEC ? kVecLane : kElem);
-  const uint32_t tag = a.tag;
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
@@ -657,7 +689,11 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
         Zb[j] = fmaf(f, Zb[j], s_Zb[w][j * 64 + lane]);
         A[j] *= f;
       }
-    if (k < a.K - 1) {
+    if (poison) {
+      // no valid ticket: this chunk's outputs become NaN, nothing is published
+#pragma unroll
+      for (int j = 0; j < V; ++j) gin[j] = __builtin_nanf("");
+    } else if (k < a.K - 1) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         st_word(my_agg + j * 64, A[j], tag);
@@ -665,12 +701,12 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
       }
     }
   }
-  if (k < a.K - 1) wg_look_back<V, W, P>(a, s_lb, k, tile, +1, tag, lane, wv, gin);
+  if (k < a.K - 1 && !poison) wg_look_back<V, W, P>(a, s_lb, k, tile, +1, tag, lane, wv, gin);
   if (wv == 0) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const float gout = fmaf(A[j], gin[j], Zb[j]);
-      st_word(my_incl + j * 64, gout, tag);
+      if (!poison) st_word(my_incl + j * 64, gout, tag);
       s_g[j * 64 + lane] = gin[j];
       if (a.dh0 && k == 0 && dok[j]) a.dh0[(int64_t)b * D + d0 + j] = gout;
     }
@@ -762,7 +798,7 @@ template <typename TU, typename TG, typename TB, int V, int R, int W, int P, boo
 __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
-  __shared__ uint32_t s_ticket;
+  __shared__ uint32_t s_ticket, s_tag;
   __shared__ float s_F[W][CH];
   __shared__ float s_Z[W][CH];
   __shared__ float s_Zb[W][CH];
@@ -770,18 +806,22 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   __shared__ LookShared<V, W, P> s_lb;
 
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  if (!take_ticket(a, tile, &s_ticket)) return;
-  const int k = a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  // an out-of-range ticket poisons the chunk this workgroup's index names
+  const bool poison = !take_ticket(a, tile, &s_ticket, &s_tag);
+  const int k = poison ? (int)(blockIdx.x / (uint32_t)a.n_tiles)
+                       : a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dtile = tile % a.n_dtiles;
   if constexpr (VEC) {
     if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
-      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, s_F, s_Z, s_Zb, s_g, s_lb);
+      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g,
+                                                           s_lb);
       return;
     }
   }
-  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, s_F, s_Z, s_Zb, s_g, s_lb);
+  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb);
 }
 
 // Sum over q < n_parts of p[q*stride + i], in q order, with the loads of
@@ -2152,13 +2192,27 @@ __global__ void zero_any_kernel(void* dst, int dt, int64_t n) {
 
 thread_local char g_err[512] = "";
 
-// Tags of the look-back words: one new nonzero value per launch, process-wide
-// (zero-filled workspaces hold tag 0, so a fresh workspace is never misread).
+// Host tags of the look-back words: one new odd value per eager launch,
+// process-wide (zero-filled workspaces hold tag 0; device-epoch tags of
+// graph-recorded launches are even, so the two kinds never meet).
 std::atomic<uint32_t> g_tag{0};
-uint32_t next_tag() {
-  uint32_t t = g_tag.fetch_add(1, std::memory_order_relaxed) + 1;
-  while (t == 0) t = g_tag.fetch_add(1, std::memory_order_relaxed) + 1;
-  return t;
+uint32_t next_tag() { return (g_tag.fetch_add(1, std::memory_order_relaxed) << 1) | 1u; }
+
+// The look-back tag of an N = 1 launch on stream st. Eager: a host tag.
+// While st is being captured into a HIP graph, a host tag would be frozen
+// into the graph and every replay would accept the words of the previous
+// replay as its own; the launch then takes its tag from the device epoch
+// instead, and the one-thread epoch_bump_kernel recorded just before it
+// advances the epoch on every replay. Returns the tag (0 = device epoch), or
+// -1 after recording a launch error.
+int64_t launch_tag(uint32_t* hdr, hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+  if (cs != hipStreamCaptureStatusActive) return next_tag();
+  hipLaunchKernelGGL(epoch_bump_kernel, dim3(1), dim3(1), 0, st, hdr);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return -1;
+  return 0;
 }
 
 int fail(int code, const char* fmt, ...) {
@@ -2552,7 +2606,9 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
     return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                 l.n_tiles);
-  a.tag = next_tag();
+  const int64_t tg = launch_tag(a.hdr, st);
+  if (tg < 0) return fail(NAJU_ERR_LAUNCH, "epoch launch failed");
+  a.tag = (uint32_t)tg;
   a.strict = (flags & NAJU_FLAG_DETERMINISTIC) != 0;
   a.ck_rows = kBChunk;
   a.Kc = (int)((T + kBChunk - 1) / kBChunk);
@@ -2645,7 +2701,9 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     if (wgs > 0x7fffffff || l.n_tiles > kMaxTiles)
       return fail(NAJU_ERR_UNSUPPORTED, "problem too large (%lld workgroups, %d channel tiles)", (long long)wgs,
                   l.n_tiles);
-    a.tag = next_tag();
+    const int64_t tg = launch_tag(a.hdr, st);
+    if (tg < 0) return fail(NAJU_ERR_LAUNCH, "epoch launch failed");
+    a.tag = (uint32_t)tg;
     a.strict = (flags & NAJU_FLAG_DETERMINISTIC) != 0;
     kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, true);
     rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
@@ -2673,11 +2731,23 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
 
 int naju_scan_workspace_status(const void* workspace, void* stream, uint32_t* status) {
   if (!workspace || !status) return fail(NAJU_ERR_INVALID, "null workspace or status pointer");
+  hipStream_t st = (hipStream_t)stream;
   uint32_t hdr[4];
-  if (hipMemcpyAsync(hdr, workspace, sizeof(hdr), hipMemcpyDeviceToHost, (hipStream_t)stream) != hipSuccess ||
-      hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+  if (hipMemcpyAsync(hdr, workspace, sizeof(hdr), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
     return fail(NAJU_ERR_LAUNCH, "could not read the workspace header");
   *status = hdr[HDR_STATUS];
+  if (hdr[HDR_STATUS] != 0) {
+    // Clear the status word and rewind every ticket counter (a status of 2
+    // means some counter was out of range); the device epoch is kept, so
+    // look-back words of earlier graph replays keep older tags.
+    char* w = (char*)workspace;
+    if (hipMemsetAsync(w + HDR_STATUS * sizeof(uint32_t), 0, sizeof(uint32_t), st) != hipSuccess ||
+        hipMemsetAsync(w + kCtrBase * sizeof(uint32_t), 0, kHeaderBytes - kCtrBase * sizeof(uint32_t), st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+      return fail(NAJU_ERR_LAUNCH, "could not clear the workspace header");
+  }
   return NAJU_OK;
 }
 

@@ -2,15 +2,25 @@
 
 Public surface, mirroring /root/reference/naju/scan.py:
 
-* ``naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None)`` -- the backend
-  callable, same 6-tensor signature as every reference backend
-  (scan.py:3-13, chunk_triton.py:203, cuda/__init__.py:66) plus an optional
-  initial state ``h0`` [B, D, N] (the reference always starts from zero,
-  scan.py:84). Differentiable; the backward returns the gradients of all
-  inputs, including ``h0``.
+* ``naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None,
+  return_final_state=False)`` -- the backend callable, same 6-tensor
+  signature as every reference backend (scan.py:3-13, chunk_triton.py:203,
+  cuda/__init__.py:66) plus an optional initial state ``h0`` [B, D, N] (the
+  reference always starts from zero, scan.py:84). Differentiable; the
+  backward returns the gradients of all inputs, including ``h0``. With
+  ``return_final_state=True`` it returns ``(y, hT)``, hT = x_{T-1} [B, D, N]
+  float32, the state a streaming decoder resumes from (pass it as ``h0`` of
+  the next segment); hT is not differentiable (no gradient flows back
+  through it), which is what inference needs.
 * ``naju_scan(..., backend=None)`` / ``resolve_backend`` / ``_BACKEND_CACHE``
   -- the dispatch of scan.py:45-76 for code that runs without the reference
-  package. The only backend name served here is ``"hip"``.
+  package. The only backend name served here is ``"hip"``. Without a GPU the
+  default name is ``"reference"`` as in scan.py:50-51, but no CPU scan ships
+  with this package: the call raises until one is registered under that
+  name (the tests register the oracle's loop).
+* ``workspace_status(device=None)`` -- reads (and clears) the status word of
+  the current stream's workspace; ``NAJU_CHECK_STATUS=1`` makes every call
+  check it and raise on a failed cross-workgroup hand-off.
 * ``register(name="hip", scan_module=None)`` -- inserts ``naju_scan_hip`` into
   the reference's ``naju.scan._BACKEND_CACHE``. ``_get`` returns cached entries
   before it validates names (scan.py:55-57) and ``resolve_backend`` lower-cases
@@ -69,6 +79,32 @@ def _stream_handle(device):
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_STATUS_MSG = {1: "a carry hand-off between workgroups exceeded its bounded wait (outputs are NaN)",
+               2: "a ticket counter was out of range: the workspace was not zero-filled (outputs are NaN)"}
+
+
+def workspace_status(device=None):
+    """Status word of the workspace of (device, current stream): 0 healthy,
+    1 or 2 after a failed call (then cleared, so the workspace is usable
+    again). Synchronises the stream."""
+    import ctypes
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index)
+    stream = _stream_handle(dev)
+    buf = _WS._bufs.get((dev.index, stream))
+    if buf is None:
+        return 0
+    st = ctypes.c_uint32(0)
+    _lib.check(_lib.lib().naju_scan_workspace_status(buf.data_ptr(), stream, ctypes.byref(st)))
+    return st.value
+
+
+def _check_status(dev):
+    if os.environ.get("NAJU_CHECK_STATUS", "0") not in ("", "0"):
+        st = workspace_status(dev)
+        if st:
+            raise _lib.NajuScanError(st, _STATUS_MSG.get(st, f"status {st}"))
+
+
 def _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0):
     """Contiguous tensors in a dtype combination the kernels serve:
     u in {f32,bf16,f16}; gates and B/C each f32 or u's dtype; D_skip, h0 f32."""
@@ -111,7 +147,7 @@ class NajuScanHip(torch.autograd.Function):
     """Autograd wrapper of naju_scan_fwd / naju_scan_bwd (include/naju_scan.h)."""
 
     @staticmethod
-    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None):
+    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False):
         Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
         out_dtype = u.dtype
         u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0)
@@ -131,17 +167,23 @@ class NajuScanHip(torch.autograd.Function):
             _lib.check(_lib.ERR_INVALID)
         ws = _WS.get(dev, stream, nbytes)
         y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
+        hT = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_hT else None
         _lib.check(L.naju_scan_fwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
-            _ptr(y), _ptr(ckpt), None, Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
+            _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
+        _check_status(dev)
         if need_grad:
             ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
             ctx.meta = (Bsz, T, D, N, dts, h0 is not None,
                         (u.dtype, f_logit.dtype, i_logit.dtype, B.dtype, C.dtype, D_skip.dtype))
-        return y if y.dtype == out_dtype else y.to(out_dtype)
+        y = y if y.dtype == out_dtype else y.to(out_dtype)
+        if want_hT:
+            ctx.mark_non_differentiable(hT)
+            return y, hT
+        return y
 
     @staticmethod
-    def backward(ctx, dy):
+    def backward(ctx, dy, *_unused_dhT):
         u_, fl_, il_, B_, C_, D_, ckpt = ctx.saved_tensors
         Bsz, T, D, N, dts, has_h0, in_dtypes = ctx.meta
         ng = ctx.needs_input_grad
@@ -162,19 +204,22 @@ class NajuScanHip(torch.autograd.Function):
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
             _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
             Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
+        _check_status(dev)
         grads = [du, dfl, dil, dB, dC, dD]
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
-        return (*grads, dh0)
+        return (*grads, dh0, None)
 
 
-def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None):
-    """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module doc)."""
-    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0)
+def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False):
+    """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module
+    doc); (y, hT) with return_final_state=True."""
+    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state))
 
 
 def resolve_backend(backend=None):
-    """Selection order of scan.py:48-52: explicit > NAJU_SCAN_BACKEND > "hip"."""
-    b = backend or os.environ.get("NAJU_SCAN_BACKEND") or "hip"
+    """Selection order of scan.py:48-52: explicit > NAJU_SCAN_BACKEND > "hip"
+    when a GPU is visible, else "reference"."""
+    b = backend or os.environ.get("NAJU_SCAN_BACKEND") or ("hip" if torch.cuda.is_available() else "reference")
     return b.lower()
 
 
@@ -183,6 +228,11 @@ def _get(b):
     if fn is None:
         if b in ("hip", "naju_amd"):
             fn = naju_scan_hip
+        elif b == "reference":
+            raise ValueError("no CPU scan backend ships with naju_amd (the reference's CPU default, "
+                             "naju/scan.py:50-51, is its sequential loop): register a callable with the "
+                             "6-tensor scan signature as _BACKEND_CACHE['reference'], or run on a GPU "
+                             "with backend 'hip'")
         else:
             raise ValueError(f"unknown scan backend {b!r}; valid: hip")
         _BACKEND_CACHE[b] = fn

@@ -137,12 +137,31 @@ def test_check_raises_with_message():
 # ------------------------------------------------------- Python mirror
 
 def test_resolve_backend_order(monkeypatch):
-    from naju_amd.scan import resolve_backend
+    """explicit > NAJU_SCAN_BACKEND > "hip" with a GPU, "reference" without
+    (naju/scan.py:48-52)."""
+    from naju_amd import scan
     monkeypatch.delenv("NAJU_SCAN_BACKEND", raising=False)
-    assert resolve_backend() == "hip"
+    monkeypatch.setattr(scan.torch.cuda, "is_available", lambda: True)
+    assert scan.resolve_backend() == "hip"
+    monkeypatch.setattr(scan.torch.cuda, "is_available", lambda: False)
+    assert scan.resolve_backend() == "reference"
     monkeypatch.setenv("NAJU_SCAN_BACKEND", "HIP")
-    assert resolve_backend() == "hip"
-    assert resolve_backend("Other") == "other"
+    assert scan.resolve_backend() == "hip"
+    assert scan.resolve_backend("Other") == "other"
+
+
+def test_cpu_default_backend_raises_clearly(monkeypatch):
+    """No CPU scan ships with the package: the CPU default names what to
+    register instead of falling back to anything."""
+    from naju_amd import scan
+    monkeypatch.delenv("NAJU_SCAN_BACKEND", raising=False)
+    monkeypatch.setattr(scan.torch.cuda, "is_available", lambda: False)
+    monkeypatch.setattr(scan, "_BACKEND_CACHE", {})
+    x = torch.zeros(1, 2, 3)
+    with pytest.raises(ValueError, match="no CPU scan backend"):
+        scan.naju_scan(x, x, x, torch.zeros(1, 2, 1), torch.zeros(1, 2, 1), torch.zeros(3))
+    scan._BACKEND_CACHE["reference"] = lambda *a: "registered"
+    assert scan.naju_scan(x, x, x, torch.zeros(1, 2, 1), torch.zeros(1, 2, 1), torch.zeros(3)) == "registered"
 
 
 def test_unknown_backend_raises():

@@ -31,6 +31,7 @@ def _setup(ins, dev):
         "dD": torch.empty(D, dtype=torch.float32, device=dev),
         "dh0": torch.empty_like(t["h0"]) if t.get("h0") is not None else None,
         "ws": torch.zeros(max(256, L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)), dtype=torch.uint8, device=dev),
+        "_inputs": t,
     }
     p = lambda x: None if x is None else x.data_ptr()  # noqa: E731
     flags = _lib.FLAG_DETERMINISTIC
@@ -82,3 +83,47 @@ def test_graph_replay_matches_eager(gpu, N, shape, dtype):
             step()
         torch.cuda.synchronize()
         assert torch.equal(bufs["y"], ref["y"])
+
+
+@pytest.mark.parametrize("N,shape,dtype", [(1, (2, 1000, 256), torch.bfloat16), (1, (1, 4096, 128), torch.float32),
+                                           (16, (2, 300, 128), torch.float32)])
+def test_graph_back_to_back_replays_with_new_inputs(gpu, N, shape, dtype):
+    """Replays follow each other with no eager call in between, each on new
+    inputs copied into the captured buffers. Every replay must equal an eager
+    call on its own inputs (run afterwards, on a second workspace): a replay
+    that accepted the previous replay's cross-workgroup hand-off words would
+    carry the previous inputs' states into its outputs."""
+    ins0 = rand_inputs(*shape, N, seed=70 + N, dtype=dtype, h0_std=0.2)
+    bufs, step, status = _setup(ins0, gpu)
+    outs = ("y", "du", "dfl", "dil", "dB", "dC", "dD", "dh0")
+    t_in = bufs["_inputs"]
+    s = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.synchronize()
+    sets, got = [], []
+    for rep in range(4):
+        # the last replay repeats the inputs of the one before it
+        ins = sets[-1] if rep == 3 else rand_inputs(*shape, N, seed=100 * rep + N, dtype=dtype, h0_std=0.2)
+        sets.append(ins)
+        for k, v in ins.items():
+            if v is not None and k in t_in:
+                t_in[k].copy_(v.to(gpu))
+        for k in outs:
+            if bufs[k] is not None:
+                bufs[k].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got.append({k: bufs[k].clone() for k in outs if bufs[k] is not None})
+        assert status() == 0
+    for rep, ins in enumerate(sets):
+        ref_bufs, ref_step, ref_status = _setup(ins, gpu)
+        ref_step()
+        torch.cuda.synchronize()
+        assert ref_status() == 0
+        for k, v in got[rep].items():
+            assert torch.equal(v, ref_bufs[k]), f"replay {rep}: {k} differs from an eager call on its inputs"

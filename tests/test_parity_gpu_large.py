@@ -57,28 +57,36 @@ def _host(t):
 def _slices_vs_oracle(inp, out, width):
     """Oracle over channel slices of one batch row set (inp / out: host float32
     arrays [b, T, D] of u, f_logit, i_logit, dy and y, du, dfl, dil; B, C
-    [b, T, 1]; D_skip [D]). Returns the per-output error accumulators and the
-    oracle's dB, dC (summed over the slices in slice order) and dD."""
+    [b, T, N]; D_skip [D]; optional h0 [b, D, N] in inp and dh0 in out).
+    Returns the per-output error accumulators and the oracle's dB, dC (summed
+    over the slices in slice order) and dD."""
     from oracle.scan_ref import oracle_bwd, oracle_fwd
     D = inp["u"].shape[2]
     starts = list(range(0, D, width))
+    h0 = inp.get("h0")
 
     def one(d0):
         sl = slice(d0, min(D, d0 + width))
         a = [np.ascontiguousarray(inp[k][:, :, sl]) for k in ("u", "f_logit", "i_logit")]
         a += [inp["B"], inp["C"], np.ascontiguousarray(inp["D_skip"][sl])]
-        ry = oracle_fwd(*a)
-        rg = oracle_bwd(*a, dy=np.ascontiguousarray(inp["dy"][:, :, sl]))
+        hs = np.ascontiguousarray(h0[:, sl]) if h0 is not None else None
+        ry = oracle_fwd(*a, h0=hs)
+        rg = oracle_bwd(*a, dy=np.ascontiguousarray(inp["dy"][:, :, sl]), h0=hs)
         errs = {}
-        for k, ref in (("y", ry), ("du", rg["du"]), ("dfl", rg["dfl"]), ("dil", rg["dil"])):
+        pairs = [("y", ry), ("du", rg["du"]), ("dfl", rg["dfl"]), ("dil", rg["dil"])]
+        for k, ref in pairs:
             e = _Err()
             e.add(out[k][:, :, sl], ref)
             errs[k] = e
+        if h0 is not None:
+            e = _Err()
+            e.add(out["dh0"][:, sl], rg["dh0"])
+            errs["dh0"] = e
         return errs, rg["dB"], rg["dC"], rg["dD"]
 
     with ThreadPoolExecutor(_WORKERS) as ex:
         res = list(ex.map(one, starts))
-    tot = {k: _Err() for k in ("y", "du", "dfl", "dil")}
+    tot = {k: _Err() for k in ("y", "du", "dfl", "dil") + (("dh0",) if h0 is not None else ())}
     for errs, _, _, _ in res:
         for k, e in errs.items():
             t = tot[k]
@@ -134,3 +142,49 @@ def test_full_size_c4_batch_row(gpu):
         ref_dD += (ins["dy"][b].double() * ins["u"][b].double()).sum(0)
     ref_dD = ref_dD.cpu().numpy()
     assert np.max(np.abs(g["dD"].double().cpu().numpy() - ref_dD)) <= 1e-4 * max(1.0, np.abs(ref_dD).max())
+
+
+def _check_row0(ins, y, g, width, n_rows=1):
+    """Batch rows [0, n_rows) of every output against the oracle over channel
+    slices (dB, dC included); dD against sum(dy*u) over the whole batch."""
+    rows = slice(0, n_rows)
+    inp = {k: _host(ins[k][rows]) for k in ("u", "f_logit", "i_logit", "dy", "B", "C")}
+    inp["D_skip"] = _host(ins["D_skip"])
+    out = {k: _host(v[rows]) for k, v in (("y", y), ("du", g["du"]), ("dfl", g["dfl"]), ("dil", g["dil"]))}
+    if ins.get("h0") is not None:
+        inp["h0"] = _host(ins["h0"][rows])
+        out["dh0"] = _host(g["dh0"][rows])
+    tot, dB, dC, _ = _slices_vs_oracle(inp, out, width)
+    for k in ("y", "du", "dfl", "dil"):
+        tot[k].check(k, (y if k == "y" else g[k]).dtype)
+    if "dh0" in tot:
+        tot["dh0"].check("dh0", torch.float32)
+    for k, ref in (("dB", dB), ("dC", dC)):
+        e = _Err()
+        e.add(_host(g[k][rows]), ref)
+        e.check(k, g[k].dtype)
+    ref_dD = (ins["dy"].double() * ins["u"].double()).sum((0, 1)).cpu().numpy()
+    assert np.max(np.abs(g["dD"].double().cpu().numpy() - ref_dD)) <= 1e-4 * max(1.0, np.abs(ref_dD).max())
+
+
+def test_full_size_c2_n64_batch_row(gpu):
+    """Benchmark configuration c2 at the mixer's N = 64 (8 x 4096 x 1024, bf16
+    streams, h0), full size on the GPU: batch row 0 of every output in full,
+    dB and dC (sums over all 1024 channels) and dh0 included."""
+    from naju_amd.workloads import config_inputs
+    ins = config_inputs("c2", N=64, seed=12, device=gpu)
+    y, g = run_hip(ins, gpu)
+    _check_row0(ins, y, g, 64)
+
+
+def test_full_size_c5_scan_layer(gpu):
+    """The scan call of one layer of the c5 LM step at full size: 8 x 2048 x
+    1536 channels, N = 64, with the mixer's autocast dtypes (u, B, C bf16;
+    gate logits f32, the gate biases' +5 / -2 initial offsets): batch row 0
+    of every output in full, dB and dC included."""
+    from tests._helpers import rand_inputs
+    ins = rand_inputs(8, 2048, 1536, 64, seed=55, dtype=torch.bfloat16, gate_dtype=torch.float32,
+                      bc_dtype=torch.bfloat16, f_shift=5.0, i_shift=-2.0, d_scale=0.0)
+    y, g = run_hip(ins, gpu)
+    assert y.dtype == torch.bfloat16 and g["dfl"].dtype == torch.float32
+    _check_row0(ins, y, g, 96)
