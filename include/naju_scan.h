@@ -131,6 +131,27 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* Allocation-free forward: naju_scan_fwd with the caller's workspace
+ * replaced by a static device array of NAJU_NOALLOC_SCRATCH_BYTES per GPU
+ * (each GPU the library runs on holds it until the process ends; its
+ * address is looked up once per device, at the first call there). No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory -- code under HIP-graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. It calls no hipMalloc / hipFree. The
+ * caller still passes every input and output (ckpt and hT optional, as in
+ * naju_scan_fwd). Shapes whose forward needs more scratch than the maximum
+ * (at N = 1 about 0.375 bytes per element of batch*T*D, i.e. up to about
+ * 83 M elements; N > 1 uses fewer time segments to fit) are rejected with
+ * NAJU_ERR_WORKSPACE. Every call on one GPU shares that GPU's array: calls
+ * that overlap in time on one GPU (different streams, threads) race. */
+#define NAJU_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int naju_scan_fwd_noalloc(const void* u, const void* f_logit,
+                          const void* i_logit, const void* B, const void* C,
+                          const float* D_skip, const float* h0, void* y,
+                          float* ckpt, float* hT, int64_t batch, int64_t T,
+                          int64_t D, int64_t N, int x_dtype, int gate_dtype,
+                          int bc_dtype, int flags, void* stream);
+
 /* Reads the workspace's device-side status word (synchronises `stream`)
  * and, when it is nonzero, clears it and rewinds the workspace's ticket
  * counters, so the workspace is usable again.

@@ -22,6 +22,7 @@ EXPORTED = (
     "naju_scan_fwd",
     "naju_scan_bwd",
     "naju_scan_workspace_status",
+    "naju_scan_fwd_noalloc",
     "naju_mixer_last_error",
     "naju_dwconv_fwd",
     "naju_dwconv_workspace_bytes",
@@ -76,6 +77,9 @@ def lib():
     # ws_bytes, stream
     L.naju_scan_bwd.argtypes = [P] * 15 + [I64] * 4 + [I] * 4 + [P, SZ, P]
     L.naju_scan_bwd.restype = I
+    # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, flags, stream
+    L.naju_scan_fwd_noalloc.argtypes = [P] * 10 + [I64] * 4 + [I] * 4 + [P]
+    L.naju_scan_fwd_noalloc.restype = I
     L.naju_scan_workspace_status.argtypes = [P, P, ctypes.POINTER(ctypes.c_uint32)]
     L.naju_scan_workspace_status.restype = I
     L.naju_mixer_last_error.argtypes = []

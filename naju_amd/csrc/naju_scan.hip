@@ -35,6 +35,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 #include <stdio.h>
 #include <string.h>
@@ -2289,11 +2290,39 @@ bool gq_ok(int64_t N, int64_t batch, int64_t D);
 int gq_channels(int64_t N);
 int gn_bwd_dt(int np);
 
-Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd) {
+// Byte offsets of the workspace regions for the layout's K, tiles and
+// segments (the backward's partial sums only when bwd).
+void place_regions(Layout& l, int64_t batch, int64_t T, int64_t D, int64_t N, bool bwd) {
+  size_t off = align_up(kHeaderBytes);
+  const size_t units = N == 1 ? (size_t)l.K * l.n_tiles : 0;
+  l.off_agg = off;
+  off = align_up(off + units * 2 * l.CH * sizeof(uint64_t));
+  l.off_incl = off;
+  off = align_up(off + units * l.CH * sizeof(uint64_t));
+  const size_t part_bc = bwd ? (size_t)l.n_dtiles * batch * T * N * sizeof(float) : 0;
+  l.off_partB = off;
+  off = align_up(off + part_bc);
+  l.off_partC = off;
+  off = align_up(off + part_bc);
+  l.off_partD = off;
+  off = align_up(off + (bwd ? (size_t)batch * (N == 1 ? l.K : l.nseg) * D * sizeof(float) : 0));
+  const size_t seg_units = l.nseg > 1 ? (size_t)batch * l.nseg * D : 0;
+  l.off_segF = off;
+  off = align_up(off + seg_units * sizeof(float));
+  l.off_segZ = off;
+  off = align_up(off + seg_units * N * sizeof(float));
+  l.off_seg0 = off;
+  off = align_up(off + seg_units * N * sizeof(float));
+  l.total = off;
+}
+
+// cap: at N > 1, fewer time segments (down to one) until the workspace fits
+// in cap bytes; the N = 1 layout has no such freedom.
+Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd,
+                   size_t cap = SIZE_MAX) {
   Layout l{};
   (void)x_dt;
   (void)g_dt;
-  size_t off = align_up(kHeaderBytes);
   if (N == 1) {
     l.V = n1_vec_width(bwd);
     l.CH = 64 * l.V;
@@ -2320,25 +2349,13 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
     l.seg_sc = (int)((l.K + want - 1) / want);
     l.nseg = (l.K + l.seg_sc - 1) / l.seg_sc;
   }
-  const size_t units = N == 1 ? (size_t)l.K * l.n_tiles : 0;
-  l.off_agg = off;
-  off = align_up(off + units * 2 * l.CH * sizeof(uint64_t));
-  l.off_incl = off;
-  off = align_up(off + units * l.CH * sizeof(uint64_t));
-  l.off_partB = off;
-  off = align_up(off + (size_t)l.n_dtiles * batch * T * N * sizeof(float));
-  l.off_partC = off;
-  off = align_up(off + (size_t)l.n_dtiles * batch * T * N * sizeof(float));
-  l.off_partD = off;
-  off = align_up(off + (size_t)batch * (N == 1 ? l.K : l.nseg) * D * sizeof(float));
-  const size_t seg_units = l.nseg > 1 ? (size_t)batch * l.nseg * D : 0;
-  l.off_segF = off;
-  off = align_up(off + seg_units * sizeof(float));
-  l.off_segZ = off;
-  off = align_up(off + seg_units * N * sizeof(float));
-  l.off_seg0 = off;
-  off = align_up(off + seg_units * N * sizeof(float));
-  l.total = off;
+  place_regions(l, batch, T, D, N, bwd);
+  while (l.total > cap && l.nseg > 1) {
+    const int want = l.nseg / 2;
+    l.seg_sc = (l.K + want - 1) / want;
+    l.nseg = (l.K + l.seg_sc - 1) / l.seg_sc;
+    place_regions(l, batch, T, D, N, bwd);
+  }
   return l;
 }
 
@@ -2524,10 +2541,16 @@ size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D, int64_t N,
   return f > b ? f : b;
 }
 
-int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+}  // extern "C"
+
+namespace {
+
+// The forward of naju_scan_fwd and naju_scan_fwd_noalloc. cap bounds the
+// layout (time segments at N > 1) to the bytes available.
+int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                   const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch, int64_t T,
                   int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
-                  size_t workspace_bytes, void* stream) {
+                  size_t workspace_bytes, void* stream, size_t cap) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
@@ -2544,7 +2567,7 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   }
   if (!u || !f_logit || !i_logit || !B || !C || !D_skip || !y)
     return fail(NAJU_ERR_INVALID, "null input/output pointer (u, f_logit, i_logit, B, C, D_skip and y are required)");
-  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false);
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, cap);
   if (!workspace || workspace_bytes < l.total)
     return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", l.total,
                 workspace ? workspace_bytes : (size_t)0);
@@ -2614,6 +2637,94 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
   a.Kc = (int)((T + kBChunk - 1) / kBChunk);
   kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, false);
   return launch(k, (unsigned)wgs, 64 * kFW, st, a);
+}
+
+// ------------------------------------------- allocation-free forward scratch
+//
+// naju_scan_fwd_noalloc runs the forward on a file-scope device array instead
+// of a caller workspace. Each GPU the library runs on holds its own copy of
+// `scratch` until the process ends. Host code never passes the array's name
+// to a kernel (in host code it is only a stand-in for the symbol): at the
+// first call on a device, with that device current, hipGetSymbolAddress gives
+// the array's device address there, kept per device in g_scratch_ptr, and the
+// launches use that address. Every call on a device shares that device's
+// array, so calls that overlap in time on one GPU race.
+constexpr size_t kScratchBytes = NAJU_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Zeroes the status word and every ticket counter of a workspace header (a
+// kernel, not a memset, so a graph that records it replays it correctly).
+// The device epoch (word 1) is left alone: resetting it inside a recorded
+// graph would give every replay the same tag.
+__global__ void clear_header_kernel(uint32_t* hdr) {
+  const int64_t n = (int64_t)(kHeaderBytes / sizeof(uint32_t));
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    if (i != HDR_EPOCH) hdr[i] = 0u;
+}
+
+// This device's scratch address; at the first call on a device also clears
+// its header on `st`. Returns null after recording an error.
+void* scratch_for_current_device(hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(NAJU_ERR_LAUNCH, "no current HIP device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr) {
+    fail(NAJU_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  hipLaunchKernelGGL(clear_header_kernel, dim3(256), dim3(256), 0, st, (uint32_t*)p);
+  const hipError_t le = hipGetLastError();
+  if (le != hipSuccess) {
+    fail(NAJU_ERR_LAUNCH, "scratch clear launch failed: %s", hipGetErrorString(le));
+    return nullptr;
+  }
+  g_scratch_ptr[dev] = p;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                  const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch, int64_t T,
+                  int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  return scan_fwd_impl(u, f_logit, i_logit, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dtype, gate_dtype,
+                       bc_dtype, flags, workspace, workspace_bytes, stream, SIZE_MAX);
+}
+
+int naju_scan_fwd_noalloc(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                          const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch,
+                          int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int flags,
+                          void* stream) {
+  g_err[0] = 0;
+  const int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
+  if (rc) return rc;
+  if (batch > 0 && T > 0 && D > 0) {
+    const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, kScratchBytes);
+    if (l.total > kScratchBytes)
+      return fail(NAJU_ERR_WORKSPACE,
+                  "naju_scan_fwd_noalloc: this shape needs %zu bytes of scratch, the static maximum is %zu "
+                  "(use naju_scan_fwd with a workspace)",
+                  l.total, kScratchBytes);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  void* ws = scratch_for_current_device(st);
+  if (!ws) return NAJU_ERR_LAUNCH;
+  return scan_fwd_impl(u, f_logit, i_logit, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dtype, gate_dtype,
+                       bc_dtype, flags, ws, kScratchBytes, stream, kScratchBytes);
 }
 
 int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
