@@ -8,15 +8,20 @@ streams with fp32 state, N=1 (B=C=1), h0 ~ N(0, 0.1^2), dy ~ N(0,1).
 
 value = algorithmic bytes of fwd+bwd per step * K / wall time of K steps
 (GB/s). The roofline object reports the dominant kernel (the backward) from
-HIP events recorded on the launch stream inside the timed region. The
-cpu_baseline leg times the sequential torch-CPU restatement of the
-reference's scan (oracle/scan_ref.py: scan_loop_torch, the algorithm of
-reference naju/scan.py:79-93) with autograd on a bounded sample of the same
-workload.
+HIP events recorded on the launch stream inside the timed region. The same
+line carries the step timed after a 1 GiB cache-flush write, and (default
+c2, N = 1 run) a "configs" table: c1, c3 and c4 at N = 1 (c3 / c4 against the
+70%-of-HBM step times), c2 at N = 64 (VALU roofline) and the c5 LM training
+step (tokens/s). The cpu_baseline leg times the sequential torch-CPU
+restatement of the reference's scan (oracle/scan_ref.py: scan_loop_torch,
+the algorithm of reference naju/scan.py:79-93) on the host cores: c1 forward
+and forward + backward at N = 1 and 64, and the benchmarked workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--N 1]
+                       [--no-extras] [--no-cpu] [--no-flush]
 """
 import argparse
+import ctypes
 import gc
 import json
 import os
@@ -37,50 +42,20 @@ def _dt_size(dt):
     return 4 if dt == torch.float32 else 2
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
-                    help="c1-c4: the scan itself; c5: the LM training step (tokens/s)")
-    ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--flush", action="store_true",
-                    help="also time steps with a 1 GiB cache-flush write before each step")
-    ap.add_argument("--tune-gemms", default=None, metavar="CSV",
-                    help="c5: time the GEMM solutions during the warmup and record them in CSV "
-                         "(default: read naju_amd/tunableop_mi355x_lm.csv)")
-    ap.add_argument("--calib-copy", action="store_true",
-                    help="first run 3 plain 512 MiB device copies (counter calibration for rocprofv3 --pmc)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
-              "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
-        sys.exit(2)
+# rooflines of the per-config lines: %-of-HBM targets from the survey's
+# measurement plan (70% of 8 TB/s on the fused fwd+bwd at N = 1)
+TARGET_FRAC = 0.70
 
-    if args.config == "c5":
-        _bench_lm(args)
-        return
 
-    import ctypes
+def _scan_case(L, config, N, dev, seed=0):
+    """Inputs, outputs and workspace of one scan configuration, plus the two
+    C-ABI calls of a step (forward, backward) as closures."""
     import torch
     from naju_amd import _lib
     from naju_amd.workloads import CONFIGS, algorithmic_bytes, config_inputs
-
-    L = _lib.lib()
-    dev = torch.device("cuda", 0)
-    if args.calib_copy:
-        src = torch.ones(1 << 27, dtype=torch.float32, device=dev)   # 512 MiB
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"calib-copy: 3 x copy of {src.numel() * 4} bytes", file=sys.stderr, flush=True)
-        del src, dst
-    cfg = CONFIGS[args.config]
-    Bsz, T, D, N = cfg["batch"], cfg["T"], cfg["D"], args.N
-    ins = config_inputs(args.config, N=N, seed=0, device=dev)
+    cfg = CONFIGS[config]
+    Bsz, T, D = cfg["batch"], cfg["T"], cfg["D"]
+    ins = config_inputs(config, N=N, seed=seed, device=dev)
     xdt = ins["u"].dtype
     DT = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
     dts = (DT[xdt], DT[ins["f_logit"].dtype], DT[ins["B"].dtype])
@@ -93,8 +68,7 @@ def main():
     dh0 = torch.empty_like(h0) if h0 is not None else None
     ws_bytes = L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    sh = stream.cuda_stream
+    sh = torch.cuda.current_stream(dev).cuda_stream
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
 
     def fwd():
@@ -106,48 +80,136 @@ def main():
                                    p(dil), p(dB), p(dC), p(dD), p(dh0), Bsz, T, D, N, *dts, 0, p(ws),
                                    ws_bytes, sh))
 
+    def status():
+        st = ctypes.c_uint32(0)
+        _lib.check(L.naju_scan_workspace_status(p(ws), sh, ctypes.byref(st)))
+        return st.value
+
     s_x, s_g, s_bc = _dt_size(xdt), _dt_size(fl.dtype), _dt_size(Bm.dtype)
     has_h0 = h0 is not None
-    bytes_fwd = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=True, bwd=False)
-    bytes_bwd = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=False, bwd=True)
-    bytes_step = bytes_fwd + bytes_bwd
+    bf = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=True, bwd=False)
+    bb = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=False, bwd=True)
+    dname = {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[xdt]
+    return dict(fwd=fwd, bwd=bwd, status=status, bytes_fwd=bf, bytes_bwd=bb, E=Bsz * T * D, dtype=dname,
+                shape=(Bsz, T, D, N), has_h0=has_h0, gate=cfg["gate"], _keep=(ins, y, ck, du, dfl, dil, dB, dC,
+                                                                              dD, dh0, ws))
 
-    for _ in range(args.warmup):
-        fwd()
-        bwd()
-    torch.cuda.synchronize()
 
-    K = args.steps
-    # the timed region: K steps back to back, nothing else on the stream
+def _time_case(case, steps, warmup, stream):
+    """K steps back to back (wall clock between synchronisations), then K
+    more with HIP events on the launch stream around each call."""
+    import torch
+    for _ in range(warmup):
+        case["fwd"]()
+        case["bwd"]()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for k in range(K):
-        fwd()
-        bwd()
+    for _ in range(steps):
+        case["fwd"]()
+        case["bwd"]()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / K
-    # per-call durations (the roofline): K more steps with HIP events around
-    # each call, on the stream the kernels run on
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
-    for k in range(K):
+    ms_step = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for k in range(steps):
         ev[k][0].record(stream)
-        fwd()
+        case["fwd"]()
         ev[k][1].record(stream)
-        bwd()
+        case["bwd"]()
         ev[k][2].record(stream)
     torch.cuda.synchronize()
     t_fwd = sorted(e[0].elapsed_time(e[1]) for e in ev)
     t_bwd = sorted(e[1].elapsed_time(e[2]) for e in ev)
-    avg_fwd = sum(t_fwd) / K
-    avg_bwd = sum(t_bwd) / K
-    med = lambda xs: xs[len(xs) // 2]  # noqa: E731
-
-    st = ctypes.c_uint32(0)
-    _lib.check(L.naju_scan_workspace_status(p(ws), sh, ctypes.byref(st)))
-    if st.value != 0:
+    if case["status"]() != 0:
         raise RuntimeError("workspace status nonzero: a carry hand-off timed out")
+    return dict(ms_step=ms_step, fwd_avg=sum(t_fwd) / steps, bwd_avg=sum(t_bwd) / steps,
+                fwd_med=t_fwd[len(t_fwd) // 2], bwd_med=t_bwd[len(t_bwd) // 2])
 
+
+def _config_entry(L, config, N, dev, steps, warmup, target_ms=None):
+    """One line of the per-configuration table: GB/s, % of HBM peak,
+    elements/s and roofline fractions of the fused fwd+bwd step."""
+    import torch
+    case = _scan_case(L, config, N, dev)
+    t = _time_case(case, steps, warmup, torch.cuda.current_stream(dev))
+    b, T, D, n = case["shape"]
+    step_bytes = case["bytes_fwd"] + case["bytes_bwd"]
+    gbs = step_bytes / (t["ms_step"] * 1e-3) / 1e9
+    e = {
+        "workload": f"naju scan fwd+bwd {config}: B={b} L={T} D={D} N={n} {case['dtype']} streams, "
+                    f"gates '{case['gate']}'" + (" with h0" if case["has_h0"] else ""),
+        "steps": steps, "ms_per_step": round(t["ms_step"], 5),
+        "GBs": round(gbs, 1), "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "elements_per_s": round(case["E"] / (t["ms_step"] * 1e-3), 1),
+        "algorithmic_bytes_per_step": step_bytes,
+        "fwd_ms_avg": round(t["fwd_avg"], 5), "bwd_ms_avg": round(t["bwd_avg"], 5),
+        "roofline_frac_step": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline_frac_bwd": round(case["bytes_bwd"] / (t["bwd_avg"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    if n > 1:
+        fl_bwd, fl_fwd = 14.0 * n * case["E"], 5.0 * n * case["E"]
+        e["roofline_compute"] = {
+            "bound": "valu", "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "bwd_achieved": round(fl_bwd / (t["bwd_avg"] * 1e-3) / 1e12, 2),
+            "fwd_achieved": round(fl_fwd / (t["fwd_avg"] * 1e-3) / 1e12, 2),
+            "frac_step": round((fl_bwd + fl_fwd) / (t["ms_step"] * 1e-3) / 1e12 / VALU_PEAK_TFLOPS, 4)}
+    if target_ms is not None:
+        e["target_ms"] = target_ms
+        e["meets_target"] = bool(t["ms_step"] <= target_ms)
+    del case
+    torch.cuda.empty_cache()
+    return e
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c1-c4: the scan itself; c5: the LM training step (tokens/s)")
+    ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the other configurations (c1, c3, c4 at N=1; c2 at N=64; the c5 LM step)")
+    ap.add_argument("--no-flush", action="store_true",
+                    help="skip the steps timed with a 1 GiB cache-flush write before each step")
+    ap.add_argument("--tune-gemms", default=None, metavar="CSV",
+                    help="c5: time the GEMM solutions during the warmup and record them in CSV "
+                         "(default: read naju_amd/tunableop_mi355x_lm.csv)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run 3 plain 512 MiB device copies (counter calibration for rocprofv3 --pmc)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
+              "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+
+    if args.config == "c5":
+        print(json.dumps(_bench_lm(args.steps, args.warmup, args.tune_gemms, line=True)), flush=True)
+        return
+
+    import torch
+    from naju_amd import _lib
+
+    L = _lib.lib()
+    dev = torch.device("cuda", 0)
+    if args.calib_copy:
+        src = torch.ones(1 << 27, dtype=torch.float32, device=dev)   # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calib-copy: 3 x copy of {src.numel() * 4} bytes", file=sys.stderr, flush=True)
+        del src, dst
+    N = args.N
+    case = _scan_case(L, args.config, N, dev)
+    stream = torch.cuda.current_stream(dev)
+    t = _time_case(case, args.steps, args.warmup, stream)
+    Bsz, T, D, _ = case["shape"]
+    bytes_fwd, bytes_bwd = case["bytes_fwd"], case["bytes_bwd"]
+    bytes_step = bytes_fwd + bytes_bwd
+    ms_step = t["ms_step"]
+    K = args.steps
     value = bytes_step / (ms_step * 1e-3) / 1e9
     out = {
         "metric": METRIC,
@@ -160,26 +222,25 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[xdt]
-        + " streams, f32 state/accum",
-        "data": "synthetic (seeded; the c2 gate/input recipe of naju_amd.workloads)",
+        "dtype": case["dtype"] + " streams, f32 state/accum",
+        "data": f"synthetic (seeded; the {args.config} gate/input recipe of naju_amd.workloads)",
         "config": {"workload": f"naju scan fwd+bwd {args.config}: B={Bsz} L={T} D={D} N={N}"
-                   + (" B=C=1" if N == 1 else " B,C~N(0,1/N)") + (" with h0" if has_h0 else ""),
+                   + (" B=C=1" if N == 1 else " B,C~N(0,1/N)") + (" with h0" if case["has_h0"] else ""),
                    "batch": Bsz, "seq_len": T, "channels": D, "d_state": N,
                    "parallelism": "single GPU", "cache_flush": False},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "elements_per_s": round(Bsz * T * D / (ms_step * 1e-3), 1),
+        "elements_per_s": round(case["E"] / (ms_step * 1e-3), 1),
         "algorithmic_bytes_per_step": bytes_step,
-        "fwd_ms_avg": round(avg_fwd, 5), "fwd_ms_median": round(med(t_fwd), 5),
-        "bwd_ms_avg": round(avg_bwd, 5), "bwd_ms_median": round(med(t_bwd), 5),
-        "fwd_GBs": round(bytes_fwd / (avg_fwd * 1e-3) / 1e9, 1),
+        "fwd_ms_avg": round(t["fwd_avg"], 5), "fwd_ms_median": round(t["fwd_med"], 5),
+        "bwd_ms_avg": round(t["bwd_avg"], 5), "bwd_ms_median": round(t["bwd_med"], 5),
+        "fwd_GBs": round(bytes_fwd / (t["fwd_avg"] * 1e-3) / 1e9, 1),
         "roofline": {
             "kernel": "naju_scan_bwd call = n1_bwd_kernel + fold_kernel" if N == 1 else "naju_scan_bwd call",
             "bound": "hbm",
-            "achieved": round(bytes_bwd / (avg_bwd * 1e-3) / 1e9, 1),
+            "achieved": round(bytes_bwd / (t["bwd_avg"] * 1e-3) / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(bytes_bwd / (avg_bwd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac": round(bytes_bwd / (t["bwd_avg"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": _traffic(args.config, N),
         },
     }
@@ -188,40 +249,68 @@ def main():
         # about 19N flop per element (5N forward, 14N backward), fp32 FMA on
         # the VALU. Packed-FP32 ops are disabled in this build, so the peak is
         # half of MI355X's 157.3 TFLOP/s vector fp32.
-        E = Bsz * T * D
-        fl_bwd = 14.0 * N * E
-        ach = fl_bwd / (avg_bwd * 1e-3) / 1e12
+        E = case["E"]
+        ach = 14.0 * N * E / (t["bwd_avg"] * 1e-3) / 1e12
         out["roofline_compute"] = {"kernel": "naju_scan_bwd call", "bound": "valu", "achieved": round(ach, 2),
                                    "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
                                    "frac": round(ach / VALU_PEAK_TFLOPS, 4),
-                                   "fwd_achieved": round(5.0 * N * E / (avg_fwd * 1e-3) / 1e12, 2)}
-    if args.flush:
+                                   "fwd_achieved": round(5.0 * N * E / (t["fwd_avg"] * 1e-3) / 1e12, 2)}
+    if not args.no_flush:
+        # the same step with a 1 GiB write before it: nothing of the step's
+        # inputs is left in the 256 MB last-level cache
         scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         tf = []
         for k in range(min(K, 20)):
             scratch.fill_(k & 0xFF)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            fwd()
-            bwd()
+            case["fwd"]()
+            case["bwd"]()
             e1.record(stream)
             torch.cuda.synchronize()
             tf.append(e0.elapsed_time(e1))
         tf.sort()
-        out["flushed_ms_median"] = round(med(tf), 5)
-        out["flushed_GBs"] = round(bytes_step / (med(tf) * 1e-3) / 1e9, 1)
+        out["flushed_ms_median"] = round(tf[len(tf) // 2], 5)
+        out["flushed_GBs"] = round(bytes_step / (tf[len(tf) // 2] * 1e-3) / 1e9, 1)
+        out["flushed_pct_hbm_peak"] = round(100.0 * out["flushed_GBs"] / HBM_PEAK_GBS, 2)
         del scratch
+    del case
+    torch.cuda.empty_cache()
+    if not args.no_extras and args.config == "c2" and N == 1:
+        # every other configuration, each with its own GB/s and roofline
+        # fraction; c3 / c4 against the 70%-of-HBM targets
+        ks, ws = max(5, min(K, 20)), max(2, min(args.warmup, 5))
+        tgt = lambda c: round(_step_bytes_of(c, 1) / (TARGET_FRAC * HBM_PEAK_GBS * 1e9) * 1e3, 4)  # noqa: E731
+        ex = {}
+        for name, cfg, n, target in (("c1_n1", "c1", 1, None), ("c3_n1", "c3", 1, tgt("c3")),
+                                     ("c4_n1", "c4", 1, tgt("c4")), ("c2_n64", "c2", 64, None)):
+            ex[name] = _config_entry(L, cfg, n, dev, ks, ws, target)
+            print(f"bench: {name} {ex[name]['ms_per_step']} ms/step {ex[name]['GBs']} GB/s", file=sys.stderr,
+                  flush=True)
+        out["target_ms_c2_n1"] = tgt("c2")
+        ex["c5_lm_step"] = _bench_lm(max(5, min(K, 10)), 3, None, line=False)
+        print(f"bench: c5 {ex['c5_lm_step']['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
+        out["configs"] = ex
     out["cpu_baseline"] = None if args.no_cpu else _cpu_baseline(args.config, N)
     print(json.dumps(out), flush=True)
 
 
-def _bench_lm(args):
+def _step_bytes_of(config, N):
+    import torch
+    from naju_amd.workloads import CONFIGS, algorithmic_bytes
+    c = CONFIGS[config]
+    s = 4 if c["dtype"] == torch.float32 else 2
+    return algorithmic_bytes(c["batch"], c["T"], c["D"], N, s, s, s, c["h0_std"] > 0)
+
+
+def _bench_lm(steps, warmup, tune_gemms=None, line=True):
     """Benchmark configuration c5: one training step of the Naju LM (12 layers,
     d_model 768, vocab 50257, N = 64) on a batch of 8 x 2048 uniformly random
     token ids: bf16 autocast forward, cross-entropy (the fused HIP kernels of
     naju_amd.xent on the bf16 logits), backward, gradient
     clipping at 1.0 and an AdamW step, with every mixer's scan on the HIP
-    kernels. value = tokens per second."""
+    kernels. value = tokens per second. line=True: the whole bench line;
+    else the entry of the per-configuration table."""
     import torch
     from naju_amd.mixer import NajuLM, build_optimizer
     from naju_amd.xent import cross_entropy
@@ -229,9 +318,9 @@ def _bench_lm(args):
     dev = torch.device("cuda", 0)
     # GEMM solutions: the recorded choice for these shapes (PyTorch
     # TunableOp), or time them now with --tune-gemms (during the warmup)
-    if args.tune_gemms:
-        gemm_tuning.tune(args.tune_gemms)
-        tuned = args.tune_gemms
+    if tune_gemms:
+        gemm_tuning.tune(tune_gemms)
+        tuned = tune_gemms
     else:
         tuned = gemm_tuning.DEFAULT if gemm_tuning.load() else None
     V, d_model, n_layers, T, Bsz = 50257, 768, 12, 2048, 8
@@ -252,7 +341,7 @@ def _bench_lm(args):
         opt.step()
         return loss
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     # Python's cyclic collector: a full collection walks every live object and
@@ -260,30 +349,37 @@ def _bench_lm(args):
     # meanwhile); the objects alive after the warmup are moved out of its way
     gc.collect()
     gc.freeze()
-    K = args.steps
+    K = steps
     t0 = time.perf_counter()
     for _ in range(K):
         loss = step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / K
+    gc.unfreeze()
     tokens = Bsz * T
     tflops = 6.0 * n_params * tokens / dt / 1e12
-    out = {
+    workload = ("naju LM training step c5: 12 layers, d_model 768, vocab 50257, N=64, "
+                "batch 8 x seq 2048, AdamW + clip 1.0")
+    roof = {"kernel": "whole training step (6 x parameters x tokens)", "bound": "mfma",
+            "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+            "frac": round(tflops / 2500.0, 4), "traffic": None}
+    loss_last = round(float(loss.detach()), 4)
+    del model, opt, ids, x, y, loss
+    torch.cuda.empty_cache()
+    if not line:
+        return {"workload": workload, "steps": K, "ms_per_step": round(dt * 1e3, 3),
+                "tokens_per_s": round(tokens / dt, 1), "model_TFLOPs": round(tflops, 1),
+                "roofline": roof, "loss_last": loss_last,
+                "gemm_choices": os.path.basename(tuned) if tuned else "library default"}
+    return {
         "metric": METRIC, "value": round(tokens / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
-        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "warmup": warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16 autocast (scan in f32 state)",
         "data": "synthetic (uniform random token ids; random init)",
-        "config": {"workload": "naju LM training step c5: 12 layers, d_model 768, vocab 50257, N=64, "
-                               "batch 8 x seq 2048, AdamW + clip 1.0",
-                   "parameters": n_params, "parallelism": "single GPU",
+        "config": {"workload": workload, "parameters": n_params, "parallelism": "single GPU",
                    "gemm_choices": os.path.basename(tuned) if tuned else "library default"},
-        "loss_last": round(float(loss.detach()), 4),
-        "roofline": {"kernel": "whole training step (6 x parameters x tokens)", "bound": "mfma",
-                     "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(tflops / 2500.0, 4), "traffic": None},
-        "cpu_baseline": None,
+        "loss_last": loss_last, "roofline": roof, "cpu_baseline": None,
     }
-    print(json.dumps(out), flush=True)
 
 
 def _traffic(config, N):
@@ -297,35 +393,101 @@ def _traffic(config, N):
         return None
 
 
+def _cpu_info():
+    """Host facts for the CPU baseline: core counts, model, SMT state."""
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    info["cpu_model"] = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    for key, path in (("smt_active", "/sys/devices/system/cpu/smt/active"),
+                      ("smt_control", "/sys/devices/system/cpu/smt/control"),
+                      ("cgroup_cpu_max", "/sys/fs/cgroup/cpu.max")):
+        try:
+            with open(path) as f:
+                info[key] = f.read().strip()
+        except OSError:
+            pass
+    return info
+
+
+def _cpu_time(fn, runs=3):
+    """1 warmup, then the median of `runs` timed runs (seconds)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts
+
+
 def _cpu_baseline(config, N):
-    """The reference's sequential scan algorithm (torch CPU, autograd) on a
-    bounded sample of the workload: all batch rows and channels, the first
-    T_s timesteps. GB/s with the same algorithmic-byte formula."""
+    """The reference's sequential scan algorithm (oracle/scan_ref.py:
+    scan_loop_torch, restating naju/scan.py:79-93) on the host cores, torch
+    intra-op threads = os.cpu_count(): 1 warmup + the median of 3 runs of
+      * configuration c1 (2 x 1024 x 256, fp32) forward under no_grad and
+        forward + backward (autograd), each at N = 1 and N = 64;
+      * a bounded sample of the benchmarked workload, forward + backward:
+        all batch rows and channels, the first timesteps up to 8 M elements
+        (1024 of c2's 4096), whose GB/s (same algorithmic-byte formula) is
+        the baseline value. The loop's backward costs O(T^2): each step's
+        u[:, t]-style selection writes a full-size gradient in its backward,
+        so the whole c2 length would be slower per element than the sample.
+    """
     import torch
     from naju_amd.workloads import CONFIGS, algorithmic_bytes, make_inputs
     from oracle.scan_ref import scan_loop_torch
-    cfg = CONFIGS[config]
-    Bsz, D = cfg["batch"], cfg["D"]
-    Ts = 1024 if config in ("c1", "c2") else 256
-    Ts = min(Ts, cfg["T"])
-    cores = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(cores)
-    ins = make_inputs(Bsz, Ts, D, N=N, dtype=torch.float32, gate=cfg["gate"], h0_std=cfg["h0_std"], seed=0,
-                      device="cpu")
+    info = _cpu_info()
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    info["torch_threads"] = torch.get_num_threads()
     names = ("u", "f_logit", "i_logit", "B", "C", "D_skip")
-    xs = [ins[k].requires_grad_(True) for k in names]
-    h0 = ins["h0"].requires_grad_(True) if ins["h0"] is not None else None
-    t0 = time.perf_counter()
-    yv = scan_loop_torch(*xs, h0=h0)
-    yv.backward(ins["dy"])
-    dt = time.perf_counter() - t0
-    s = 4 if cfg["dtype"] == torch.float32 else 2
-    nbytes = algorithmic_bytes(Bsz, Ts, D, N, s, s, s, h0 is not None)
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "seconds": round(dt, 2),
-            "sample": f"{config} fwd+bwd, all {Bsz} batch rows x {D} channels, first {Ts} of {cfg['T']} "
-                      f"timesteps, N={N}; torch-CPU loop restating naju/scan.py:79-93 with autograd, fp32 "
-                      f"arithmetic; bytes counted at the workload's dtypes"}
+
+    def case(cfg_name, T, n, grad):
+        cfg = CONFIGS[cfg_name]
+        Bsz, D = cfg["batch"], cfg["D"]
+        ins = make_inputs(Bsz, T, D, N=n, dtype=torch.float32, gate=cfg["gate"], h0_std=cfg["h0_std"], seed=0,
+                          device="cpu")
+
+        def run():
+            if grad:
+                xs = [ins[k].clone().requires_grad_(True) for k in names]
+                h0 = ins["h0"].clone().requires_grad_(True) if ins["h0"] is not None else None
+                scan_loop_torch(*xs, h0=h0).backward(ins["dy"])
+            else:
+                with torch.no_grad():
+                    scan_loop_torch(*[ins[k] for k in names], h0=ins["h0"])
+
+        med, ts = _cpu_time(run)
+        s = 4 if cfg["dtype"] == torch.float32 else 2
+        nbytes = algorithmic_bytes(Bsz, T, D, n, s, s, s, ins["h0"] is not None, fwd=True, bwd=grad)
+        return {"seconds_median": round(med, 4), "seconds": [round(t, 4) for t in ts],
+                "GBs": round(nbytes / med / 1e9, 5), "elements_per_s": round(Bsz * T * D / med, 1)}
+
+    c1 = {}
+    for n in (1, 64):
+        c1[f"fwd_nograd_N{n}"] = case("c1", 1024, n, False)
+        c1[f"fwd_bwd_N{n}"] = case("c1", 1024, n, True)
+    cfg = CONFIGS[config]
+    Ts = min(cfg["T"], max(1, (8 << 20) // (cfg["batch"] * cfg["D"] * max(1, N // 16))))
+    main_case = case(config, Ts, N, True)
+    part = "the whole workload" if Ts == cfg["T"] else f"first {Ts} of {cfg['T']} timesteps"
+    return {"value": main_case["GBs"], "unit": "GB/s", "cores": info["torch_threads"], "kind": "port",
+            "seconds": main_case["seconds_median"],
+            "sample": f"{config} fwd+bwd, all {cfg['batch']} batch rows x {cfg['D']} channels, {part}, N={N}; "
+                      f"torch-CPU loop restating naju/scan.py:79-93 with autograd (its backward is O(T^2)), fp32 "
+                      f"arithmetic, bytes counted at the workload's dtypes; 1 warmup + median of 3",
+            "elements_per_s": main_case["elements_per_s"], "c1": c1, "host": info}
 
 
 if __name__ == "__main__":
