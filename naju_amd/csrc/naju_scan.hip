@@ -41,43 +41,11 @@
 #include <string.h>
 
 #include "naju_scan.h"
+#include "scan_internal.h"
 
 namespace {
 
-typedef __bf16 bf16_t;
-typedef _Float16 f16_t;
-
-// ------------------------------------------------------------------ helpers
-
-__device__ __forceinline__ float to_f32(float x) { return x; }
-__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
-__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
-
-template <typename T>
-__device__ __forceinline__ T from_f32(float x) {
-  return (T)x;
-}
-
-// sigmoid(x) = 1 / (1 + 2^(-x*log2 e)); exact 0 and 1 at -inf and +inf,
-// so hard-reset (f=0) and pure-retention (f=1) gates stay exact.
-__device__ __forceinline__ float sigm(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
-}
-
-// Load with a runtime dtype code (B_t / C_t scalars and other small streams).
-__device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
-  if (dt == NAJU_DTYPE_F32) return ((const float*)p)[i];
-  if (dt == NAJU_DTYPE_BF16) return (float)((const bf16_t*)p)[i];
-  return (float)((const f16_t*)p)[i];
-}
-__device__ __forceinline__ void st_any(void* p, int dt, int64_t i, float v) {
-  if (dt == NAJU_DTYPE_F32)
-    ((float*)p)[i] = v;
-  else if (dt == NAJU_DTYPE_BF16)
-    ((bf16_t*)p)[i] = (bf16_t)v;
-  else
-    ((f16_t*)p)[i] = (f16_t)v;
-}
+using namespace naju_detail;
 
 // V consecutive elements starting at element d0 of row `p`, by access mode:
 //   kVecAll : one aligned vector access, no bounds check (the caller knows
@@ -169,69 +137,6 @@ __device__ __forceinline__ void st_word(uint64_t* p, float v, uint32_t tag) {
 }
 __device__ __forceinline__ bool word_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
-
-// Workspace header, a fixed-size region that no other part of any layout
-// ever overlaps (so its counters, which must start at zero, are only ever
-// written by the ticket logic below): word 0 is the status word; word 1 the
-// device epoch (look-back tags of launches recorded into a HIP graph, see
-// epoch_bump_kernel); tile t's ticket counter is word kCtrBase + t*kCtrStride,
-// t < kMaxTiles.
-enum { HDR_STATUS = 0, HDR_EPOCH = 1 };
-constexpr int kCtrBase = 64;
-constexpr int kCtrStride = 4;
-constexpr int kMaxTiles = 1 << 16;
-constexpr size_t kHeaderBytes = ((size_t)kCtrBase + (size_t)kMaxTiles * kCtrStride) * sizeof(uint32_t);
-// Bound on idle polls of one look-back. A poll is a few device-scope loads
-// plus a short sleep (~1 us), so the bound is about a second, far beyond any
-// legitimate wait (microseconds); past it the carry becomes NaN and the
-// status word records the failure, so every wave still exits.
-constexpr uint32_t kSpinLimit = 1u << 20;
-
-// Kernel arguments (one struct for every kernel; unused fields are null).
-struct ScanArgs {
-  const void* u;
-  const void* fl;
-  const void* il;
-  const void* Bm;
-  const void* Cm;
-  const float* Dsk;
-  const float* h0;
-  const void* dy;
-  void* y;
-  float* ckpt;
-  float* hT;
-  void* du;
-  void* dfl;
-  void* dil;
-  float* dh0;
-  float* partB;  // [n_dtiles][batch][T][N]
-  float* partC;
-  float* partD;  // N = 1: [batch][K][D]; N > 1: [batch][nseg][D]
-  float* segF;   // N > 1, per time segment: [batch][nseg][D] decay over the segment
-  float* segZ;   // [batch][nseg][D][N] the segment's state map from a zero state
-  float* seg0;   // [batch][nseg][D][N] the state (adjoint carry) entering each segment
-  int nseg;      // N > 1: time segments (one workgroup each per channel tile)
-  int seg_sc;    // N > 1: sub-chunks per time segment
-  uint32_t* hdr;
-  uint64_t* agg;   // [K][n_tiles][2][CH]
-  uint64_t* incl;  // [K][n_tiles][CH]
-  int64_t T;
-  int64_t D;
-  int N;
-  int batch;
-  int bc_dt;
-  int n_dtiles;
-  int n_tiles;
-  int K;
-  int ck_rows;  // N = 1 forward: rows per checkpoint interval (the backward's chunk length)
-  int Kc;       // N = 1 forward: number of checkpoint intervals
-  // N = 1: this launch's look-back tag. Nonzero: a host tag (odd, new for
-  // every eager launch). Zero: the launch was recorded into a HIP graph, and
-  // the tag comes from the device epoch, which the one-thread
-  // epoch_bump_kernel recorded right before it advances on every replay.
-  uint32_t tag;
-  int strict;    // N = 1: take carries from the immediate predecessor's inclusive carry only
-};
 
 // Look-back tag of a launch from the device epoch E: even and nonzero, so it
 // never equals a host tag (odd) or the tag 0 of a zero-filled workspace.
@@ -2287,6 +2192,10 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int np_of(int64_t N);
 bool gq_ok(int64_t N, int64_t batch, int64_t D);
+// The chunked matrix-core kernels serve 9 <= N <= 64 in the directions that
+// have them.
+constexpr bool kMcBwd = false;
+bool use_mc(int64_t N, bool bwd) { return mc_ok(N) && (!bwd || kMcBwd); }
 int gq_channels(int64_t N);
 int gn_bwd_dt(int np);
 
@@ -2323,10 +2232,15 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   Layout l{};
   (void)x_dt;
   (void)g_dt;
+  const bool mc = use_mc(N, bwd);
   if (N == 1) {
     l.V = n1_vec_width(bwd);
     l.CH = 64 * l.V;
     l.L = bwd ? kBChunk : kFChunk;
+  } else if (mc) {  // chunked matrix-core kernels: kMcDT channels, kMcQ-row sub-blocks
+    l.V = 1;
+    l.CH = kMcDT;
+    l.L = kMcQ;
   } else {  // general N: channel tiles walking T, checkpoint every kGnCK rows
     l.V = 1;
     l.CH = bwd ? gn_bwd_dt(np_of(N)) : kGnDT;  // the backward kernel's tiles (dB/dC partials)
@@ -2337,12 +2251,13 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.n_tiles = (int)(batch * l.n_dtiles);
   l.nseg = 1;
   l.seg_sc = l.K;
-  if (N > 1 && l.n_tiles > 0 && l.K > 0 && (bwd || !gq_ok(N, batch, D))) {
+  if (N > 1 && l.n_tiles > 0 && l.K > 0 && (mc || bwd || !gq_ok(N, batch, D))) {
     // forward (lanes over channels): about kGcTargetWaves waves; backward
-    // (8-wave workgroups over 64 channels): about kGnTargetWgs workgroups
-    const int64_t per_seg = bwd ? l.n_tiles : batch * ((D + 63) / 64);
+    // (8-wave workgroups over 64 channels) and the chunked kernels (4-wave
+    // workgroups): about kGnTargetWgs workgroups
+    const int64_t per_seg = (mc || bwd) ? l.n_tiles : batch * ((D + 63) / 64);
     // (the 8-wave NP = 128 backward runs one workgroup per CU: 1024)
-    const int64_t target = bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
+    const int64_t target = mc ? kGnTargetWgs : bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
     int64_t want = (target + per_seg - 1) / per_seg;
     if (want > l.K) want = l.K;
     if (want < 1) want = 1;
@@ -2529,7 +2444,8 @@ int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N, int
                              int bc_dtype) {
   if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return -1;
   // N = 1: one state per backward chunk; N > 1: per forward sub-chunk
-  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, N == 1);
+  if (N > 1) return batch * ((T + kGnCK - 1) / kGnCK) * D * N;  // the state every kGnCK rows
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true);
   return batch * (int64_t)l.K * D * N;
 }
 
@@ -2606,6 +2522,26 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
     a.segF = (float*)(ws + l.off_segF);
     a.segZ = (float*)(ws + l.off_segZ);
     a.seg0 = (float*)(ws + l.off_seg0);
+    if (use_mc(N, false)) {
+      // chunked matrix-core forward: segment maps, their carry, the scan
+      a.n_dtiles = l.n_dtiles;
+      a.n_tiles = l.n_tiles;
+      a.ck_rows = kGnCK;
+      a.Kc = (int)((T + kGnCK - 1) / kGnCK);
+      if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+      hipError_t e = hipSuccess;
+      if (l.nseg > 1) {
+        e = mc_fwd_launch(a, true, x_dtype, gate_dtype, y_dt, st);
+        if (e == hipSuccess) {
+          const int64_t n = (int64_t)a.batch * a.D * a.N;
+          hipLaunchKernelGGL(gn_seg_carry_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, 1);
+          e = hipGetLastError();
+        }
+      }
+      if (e == hipSuccess) e = mc_fwd_launch(a, false, x_dtype, gate_dtype, y_dt, st);
+      if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+      return NAJU_OK;
+    }
     if (gq_ok(N, batch, D)) {
       // one workgroup per (batch row, channel group), over all of T
       const int64_t grid = batch * ((D + gq_channels(N) - 1) / gq_channels(N));

@@ -1,0 +1,136 @@
+// scan_internal.h -- definitions shared by the scan's translation units
+// (naju_scan.hip: the N = 1 kernels, the direct general-N kernels and the C
+// ABI; naju_scan_mc.hip: the chunked matrix-core kernels for 9 <= N <= 64).
+// Internal to the library; not part of the C ABI.
+#ifndef NAJU_SCAN_INTERNAL_H
+#define NAJU_SCAN_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "naju_scan.h"
+
+namespace naju_detail {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+// ------------------------------------------------------------------ helpers
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  return (T)x;
+}
+
+// sigmoid(x) = 1 / (1 + 2^(-x*log2 e)); exact 0 and 1 at -inf and +inf,
+// so hard-reset (f=0) and pure-retention (f=1) gates stay exact.
+__device__ __forceinline__ float sigm(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
+// Load with a runtime dtype code (B_t / C_t scalars and other small streams).
+__device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
+  if (dt == NAJU_DTYPE_F32) return ((const float*)p)[i];
+  if (dt == NAJU_DTYPE_BF16) return (float)((const bf16_t*)p)[i];
+  return (float)((const f16_t*)p)[i];
+}
+__device__ __forceinline__ void st_any(void* p, int dt, int64_t i, float v) {
+  if (dt == NAJU_DTYPE_F32)
+    ((float*)p)[i] = v;
+  else if (dt == NAJU_DTYPE_BF16)
+    ((bf16_t*)p)[i] = (bf16_t)v;
+  else
+    ((f16_t*)p)[i] = (f16_t)v;
+}
+
+// Workspace header, a fixed-size region that no other part of any layout
+// ever overlaps (so its counters, which must start at zero, are only ever
+// written by the ticket logic below): word 0 is the status word; word 1 the
+// device epoch (look-back tags of launches recorded into a HIP graph, see
+// epoch_bump_kernel); tile t's ticket counter is word kCtrBase + t*kCtrStride,
+// t < kMaxTiles.
+enum { HDR_STATUS = 0, HDR_EPOCH = 1 };
+constexpr int kCtrBase = 64;
+constexpr int kCtrStride = 4;
+constexpr int kMaxTiles = 1 << 16;
+constexpr size_t kHeaderBytes = ((size_t)kCtrBase + (size_t)kMaxTiles * kCtrStride) * sizeof(uint32_t);
+// Bound on idle polls of one look-back. A poll is a few device-scope loads
+// plus a short sleep (~1 us), so the bound is about a second, far beyond any
+// legitimate wait (microseconds); past it the carry becomes NaN and the
+// status word records the failure, so every wave still exits.
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+// Kernel arguments (one struct for every kernel; unused fields are null).
+struct ScanArgs {
+  const void* u;
+  const void* fl;
+  const void* il;
+  const void* Bm;
+  const void* Cm;
+  const float* Dsk;
+  const float* h0;
+  const void* dy;
+  void* y;
+  float* ckpt;
+  float* hT;
+  void* du;
+  void* dfl;
+  void* dil;
+  float* dh0;
+  float* partB;  // [n_dtiles][batch][T][N]
+  float* partC;
+  float* partD;  // N = 1: [batch][K][D]; N > 1: [batch][nseg][D]
+  float* segF;   // N > 1, per time segment: [batch][nseg][D] decay over the segment
+  float* segZ;   // [batch][nseg][D][N] the segment's state map from a zero state
+  float* seg0;   // [batch][nseg][D][N] the state (adjoint carry) entering each segment
+  int nseg;      // N > 1: time segments (one workgroup each per channel tile)
+  int seg_sc;    // N > 1: sub-chunks per time segment
+  uint32_t* hdr;
+  uint64_t* agg;   // [K][n_tiles][2][CH]
+  uint64_t* incl;  // [K][n_tiles][CH]
+  int64_t T;
+  int64_t D;
+  int N;
+  int batch;
+  int bc_dt;
+  int n_dtiles;
+  int n_tiles;
+  int K;
+  int ck_rows;  // N = 1 forward: rows per checkpoint interval (the backward's chunk length)
+  int Kc;       // N = 1 forward: number of checkpoint intervals
+  // N = 1: this launch's look-back tag. Nonzero: a host tag (odd, new for
+  // every eager launch). Zero: the launch was recorded into a HIP graph, and
+  // the tag comes from the device epoch, which the one-thread
+  // epoch_bump_kernel recorded right before it advances on every replay.
+  uint32_t tag;
+  int strict;    // N = 1: take carries from the immediate predecessor's inclusive carry only
+};
+
+// ------------------------------------------ chunked matrix-core path (N > 8)
+//
+// naju_scan_mc.hip. Workgroups of kMcW waves own kMcDT channels of one batch
+// row and walk one time segment in sub-blocks of kMcQ rows; the state entering
+// each checkpoint interval of a.ck_rows rows (a multiple of kMcQ) is written
+// to the checkpoint as [batch][a.Kc][D][N].
+constexpr int kMcQ = 16;
+constexpr int kMcW = 4;
+constexpr int kMcDT = 16 * kMcW;
+
+// True when the chunked kernels serve this state size.
+inline bool mc_ok(int64_t N) { return N > 8 && N <= 64; }
+
+// Forward: map = true computes the maps of segments 0 .. nseg-2 (segF /
+// segZ); map = false the scan itself from h0 or the carried segment states.
+hipError_t mc_fwd_launch(const ScanArgs& a, bool map, int x_dt, int g_dt, int y_dt, hipStream_t st);
+// Backward: map = true the adjoint maps of segments 1 .. nseg-1; map = false
+// du, dfl, dil, dh0 and the dB / dC / dD partials.
+hipError_t mc_bwd_launch(const ScanArgs& a, bool map, int x_dt, int g_dt, int du_dt, int dg_dt, hipStream_t st);
+
+}  // namespace naju_detail
+
+#endif  // NAJU_SCAN_INTERNAL_H
