@@ -1455,61 +1455,6 @@ constexpr int kGnH = 16;          // rows per adjoint half
 constexpr int kGnRG = 8;          // rows per reduction group
 constexpr int kGnRP = kGnCK + 4;  // LDS row pitch (floats) of the transposed tiles
 
-// Lane exchange for the butterfly steps below: the value of the partner lane
-// that differs in bit log2(m) (and, for m = 8 / 4, in the lower bits too:
-// row_mirror pairs i with 15 - i, row_half_mirror i with 7 - i).
-template <int m>
-__device__ __forceinline__ float dpp_partner(float x) {
-  constexpr int ctrl = m == 8 ? 0x140 : m == 4 ? 0x141 : m == 2 ? 0x4E : 0xB1;
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
-}
-
-// (lo, hi) -> lanes with bit log2(m) clear get lo + partner's lo, lanes with
-// it set get hi + partner's hi, m = 32 or 16 (one lane-swap instruction).
-template <int m>
-__device__ __forceinline__ float swap_sum(float lo, float hi) {
-  if constexpr (m == 32) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  } else {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-}
-
-// Transposing butterfly over aligned groups of LG lanes of the M entries of
-// v (the same scheme as tr_reduce, with DPP and lane-swap exchanges). On
-// return, lane l of a group holds the group sums of entries
-// [l*M/LG, (l+1)*M/LG) in v[0 ..) when M >= LG, else entry l / (LG/M) in
-// v[0]. Fixed order: run-to-run identical.
-template <int LG, int K, int M>
-__device__ __forceinline__ void trd_step(float (&v)[M], int lane) {
-  if constexpr (LG > 1) {
-    constexpr int m = LG / 2;
-    if constexpr (K >= 2) {
-      constexpr int h = K / 2;
-      if constexpr (m >= 16) {
-#pragma unroll
-        for (int j = 0; j < h; ++j) v[j] = swap_sum<m>(v[j], v[j + h]);
-      } else {
-        const bool hi = (lane & m) != 0;
-#pragma unroll
-        for (int j = 0; j < h; ++j) {
-          const float keep = hi ? v[j + h] : v[j], send = hi ? v[j] : v[j + h];
-          v[j] = keep + dpp_partner<m>(send);
-        }
-      }
-      trd_step<m, h, M>(v, lane);
-    } else {
-      if constexpr (m >= 16)
-        v[0] = swap_sum<m>(v[0], v[0]);
-      else
-        v[0] += dpp_partner<m>(v[0]);
-      trd_step<m, 1, M>(v, lane);
-    }
-  }
-}
-
 // Value of lane l ^ m for the lanes with bit log2(m) clear.
 template <int m>
 __device__ __forceinline__ float from_upper(float x) {
@@ -2194,8 +2139,11 @@ int np_of(int64_t N);
 bool gq_ok(int64_t N, int64_t batch, int64_t D);
 // The chunked matrix-core kernels serve 9 <= N <= 64 in the directions that
 // have them.
-constexpr bool kMcBwd = false;
+constexpr bool kMcBwd = true;
 bool use_mc(int64_t N, bool bwd) { return mc_ok(N) && (!bwd || kMcBwd); }
+// Rows per checkpoint interval of the general-N forward: the chunked
+// backward reads the state entering every kMcQ-row sub-block.
+int64_t gn_ck_rows(int64_t N) { return use_mc(N, true) ? kMcQ : kGnCK; }
 int gq_channels(int64_t N);
 int gn_bwd_dt(int np);
 
@@ -2237,9 +2185,9 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
     l.V = n1_vec_width(bwd);
     l.CH = 64 * l.V;
     l.L = bwd ? kBChunk : kFChunk;
-  } else if (mc) {  // chunked matrix-core kernels: kMcDT channels, kMcQ-row sub-blocks
+  } else if (mc) {  // chunked matrix-core kernels: kMcDT (kMcDTB) channels, kMcQ-row sub-blocks
     l.V = 1;
-    l.CH = kMcDT;
+    l.CH = bwd ? kMcDTB : kMcDT;
     l.L = kMcQ;
   } else {  // general N: channel tiles walking T, checkpoint every kGnCK rows
     l.V = 1;
@@ -2444,7 +2392,7 @@ int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N, int
                              int bc_dtype) {
   if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return -1;
   // N = 1: one state per backward chunk; N > 1: per forward sub-chunk
-  if (N > 1) return batch * ((T + kGnCK - 1) / kGnCK) * D * N;  // the state every kGnCK rows
+  if (N > 1) return batch * ((T + gn_ck_rows(N) - 1) / gn_ck_rows(N)) * D * N;  // the state every gn_ck_rows rows
   const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true);
   return batch * (int64_t)l.K * D * N;
 }
@@ -2526,8 +2474,8 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
       // chunked matrix-core forward: segment maps, their carry, the scan
       a.n_dtiles = l.n_dtiles;
       a.n_tiles = l.n_tiles;
-      a.ck_rows = kGnCK;
-      a.Kc = (int)((T + kGnCK - 1) / kGnCK);
+      a.ck_rows = (int)gn_ck_rows(N);
+      a.Kc = (int)((T + a.ck_rows - 1) / a.ck_rows);
       if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
       hipError_t e = hipSuccess;
       if (l.nseg > 1) {
@@ -2736,6 +2684,24 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     a.segZ = (float*)(ws + l.off_segZ);
     a.seg0 = (float*)(ws + l.off_seg0);
     if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+    if (use_mc(N, true)) {
+      // chunked matrix-core backward: adjoint segment maps, their carry, the
+      // backward itself
+      a.ck_rows = kMcQ;
+      a.Kc = (int)((T + kMcQ - 1) / kMcQ);
+      hipError_t e = hipSuccess;
+      if (l.nseg > 1) {
+        e = mc_bwd_launch(a, true, x_dtype, gate_dtype, du_dt, dg_dt, st);
+        if (e == hipSuccess) {
+          const int64_t n = (int64_t)a.batch * a.D * a.N;
+          hipLaunchKernelGGL(gn_seg_carry_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, -1);
+          e = hipGetLastError();
+        }
+      }
+      if (e == hipSuccess) e = mc_bwd_launch(a, false, x_dtype, gate_dtype, du_dt, dg_dt, st);
+      if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+      goto fold;
+    }
     rc = gn_segments(a, l, x_dtype, gate_dtype, true, st);
     if (rc) return rc;
     hipLaunchKernelGGL(pick_gn_bwd(np_of(N)), dim3((unsigned)((int64_t)l.n_tiles * l.nseg)),
@@ -2756,6 +2722,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
     if (rc) return rc;
   }
+fold:
   if (dB || dC || dD) {
     const int64_t btn = batch * T * N;
     // enough workgroups for about one pass of the threads over the entries

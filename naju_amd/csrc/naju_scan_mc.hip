@@ -410,6 +410,620 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
   }
 }
 
+// ----------------------------------------------------------------- backward
+//
+// Adjoint in carry form: g_t is the carry entering row t from the future
+// (f_{t+1} xbar_{t+1}), xbar_t = C_t dy_t + g_t. Over a sub-block with
+// entering state X [N x ch] (the forward's checkpoint, every kMcQ rows) and
+// carry ghat entering its last row:
+//   xbar_t = sum_{s>=t} P[s,t] C_s dy_s + Pe_t ghat
+//   dws_t  = xbar_t . B_t = sum_{s>=t} P[s,t] dy_s G[s][t] + Pe_t (B_t . ghat)
+//   xbar_t . x_t = Pf_t sum_{s>=t} P[s,t] dy_s (C_s . X)
+//                + sum_{s>=t>=r} P[s,r] dy_s w_r G[s][r]          (rectangle)
+//                + Pe_t Pf_t (ghat . X) + Pe_t sum_{r<=t} P[t,r] w_r (B_r . ghat)
+//   dfl_t  = (1 - f_t) (xbar_t . x_t - w_t dws_t)  (= f(1-f) xbar_t . x_{t-1},
+//            no division; exactly 0 at f = 1, and set to 0 at f = 0)
+//   du_t   = i_t dws_t + D dy_t,   dil_t = (1 - i_t) dws_t w_t
+//   dC_t   = sum_d (dy Pf)_t[d] X[.][d] + sum_{r<=t} H[t][r] B_r
+//   dB_t   = sum_d (w Pe)_t[d] ghat[.][d] + sum_{s>=t} H[s][t] C_s
+//            with H[s][r] = sum_d dy_s P[s,r] w_r (the wave's 16 channels)
+//   ghat'  = Pall ghat + C^T (Pf dy)   (the carry leaving the first row)
+// (naju/cuda/naju_cuda.cu:104-141 restated per sub-block.) C X, B ghat,
+// G = C B^T, the dB / dC products and the carry update run on the matrix
+// cores; the per-channel sums over pairs of rows on the vector units.
+//
+// Layouts. "D layout" as in the forward: lane (j, g) value r holds row
+// 4r + g of channel j, or state entry n = 16m + 4g + r of channel j. "T
+// layout": lane (j, g) value r holds entry n = 16m + j of channel 4g + r.
+// ghat is kept in both (the two carry updates read the same operands with
+// the A and B roles swapped); X is read from the checkpoint in both.
+//
+// LDS per workgroup (NP = 64): B / C staged as Bn, C [t][n] and Bt, Ct
+// [n][p(t)] (19 KB), per wave the gate tiles f, w, dy, i [channel][row]
+// (5 KB) and a pool of seven [16][TP] tiles (8.75 KB) that holds G, G^T,
+// gathers, the rectangle sums' partials, (dy Pf) / (w Pe), H / H^T and
+// finally the wave's dB / dC, which the workgroup adds in wave order.
+template <int NP, bool MAP>
+struct McBwdLds {
+  static constexpr int P = NP + 4;
+  static constexpr int POOL = 9 * 16 * TP;  // floats of a wave's pool
+  float Bn[MAP ? 1 : kMcQ][MAP ? 4 : P];
+  float C[MAP ? 1 : kMcQ][MAP ? 4 : P];
+  float Bt[MAP ? 1 : NP][TP];
+  float Ct[NP][TP];
+  float gate[kMcWB][MAP ? 2 : 4][16][TP];  // f, dy, w, i as [channel][row]; later dfl, du, dil
+  float pool[MAP ? 1 : kMcWB][POOL];
+};
+
+template <int NP, bool MAP, typename TU, typename TG, typename TB>
+struct McInB {
+  float f[4], dy[4], i[MAP ? 1 : 4], u[MAP ? 1 : 4], b[MAP ? 1 : 4], c[4];
+
+  __device__ __forceinline__ void load(const ScanArgs& a, int b_row, int64_t t0, int64_t dw, int rho, int cq,
+                                       int tid, bool vec) {
+    const int64_t T = a.T, D = a.D;
+    const int64_t rows = T - t0 < kMcQ ? T - t0 : kMcQ;
+    // row t0 of the batch row (uniform) plus a 32-bit in-bounds offset:
+    // row min(rho, rows - 1), channel clamped to D - 1
+    const int64_t base = ((int64_t)b_row * T + t0) * D;
+    const uint32_t off = (uint32_t)((rho < rows ? rho : rows - 1) * D);
+    if (vec) {
+      const uint32_t o = off + (uint32_t)(dw + cq);
+      ld4v<TG, true>((const TG*)a.fl + base, o, f);
+      ld4v<TU, true>((const TU*)a.dy + base, o, dy);
+      if constexpr (!MAP) {
+        ld4v<TG, true>((const TG*)a.il + base, o, i);
+        ld4v<TU, true>((const TU*)a.u + base, o, u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t dd = dw + cq + e < D ? dw + cq + e : D - 1;
+        const uint32_t o = off + (uint32_t)dd;
+        f[e] = to_f32(((const TG*)a.fl + base)[o]);
+        dy[e] = to_f32(((const TU*)a.dy + base)[o]);
+        if constexpr (!MAP) {
+          i[e] = to_f32(((const TG*)a.il + base)[o]);
+          u[e] = to_f32(((const TU*)a.u + base)[o]);
+        }
+      }
+    }
+    if (tid < 4 * NP) {
+      const int N = a.N;
+      const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
+      const int64_t bb = ((int64_t)b_row * T + t0) * N;
+      const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * N);
+      if (N == NP) {
+        ld4v<TB, true>((const TB*)a.Cm + bb, ro + n0, c);
+        if constexpr (!MAP) ld4v<TB, true>((const TB*)a.Bm + bb, ro + n0, b);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t o = ro + (uint32_t)(n0 + e < N ? n0 + e : N - 1);
+          c[e] = to_f32(((const TB*)a.Cm + bb)[o]);
+          if constexpr (!MAP) b[e] = to_f32(((const TB*)a.Bm + bb)[o]);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void stage(McBwdLds<NP, MAP>& sh, const ScanArgs& a, int64_t t0, int tid) const {
+    if (tid < 4 * NP) {
+      const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
+      const bool rok = t0 + row < a.T;
+      const int pr = 4 * (row & 3) + (row >> 2);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = rok && n0 + e < a.N;
+        const float vc = ok ? c[e] : 0.f;
+        sh.Ct[n0 + e][pr] = vc;
+        if constexpr (!MAP) {
+          const float vb = ok ? b[e] : 0.f;
+          sh.Bt[n0 + e][pr] = vb;
+          sh.Bn[row][n0 + e] = vb;
+          sh.C[row][n0 + e] = vc;
+        }
+      }
+    }
+  }
+};
+
+// Four floats at p (16-byte aligned) as an array.
+__device__ __forceinline__ void rd4(const float* p, float (&o)[4]) {
+  const float4 v = *(const float4*)p;
+  o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
+}
+__device__ __forceinline__ void wr4(float* p, float a0, float a1, float a2, float a3) {
+  *(float4*)p = make_float4(a0, a1, a2, a3);
+}
+
+// Four values of the load layout (row rho, channels cq .. cq+3) from a
+// [channel][row] tile into a [batch, T, D] stream of element type TT.
+template <typename TT>
+__device__ __forceinline__ void store_row4(void* p, int64_t o, const float (*tl)[TP], int cq, int rho, bool vec,
+                                           int64_t nval) {
+  typedef TT v4 __attribute__((ext_vector_type(4)));
+  v4 x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = (TT)tl[cq + e][rho];
+  if (vec) {
+    *(v4*)((TT*)p + o) = x;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < nval) ((TT*)p)[o + e] = x[e];
+  }
+}
+
+template <int NP, bool MAP, typename TU, typename TG, typename TB>
+__global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, int du_dt, int dg_dt) {
+  constexpr int MT = NP / 16;
+  constexpr int P = NP + 4;
+  using In = McInB<NP, MAP, TU, TG, TB>;
+  __shared__ __align__(16) McBwdLds<NP, MAP> sh;
+
+  const int N = a.N;
+  const int64_t T = a.T, D = a.D;
+  const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
+  const int seg = (int)(blockIdx.x / (uint32_t)a.n_tiles) + (MAP ? 1 : 0);
+  const int b = tile / a.n_dtiles;
+  const int dtile = tile - b * a.n_dtiles;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int64_t dw = (int64_t)dtile * kMcDTB + 16 * wv;
+  const int64_t d = dw + j;
+  const bool dok = d < D;
+  const int KS = (int)((T + Q - 1) / Q);
+  const int sb0 = seg * a.seg_sc;
+  const int sb1 = sb0 + a.seg_sc < KS ? sb0 + a.seg_sc : KS;
+  const bool vec = dw + 16 <= D && D % 4 == 0;
+  const int rho = lane >> 2, cq = (lane & 3) * 4;
+  const int ncq = (int)(D - dw - cq < 4 ? (D - dw - cq < 0 ? 0 : D - dw - cq) : 4);  // valid of cq .. cq+3
+  const float Dv = (!MAP && dok) ? a.Dsk[d] : 0.f;
+
+  // adjoint carry in the D layout: gh[m][r] = entry 16m + 4g + r of channel j
+  f4_t gh[MT];
+  {
+    const float* gin = (!MAP && a.nseg > 1) ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N : nullptr;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = 16 * m + 4 * g + r;
+        gh[m][r] = (gin && dok && n < N) ? gin[d * N + n] : 0.f;
+      }
+  }
+  float Fseg = 1.f;
+  float dDacc[4] = {0.f, 0.f, 0.f, 0.f};
+
+  float (*Tf)[TP] = sh.gate[wv][0];
+  float (*Tdy)[TP] = sh.gate[wv][1];
+
+  In cur, nxt;
+  if (sb0 < sb1) cur.load(a, b, (int64_t)(sb1 - 1) * Q, dw, rho, cq, tid, vec);
+  for (int sb = sb1 - 1; sb >= sb0; --sb) {
+    // The lane's indices, recomputed every sub-block from an opaque copy of
+    // the lane id (they shadow the ones above): otherwise every
+    // lane-dependent LDS and global address is hoisted out of the loop, and
+    // holding them all costs more registers than recomputing them.
+    int lane_l = lane;
+    asm volatile("" : "+v"(lane_l));
+    const int j = lane_l & 15, g = lane_l >> 4;
+    const int rho = lane_l >> 2, cq = (lane_l & 3) * 4;
+    const int arow = 4 * (j & 3) + (j >> 2);
+    const int ncq = (int)(D - dw - cq < 4 ? (D - dw - cq < 0 ? 0 : D - dw - cq) : 4);
+    const int64_t d = dw + j;
+    const bool dok = d < D;
+    const int64_t dcl = dok ? d : D - 1;
+    const int tid = 64 * wv + lane_l;
+    const int64_t t0 = (int64_t)sb * Q;
+    // ---- stage B / C; gates in the load layout (each element once; rows
+    // past T and channels past D are the neutral step f = 1, i = w = dy = 0)
+    cur.stage(sh, a, t0, tid);
+    const bool rok = t0 + rho < T;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool ok = rok && e < ncq;
+      Tf[cq + e][rho] = ok ? sigm(cur.f[e]) : 1.f;
+      Tdy[cq + e][rho] = ok ? cur.dy[e] : 0.f;
+      if constexpr (!MAP) {
+        const float ig = ok ? sigm(cur.i[e]) : 0.f;
+        sh.gate[wv][3][cq + e][rho] = ig;
+        sh.gate[wv][2][cq + e][rho] = ok ? ig * cur.u[e] : 0.f;
+        dDacc[e] = fmaf(ok ? cur.dy[e] : 0.f, ok ? cur.u[e] : 0.f, dDacc[e]);
+      }
+    }
+    __syncthreads();  // staging visible
+    if (sb - 1 >= sb0) nxt.load(a, b, t0 - Q, dw, rho, cq, tid, vec);
+    asm volatile("" ::: "memory");
+
+    // this lane's channel: gates and dy over all rows, decays of the own rows
+    float fa[Q];
+#pragma unroll
+    for (int q4 = 0; q4 < Q; q4 += 4) {
+      float f4[4];
+      rd4(&Tf[j][q4], f4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) fa[q4 + e] = f4[e];
+    }
+    float pf[4], pe[4], dy_o[4], pfdy[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dy_o[r] = Tdy[j][4 * r + g];
+    const float Pall = own_decays(fa, g, pf, pe);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pfdy[r] = pf[r] * dy_o[r];
+
+    if constexpr (!MAP) {
+      float (*Tw)[TP] = sh.gate[wv][2];
+      float (*Ti)[TP] = sh.gate[wv][3];
+      float* pl = sh.pool[wv];
+      float (*TGm)[TP] = (float (*)[TP])(pl + 0 * 16 * TP);  // G[s][t]
+      float (*TGT)[TP] = (float (*)[TP])(pl + 1 * 16 * TP);  // G[s][t] at [t][s]
+      float (*Tx1)[TP] = (float (*)[TP])(pl + 2 * 16 * TP);  // gathers, then row sums
+      float (*Tx2)[TP] = (float (*)[TP])(pl + 3 * 16 * TP);
+      float (*TH)[TP] = (float (*)[TP])(pl + 4 * 16 * TP);   // H[t][p(r)]
+      float (*THT)[TP] = (float (*)[TP])(pl + 5 * 16 * TP);  // H[s][t] at [t][p(s)]
+      // column partials of the rectangle sums: group g in pool tile 6 + g for
+      // g < 3, group 3 in tile 3 (free by then)
+      // ---- G = C B^T (k-step (q, r') takes n = 16q + 4k + r')
+      {
+        f4_t G = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < MT; ++q) {
+          float c4[4], b4[4];
+          rd4(&sh.C[j][16 * q + 4 * g], c4);
+          rd4(&sh.Bn[j][16 * q + 4 * g], b4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) G = mma(c4[e], b4[e], G);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) TGm[4 * g + r][j] = G[r];
+        wr4(&TGT[j][4 * g], G[0], G[1], G[2], G[3]);
+      }
+      // ---- C X and B ghat for the own rows (MFMA row 4g + r = time row
+      // 4r + g), and ghat . X per channel; X from the checkpoint
+      f4_t cx = {0.f, 0.f, 0.f, 0.f}, bg = {0.f, 0.f, 0.f, 0.f};
+      float gX = 0.f;
+      {
+        const float* ck = a.ckpt + ((int64_t)b * a.Kc + sb) * D * N + dcl * N;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const int n = 16 * m + 4 * g;
+          float x4[4];
+          if ((N & 3) == 0) {
+            const int nc = n < N ? n : N - 4;
+            rd4(ck + nc, x4);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x4[r] = ck[n + r < N ? n + r : N - 1];
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x4[r] = (dok && n + r < N) ? x4[r] : 0.f;
+          float c4[4], b4[4];
+          rd4(&sh.C[arow][16 * m + 4 * g], c4);
+          rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cx = mma(c4[e], x4[e], cx);
+            bg = mma(b4[e], gh[m][e], bg);
+            gX = fmaf(gh[m][e], x4[e], gX);
+          }
+        }
+      }
+      gX += __shfl_xor(gX, 16, 64);
+      gX += __shfl_xor(gX, 32, 64);
+      // ---- V1 = sum_{s>=t} P[s,t] dy_s G[s][t], V2 = sum_{s>=t} P[s,t] dy_s (C X)_s
+      // (Horner from s = 15 down), V3 = sum_{r<=t} P[t,r] w_r (B ghat)_r
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = cx[r], Tx2[j][4 * r + g] = bg[r];
+      asm volatile("" ::: "memory");
+      // (operands are read from the tiles in 4-row chunks as they are needed,
+      // which keeps the live registers low)
+      float V1[4], V2[4], V3[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 4 * r + g;
+        float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+        for (int s4 = 12; s4 >= 4 * r; s4 -= 4) {
+          float gt4[4], y4[4], c4[4];
+          rd4(&TGT[t][s4], gt4);
+          rd4(&Tdy[j][s4], y4);
+          rd4(&Tx1[j][s4], c4);
+#pragma unroll
+          for (int e = 3; e >= 0; --e) {
+            const int s = s4 + e;
+            const float fs = s < Q - 1 ? fa[s + 1] : 1.f;
+            if (s >= 4 * r + 3) {
+              a1 = fmaf(a1, fs, y4[e] * gt4[e]);
+              a2 = fmaf(a2, fs, y4[e] * c4[e]);
+            } else {
+              const bool in = s >= t;
+              a1 = in ? fmaf(a1, fs, y4[e] * gt4[e]) : a1;
+              a2 = in ? fmaf(a2, fs, y4[e] * c4[e]) : a2;
+            }
+          }
+        }
+        V1[r] = a1;
+        V2[r] = a2;
+        float a3 = 0.f;
+#pragma unroll
+        for (int q4 = 0; q4 <= 4 * r; q4 += 4) {
+          float w4[4], b4[4];
+          rd4(&Tw[j][q4], w4);
+          rd4(&Tx2[j][q4], b4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int q = q4 + e;
+            if (q <= 4 * r) {
+              a3 = fmaf(a3, fa[q], w4[e] * b4[e]);
+            } else {
+              const bool in = q <= t;
+              a3 = fmaf(a3, in ? fa[q] : 1.f, in ? w4[e] * b4[e] : 0.f);
+            }
+          }
+        }
+        V3[r] = a3;
+      }
+      // ---- rectangle sums A3_t = sum_{s>=t>=r} M[s][r] with M = K G[s][r],
+      // K[s][r] = P[s,r] dy_s w_r; per row block r the K of the own row
+      // s = 4r + g (16 slots, q <= 4r + 3) are summed over the wave's 16
+      // channels by a transposing butterfly in each 16-lane row, after which
+      // lane j holds slot q = j: H[s][j]
+      float cp[Q], rs[4];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) cp[q] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s = 4 * r + g;
+        float hv[Q];
+        float Pz = 0.f, rsum = 0.f;
+#pragma unroll
+        for (int q4 = 4 * r; q4 >= 0; q4 -= 4) {
+          float w4[4], g4[4];
+          rd4(&Tw[j][q4], w4);
+          rd4(&TGm[s][q4], g4);
+#pragma unroll
+          for (int e = 3; e >= 0; --e) {
+            const int q = q4 + e;
+            // Pz = P[s, q] = prod_{q < q' <= s} f for q <= s, 0 for q > s
+            // (a product chain with no masked multiply, so that it stays
+            // straight-line code)
+            if (q == 4 * r + 3) {
+              Pz = q == s ? 1.f : 0.f;
+            } else if (q >= 4 * r) {
+              Pz = q == s ? 1.f : Pz * fa[q + 1];
+            } else {
+              Pz = Pz * fa[q + 1];
+            }
+            const float kv = Pz * (dy_o[r] * w4[e]);
+            hv[q] = kv;
+            const float mv = kv * g4[e];
+            rsum += mv;
+            cp[q] += mv;
+          }
+        }
+#pragma unroll
+        for (int q = 4 * r + 4; q < Q; ++q) hv[q] = 0.f;
+        rs[r] = rsum;
+        trd_step<16, Q, Q>(hv, lane);
+        // lane j: H[s][j] (zero for j > s: every slot past s held zeros);
+        // over r and the lanes every entry of both tiles is written
+        TH[s][4 * (j & 3) + (j >> 2)] = hv[0];
+        THT[j][4 * (s & 3) + (s >> 2)] = hv[0];
+      }
+      // row sums of all 16 rows, and column sums over the channel's lanes
+      // (group g's partials in pool tile 6 + g for g < 3, tile 3 for g = 3)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = rs[r];
+      {
+        float* tc = pl + (g < 3 ? 6 + g : 3) * 16 * TP;
+#pragma unroll
+        for (int q4 = 0; q4 < Q; q4 += 4) wr4(tc + j * TP + q4, cp[q4], cp[q4 + 1], cp[q4 + 2], cp[q4 + 3]);
+      }
+      asm volatile("" ::: "memory");
+      // A3_t = sum_{s>=t} rowsum[s] - sum_{q>t} colsum[q]
+      float A3[4];
+      {
+        float sufR = 0.f, sufC = 0.f;
+#pragma unroll
+        for (int r = 3; r >= 0; --r) {
+          float r4[4], c0[4], c1[4], c2[4], c3[4], cs[4];
+          rd4(&Tx1[j][4 * r], r4);
+          rd4(pl + 6 * 16 * TP + j * TP + 4 * r, c0);
+          rd4(pl + 7 * 16 * TP + j * TP + 4 * r, c1);
+          rd4(pl + 8 * 16 * TP + j * TP + 4 * r, c2);
+          rd4(pl + 3 * 16 * TP + j * TP + 4 * r, c3);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cs[e] = (c0[e] + c1[e]) + (c2[e] + c3[e]);
+          const float sR = sufR + r4[3] + (g <= 2 ? r4[2] : 0.f) + (g <= 1 ? r4[1] : 0.f) + (g <= 0 ? r4[0] : 0.f);
+          const float sC = sufC + (g < 3 ? cs[3] : 0.f) + (g < 2 ? cs[2] : 0.f) + (g < 1 ? cs[1] : 0.f);
+          A3[r] = sR - sC;
+          sufR += (r4[0] + r4[1]) + (r4[2] + r4[3]);
+          sufC += (cs[0] + cs[1]) + (cs[2] + cs[3]);
+        }
+      }
+      // ---- outputs of the own rows into the gate tiles (dfl over f, du over
+      // i, dil over w), stored in the load layout
+      float q1[4], q2[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float f_o = Tf[j][4 * r + g], i_o = Ti[j][4 * r + g], w_o = Tw[j][4 * r + g];
+        const float dws = fmaf(pe[r], bg[r], V1[r]);
+        const float xx = fmaf(pf[r], V2[r], A3[r]) + pe[r] * fmaf(pf[r], gX, V3[r]);
+        const float dfl = f_o == 0.f ? 0.f : (1.f - f_o) * fmaf(-w_o, dws, xx);
+        const float du = fmaf(i_o, dws, Dv * dy_o[r]);
+        const float dil = (1.f - i_o) * (dws * w_o);
+        q1[r] = pfdy[r];
+        q2[r] = w_o * pe[r];
+        Tf[j][4 * r + g] = dfl;
+        Ti[j][4 * r + g] = du;
+        Tw[j][4 * r + g] = dil;
+      }
+      asm volatile("" ::: "memory");
+      if (rok && ncq > 0) {
+        const int64_t o = ((int64_t)b * T + t0 + rho) * D + dw + cq;
+        if (a.du) {
+          if (du_dt == NAJU_DTYPE_F32) store_row4<float>(a.du, o, Ti, cq, rho, vec, ncq);
+          else store_row4<TU>(a.du, o, Ti, cq, rho, vec, ncq);
+        }
+        if (dg_dt == NAJU_DTYPE_F32) {
+          if (a.dfl) store_row4<float>(a.dfl, o, Tf, cq, rho, vec, ncq);
+          if (a.dil) store_row4<float>(a.dil, o, Tw, cq, rho, vec, ncq);
+        } else {
+          if (a.dfl) store_row4<TG>(a.dfl, o, Tf, cq, rho, vec, ncq);
+          if (a.dil) store_row4<TG>(a.dil, o, Tw, cq, rho, vec, ncq);
+        }
+      }
+      // ---- dC^T [n][t] and dB^T [n][t] per 16-entry tile of n (channel part:
+      // K = channel 4g + kk; H part: K = row 4kk + g). The MFMA A operands X
+      // and ghat (entering this sub-block) per channel and entry come through
+      // this wave's pool as [16 channels][P] tiles, written in the D layout
+      // and read transposed.
+      float (*TQ1)[TP] = (float (*)[TP])(pl + 6 * 16 * TP);  // (dy Pf)[t][d]
+      float (*TQ2)[TP] = (float (*)[TP])(pl + 7 * 16 * TP);  // (w Pe)[t][d]
+#pragma unroll
+      for (int r = 0; r < 4; ++r) TQ1[4 * r + g][j] = q1[r], TQ2[4 * r + g][j] = q2[r];
+      asm volatile("" ::: "memory");
+      float qv1[4], qv2[4], hq[4], htq[4];
+      rd4(&TQ1[j][4 * g], qv1);
+      rd4(&TQ2[j][4 * g], qv2);
+      rd4(&TH[j][4 * g], hq);
+      rd4(&THT[j][4 * g], htq);
+      asm volatile("" ::: "memory");
+      float* TX = pl;           // X [channel][n]
+      float* TGh = pl + 16 * P;  // ghat [channel][n]
+      {
+        const float* ck = a.ckpt + ((int64_t)b * a.Kc + sb) * D * N + dcl * N;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const int n = 16 * m + 4 * g;
+          float x4[4];
+          if ((N & 3) == 0) {
+            rd4(ck + (n < N ? n : N - 4), x4);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x4[r] = ck[n + r < N ? n + r : N - 1];
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x4[r] = (dok && n + r < N) ? x4[r] : 0.f;
+          wr4(TX + j * P + n, x4[0], x4[1], x4[2], x4[3]);
+          wr4(TGh + j * P + n, gh[m][0], gh[m][1], gh[m][2], gh[m][3]);
+        }
+      }
+      asm volatile("" ::: "memory");
+      f4_t dCt[MT], dBt[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float bt4[4], ct4[4];
+        rd4(&sh.Bt[16 * m + j][4 * g], bt4);
+        rd4(&sh.Ct[16 * m + j][4 * g], ct4);
+        f4_t accC = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          accC = mma(TX[(4 * g + e) * P + 16 * m + j], qv1[e], accC);
+          accB = mma(TGh[(4 * g + e) * P + 16 * m + j], qv2[e], accB);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          accC = mma(bt4[e], hq[e], accC);
+          accB = mma(ct4[e], htq[e], accB);
+        }
+        dCt[m] = accC;
+        dBt[m] = accB;
+      }
+      // ---- carry update: ghat <- Pall ghat + C^T (Pf dy)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float ct4[4];
+        rd4(&sh.Ct[16 * m + j][4 * g], ct4);
+        gh[m] *= Pall;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
+      }
+      // ---- the wave's dC / dB [t][n] into its pool (its reads of the pool
+      // are done; other waves read it after the barrier), then the workgroup
+      // adds the waves' in wave order
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        wr4(pl + (0 * 16 + j) * P + 16 * m + 4 * g, dCt[m][0], dCt[m][1], dCt[m][2], dCt[m][3]);
+        wr4(pl + (1 * 16 + j) * P + 16 * m + 4 * g, dBt[m][0], dBt[m][1], dBt[m][2], dBt[m][3]);
+      }
+      __syncthreads();
+      {
+        const int64_t btn = (int64_t)a.batch * T * N;
+        constexpr int NE = 2 * 16 * NP;
+        constexpr int NTH = 64 * kMcWB;
+#pragma unroll
+        for (int k = 0; k < (NE + NTH - 1) / NTH; ++k) {
+          const int e = tid + NTH * k;
+          const int qd = e / (16 * NP), t = (e / NP) % 16, n = e % NP;
+          if (e < NE && t0 + t < T && n < N) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < kMcWB; ++w) acc += sh.pool[w][(qd * 16 + t) * P + n];
+            float* dst = qd == 0 ? a.partC : a.partB;
+            if (dst) dst[(int64_t)dtile * btn + ((int64_t)b * T + t0 + t) * N + n] = acc;
+          }
+        }
+      }
+    } else {
+      // MAP: the adjoint map of the segment (ghat from zero, decay product)
+      Fseg *= Pall;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float ct4[4];
+        rd4(&sh.Ct[16 * m + j][4 * g], ct4);
+        gh[m] *= Pall;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
+      }
+    }
+    __syncthreads();  // every wave is done with the staging, its tiles and the pools
+    cur = nxt;
+  }
+  if constexpr (MAP) {
+    if (!dok) return;
+    const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = 16 * m + 4 * g + r;
+        if (n < N) a.segZ[o * N + n] = gh[m][r];
+      }
+    if (g == 0) a.segF[o] = Fseg;
+  } else {
+    if (a.dh0 && seg == 0 && dok) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = 16 * m + 4 * g + r;
+          if (n < N) a.dh0[((int64_t)b * D + d) * N + n] = gh[m][r];
+        }
+    }
+    // dD of the segment: lanes with the same cq hold the same four channels
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = dDacc[e];
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      dDacc[e] = v;
+    }
+    if (a.partD && rho == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < ncq) a.partD[((int64_t)b * a.nseg + seg) * D + dw + cq + e] = dDacc[e];
+    }
+  }
+}
+
 int np16(int64_t N) { return N <= 16 ? 16 : (N <= 32 ? 32 : 64); }
 
 }  // namespace
@@ -433,6 +1047,24 @@ mc_fwd_t pick_fwd_u(int g_dt, int bc_dt, int np, bool map) {
   return bf ? pick_fwd_np<TU, TU, float>(np, map) : pick_fwd_np<TU, TU, TU>(np, map);
 }
 
+typedef void (*mc_bwd_t)(ScanArgs, int, int);
+
+template <typename TU, typename TG, typename TB>
+mc_bwd_t pick_bwd_np(int np, bool map) {
+  switch (np) {
+    case 16: return map ? mc_bwd_kernel<16, true, TU, TG, TB> : mc_bwd_kernel<16, false, TU, TG, TB>;
+    case 32: return map ? mc_bwd_kernel<32, true, TU, TG, TB> : mc_bwd_kernel<32, false, TU, TG, TB>;
+    default: return map ? mc_bwd_kernel<64, true, TU, TG, TB> : mc_bwd_kernel<64, false, TU, TG, TB>;
+  }
+}
+
+template <typename TU>
+mc_bwd_t pick_bwd_u(int g_dt, int bc_dt, int np, bool map) {
+  const bool gf = g_dt == NAJU_DTYPE_F32, bf = bc_dt == NAJU_DTYPE_F32;
+  if (gf) return bf ? pick_bwd_np<TU, float, float>(np, map) : pick_bwd_np<TU, float, TU>(np, map);
+  return bf ? pick_bwd_np<TU, TU, float>(np, map) : pick_bwd_np<TU, TU, TU>(np, map);
+}
+
 hipError_t mc_fwd_launch(const ScanArgs& a, bool map, int x_dt, int g_dt, int y_dt, hipStream_t st) {
   const int segs = map ? a.nseg - 1 : a.nseg;
   const unsigned grid = (unsigned)((int64_t)a.n_tiles * segs);
@@ -446,8 +1078,15 @@ hipError_t mc_fwd_launch(const ScanArgs& a, bool map, int x_dt, int g_dt, int y_
 }
 
 hipError_t mc_bwd_launch(const ScanArgs& a, bool map, int x_dt, int g_dt, int du_dt, int dg_dt, hipStream_t st) {
-  (void)a, (void)map, (void)x_dt, (void)g_dt, (void)du_dt, (void)dg_dt, (void)st;
-  return hipErrorNotSupported;
+  const int segs = map ? a.nseg - 1 : a.nseg;
+  const unsigned grid = (unsigned)((int64_t)a.n_tiles * segs);
+  if (grid == 0) return hipSuccess;
+  const int np = np16(a.N);
+  mc_bwd_t k = x_dt == NAJU_DTYPE_F32    ? pick_bwd_np<float, float, float>(np, map)
+               : x_dt == NAJU_DTYPE_BF16 ? pick_bwd_u<bf16_t>(g_dt, a.bc_dt, np, map)
+                                         : pick_bwd_u<f16_t>(g_dt, a.bc_dt, np, map);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(64 * kMcWB), 0, st, a, du_dt, dg_dt);
+  return hipGetLastError();
 }
 
 }  // namespace naju_detail

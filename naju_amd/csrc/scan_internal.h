@@ -111,6 +111,61 @@ struct ScanArgs {
   int strict;    // N = 1: take carries from the immediate predecessor's inclusive carry only
 };
 
+// Lane exchange for the butterfly steps below: the value of the partner lane
+// that differs in bit log2(m) (and, for m = 8 / 4, in the lower bits too:
+// row_mirror pairs i with 15 - i, row_half_mirror i with 7 - i).
+template <int m>
+__device__ __forceinline__ float dpp_partner(float x) {
+  constexpr int ctrl = m == 8 ? 0x140 : m == 4 ? 0x141 : m == 2 ? 0x4E : 0xB1;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
+}
+
+// (lo, hi) -> lanes with bit log2(m) clear get lo + partner's lo, lanes with
+// it set get hi + partner's hi, m = 32 or 16 (one lane-swap instruction).
+template <int m>
+__device__ __forceinline__ float swap_sum(float lo, float hi) {
+  if constexpr (m == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// Transposing butterfly over aligned groups of LG lanes of the M entries of
+// v (the same scheme as tr_reduce, with DPP and lane-swap exchanges). On
+// return, lane l of a group holds the group sums of entries
+// [l*M/LG, (l+1)*M/LG) in v[0 ..) when M >= LG, else entry l / (LG/M) in
+// v[0]. Fixed order: run-to-run identical.
+template <int LG, int K, int M>
+__device__ __forceinline__ void trd_step(float (&v)[M], int lane) {
+  if constexpr (LG > 1) {
+    constexpr int m = LG / 2;
+    if constexpr (K >= 2) {
+      constexpr int h = K / 2;
+      if constexpr (m >= 16) {
+#pragma unroll
+        for (int j = 0; j < h; ++j) v[j] = swap_sum<m>(v[j], v[j + h]);
+      } else {
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int j = 0; j < h; ++j) {
+          const float keep = hi ? v[j + h] : v[j], send = hi ? v[j] : v[j + h];
+          v[j] = keep + dpp_partner<m>(send);
+        }
+      }
+      trd_step<m, h, M>(v, lane);
+    } else {
+      if constexpr (m >= 16)
+        v[0] = swap_sum<m>(v[0], v[0]);
+      else
+        v[0] += dpp_partner<m>(v[0]);
+      trd_step<m, 1, M>(v, lane);
+    }
+  }
+}
+
 // ------------------------------------------ chunked matrix-core path (N > 8)
 //
 // naju_scan_mc.hip. Workgroups of kMcW waves own kMcDT channels of one batch
@@ -120,6 +175,10 @@ struct ScanArgs {
 constexpr int kMcQ = 16;
 constexpr int kMcW = 4;
 constexpr int kMcDT = 16 * kMcW;
+// the backward's workgroups: kMcWB waves over kMcDTB channels (its dB / dC
+// partial sums are per kMcDTB-channel tile)
+constexpr int kMcWB = 8;
+constexpr int kMcDTB = 16 * kMcWB;
 
 // True when the chunked kernels serve this state size.
 inline bool mc_ok(int64_t N) { return N > 8 && N <= 64; }

@@ -51,9 +51,13 @@ def test_size_queries():
     assert n > 0 and n % (8 * 1024) == 0 and n <= 8 * 1024 * 4096
     ws = L.naju_scan_workspace_bytes(8, 4096, 1024, 1, BF16, BF16, BF16)
     assert ws > 0 and ws % 256 == 0
-    # general N: one float per (b, 32-row sub-chunk, d, n)
+    # general N: one float per (b, sub-block, d, n); the chunked kernels
+    # (9 <= N <= 64) keep the state entering every 16-row sub-block, the
+    # others every 32 rows
     n64 = L.naju_scan_ckpt_elems(8, 4096, 1024, 64, BF16, F32, BF16)
-    assert n64 == 8 * (4096 // 32) * 1024 * 64
+    assert n64 == 8 * (4096 // 16) * 1024 * 64
+    n8 = L.naju_scan_ckpt_elems(8, 4096, 1024, 8, BF16, F32, BF16)
+    assert n8 == 8 * (4096 // 32) * 1024 * 8
     # invalid requests report 0 / -1 and set the message
     assert L.naju_scan_workspace_bytes(8, 4096, 1024, 0, BF16, BF16, BF16) == 0
     assert b"N" in L.naju_scan_last_error()
