@@ -537,21 +537,47 @@ __device__ __forceinline__ void wr4(float* p, float a0, float a1, float a2, floa
   *(float4*)p = make_float4(a0, a1, a2, a3);
 }
 
+// The checkpointed state entering sub-block sb of batch row b for channel
+// dcl (dok: the channel exists), in the D layout: x[m][r] = entry
+// 16m + 4g + r, zero past N and for channels past D.
+template <int MT>
+__device__ __forceinline__ void load_ckpt(f4_t (&x)[MT], const ScanArgs& a, int b, int sb, int64_t dcl, bool dok,
+                                          int g) {
+  const int N = a.N;
+  const float* ck = a.ckpt + ((int64_t)b * a.Kc + sb) * a.D * N;  // uniform
+  const uint32_t co = (uint32_t)(dcl * N);
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int n = 16 * m + 4 * g;
+    float x4[4];
+    if ((N & 3) == 0) {
+      rd4(ck + (co + (uint32_t)(n < N ? n : N - 4)), x4);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x4[r] = ck[co + (uint32_t)(n + r < N ? n + r : N - 1)];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[m][r] = (dok && n + r < N) ? x4[r] : 0.f;
+  }
+}
+
 // Four values of the load layout (row rho, channels cq .. cq+3) from a
-// [channel][row] tile into a [batch, T, D] stream of element type TT.
+// [channel][row] tile into a [batch, T, D] stream of element type TT at
+// (uniform) base p plus the 32-bit element offset o.
 template <typename TT>
-__device__ __forceinline__ void store_row4(void* p, int64_t o, const float (*tl)[TP], int cq, int rho, bool vec,
-                                           int64_t nval) {
+__device__ __forceinline__ void store_row4(void* p, uint32_t o, const float (*tl)[TP], int cq, int rho, bool vec,
+                                           int nval) {
   typedef TT v4 __attribute__((ext_vector_type(4)));
   v4 x;
 #pragma unroll
   for (int e = 0; e < 4; ++e) x[e] = (TT)tl[cq + e][rho];
+  TT* q = (TT*)p;
   if (vec) {
-    *(v4*)((TT*)p + o) = x;
+    *(v4*)(q + o) = x;
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (e < nval) ((TT*)p)[o + e] = x[e];
+      if (e < nval) q[o + e] = x[e];
   }
 }
 
@@ -602,7 +628,13 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
   float (*Tdy)[TP] = sh.gate[wv][1];
 
   In cur, nxt;
-  if (sb0 < sb1) cur.load(a, b, (int64_t)(sb1 - 1) * Q, dw, rho, cq, tid, vec);
+  // the checkpointed state entering the current (xc) and the next (xn)
+  // sub-block, loaded one sub-block ahead like the inputs
+  f4_t xc[MAP ? 1 : MT], xn[MAP ? 1 : MT];
+  if (sb0 < sb1) {
+    cur.load(a, b, (int64_t)(sb1 - 1) * Q, dw, rho, cq, tid, vec);
+    if constexpr (!MAP) load_ckpt<MT>(xc, a, b, sb1 - 1, dok ? d : D - 1, dok, g);
+  }
   for (int sb = sb1 - 1; sb >= sb0; --sb) {
     // The lane's indices, recomputed every sub-block from an opaque copy of
     // the lane id (they shadow the ones above): otherwise every
@@ -636,7 +668,10 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       }
     }
     __syncthreads();  // staging visible
-    if (sb - 1 >= sb0) nxt.load(a, b, t0 - Q, dw, rho, cq, tid, vec);
+    if (sb - 1 >= sb0) {
+      nxt.load(a, b, t0 - Q, dw, rho, cq, tid, vec);
+      if constexpr (!MAP) load_ckpt<MT>(xn, a, b, sb - 1, dcl, dok, g);
+    }
     asm volatile("" ::: "memory");
 
     // this lane's channel: gates and dy over all rows, decays of the own rows
@@ -687,28 +722,16 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       f4_t cx = {0.f, 0.f, 0.f, 0.f}, bg = {0.f, 0.f, 0.f, 0.f};
       float gX = 0.f;
       {
-        const float* ck = a.ckpt + ((int64_t)b * a.Kc + sb) * D * N + dcl * N;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const int n = 16 * m + 4 * g;
-          float x4[4];
-          if ((N & 3) == 0) {
-            const int nc = n < N ? n : N - 4;
-            rd4(ck + nc, x4);
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x4[r] = ck[n + r < N ? n + r : N - 1];
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) x4[r] = (dok && n + r < N) ? x4[r] : 0.f;
           float c4[4], b4[4];
           rd4(&sh.C[arow][16 * m + 4 * g], c4);
           rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            cx = mma(c4[e], x4[e], cx);
+            cx = mma(c4[e], xc[m][e], cx);
             bg = mma(b4[e], gh[m][e], bg);
-            gX = fmaf(gh[m][e], x4[e], gX);
+            gX = fmaf(gh[m][e], xc[m][e], gX);
           }
         }
       }
@@ -864,17 +887,22 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       }
       asm volatile("" ::: "memory");
       if (rok && ncq > 0) {
-        const int64_t o = ((int64_t)b * T + t0 + rho) * D + dw + cq;
-        if (a.du) {
-          if (du_dt == NAJU_DTYPE_F32) store_row4<float>(a.du, o, Ti, cq, rho, vec, ncq);
-          else store_row4<TU>(a.du, o, Ti, cq, rho, vec, ncq);
+        const int64_t ob = ((int64_t)b * T + t0) * D;  // uniform
+        const uint32_t o = (uint32_t)(rho * D + dw + cq);
+        void* du_p = a.du ? (char*)a.du + ob * (du_dt == NAJU_DTYPE_F32 ? 4 : 2) : nullptr;
+        const int gsz = dg_dt == NAJU_DTYPE_F32 ? 4 : 2;
+        void* dfl_p = a.dfl ? (char*)a.dfl + ob * gsz : nullptr;
+        void* dil_p = a.dil ? (char*)a.dil + ob * gsz : nullptr;
+        if (du_p) {
+          if (du_dt == NAJU_DTYPE_F32) store_row4<float>(du_p, o, Ti, cq, rho, vec, ncq);
+          else store_row4<TU>(du_p, o, Ti, cq, rho, vec, ncq);
         }
         if (dg_dt == NAJU_DTYPE_F32) {
-          if (a.dfl) store_row4<float>(a.dfl, o, Tf, cq, rho, vec, ncq);
-          if (a.dil) store_row4<float>(a.dil, o, Tw, cq, rho, vec, ncq);
+          if (dfl_p) store_row4<float>(dfl_p, o, Tf, cq, rho, vec, ncq);
+          if (dil_p) store_row4<float>(dil_p, o, Tw, cq, rho, vec, ncq);
         } else {
-          if (a.dfl) store_row4<TG>(a.dfl, o, Tf, cq, rho, vec, ncq);
-          if (a.dil) store_row4<TG>(a.dil, o, Tw, cq, rho, vec, ncq);
+          if (dfl_p) store_row4<TG>(dfl_p, o, Tf, cq, rho, vec, ncq);
+          if (dil_p) store_row4<TG>(dil_p, o, Tw, cq, rho, vec, ncq);
         }
       }
       // ---- dC^T [n][t] and dB^T [n][t] per 16-entry tile of n (channel part:
@@ -896,20 +924,10 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       float* TX = pl;           // X [channel][n]
       float* TGh = pl + 16 * P;  // ghat [channel][n]
       {
-        const float* ck = a.ckpt + ((int64_t)b * a.Kc + sb) * D * N + dcl * N;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const int n = 16 * m + 4 * g;
-          float x4[4];
-          if ((N & 3) == 0) {
-            rd4(ck + (n < N ? n : N - 4), x4);
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x4[r] = ck[n + r < N ? n + r : N - 1];
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) x4[r] = (dok && n + r < N) ? x4[r] : 0.f;
-          wr4(TX + j * P + n, x4[0], x4[1], x4[2], x4[3]);
+          wr4(TX + j * P + n, xc[m][0], xc[m][1], xc[m][2], xc[m][3]);
           wr4(TGh + j * P + n, gh[m][0], gh[m][1], gh[m][2], gh[m][3]);
         }
       }
@@ -954,19 +972,38 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       }
       __syncthreads();
       {
-        const int64_t btn = (int64_t)a.batch * T * N;
-        constexpr int NE = 2 * 16 * NP;
+        // thread tid sums four consecutive entries n .. n+3 of row t of dC
+        // (qd = 0) or dB (qd = 1) over the waves, in wave order
+        constexpr int NQ = NP / 4;
+        constexpr int NE4 = 2 * 16 * NQ;
         constexpr int NTH = 64 * kMcWB;
+        const int64_t btn = (int64_t)a.batch * T * N;
+        const int64_t pb = (int64_t)dtile * btn + ((int64_t)b * T + t0) * N;  // uniform
 #pragma unroll
-        for (int k = 0; k < (NE + NTH - 1) / NTH; ++k) {
-          const int e = tid + NTH * k;
-          const int qd = e / (16 * NP), t = (e / NP) % 16, n = e % NP;
-          if (e < NE && t0 + t < T && n < N) {
-            float acc = 0.f;
+        for (int k = 0; k < (NE4 + NTH - 1) / NTH; ++k) {
+          const int e4 = tid + NTH * k;
+          const int qd = e4 / (16 * NQ), t = (e4 / NQ) % 16, n = 4 * (e4 % NQ);
+          if ((NE4 % NTH == 0 || e4 < NE4) && t0 + t < T && n < N) {
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int w = 0; w < kMcWB; ++w) acc += sh.pool[w][(qd * 16 + t) * P + n];
+            for (int w = 0; w < kMcWB; ++w) {
+              float v4[4];
+              rd4(&sh.pool[w][(qd * 16 + t) * P + n], v4);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[e] += v4[e];
+            }
             float* dst = qd == 0 ? a.partC : a.partB;
-            if (dst) dst[(int64_t)dtile * btn + ((int64_t)b * T + t0 + t) * N + n] = acc;
+            if (dst) {
+              float* q = dst + pb;
+              const uint32_t o = (uint32_t)(t * N + n);
+              if ((N & 3) == 0) {
+                *(float4*)(q + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  if (n + e < N) q[o + e] = acc[e];
+              }
+            }
           }
         }
       }
@@ -982,8 +1019,17 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
       }
     }
-    __syncthreads();  // every wave is done with the staging, its tiles and the pools
+    // MAP: every wave is done with the staged C before it is restaged. The
+    // scan needs no barrier here: every read of the staged B / C happens
+    // before the partial-sum barrier above, and a wave writes its pool again
+    // only after the next staging barrier, which every wave reaches after
+    // its share of the partial sums.
+    if constexpr (MAP) __syncthreads();
     cur = nxt;
+    if constexpr (!MAP) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) xc[m] = xn[m];
+    }
   }
   if constexpr (MAP) {
     if (!dok) return;
