@@ -176,9 +176,9 @@ struct McIn {
 // ------------------------------------------------------------------ forward
 //
 // One workgroup per (batch row, kMcDT channels, time segment); the segment's
-// sub-blocks are walked in order, the inputs of sub-block sb + 1 loaded while
-// sb is computed, B and C double-buffered in LDS (one barrier per
-// sub-block). MAP: the segment's map from a zero state (decay per channel
+// sub-blocks are walked in order, the inputs of sub-block sb + 2 loaded while
+// sb is computed, those of sb + 1 staged at its end, B and C double-buffered in LDS (one
+// barrier per sub-block). MAP: the segment's map from a zero state (decay per channel
 // into segF, state into segZ) for the carry pass over the segments; otherwise
 // y, the checkpoint and hT from the entering state (h0, or seg0 when T is
 // split into segments).
@@ -230,15 +230,18 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
   // A-operand row of C X: MFMA row i = lane % 16 holds time row 4(i%4) + i/4
   const int arow = 4 * (j & 3) + (j >> 2);
 
-  In cur, nxt;
+  // inputs of sub-blocks sb (cur), sb + 1 (nxt) and sb + 2 (nx2): each is
+  // loaded two sub-blocks ahead of its use
+  In cur, nxt, nx2;
   if (sb0 < sb1) {
     cur.load(a, b, (int64_t)sb0 * Q, dw, rho, cq, tid, vec);
     cur.stage(sh, 0, a, (int64_t)sb0 * Q, tid);
   }
+  if (sb0 + 1 < sb1) nxt.load(a, b, (int64_t)(sb0 + 1) * Q, dw, rho, cq, tid, vec);
   for (int sb = sb0; sb < sb1; ++sb) {
     const int buf = (sb - sb0) & 1;
     const int64_t t0 = (int64_t)sb * Q;
-    if (sb + 1 < sb1) nxt.load(a, b, t0 + Q, dw, rho, cq, tid, vec);
+    if (sb + 2 < sb1) nx2.load(a, b, t0 + 2 * Q, dw, rho, cq, tid, vec);
     // gates in the load layout, each element computed once; rows past T
     // and channels past D are the neutral step f = 1, w = u = 0
     const bool rok = t0 + rho < T;
@@ -250,7 +253,6 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
       s_t[wv][2][cq + e][rho] = ok ? cur.u[e] : 0.f;
     }
     __syncthreads();  // B / C of sb are staged; every wave is done with sb - 1
-    if (sb + 1 < sb1) nxt.stage(sh, buf ^ 1, a, t0 + Q, tid);  // the other buffer is free now
     if constexpr (!MAP) {
       // G = C B^T of the sub-block, G[t][s] = sum_n C[t][n] B[s][n] (k-step
       // (q, r') takes n = 16q + 4k + r'), into this wave's LDS tile
@@ -386,7 +388,11 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
       X[m] = mma(bt.z, wp[2], X[m]);
       X[m] = mma(bt.w, wp[3], X[m]);
     }
+    // B / C of sb + 1 into the other buffer (free since the barrier above),
+    // as late as possible so that their loads have the whole sub-block to land
+    if (sb + 1 < sb1) nxt.stage(sh, buf ^ 1, a, t0 + Q, tid);
     cur = nxt;
+    nxt = nx2;
   }
   if (!dok) return;
   if (MAP) {
@@ -627,7 +633,9 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
   float (*Tf)[TP] = sh.gate[wv][0];
   float (*Tdy)[TP] = sh.gate[wv][1];
 
-  In cur, nxt;
+  // inputs of sub-blocks sb (cur) and sb - 1 (nxt), loaded one sub-block
+  // ahead; MAP (little work per sub-block) also those of sb - 2 (nx2)
+  In cur, nxt, nx2;
   // the checkpointed state entering the current (xc) and the next (xn)
   // sub-block, loaded one sub-block ahead like the inputs
   f4_t xc[MAP ? 1 : MT], xn[MAP ? 1 : MT];
@@ -635,6 +643,7 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
     cur.load(a, b, (int64_t)(sb1 - 1) * Q, dw, rho, cq, tid, vec);
     if constexpr (!MAP) load_ckpt<MT>(xc, a, b, sb1 - 1, dok ? d : D - 1, dok, g);
   }
+  if (MAP && sb1 - 2 >= sb0) nxt.load(a, b, (int64_t)(sb1 - 2) * Q, dw, rho, cq, tid, vec);
   for (int sb = sb1 - 1; sb >= sb0; --sb) {
     // The lane's indices, recomputed every sub-block from an opaque copy of
     // the lane id (they shadow the ones above): otherwise every
@@ -668,9 +677,11 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       }
     }
     __syncthreads();  // staging visible
-    if (sb - 1 >= sb0) {
+    if constexpr (MAP) {
+      if (sb - 2 >= sb0) nx2.load(a, b, t0 - 2 * Q, dw, rho, cq, tid, vec);
+    } else if (sb - 1 >= sb0) {
       nxt.load(a, b, t0 - Q, dw, rho, cq, tid, vec);
-      if constexpr (!MAP) load_ckpt<MT>(xn, a, b, sb - 1, dcl, dok, g);
+      load_ckpt<MT>(xn, a, b, sb - 1, dcl, dok, g);
     }
     asm volatile("" ::: "memory");
 
@@ -1026,7 +1037,9 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
     // its share of the partial sums.
     if constexpr (MAP) __syncthreads();
     cur = nxt;
-    if constexpr (!MAP) {
+    if constexpr (MAP) {
+      nxt = nx2;
+    } else {
 #pragma unroll
       for (int m = 0; m < MT; ++m) xc[m] = xn[m];
     }
