@@ -36,6 +36,25 @@
  *     chunk composes whichever predecessors' maps are ready first, so N = 1
  *     results repeat to float32 rounding only. N > 1 is always bitwise
  *     deterministic.
+ *   NAJU_CKPT_ROWS(r) (bits 8-15): the forward's checkpoint interval for
+ *     N > 1, r rows (a multiple of 16, up to 4080; 0 = the default). The
+ *     checkpoint holds the state every r rows (batch*ceil(T/r)*D*N floats).
+ *     The default is 16 rows for 9 <= N <= 64 (the state entering every
+ *     sub-block of the matrix-core backward) and 32 rows otherwise; a longer
+ *     interval is the memory-light mode of the reference's recompute backend
+ *     (naju/cuda/__init__.py:9-12, CK = 32 in naju/cuda/naju_cuda.cu:25):
+ *     the checkpoint then also holds the state entering each of the
+ *     forward's time segments after the first (a few [batch,D,N] blocks),
+ *     and the backward first recomputes the state at every 16-row sub-block
+ *     from it into its workspace (one forward-like pass over u, f_logit,
+ *     i_logit and B), so the memory held between forward and backward
+ *     shrinks about r/16-fold at the cost of that pass. Every gradient is
+ *     bitwise the one of the default interval. Served for 9 <= N <= 64 by
+ *     naju_scan_fwd (not by naju_scan_fwd_noalloc when its scratch forces
+ *     fewer time segments); other N accept only their default
+ *     (NAJU_ERR_UNSUPPORTED otherwise). The backward must be given the
+ *     forward's flags value for these bits, and the size queries below have
+ *     _ex forms that take it.
  *
  * Workspace: naju_scan_workspace_bytes() bytes of device memory that MUST be
  * zero-filled once before its first use; every call leaves it reusable
@@ -70,6 +89,9 @@ extern "C" {
 
 #define NAJU_FLAG_OUT_F32 1
 #define NAJU_FLAG_DETERMINISTIC 2
+#define NAJU_CKPT_SHIFT 8
+#define NAJU_CKPT_MASK (0xFF << NAJU_CKPT_SHIFT)
+#define NAJU_CKPT_ROWS(r) ((((r) / 16) & 0xFF) << NAJU_CKPT_SHIFT)
 
 #define NAJU_OK 0
 #define NAJU_ERR_INVALID -1     /* bad pointer, shape or dtype code        */
@@ -95,6 +117,20 @@ int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N,
 size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D,
                                  int64_t N, int x_dtype, int gate_dtype,
                                  int bc_dtype);
+
+/* The two size queries for the flags value given to naju_scan_fwd /
+ * naju_scan_bwd (only its NAJU_CKPT_ROWS bits matter; flags = 0 gives the
+ * figures above). A longer checkpoint interval gives a smaller checkpoint
+ * and, for the backward's recomputed states, a larger workspace. No
+ * counterpart in the reference, whose interval is a compile-time constant.
+ * Both return -1 / 0 (with naju_scan_last_error) for an interval the shape
+ * does not serve. */
+int64_t naju_scan_ckpt_elems_ex(int64_t batch, int64_t T, int64_t D,
+                                int64_t N, int x_dtype, int gate_dtype,
+                                int bc_dtype, int flags);
+size_t naju_scan_workspace_bytes_ex(int64_t batch, int64_t T, int64_t D,
+                                    int64_t N, int x_dtype, int gate_dtype,
+                                    int bc_dtype, int flags);
 
 /* Forward scan. Replaces the forward of every reference backend: the
  * sequential loop of naju/scan.py:79-93, _ChunkScanTriton.forward

@@ -13,12 +13,24 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnaju_sca
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = 0, -1, -2, -3, -4
 FLAG_OUT_F32, FLAG_DETERMINISTIC = 1, 2
+CKPT_SHIFT, CKPT_MASK = 8, 0xFF << 8
+
+
+def ckpt_rows_flag(rows):
+    """The NAJU_CKPT_ROWS(rows) flag bits (rows a multiple of 16 below 4096;
+    0 or None = the default interval)."""
+    rows = int(rows or 0)
+    if rows < 0 or rows % 16 or rows >= 4096:
+        raise ValueError(f"checkpoint interval must be a multiple of 16 below 4096, got {rows}")
+    return (rows // 16) << CKPT_SHIFT
 
 EXPORTED = (
     "naju_scan_version",
     "naju_scan_last_error",
     "naju_scan_ckpt_elems",
     "naju_scan_workspace_bytes",
+    "naju_scan_ckpt_elems_ex",
+    "naju_scan_workspace_bytes_ex",
     "naju_scan_fwd",
     "naju_scan_bwd",
     "naju_scan_workspace_status",
@@ -69,6 +81,10 @@ def lib():
     L.naju_scan_ckpt_elems.restype = I64
     L.naju_scan_workspace_bytes.argtypes = [I64] * 4 + [I] * 3
     L.naju_scan_workspace_bytes.restype = SZ
+    L.naju_scan_ckpt_elems_ex.argtypes = [I64] * 4 + [I] * 4
+    L.naju_scan_ckpt_elems_ex.restype = I64
+    L.naju_scan_workspace_bytes_ex.argtypes = [I64] * 4 + [I] * 4
+    L.naju_scan_workspace_bytes_ex.restype = SZ
     # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, flags, ws, ws_bytes,
     # stream
     L.naju_scan_fwd.argtypes = [P] * 10 + [I64] * 4 + [I] * 4 + [P, SZ, P]
@@ -122,6 +138,11 @@ def lib():
     L.naju_xent_bwd.restype = I
     _lib = L
     return _lib
+
+
+def last_error():
+    """naju_scan_last_error() as str."""
+    return lib().naju_scan_last_error().decode(errors="replace")
 
 
 def check(rc):

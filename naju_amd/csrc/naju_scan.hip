@@ -2118,7 +2118,8 @@ int n1_vec_width(bool bwd) { return bwd ? kBV : kFV; }
 struct Layout {
   int V, CH, L, K, n_dtiles, n_tiles;
   int nseg, seg_sc;  // N > 1: time segments
-  size_t off_agg, off_incl, off_partB, off_partC, off_partD, off_segF, off_segZ, off_seg0, total;
+  int ck_rows;       // the forward's checkpoint interval
+  size_t off_agg, off_incl, off_partB, off_partC, off_partD, off_segF, off_segZ, off_seg0, off_dense, total;
 };
 
 // N > 1: enough time segments that about kGnTargetWgs workgroups run per
@@ -2144,6 +2145,17 @@ bool use_mc(int64_t N, bool bwd) { return mc_ok(N) && (!bwd || kMcBwd); }
 // Rows per checkpoint interval of the general-N forward: the chunked
 // backward reads the state entering every kMcQ-row sub-block.
 int64_t gn_ck_rows(int64_t N) { return use_mc(N, true) ? kMcQ : kGnCK; }
+// The checkpoint interval the flags ask for (NAJU_CKPT_ROWS; 0 = the
+// default: the backward's chunk at N = 1, gn_ck_rows at N > 1), or -1 when
+// the shape does not serve it: longer intervals than the default only on the
+// matrix-core path, whose backward recomputes the states between.
+int64_t seg_states(int64_t batch, int64_t T, int64_t D, int64_t N, int rows);
+int ckpt_rows(int flags, int64_t N) {
+  const int r = ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16;
+  const int def = N == 1 ? kBChunk : (int)gn_ck_rows(N);
+  if (r == 0 || r == def) return def;
+  return (N > 1 && use_mc(N, true)) ? r : -1;
+}
 int gq_channels(int64_t N);
 int gn_bwd_dt(int np);
 
@@ -2170,14 +2182,32 @@ void place_regions(Layout& l, int64_t batch, int64_t T, int64_t D, int64_t N, bo
   off = align_up(off + seg_units * N * sizeof(float));
   l.off_seg0 = off;
   off = align_up(off + seg_units * N * sizeof(float));
+  // the backward's recomputed state at every sub-block when the forward's
+  // checkpoint interval is longer than the sub-block
+  const bool dense = bwd && N > 1 && use_mc(N, true) && l.ck_rows > kMcQ;
+  l.off_dense = off;
+  off = align_up(off + (dense ? (size_t)batch * ((T + kMcQ - 1) / kMcQ) * D * N * sizeof(float) : 0));
   l.total = off;
 }
 
 // cap: at N > 1, fewer time segments (down to one) until the workspace fits
 // in cap bytes; the N = 1 layout has no such freedom.
 Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd,
-                   size_t cap = SIZE_MAX) {
+                   size_t cap, int ck_rows);
+
+// The checkpoint's segment-start states (a checkpoint interval longer than
+// the matrix-core sub-block): batch * nseg * D * N floats for the forward's
+// (uncapped) segmentation, 0 otherwise.
+int64_t seg_states(int64_t batch, int64_t T, int64_t D, int64_t N, int rows) {
+  if (N == 1 || !use_mc(N, false) || rows <= kMcQ) return 0;
+  const Layout f = make_layout(batch, T, D, N, 0, 0, false, SIZE_MAX, rows);
+  return f.nseg > 1 ? batch * f.nseg * D * N : 0;
+}
+
+Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd,
+                   size_t cap = SIZE_MAX, int ck_rows = 0) {
   Layout l{};
+  l.ck_rows = ck_rows;
   (void)x_dt;
   (void)g_dt;
   const bool mc = use_mc(N, bwd);
@@ -2388,21 +2418,39 @@ int naju_scan_version(void) { return (0 << 16) | 1; }
 
 const char* naju_scan_last_error(void) { return g_err; }
 
-int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
-                             int bc_dtype) {
+int64_t naju_scan_ckpt_elems_ex(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
+                                int bc_dtype, int flags) {
   if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return -1;
-  // N = 1: one state per backward chunk; N > 1: per forward sub-chunk
-  if (N > 1) return batch * ((T + gn_ck_rows(N) - 1) / gn_ck_rows(N)) * D * N;  // the state every gn_ck_rows rows
+  const int rows = ckpt_rows(flags, N);
+  if (rows < 0) return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+                            ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N), -1;
+  // N = 1: one state per backward chunk; N > 1: the state every `rows` rows
+  // (with a longer interval than the default, also the state entering every
+  // forward time segment after the first)
+  if (N > 1) return batch * ((T + rows - 1) / rows) * D * N + seg_states(batch, T, D, N, rows);
   const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true);
   return batch * (int64_t)l.K * D * N;
 }
 
+int64_t naju_scan_ckpt_elems(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
+                             int bc_dtype) {
+  return naju_scan_ckpt_elems_ex(batch, T, D, N, x_dtype, gate_dtype, bc_dtype, 0);
+}
+
+size_t naju_scan_workspace_bytes_ex(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
+                                    int bc_dtype, int flags) {
+  if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return 0;
+  const int rows = ckpt_rows(flags, N);
+  if (rows < 0) return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+                            ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N), 0;
+  const size_t f = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, SIZE_MAX, rows).total;
+  const size_t b = make_layout(batch, T, D, N, x_dtype, gate_dtype, true, SIZE_MAX, rows).total;
+  return f > b ? f : b;
+}
+
 size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype, int gate_dtype,
                                  int bc_dtype) {
-  if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return 0;
-  const size_t f = make_layout(batch, T, D, N, x_dtype, gate_dtype, false).total;
-  const size_t b = make_layout(batch, T, D, N, x_dtype, gate_dtype, true).total;
-  return f > b ? f : b;
+  return naju_scan_workspace_bytes_ex(batch, T, D, N, x_dtype, gate_dtype, bc_dtype, 0);
 }
 
 }  // extern "C"
@@ -2418,7 +2466,12 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
-  if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC)) return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC | NAJU_CKPT_MASK))
+    return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  const int ck_rows = ckpt_rows(flags, N);
+  if (ck_rows < 0)
+    return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+                ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N);
   const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || D == 0) return NAJU_OK;
@@ -2474,8 +2527,16 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
       // chunked matrix-core forward: segment maps, their carry, the scan
       a.n_dtiles = l.n_dtiles;
       a.n_tiles = l.n_tiles;
-      a.ck_rows = (int)gn_ck_rows(N);
+      a.ck_rows = ck_rows;
       a.Kc = (int)((T + a.ck_rows - 1) / a.ck_rows);
+      if (ck_rows > kMcQ && l.nseg > 1) {
+        // the segment-start states follow the interval states in ckpt; the
+        // backward's recompute assumes the uncapped segmentation
+        if (l.nseg != make_layout(batch, T, D, N, x_dtype, gate_dtype, false, SIZE_MAX, ck_rows).nseg)
+          return fail(NAJU_ERR_UNSUPPORTED, "a checkpoint interval above %d rows needs the full workspace "
+                      "(use naju_scan_fwd)", kMcQ);
+        a.segst = ckpt ? ckpt + (int64_t)batch * a.Kc * D * N : nullptr;
+      }
       if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
       hipError_t e = hipSuccess;
       if (l.nseg > 1) {
@@ -2619,7 +2680,12 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
-  if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC)) return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC | NAJU_CKPT_MASK))
+    return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
+  const int ck_rows = ckpt_rows(flags, N);
+  if (ck_rows < 0)
+    return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+                ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N);
   const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   if (batch == 0 || T == 0 || D == 0) {
@@ -2638,7 +2704,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   if (!u || !f_logit || !i_logit || !B || !C || !D_skip || !dy)
     return fail(NAJU_ERR_INVALID, "null input pointer (u, f_logit, i_logit, B, C, D_skip and dy are required)");
   if (!ckpt) return fail(NAJU_ERR_INVALID, "ckpt is required (write it with naju_scan_fwd)");
-  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true);
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true, SIZE_MAX, ck_rows);
   if (!workspace || workspace_bytes < l.total)
     return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", l.total,
                 workspace ? workspace_bytes : (size_t)0);
@@ -2687,10 +2753,33 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     if (use_mc(N, true)) {
       // chunked matrix-core backward: adjoint segment maps, their carry, the
       // backward itself
+      hipError_t e = hipSuccess;
+      if (ck_rows > kMcQ) {
+        // memory-light checkpoint: the state entering every sub-block,
+        // recomputed from the forward's checkpoint into the workspace by the
+        // forward's kernels (one workgroup per checkpoint interval and
+        // kMcDT channels), bitwise as the forward computed it
+        ScanArgs r = a;
+        r.recomp = 1;
+        r.ck_src = ckpt;
+        r.Kc_src = (int)((T + ck_rows - 1) / ck_rows);
+        const Layout lf = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, SIZE_MAX, ck_rows);
+        r.seg_sc_f = lf.seg_sc;
+        r.nseg_f = lf.nseg;
+        r.segst = (float*)ckpt + (int64_t)batch * r.Kc_src * D * N;
+        r.ckpt = (float*)(ws + l.off_dense);
+        r.Kc = (int)((T + kMcQ - 1) / kMcQ);
+        r.seg_sc = ck_rows / kMcQ;
+        r.nseg = r.Kc_src + 1;  // the map launch runs segments 0 .. nseg - 2
+        r.n_dtiles = (int)((D + kMcDT - 1) / kMcDT);
+        r.n_tiles = (int)(batch * r.n_dtiles);
+        if ((int64_t)r.n_tiles * r.Kc_src > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
+        e = mc_fwd_launch(r, true, x_dtype, gate_dtype, x_dtype, st);
+        a.ckpt = r.ckpt;
+      }
       a.ck_rows = kMcQ;
       a.Kc = (int)((T + kMcQ - 1) / kMcQ);
-      hipError_t e = hipSuccess;
-      if (l.nseg > 1) {
+      if (e == hipSuccess && l.nseg > 1) {
         e = mc_bwd_launch(a, true, x_dtype, gate_dtype, du_dt, dg_dt, st);
         if (e == hipSuccess) {
           const int64_t n = (int64_t)a.batch * a.D * a.N;

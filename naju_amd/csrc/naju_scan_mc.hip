@@ -177,11 +177,13 @@ struct McIn {
 //
 // One workgroup per (batch row, kMcDT channels, time segment); the segment's
 // sub-blocks are walked in order, the inputs of sub-block sb + 2 loaded while
-// sb is computed, those of sb + 1 staged at its end, B and C double-buffered in LDS (one
-// barrier per sub-block). MAP: the segment's map from a zero state (decay per channel
-// into segF, state into segZ) for the carry pass over the segments; otherwise
-// y, the checkpoint and hT from the entering state (h0, or seg0 when T is
-// split into segments).
+// sb is computed, those of sb + 1 staged at its end, B and C double-buffered
+// in LDS (one barrier per sub-block). MAP: the segment's map from a zero
+// state (decay per channel into segF, state into segZ) for the carry pass
+// over the segments, or with a.recomp the states entering the segment's
+// sub-blocks, from its checkpoint (one segment per checkpoint interval),
+// into a.ckpt; otherwise y, the checkpoint and hT from the entering state
+// (h0, or seg0 when T is split into segments).
 template <int NP, bool MAP, typename TU, typename TG, typename TB>
 __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int y_dt) {
   constexpr int MT = NP / 16;  // 16-entry tiles of the state index
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
   // state entries n = 16m + 4g + r of channel d
   f4_t X[MT];
   {
-    const float* xin = MAP ? nullptr
+    const float* xin = MAP ? (a.recomp ? a.ck_src + ((int64_t)b * a.Kc_src + seg) * D * N : nullptr)
                            : (a.nseg > 1 ? a.seg0 + ((int64_t)b * a.nseg + seg) * D * N
                                          : (a.h0 ? a.h0 + (int64_t)b * D * N : nullptr));
 #pragma unroll
@@ -222,6 +224,15 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
         const int n = 16 * m + 4 * g + r;
         X[m][r] = (xin && dok && n < N) ? xin[d * N + n] : 0.f;
       }
+    // the state entering the segment, kept for the backward's recompute
+    if (!MAP && a.segst && seg > 0 && dok) {
+      float* st = a.segst + (((int64_t)b * a.nseg + seg) * D + d) * N;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * m + 4 * g + r < N) st[16 * m + 4 * g + r] = X[m][r];
+    }
   }
   float Fseg = 1.f;
   const float Dv = (!MAP && dok) ? a.Dsk[d] : 0.f;
@@ -374,6 +385,33 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
       }
     } else {
       Fseg *= Pall;
+      if (a.recomp && sb != sb0 && sb % a.seg_sc_f == 0) {
+        // a forward segment starts here: the forward's state came from the
+        // carry over the segments, not from stepping
+        const float* st = a.segst + (((int64_t)b * a.nseg_f + sb / a.seg_sc_f) * D + (dok ? d : D - 1)) * N;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = 16 * m + 4 * g + r;
+            X[m][r] = (dok && n < N) ? st[n] : 0.f;
+          }
+      }
+      if (a.recomp && dok) {
+        // the state entering sb, as the scan's checkpoint holds it
+        float* ck = a.ckpt + (((int64_t)b * a.Kc + sb) * D + d) * N;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const int n = 16 * m + 4 * g;
+          if ((N & 3) == 0) {
+            if (n < N) *(float4*)(ck + n) = make_float4(X[m][0], X[m][1], X[m][2], X[m][3]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < N) ck[n + r] = X[m][r];
+          }
+        }
+      }
     }
     // X <- Pall X + B^T (Pe w): k-step s takes rows 4s + k
     float wp[4];
@@ -396,6 +434,7 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
   }
   if (!dok) return;
   if (MAP) {
+    if (a.recomp) return;
     const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
 #pragma unroll
     for (int m = 0; m < MT; ++m)

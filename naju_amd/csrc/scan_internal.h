@@ -101,8 +101,23 @@ struct ScanArgs {
   int n_dtiles;
   int n_tiles;
   int K;
-  int ck_rows;  // N = 1 forward: rows per checkpoint interval (the backward's chunk length)
-  int Kc;       // N = 1 forward: number of checkpoint intervals
+  int ck_rows;  // rows per checkpoint interval of ckpt
+  int Kc;       // number of checkpoint intervals of ckpt
+  // Chunked matrix-core forward map launch with recomp = 1: the backward's
+  // recompute of the state entering every sub-block (into ckpt, Kc of them)
+  // from the forward's checkpoint ck_src (Kc_src intervals, one segment
+  // each) instead of a segment map.
+  const float* ck_src;
+  int Kc_src;
+  int recomp;
+  // With a checkpoint interval longer than the sub-block: the state entering
+  // each forward time segment s >= 1 ([batch][nseg_f][D][N], after the
+  // interval states in the checkpoint), written by the forward and restored
+  // by the recompute at those sub-blocks (the forward's segmentation:
+  // seg_sc_f sub-blocks per segment, nseg_f segments).
+  float* segst;
+  int seg_sc_f;
+  int nseg_f;
   // N = 1: this launch's look-back tag. Nonzero: a host tag (odd, new for
   // every eager launch). Zero: the launch was recorded into a HIP graph, and
   // the tag comes from the device epoch, which the one-thread

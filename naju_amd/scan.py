@@ -147,7 +147,7 @@ class NajuScanHip(torch.autograd.Function):
     """Autograd wrapper of naju_scan_fwd / naju_scan_bwd (include/naju_scan.h)."""
 
     @staticmethod
-    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False):
+    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False, ckpt_rows=0):
         Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
         out_dtype = u.dtype
         u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0)
@@ -156,25 +156,26 @@ class NajuScanHip(torch.autograd.Function):
         dev = u_.device
         stream = _stream_handle(dev)
         need_grad = any(ctx.needs_input_grad)
+        flags = _flags() | _lib.ckpt_rows_flag(ckpt_rows)
         ckpt = None
         if need_grad:
-            n = L.naju_scan_ckpt_elems(Bsz, T, D, N, *dts)
+            n = L.naju_scan_ckpt_elems_ex(Bsz, T, D, N, *dts, flags)
             if n < 0:
-                _lib.check(_lib.ERR_INVALID)
+                _lib.check(_lib.ERR_UNSUPPORTED if "interval" in _lib.last_error() else _lib.ERR_INVALID)
             ckpt = torch.empty(max(n, 1), dtype=torch.float32, device=dev)
-        nbytes = L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts)
+        nbytes = L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags)
         if nbytes == 0 and Bsz * T * D > 0:
-            _lib.check(_lib.ERR_INVALID)
+            _lib.check(_lib.ERR_UNSUPPORTED if "interval" in _lib.last_error() else _lib.ERR_INVALID)
         ws = _WS.get(dev, stream, nbytes)
         y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
         hT = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_hT else None
         _lib.check(L.naju_scan_fwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
-            _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
+            _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
         _check_status(dev)
         if need_grad:
             ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
-            ctx.meta = (Bsz, T, D, N, dts, h0 is not None,
+            ctx.meta = (Bsz, T, D, N, dts, flags, h0 is not None,
                         (u.dtype, f_logit.dtype, i_logit.dtype, B.dtype, C.dtype, D_skip.dtype))
         y = y if y.dtype == out_dtype else y.to(out_dtype)
         if want_hT:
@@ -185,7 +186,7 @@ class NajuScanHip(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy, *_unused_dhT):
         u_, fl_, il_, B_, C_, D_, ckpt = ctx.saved_tensors
-        Bsz, T, D, N, dts, has_h0, in_dtypes = ctx.meta
+        Bsz, T, D, N, dts, flags, has_h0, in_dtypes = ctx.meta
         ng = ctx.needs_input_grad
         dev = u_.device
         dy = dy.to(u_.dtype).contiguous()
@@ -199,21 +200,25 @@ class NajuScanHip(torch.autograd.Function):
         dh0 = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_h0 else None
         L = _lib.lib()
         stream = _stream_handle(dev)
-        ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes(Bsz, T, D, N, *dts))
+        ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags))
         _lib.check(L.naju_scan_bwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
             _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
-            Bsz, T, D, N, *dts, _flags(), ws.data_ptr(), ws.numel(), stream))
+            Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
         _check_status(dev)
         grads = [du, dfl, dil, dB, dC, dD]
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
-        return (*grads, dh0, None)
+        return (*grads, dh0, None, None)
 
 
-def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False):
+def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False, ckpt_rows=None):
     """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module
-    doc); (y, hT) with return_final_state=True."""
-    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state))
+    doc); (y, hT) with return_final_state=True. ckpt_rows: the checkpoint
+    interval kept for the backward (None = the default; a longer interval,
+    a multiple of 16 served at 9 <= N <= 64, is the memory-light mode: the
+    backward recomputes the states between, with bitwise the same
+    gradients)."""
+    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state), int(ckpt_rows or 0))
 
 
 def resolve_backend(backend=None):

@@ -363,3 +363,50 @@ def test_unknown_flag_bits_rejected():
     fake = 0x1000
     rc = L.naju_scan_fwd(*([fake] * 6), None, fake, fake, None, 2, 8, 16, 1, F32, F32, F32, 4, fake, 1 << 30, None)
     assert rc == _lib.ERR_INVALID and b"flag" in L.naju_scan_last_error()
+
+
+def test_checkpoint_interval_size_queries_and_checks():
+    """NAJU_CKPT_ROWS: the checkpoint shrinks with the interval on the
+    matrix-core path (9 <= N <= 64) while the backward's workspace gains the
+    recomputed per-sub-block states; other N accept only their default."""
+    L = _lib.lib()
+    fl = _lib.ckpt_rows_flag
+    B_, T, D = 8, 4096, 1024
+    base = L.naju_scan_ckpt_elems(B_, T, D, 64, BF16, F32, BF16)
+    assert L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, 0) == base
+    assert L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, fl(16)) == base
+    for rows in (32, 48, 64, 128, 4080):
+        n = L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, fl(rows))
+        # the interval states, then the state entering each of the forward's
+        # time segments (a whole number of [batch, D, N] blocks, fewer than
+        # the intervals here)
+        states = B_ * (-(-T // rows)) * D * 64
+        assert n >= states and (n - states) % (B_ * D * 64) == 0 and n - states < B_ * 64 * D * 64
+    ws0 = L.naju_scan_workspace_bytes_ex(B_, T, D, 64, BF16, F32, BF16, 0)
+    assert ws0 == L.naju_scan_workspace_bytes(B_, T, D, 64, BF16, F32, BF16)
+    ws64 = L.naju_scan_workspace_bytes_ex(B_, T, D, 64, BF16, F32, BF16, fl(64))
+    # the recomputed states: one float per (b, 16-row sub-block, d, n)
+    assert ws64 >= ws0 + B_ * (T // 16) * D * 64 * 4
+    # ragged T: the last interval is partial
+    n = L.naju_scan_ckpt_elems_ex(2, 300, 96, 33, F32, F32, F32, fl(64))
+    assert n >= 2 * 5 * 96 * 33 and (n - 2 * 5 * 96 * 33) % (2 * 96 * 33) == 0
+    # other N: only the default interval (32 rows at N <= 8 and N > 64, the
+    # backward's chunk at N = 1)
+    assert L.naju_scan_ckpt_elems_ex(2, 300, 96, 4, F32, F32, F32, fl(32)) == 2 * 10 * 96 * 4
+    for N, rows in ((4, 64), (128, 64), (1, 32), (8, 16)):
+        assert L.naju_scan_ckpt_elems_ex(2, 300, 96, N, F32, F32, F32, fl(rows)) == -1
+        assert b"interval" in L.naju_scan_last_error()
+        assert L.naju_scan_workspace_bytes_ex(2, 300, 96, N, F32, F32, F32, fl(rows)) == 0
+        assert b"interval" in L.naju_scan_last_error()
+        # the scan calls reject it on the host, before touching any pointer
+        fake = 0x1000
+        rc = L.naju_scan_fwd(*([fake] * 6), None, fake, fake, None, 2, 300, 96, N, F32, F32, F32, fl(rows), fake,
+                             1 << 30, None)
+        assert rc == _lib.ERR_UNSUPPORTED and b"interval" in L.naju_scan_last_error()
+        rc = L.naju_scan_bwd(*([fake] * 8), *([None] * 7), 2, 300, 96, N, F32, F32, F32, fl(rows), fake, 1 << 30,
+                             None)
+        assert rc == _lib.ERR_UNSUPPORTED and b"interval" in L.naju_scan_last_error()
+    with pytest.raises(ValueError):
+        fl(24)
+    with pytest.raises(ValueError):
+        fl(4096)
