@@ -511,7 +511,7 @@ template <typename TU, typename TG, typename TB, int V, int R, int W, int P, boo
 __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, int lane, int wv, uint32_t tag,
                                             bool poison, float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
                                             float (&s_Zb)[W][64 * V], float (&s_g)[64 * V],
-                                            LookShared<V, W, P>& s_lb) {
+                                            LookShared<V, W, P>& s_lb, float (&s_pq)[W][2 * R][64]) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
   using TDG = std::conditional_t<F32O, float, TG>;  // dfl, dil dtype
   constexpr int CH = 64 * V;
@@ -644,14 +644,14 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
 
   // reverse sweep: gradients (naju/cuda/naju_cuda.cu:116-140 restated);
   // f(1-f) and i(1-i) as fma(-f, f, f), exactly 0 at f in {0, 1}.
-  // pq[r] / pq[R + r]: this lane's terms of the dB / dC sums of row r
-  float pq[2 * R], dDs[V];
+  // This lane's terms of the dB / dC sums of row r go to s_pq[wv][r] /
+  // s_pq[wv][R + r] (in LDS rather than registers: 2R fewer live VGPRs).
+  float dDs[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) dDs[j] = 0.f;
 #pragma unroll
   for (int r = R - 1; r >= 0; --r) {
-    pq[r] = 0.f;
-    pq[R + r] = 0.f;
+    float pb = 0.f, pc = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const float f = xf[r][j], ig = xi[r][j], x = xu[r][j], gy = xg[r][j];
@@ -659,29 +659,45 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
       const float xb = fmaf(gy, Ct[r], g[j]);
       const float iu = ig * x;
       const float dws = xb * Bt[r];
-      pq[r] = fmaf(xb, iu, pq[r]);
-      pq[R + r] = fmaf(gy, xs[r][j], pq[R + r]);
+      pb = fmaf(xb, iu, pb);
+      pc = fmaf(gy, xs[r][j], pc);
       dDs[j] = fmaf(gy, x, dDs[j]);
       g[j] = f * xb;
       xf[r][j] = fmaf(-f, f, f) * (xb * xprev);  // dfl
       xi[r][j] = fmaf(-ig, ig, ig) * (dws * x);  // dil
       xu[r][j] = fmaf(ig, dws, Dv[j] * gy);      // du
     }
+    s_pq[wv][r][lane] = pb;
+    s_pq[wv][R + r][lane] = pc;
   }
   if (a.du) st_rows<TDU, V, R, M, !FULL>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
   if (a.dfl) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
   if (a.dil) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
   if (a.partB || a.partC) {
-    // partial sums over this tile's channels, stored [dtile][b*T + t]: after
-    // the wave-wide sums, lane l holds entry l / (64 / 2R) of pq
-    wave_sums<2 * R>(pq, lane);
+    // partial sums over this tile's channels, stored [dtile][b*T + t]: the Q
+    // lanes 64i/2R .. of entry i (row r of dB, i < R, or of dC) each add
+    // SPAN of the wave's terms (in a rotated order that keeps the eight lanes
+    // of a 16-byte LDS read on distinct banks), then combine in lane order
+    static_assert(64 % (2 * R) == 0, "2R must divide the wave");
     constexpr int Q = 64 / (2 * R);
-    const int i = lane / Q;
+    constexpr int SPAN = 64 / Q;
+    static_assert(SPAN % 4 == 0, "16-byte reads");
+    asm volatile("" ::: "memory");  // the wave reads back its own stores
+    const int i = lane / Q, part = lane % Q;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < SPAN; c += 4) {
+      const int col = part * SPAN + ((c + 4 * i + 16 * part) % SPAN);
+      const float4 v = *(const float4*)&s_pq[wv][i][col];
+      acc += (v.x + v.y) + (v.z + v.w);
+    }
+#pragma unroll
+    for (int m = 1; m < Q; m <<= 1) acc += __shfl_xor(acc, m, 64);
     const int r = i < R ? i : i - R;
     const int64_t t = t0 + r;
-    if (lane % Q == 0 && (FULL || t < T)) {
+    if (part == 0 && (FULL || t < T)) {
       float* dst = i < R ? a.partB : a.partC;
-      if (dst) dst[(int64_t)dtile * a.batch * T + (int64_t)b * T + t] = pq[0];
+      if (dst) dst[(int64_t)dtile * a.batch * T + (int64_t)b * T + t] = acc;
     }
   }
   if (a.partD) {
@@ -710,6 +726,7 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   __shared__ float s_Zb[W][CH];
   __shared__ float s_g[CH];
   __shared__ LookShared<V, W, P> s_lb;
+  __shared__ __align__(16) float s_pq[W][2 * R][64];
 
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
   // an out-of-range ticket poisons the chunk this workgroup's index names
@@ -723,11 +740,12 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   if constexpr (VEC) {
     if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
       n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g,
-                                                           s_lb);
+                                                           s_lb, s_pq);
       return;
     }
   }
-  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb);
+  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb,
+                                                        s_pq);
 }
 
 // Sum over q < n_parts of p[q*stride + i], in q order, with the loads of
