@@ -176,8 +176,8 @@ struct McIn {
 // ------------------------------------------------------------------ forward
 //
 // One workgroup per (batch row, kMcDT channels, time segment); the segment's
-// sub-blocks are walked in order, the inputs of sub-block sb + 2 loaded while
-// sb is computed, those of sb + 1 staged at its end, B and C double-buffered
+// sub-blocks are walked in order, the inputs of sub-block sb + 1 loaded while
+// sb is computed and staged at its end, B and C double-buffered
 // in LDS (one barrier per sub-block). MAP: the segment's map from a zero
 // state (decay per channel into segF, state into segZ) for the carry pass
 // over the segments, or with a.recomp the states entering the segment's
@@ -185,7 +185,7 @@ struct McIn {
 // into a.ckpt; otherwise y, the checkpoint and hT from the entering state
 // (h0, or seg0 when T is split into segments).
 template <int NP, bool MAP, typename TU, typename TG, typename TB>
-__global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int y_dt) {
+__global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) void mc_fwd_kernel(const ScanArgs a, int y_dt) {
   constexpr int MT = NP / 16;  // 16-entry tiles of the state index
   using In = McIn<NP, MAP, TU, TG, TB>;
   __shared__ __align__(16) McBC<NP, MAP> sh;
@@ -241,18 +241,28 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
   // A-operand row of C X: MFMA row i = lane % 16 holds time row 4(i%4) + i/4
   const int arow = 4 * (j & 3) + (j >> 2);
 
-  // inputs of sub-blocks sb (cur), sb + 1 (nxt) and sb + 2 (nx2): each is
-  // loaded two sub-blocks ahead of its use
-  In cur, nxt, nx2;
+  // inputs of sub-blocks sb (cur) and sb + 1 (nxt), loaded one sub-block
+  // ahead of their use
+  In cur, nxt;
   if (sb0 < sb1) {
     cur.load(a, b, (int64_t)sb0 * Q, dw, rho, cq, tid, vec);
     cur.stage(sh, 0, a, (int64_t)sb0 * Q, tid);
   }
-  if (sb0 + 1 < sb1) nxt.load(a, b, (int64_t)(sb0 + 1) * Q, dw, rho, cq, tid, vec);
   for (int sb = sb0; sb < sb1; ++sb) {
+    // The lane's indices, recomputed every sub-block from an opaque copy of
+    // the lane id (they shadow the ones above), so that the lane-dependent
+    // LDS and global addresses are not all hoisted out of the loop and held.
+    int lane_l = lane;
+    asm volatile("" : "+v"(lane_l));
+    const int j = lane_l & 15, g = lane_l >> 4;
+    const int rho = lane_l >> 2, cq = (lane_l & 3) * 4;
+    const int arow = 4 * (j & 3) + (j >> 2);
+    const int64_t d = dw + j;
+    const bool dok = d < D;
+    const int tid = 64 * wv + lane_l;
     const int buf = (sb - sb0) & 1;
     const int64_t t0 = (int64_t)sb * Q;
-    if (sb + 2 < sb1) nx2.load(a, b, t0 + 2 * Q, dw, rho, cq, tid, vec);
+    if (sb + 1 < sb1) nxt.load(a, b, t0 + Q, dw, rho, cq, tid, vec);
     // gates in the load layout, each element computed once; rows past T
     // and channels past D are the neutral step f = 1, w = u = 0
     const bool rok = t0 + rho < T;
@@ -284,13 +294,11 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
     // accesses in order, the compiler must not move them)
     asm volatile("" ::: "memory");
     // this lane's channel over all Q rows, and its own rows 4r + g
-    float fa[Q], wa[Q];
+    float fa[Q];
 #pragma unroll
     for (int q4 = 0; q4 < Q; q4 += 4) {
       const float4 f4 = *(const float4*)&s_t[wv][0][j][q4];
-      const float4 w4 = *(const float4*)&s_t[wv][1][j][q4];
       fa[q4] = f4.x, fa[q4 + 1] = f4.y, fa[q4 + 2] = f4.z, fa[q4 + 3] = f4.w;
-      wa[q4] = w4.x, wa[q4 + 1] = w4.y, wa[q4 + 2] = w4.z, wa[q4 + 3] = w4.w;
     }
     float w_o[4], u_o[4];
 #pragma unroll
@@ -313,15 +321,17 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
         float acc = 0.f;
 #pragma unroll
         for (int s4 = 0; s4 <= 4 * r; s4 += 4) {
+          // w of rows s4 .. s4+3 read where used (fewer live registers)
           const float4 G4 = *(const float4*)&s_G[wv][t][s4];
+          const float4 W4 = *(const float4*)&s_t[wv][1][j][s4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int s = s4 + e;
             if (s <= 4 * r) {
-              acc = fmaf(acc, fa[s], (&G4.x)[e] * wa[s]);
+              acc = fmaf(acc, fa[s], (&G4.x)[e] * (&W4.x)[e]);
             } else {
               const bool in = s <= t;
-              acc = fmaf(acc, in ? fa[s] : 1.f, in ? (&G4.x)[e] * wa[s] : 0.f);
+              acc = fmaf(acc, in ? fa[s] : 1.f, in ? (&G4.x)[e] * (&W4.x)[e] : 0.f);
             }
           }
         }
@@ -430,7 +440,6 @@ __global__ __launch_bounds__(64 * kMcW) void mc_fwd_kernel(const ScanArgs a, int
     // as late as possible so that their loads have the whole sub-block to land
     if (sb + 1 < sb1) nxt.stage(sh, buf ^ 1, a, t0 + Q, tid);
     cur = nxt;
-    nxt = nx2;
   }
   if (!dok) return;
   if (MAP) {
