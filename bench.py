@@ -34,6 +34,17 @@ if _ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 VALU_PEAK_TFLOPS = 157.3 / 2  # fp32 FMA without packed-FP32 instructions
+MFMA_F32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA (v_mfma_f32_16x16x4_f32)
+
+
+def compute_roof(n):
+    """The compute bound of the general-N scan kernels at state size n:
+    9 <= n <= 64 run the chunked form on the fp32 matrix cores, the others on
+    the VALU. Work is counted as the recurrence's own 19n flop per element
+    (5n forward, 14n backward), whichever units do it."""
+    if 9 <= n <= 64:
+        return "mfma", MFMA_F32_PEAK_TFLOPS
+    return "valu", VALU_PEAK_TFLOPS
 METRIC = "fwd+bwd scan GB/s (% of HBM peak) at B8 L4096 D1024; LM tokens/s"
 
 
@@ -147,11 +158,12 @@ def _config_entry(L, config, N, dev, steps, warmup, target_ms=None):
     }
     if n > 1:
         fl_bwd, fl_fwd = 14.0 * n * case["E"], 5.0 * n * case["E"]
+        bound, peak = compute_roof(n)
         e["roofline_compute"] = {
-            "bound": "valu", "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "bound": bound, "peak": peak, "unit": "TFLOP/s", "work": "19N flop per element",
             "bwd_achieved": round(fl_bwd / (t["bwd_avg"] * 1e-3) / 1e12, 2),
             "fwd_achieved": round(fl_fwd / (t["fwd_avg"] * 1e-3) / 1e12, 2),
-            "frac_step": round((fl_bwd + fl_fwd) / (t["ms_step"] * 1e-3) / 1e12 / VALU_PEAK_TFLOPS, 4)}
+            "frac_step": round((fl_bwd + fl_fwd) / (t["ms_step"] * 1e-3) / 1e12 / peak, 4)}
     if target_ms is not None:
         e["target_ms"] = target_ms
         e["meets_target"] = bool(t["ms_step"] <= target_ms)
@@ -246,14 +258,15 @@ def main():
     }
     if N > 1:
         # General N is compute-bound: the recurrence, readout and adjoint are
-        # about 19N flop per element (5N forward, 14N backward), fp32 FMA on
-        # the VALU. Packed-FP32 ops are disabled in this build, so the peak is
-        # half of MI355X's 157.3 TFLOP/s vector fp32.
+        # about 19N flop per element (5N forward, 14N backward). 9 <= N <= 64
+        # runs on the fp32 matrix cores (157.3 TFLOP/s dense), other N on the
+        # VALU (packed-FP32 ops are disabled in this build: half of 157.3).
         E = case["E"]
+        bound, peak = compute_roof(N)
         ach = 14.0 * N * E / (t["bwd_avg"] * 1e-3) / 1e12
-        out["roofline_compute"] = {"kernel": "naju_scan_bwd call", "bound": "valu", "achieved": round(ach, 2),
-                                   "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                   "frac": round(ach / VALU_PEAK_TFLOPS, 4),
+        out["roofline_compute"] = {"kernel": "naju_scan_bwd call", "bound": bound, "achieved": round(ach, 2),
+                                   "peak": peak, "unit": "TFLOP/s", "work": "19N flop per element",
+                                   "frac": round(ach / peak, 4),
                                    "fwd_achieved": round(5.0 * N * E / (t["fwd_avg"] * 1e-3) / 1e12, 2)}
     if not args.no_flush:
         # the same step with a 1 GiB write before it: nothing of the step's
