@@ -189,8 +189,8 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
   constexpr int MT = NP / 16;  // 16-entry tiles of the state index
   using In = McIn<NP, MAP, TU, TG, TB>;
   __shared__ __align__(16) McBC<NP, MAP> sh;
-  __shared__ __align__(16) float s_t[kMcW][3][16][TP];  // per wave: f, w, u (then y) as [channel][row]
-  __shared__ __align__(16) float s_G[MAP ? 1 : kMcW][Q][Q + 4];  // per wave: G = C B^T
+  // per wave: f (later G for the exact path, then y) and w = i u as [channel][row]
+  __shared__ __align__(16) float s_t[kMcW][2][16][TP];
 
   const int N = a.N;
   const int64_t T = a.T, D = a.D;
@@ -235,11 +235,12 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
     }
   }
   float Fseg = 1.f;
-  const float Dv = (!MAP && dok) ? a.Dsk[d] : 0.f;
   // load role: row rho, channels cq .. cq+3 of the wave's 16
   const int rho = lane >> 2, cq = (lane & 3) * 4;
-  // A-operand row of C X: MFMA row i = lane % 16 holds time row 4(i%4) + i/4
-  const int arow = 4 * (j & 3) + (j >> 2);
+  // D of the load role's channels (the D u term of y is added there)
+  float Dvc[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Dvc[e] = (!MAP && dw + cq + e < D) ? a.Dsk[dw + cq + e] : 0.f;
 
   // inputs of sub-blocks sb (cur) and sb + 1 (nxt), loaded one sub-block
   // ahead of their use
@@ -266,29 +267,30 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
     // gates in the load layout, each element computed once; rows past T
     // and channels past D are the neutral step f = 1, w = u = 0
     const bool rok = t0 + rho < T;
+    float uu[4];  // u of the load role (0 past T / D), for the D u term
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bool ok = rok && dw + cq + e < D;
       s_t[wv][0][cq + e][rho] = ok ? sigm(cur.f[e]) : 1.f;
       s_t[wv][1][cq + e][rho] = ok ? sigm(cur.i[e]) * cur.u[e] : 0.f;
-      s_t[wv][2][cq + e][rho] = ok ? cur.u[e] : 0.f;
+      uu[e] = ok ? cur.u[e] : 0.f;
     }
     __syncthreads();  // B / C of sb are staged; every wave is done with sb - 1
+    // G[t][s] = C_t . B_s of the sub-block, in the layout of an A operand
+    // whose MFMA row i is time row arow(i): Gp[r] = G[arow(j)][4r + g]
+    // (the product B_(arow) C_(arow)^T transposed; k-step (q, r') takes
+    // n = 16q + 4k + r')
+    f4_t Gp = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!MAP) {
-      // G = C B^T of the sub-block, G[t][s] = sum_n C[t][n] B[s][n] (k-step
-      // (q, r') takes n = 16q + 4k + r'), into this wave's LDS tile
-      f4_t G = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < NP / 16; ++q) {
-        const float4 c4 = *(const float4*)&sh.C[buf][j][16 * q + 4 * g];
-        const float4 b4 = *(const float4*)&sh.Bn[buf][j][16 * q + 4 * g];
-        G = mma(c4.x, b4.x, G);
-        G = mma(c4.y, b4.y, G);
-        G = mma(c4.z, b4.z, G);
-        G = mma(c4.w, b4.w, G);
+        const float4 c4 = *(const float4*)&sh.C[buf][arow][16 * q + 4 * g];
+        const float4 b4 = *(const float4*)&sh.Bn[buf][arow][16 * q + 4 * g];
+        Gp = mma(b4.x, c4.x, Gp);
+        Gp = mma(b4.y, c4.y, Gp);
+        Gp = mma(b4.z, c4.z, Gp);
+        Gp = mma(b4.w, c4.w, Gp);
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_G[wv][4 * g + r][j] = G[r];
     }
     // (the wave reads back what its own lanes wrote: LDS keeps a wave's
     // accesses in order, the compiler must not move them)
@@ -300,42 +302,62 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
       const float4 f4 = *(const float4*)&s_t[wv][0][j][q4];
       fa[q4] = f4.x, fa[q4 + 1] = f4.y, fa[q4 + 2] = f4.z, fa[q4 + 3] = f4.w;
     }
-    float w_o[4], u_o[4];
+    float w_o[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      w_o[r] = s_t[wv][1][j][4 * r + g];
-      u_o[r] = s_t[wv][2][j][4 * r + g];
-    }
+    for (int r = 0; r < 4; ++r) w_o[r] = s_t[wv][1][j][4 * r + g];
     // decays of the own rows: pf = prod_{q <= t} f, pe = prod_{q > t} f
     float pf[4], pe[4];
     const float Pall = own_decays(fa, g, pf, pe);
 
     if constexpr (!MAP) {
-      // intra-sub-block part of y for the own rows t = 4r + g:
-      // S_k = f_k S_{k-1} + G[t][k] w_k for k = 0 .. t (Horner); rows k <= 4r
-      // are in every lane's range, rows 4r+1 .. 4r+3 only in some
+      // intra-sub-block part of y for the own rows t = 4r + g,
+      // S[t] = sum_{s<=t} P[t,s] G[t][s] w_s.
       float S[4];
+      if (__all(Pall >= kMcRatioMin)) {
+        // Every channel of the wave keeps its decay over the sub-block above
+        // kMcRatioMin: P[t,s] = Pf[t] / Pf[s] (products from row 0) in
+        // floating point, and S = Pf * (masked G) (w / Pf) is one 16 x 16 x 16
+        // product: MFMA row i is time row arow(i), k-step e takes row
+        // s = 4e + g, whose w / Pf this lane holds (its own row e).
+        f4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 4 * r + g;
-        float acc = 0.f;
+        for (int e = 0; e < 4; ++e) {
+          const float gm = 4 * e + g <= arow ? Gp[e] : 0.f;
+          acc = mma(gm, w_o[e] * __builtin_amdgcn_rcpf(pf[e]), acc);
+        }
 #pragma unroll
-        for (int s4 = 0; s4 <= 4 * r; s4 += 4) {
-          // w of rows s4 .. s4+3 read where used (fewer live registers)
-          const float4 G4 = *(const float4*)&s_G[wv][t][s4];
-          const float4 W4 = *(const float4*)&s_t[wv][1][j][s4];
+        for (int r = 0; r < 4; ++r) S[r] = pf[r] * acc[r];
+      } else {
+        // exact products: Horner S_k = f_k S_{k-1} + G[t][k] w_k for
+        // k = 0 .. t; rows k <= 4r are in every lane's range, rows
+        // 4r+1 .. 4r+3 only in some. G goes through the f tile (read into
+        // fa already) as [t][s].
+        float (*TGt)[TP] = s_t[wv][0];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int s = s4 + e;
-            if (s <= 4 * r) {
-              acc = fmaf(acc, fa[s], (&G4.x)[e] * (&W4.x)[e]);
-            } else {
-              const bool in = s <= t;
-              acc = fmaf(acc, in ? fa[s] : 1.f, in ? (&G4.x)[e] * (&W4.x)[e] : 0.f);
+        for (int r = 0; r < 4; ++r) TGt[arow][4 * r + g] = Gp[r];
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 4 * r + g;
+          float acc = 0.f;
+#pragma unroll
+          for (int s4 = 0; s4 <= 4 * r; s4 += 4) {
+            // w of rows s4 .. s4+3 read where used (fewer live registers)
+            const float4 G4 = *(const float4*)&TGt[t][s4];
+            const float4 W4 = *(const float4*)&s_t[wv][1][j][s4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int s = s4 + e;
+              if (s <= 4 * r) {
+                acc = fmaf(acc, fa[s], (&G4.x)[e] * (&W4.x)[e]);
+              } else {
+                const bool in = s <= t;
+                acc = fmaf(acc, in ? fa[s] : 1.f, in ? (&G4.x)[e] * (&W4.x)[e] : 0.f);
+              }
             }
           }
+          S[r] = acc;
         }
-        S[r] = acc;
       }
       // C X for the own rows (MFMA row i = 4g + r is time row 4r + g)
       f4_t cx = {0.f, 0.f, 0.f, 0.f};
@@ -362,15 +384,16 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
           }
         }
       }
-      // y of the own rows into the u tile, then stored in the load layout
-      // (row rho, channels cq .. cq+3)
+      // y of the own rows (less D u) through the f tile, then stored in the
+      // load layout (row rho, channels cq .. cq+3) with D u added
+      asm volatile("" ::: "memory");
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_t[wv][2][j][4 * r + g] = fmaf(pf[r], cx[r], fmaf(Dv, u_o[r], S[r]));
+      for (int r = 0; r < 4; ++r) s_t[wv][0][j][4 * r + g] = fmaf(pf[r], cx[r], S[r]);
       asm volatile("" ::: "memory");
       if (rok) {
         float yv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) yv[e] = s_t[wv][2][cq + e][rho];
+        for (int e = 0; e < 4; ++e) yv[e] = fmaf(Dvc[e], uu[e], s_t[wv][0][cq + e][rho]);
         const int64_t o = ((int64_t)b * T + t0 + rho) * D + dw + cq;
         if (y_dt == NAJU_DTYPE_F32) {
           if (vec)

@@ -195,6 +195,14 @@ constexpr int kMcDT = 16 * kMcW;
 constexpr int kMcWB = 8;
 constexpr int kMcDTB = 16 * kMcWB;
 
+// Below this decay over a sub-block (product of its 16 f of one channel),
+// the chunked kernels form the intra-sub-block decay terms as exact
+// products; above it, as ratios Pf[t] / Pf[s] of the running products from
+// the sub-block's first row, which turns those terms into matrix products
+// (1 / Pf stays below 2^60, so no intermediate overflows). A hard reset
+// (f = 0) is always below it.
+constexpr float kMcRatioMin = 0x1p-60f;
+
 // True when the chunked kernels serve this state size.
 inline bool mc_ok(int64_t N) { return N > 8 && N <= 64; }
 
