@@ -782,172 +782,223 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       float (*Tx2)[TP] = (float (*)[TP])(pl + 3 * 16 * TP);
       float (*TH)[TP] = (float (*)[TP])(pl + 4 * 16 * TP);   // H[t][p(r)]
       float (*THT)[TP] = (float (*)[TP])(pl + 5 * 16 * TP);  // H[s][t] at [t][p(s)]
-      // column partials of the rectangle sums: group g in pool tile 6 + g for
-      // g < 3, group 3 in tile 3 (free by then)
-      // ---- G = C B^T (k-step (q, r') takes n = 16q + 4k + r')
-      {
-        f4_t G = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < MT; ++q) {
-          float c4[4], b4[4];
-          rd4(&sh.C[j][16 * q + 4 * g], c4);
-          rd4(&sh.Bn[j][16 * q + 4 * g], b4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) G = mma(c4[e], b4[e], G);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) TGm[4 * g + r][j] = G[r];
-        wr4(&TGT[j][4 * g], G[0], G[1], G[2], G[3]);
-      }
-      // ---- C X and B ghat for the own rows (MFMA row 4g + r = time row
-      // 4r + g), and ghat . X per channel; X from the checkpoint
-      f4_t cx = {0.f, 0.f, 0.f, 0.f}, bg = {0.f, 0.f, 0.f, 0.f};
+      // ---- G[t][s] = C_t . B_s in the layout of an A operand whose MFMA row
+      // i is time row arow(i): Gp[r] = G[arow(j)][4r + g] (k-step (q, r')
+      // takes n = 16q + 4k + r'); C X and B ghat for the own rows (MFMA row
+      // 4g + r = time row 4r + g) and ghat . X per channel from the same reads
+      f4_t Gp = {0.f, 0.f, 0.f, 0.f}, cx = {0.f, 0.f, 0.f, 0.f}, bg = {0.f, 0.f, 0.f, 0.f};
       float gX = 0.f;
-      {
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          float c4[4], b4[4];
-          rd4(&sh.C[arow][16 * m + 4 * g], c4);
-          rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
+      for (int m = 0; m < MT; ++m) {
+        float c4[4], b4[4];
+        rd4(&sh.C[arow][16 * m + 4 * g], c4);
+        rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            cx = mma(c4[e], xc[m][e], cx);
-            bg = mma(b4[e], gh[m][e], bg);
-            gX = fmaf(gh[m][e], xc[m][e], gX);
-          }
+        for (int e = 0; e < 4; ++e) {
+          Gp = mma(b4[e], c4[e], Gp);
+          cx = mma(c4[e], xc[m][e], cx);
+          bg = mma(b4[e], gh[m][e], bg);
+          gX = fmaf(gh[m][e], xc[m][e], gX);
         }
       }
       gX += __shfl_xor(gX, 16, 64);
       gX += __shfl_xor(gX, 32, 64);
-      // ---- V1 = sum_{s>=t} P[s,t] dy_s G[s][t], V2 = sum_{s>=t} P[s,t] dy_s (C X)_s
-      // (Horner from s = 15 down), V3 = sum_{r<=t} P[t,r] w_r (B ghat)_r
+      // ---- the decay terms of the own rows t:
+      //   V1_t = sum_{s>=t} P[s,t] dy_s G[s][t], V2_t = sum_{s>=t} P[s,t] dy_s (C X)_s,
+      //   V3_t = sum_{r<=t} P[t,r] w_r (B ghat)_r,
+      //   A3_t = sum_{s>=t>=r} M[s][r], M[s][r] = P[s,r] dy_s w_r G[s][r],
+      // and H[s][r] = sum over the wave's channels of P[s,r] dy_s w_r.
+      float V1[4], V2[4], V3[4], A3[4];
+      if (__all(Pall >= kMcRatioMin)) {
+        // Every channel's decay over the sub-block stays above kMcRatioMin:
+        // P[s,t] = Pf[s] / Pf[t] in floating point, with a = Pf dy and
+        // b = w / Pf, and every term is a 16 x 16 x 16 product (MFMA row i =
+        // time row arow(i), k-step e = row 4e + g, whose a and b this lane
+        // holds): V1 = (masked G^T a) / Pf, V2 = (masked ones (a C X)) / Pf,
+        // V3 = Pf (masked ones (b B ghat)), rowsum = a (masked G b),
+        // colsum = b (masked G^T a), A3 = suffix sums of rowsum minus strict
+        // suffix sums of colsum; H = a^T b over the channels (k = channel).
+        float ip[4], ra[4], rb[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = cx[r], Tx2[j][4 * r + g] = bg[r];
-      asm volatile("" ::: "memory");
-      // (operands are read from the tiles in 4-row chunks as they are needed,
-      // which keeps the live registers low)
-      float V1[4], V2[4], V3[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 4 * r + g;
-        float a1 = 0.f, a2 = 0.f;
-#pragma unroll
-        for (int s4 = 12; s4 >= 4 * r; s4 -= 4) {
-          float gt4[4], y4[4], c4[4];
-          rd4(&TGT[t][s4], gt4);
-          rd4(&Tdy[j][s4], y4);
-          rd4(&Tx1[j][s4], c4);
-#pragma unroll
-          for (int e = 3; e >= 0; --e) {
-            const int s = s4 + e;
-            const float fs = s < Q - 1 ? fa[s + 1] : 1.f;
-            if (s >= 4 * r + 3) {
-              a1 = fmaf(a1, fs, y4[e] * gt4[e]);
-              a2 = fmaf(a2, fs, y4[e] * c4[e]);
-            } else {
-              const bool in = s >= t;
-              a1 = in ? fmaf(a1, fs, y4[e] * gt4[e]) : a1;
-              a2 = in ? fmaf(a2, fs, y4[e] * c4[e]) : a2;
-            }
-          }
+        for (int r = 0; r < 4; ++r) {
+          ip[r] = __builtin_amdgcn_rcpf(pf[r]);
+          ra[r] = pf[r] * dy_o[r];
+          rb[r] = Tw[j][4 * r + g] * ip[r];
         }
-        V1[r] = a1;
-        V2[r] = a2;
-        float a3 = 0.f;
+        float (*TGs)[TP] = TGm;  // G[t][s]
+        float (*Ta)[TP] = TGT;   // a as [channel][row]
+        float (*Tb)[TP] = Tx1;   // b as [channel][row]
 #pragma unroll
-        for (int q4 = 0; q4 <= 4 * r; q4 += 4) {
-          float w4[4], b4[4];
-          rd4(&Tw[j][q4], w4);
-          rd4(&Tx2[j][q4], b4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int q = q4 + e;
-            if (q <= 4 * r) {
-              a3 = fmaf(a3, fa[q], w4[e] * b4[e]);
-            } else {
-              const bool in = q <= t;
-              a3 = fmaf(a3, in ? fa[q] : 1.f, in ? w4[e] * b4[e] : 0.f);
-            }
-          }
+        for (int r = 0; r < 4; ++r) {
+          TGs[arow][4 * r + g] = Gp[r];
+          Ta[j][4 * r + g] = ra[r];
+          Tb[j][4 * r + g] = rb[r];
         }
-        V3[r] = a3;
-      }
-      // ---- rectangle sums A3_t = sum_{s>=t>=r} M[s][r] with M = K G[s][r],
-      // K[s][r] = P[s,r] dy_s w_r; per row block r the K of the own row
-      // s = 4r + g (16 slots, q <= 4r + 3) are summed over the wave's 16
-      // channels by a transposing butterfly in each 16-lane row, after which
-      // lane j holds slot q = j: H[s][j]
-      float cp[Q], rs[4];
+        asm volatile("" ::: "memory");
+        f4_t D1 = {0.f, 0.f, 0.f, 0.f}, D2 = D1, D3 = D1, R1 = D1, DH = D1, D4 = D1;
 #pragma unroll
-      for (int q = 0; q < Q; ++q) cp[q] = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int s = 4 * r + g;
-        float hv[Q];
-        float Pz = 0.f, rsum = 0.f;
-#pragma unroll
-        for (int q4 = 4 * r; q4 >= 0; q4 -= 4) {
-          float w4[4], g4[4];
-          rd4(&Tw[j][q4], w4);
-          rd4(&TGm[s][q4], g4);
-#pragma unroll
-          for (int e = 3; e >= 0; --e) {
-            const int q = q4 + e;
-            // Pz = P[s, q] = prod_{q < q' <= s} f for q <= s, 0 for q > s
-            // (a product chain with no masked multiply, so that it stays
-            // straight-line code)
-            if (q == 4 * r + 3) {
-              Pz = q == s ? 1.f : 0.f;
-            } else if (q >= 4 * r) {
-              Pz = q == s ? 1.f : Pz * fa[q + 1];
-            } else {
-              Pz = Pz * fa[q + 1];
-            }
-            const float kv = Pz * (dy_o[r] * w4[e]);
-            hv[q] = kv;
-            const float mv = kv * g4[e];
-            rsum += mv;
-            cp[q] += mv;
-          }
+        for (int e = 0; e < 4; ++e) {
+          const int s = 4 * e + g;
+          const bool ge = s >= arow, le = s <= arow;
+          D1 = mma(ge ? TGs[s][arow] : 0.f, ra[e], D1);
+          D2 = mma(ge ? 1.f : 0.f, ra[e] * cx[e], D2);
+          D3 = mma(le ? 1.f : 0.f, rb[e] * bg[e], D3);
+          R1 = mma(le ? Gp[e] : 0.f, rb[e], R1);
+          DH = mma(Ta[s][j], Tb[s][j], DH);
         }
 #pragma unroll
-        for (int q = 4 * r + 4; q < Q; ++q) hv[q] = 0.f;
-        rs[r] = rsum;
-        trd_step<16, Q, Q>(hv, lane);
-        // lane j: H[s][j] (zero for j > s: every slot past s held zeros);
-        // over r and the lanes every entry of both tiles is written
-        TH[s][4 * (j & 3) + (j >> 2)] = hv[0];
-        THT[j][4 * (s & 3) + (s >> 2)] = hv[0];
-      }
-      // row sums of all 16 rows, and column sums over the channel's lanes
-      // (group g's partials in pool tile 6 + g for g < 3, tile 3 for g = 3)
+        for (int e = 0; e < 4; ++e) {
+          const int s = 4 * e + g;
+          D4 = mma(s >= arow ? 1.f : 0.f, ra[e] * R1[e], D4);
+          D4 = mma(s > arow ? 1.f : 0.f, -(rb[e] * D1[e]), D4);
+        }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = rs[r];
-      {
-        float* tc = pl + (g < 3 ? 6 + g : 3) * 16 * TP;
+        for (int r = 0; r < 4; ++r) {
+          V1[r] = D1[r] * ip[r];
+          V2[r] = D2[r] * ip[r];
+          V3[r] = D3[r] * pf[r];
+          A3[r] = D4[r];
+          // lane (j, g) holds H[4g + r][j], zero for j > 4g + r
+          const float h = j <= 4 * g + r ? DH[r] : 0.f;
+          TH[4 * g + r][4 * (j & 3) + (j >> 2)] = h;
+          THT[j][4 * r + g] = h;
+        }
+      } else {
+        // exact products: G as [t][s] and [s][t] tiles, Horner chains and a
+        // butterfly over the channels
 #pragma unroll
-        for (int q4 = 0; q4 < Q; q4 += 4) wr4(tc + j * TP + q4, cp[q4], cp[q4 + 1], cp[q4 + 2], cp[q4 + 3]);
-      }
-      asm volatile("" ::: "memory");
-      // A3_t = sum_{s>=t} rowsum[s] - sum_{q>t} colsum[q]
-      float A3[4];
-      {
-        float sufR = 0.f, sufC = 0.f;
+        for (int r = 0; r < 4; ++r) {
+          TGm[arow][4 * r + g] = Gp[r];
+          TGT[4 * r + g][arow] = Gp[r];
+        }
+        // ---- V1 = sum_{s>=t} P[s,t] dy_s G[s][t], V2 = sum_{s>=t} P[s,t] dy_s (C X)_s
+        // (Horner from s = 15 down), V3 = sum_{r<=t} P[t,r] w_r (B ghat)_r
 #pragma unroll
-        for (int r = 3; r >= 0; --r) {
-          float r4[4], c0[4], c1[4], c2[4], c3[4], cs[4];
-          rd4(&Tx1[j][4 * r], r4);
-          rd4(pl + 6 * 16 * TP + j * TP + 4 * r, c0);
-          rd4(pl + 7 * 16 * TP + j * TP + 4 * r, c1);
-          rd4(pl + 8 * 16 * TP + j * TP + 4 * r, c2);
-          rd4(pl + 3 * 16 * TP + j * TP + 4 * r, c3);
+        for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = cx[r], Tx2[j][4 * r + g] = bg[r];
+        asm volatile("" ::: "memory");
+        // (operands are read from the tiles in 4-row chunks as they are needed,
+        // which keeps the live registers low)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) cs[e] = (c0[e] + c1[e]) + (c2[e] + c3[e]);
-          const float sR = sufR + r4[3] + (g <= 2 ? r4[2] : 0.f) + (g <= 1 ? r4[1] : 0.f) + (g <= 0 ? r4[0] : 0.f);
-          const float sC = sufC + (g < 3 ? cs[3] : 0.f) + (g < 2 ? cs[2] : 0.f) + (g < 1 ? cs[1] : 0.f);
-          A3[r] = sR - sC;
-          sufR += (r4[0] + r4[1]) + (r4[2] + r4[3]);
-          sufC += (cs[0] + cs[1]) + (cs[2] + cs[3]);
+        for (int r = 0; r < 4; ++r) {
+          const int t = 4 * r + g;
+          float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+          for (int s4 = 12; s4 >= 4 * r; s4 -= 4) {
+            float gt4[4], y4[4], c4[4];
+            rd4(&TGT[t][s4], gt4);
+            rd4(&Tdy[j][s4], y4);
+            rd4(&Tx1[j][s4], c4);
+#pragma unroll
+            for (int e = 3; e >= 0; --e) {
+              const int s = s4 + e;
+              const float fs = s < Q - 1 ? fa[s + 1] : 1.f;
+              if (s >= 4 * r + 3) {
+                a1 = fmaf(a1, fs, y4[e] * gt4[e]);
+                a2 = fmaf(a2, fs, y4[e] * c4[e]);
+              } else {
+                const bool in = s >= t;
+                a1 = in ? fmaf(a1, fs, y4[e] * gt4[e]) : a1;
+                a2 = in ? fmaf(a2, fs, y4[e] * c4[e]) : a2;
+              }
+            }
+          }
+          V1[r] = a1;
+          V2[r] = a2;
+          float a3 = 0.f;
+#pragma unroll
+          for (int q4 = 0; q4 <= 4 * r; q4 += 4) {
+            float w4[4], b4[4];
+            rd4(&Tw[j][q4], w4);
+            rd4(&Tx2[j][q4], b4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int q = q4 + e;
+              if (q <= 4 * r) {
+                a3 = fmaf(a3, fa[q], w4[e] * b4[e]);
+              } else {
+                const bool in = q <= t;
+                a3 = fmaf(a3, in ? fa[q] : 1.f, in ? w4[e] * b4[e] : 0.f);
+              }
+            }
+          }
+          V3[r] = a3;
+        }
+        // ---- rectangle sums A3_t = sum_{s>=t>=r} M[s][r] with M = K G[s][r],
+        // K[s][r] = P[s,r] dy_s w_r; per row block r the K of the own row
+        // s = 4r + g (16 slots, q <= 4r + 3) are summed over the wave's 16
+        // channels by a transposing butterfly in each 16-lane row, after which
+        // lane j holds slot q = j: H[s][j]
+        float cp[Q], rs[4];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) cp[q] = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = 4 * r + g;
+          float hv[Q];
+          float Pz = 0.f, rsum = 0.f;
+#pragma unroll
+          for (int q4 = 4 * r; q4 >= 0; q4 -= 4) {
+            float w4[4], g4[4];
+            rd4(&Tw[j][q4], w4);
+            rd4(&TGm[s][q4], g4);
+#pragma unroll
+            for (int e = 3; e >= 0; --e) {
+              const int q = q4 + e;
+              // Pz = P[s, q] = prod_{q < q' <= s} f for q <= s, 0 for q > s
+              // (a product chain with no masked multiply, so that it stays
+              // straight-line code)
+              if (q == 4 * r + 3) {
+                Pz = q == s ? 1.f : 0.f;
+              } else if (q >= 4 * r) {
+                Pz = q == s ? 1.f : Pz * fa[q + 1];
+              } else {
+                Pz = Pz * fa[q + 1];
+              }
+              const float kv = Pz * (dy_o[r] * w4[e]);
+              hv[q] = kv;
+              const float mv = kv * g4[e];
+              rsum += mv;
+              cp[q] += mv;
+            }
+          }
+#pragma unroll
+          for (int q = 4 * r + 4; q < Q; ++q) hv[q] = 0.f;
+          rs[r] = rsum;
+          trd_step<16, Q, Q>(hv, lane);
+          // lane j: H[s][j] (zero for j > s: every slot past s held zeros);
+          // over r and the lanes every entry of both tiles is written
+          TH[s][4 * (j & 3) + (j >> 2)] = hv[0];
+          THT[j][4 * (s & 3) + (s >> 2)] = hv[0];
+        }
+        // row sums of all 16 rows, and column sums over the channel's lanes
+        // (group g's partials in pool tile 6 + g for g < 3, tile 3 for g = 3)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = rs[r];
+        {
+          float* tc = pl + (g < 3 ? 6 + g : 3) * 16 * TP;
+#pragma unroll
+          for (int q4 = 0; q4 < Q; q4 += 4) wr4(tc + j * TP + q4, cp[q4], cp[q4 + 1], cp[q4 + 2], cp[q4 + 3]);
+        }
+        asm volatile("" ::: "memory");
+        // A3_t = sum_{s>=t} rowsum[s] - sum_{q>t} colsum[q]
+        {
+          float sufR = 0.f, sufC = 0.f;
+#pragma unroll
+          for (int r = 3; r >= 0; --r) {
+            float r4[4], c0[4], c1[4], c2[4], c3[4], cs[4];
+            rd4(&Tx1[j][4 * r], r4);
+            rd4(pl + 6 * 16 * TP + j * TP + 4 * r, c0);
+            rd4(pl + 7 * 16 * TP + j * TP + 4 * r, c1);
+            rd4(pl + 8 * 16 * TP + j * TP + 4 * r, c2);
+            rd4(pl + 3 * 16 * TP + j * TP + 4 * r, c3);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cs[e] = (c0[e] + c1[e]) + (c2[e] + c3[e]);
+            const float sR = sufR + r4[3] + (g <= 2 ? r4[2] : 0.f) + (g <= 1 ? r4[1] : 0.f) + (g <= 0 ? r4[0] : 0.f);
+            const float sC = sufC + (g < 3 ? cs[3] : 0.f) + (g < 2 ? cs[2] : 0.f) + (g < 1 ? cs[1] : 0.f);
+            A3[r] = sR - sC;
+            sufR += (r4[0] + r4[1]) + (r4[2] + r4[3]);
+            sufC += (cs[0] + cs[1]) + (cs[2] + cs[3]);
+          }
         }
       }
       // ---- outputs of the own rows into the gate tiles (dfl over f, du over
