@@ -197,11 +197,12 @@ constexpr int kMcDTB = 16 * kMcWB;
 
 // Below this decay over a sub-block (product of its 16 f of one channel),
 // the chunked kernels form the intra-sub-block decay terms as exact
-// products; above it, as ratios Pf[t] / Pf[s] of the running products from
-// the sub-block's first row, which turns those terms into matrix products
-// (1 / Pf stays below 2^60, so no intermediate overflows). A hard reset
+// products; at or above it, as ratios Pf[t] / Pf[s] of the running products
+// from the sub-block's first row, which turns those terms into matrix
+// products. 1 / Pf then stays at most 2^30, far from overflow, and Pf dy
+// leaves the normal range only for |dy| below about 2^-96. A hard reset
 // (f = 0) is always below it.
-constexpr float kMcRatioMin = 0x1p-60f;
+constexpr float kMcRatioMin = 0x1p-30f;
 
 // True when the chunked kernels serve this state size.
 inline bool mc_ok(int64_t N) { return N > 8 && N <= 64; }

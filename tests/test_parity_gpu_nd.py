@@ -77,6 +77,28 @@ def test_edge_gates_general_n(gpu):
     assert torch.all(gr["dfl"].cpu()[(sel < 0.1) | (sel >= 0.9)] == 0)
 
 
+def test_ratio_and_exact_decay_paths(gpu):
+    """The matrix-core kernels form the in-sub-block decay terms as ratios
+    of running products when every channel of a 16-channel group keeps its
+    16-row decay at or above 2^-30, as exact products otherwise. Channel
+    groups here sit just above the bound (1/Pf up to 2^29), just below it
+    in one channel only, well inside, and far below; all against the
+    oracle at the fp32 tolerance."""
+    import math
+    b, T, D, N = 2, 70, 64, 32
+    ins = rand_inputs(b, T, D, N, seed=21, h0_std=0.3)
+    logit = lambda f: math.log(f / (1.0 - f))  # noqa: E731
+    fl = ins["f_logit"].clone()
+    fl[:, :, 0:16] = logit(2.0 ** (-29.0 / 16.0)) + 0.001 * fl[:, :, 0:16]   # product about 2^-29
+    fl[:, :, 16:32] = fl[:, :, 16:32] + 0.0                                   # the recipe's gates
+    fl[:, :, 16] = logit(2.0 ** (-31.0 / 16.0))                               # one channel below 2^-30
+    fl[:, :, 48:64] = logit(0.05) + 0.1 * fl[:, :, 48:64]                     # far below
+    ins["f_logit"] = fl
+    y, g = run_hip(ins, gpu)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
 def test_deterministic_general_n(gpu):
     """No look-back and fixed-order sums: two runs are bitwise identical."""
     ins = rand_inputs(2, 200, 130, 64, seed=13, dtype=torch.bfloat16)
