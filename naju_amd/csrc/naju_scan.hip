@@ -2146,6 +2146,18 @@ struct Layout {
 #define NAJU_GN_TARGET_WGS 1536  // two rounds of three 4-wave workgroups per CU
 #endif
 constexpr int kGnTargetWgs = NAJU_GN_TARGET_WGS;
+// The chunked matrix-core kernels' segment targets (workgroups per launch):
+// the forward runs four 4-wave workgroups per CU, the backward one 8-wave
+// workgroup per CU, whose per-segment start-up (the carry, the first loads)
+// favours longer segments.
+#ifndef NAJU_MC_FWD_TARGET
+#define NAJU_MC_FWD_TARGET 1024
+#endif
+#ifndef NAJU_MC_BWD_TARGET
+#define NAJU_MC_BWD_TARGET 768
+#endif
+constexpr int kMcFwdTarget = NAJU_MC_FWD_TARGET;
+constexpr int kMcBwdTarget = NAJU_MC_BWD_TARGET;
 constexpr int kGcTargetWaves = 2048;
 // gq_fwd_kernel serves a forward whose batch x channel-group grid holds at
 // least three 4-wave workgroups per CU (256 CUs); smaller grids take the
@@ -2253,7 +2265,8 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
     // workgroups): about kGnTargetWgs workgroups
     const int64_t per_seg = (mc || bwd) ? l.n_tiles : batch * ((D + 63) / 64);
     // (the 8-wave NP = 128 backward runs one workgroup per CU: 1024)
-    const int64_t target = mc ? kGnTargetWgs : bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
+    const int64_t target = mc ? (bwd ? kMcBwdTarget : kMcFwdTarget)
+                              : bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
     int64_t want = (target + per_seg - 1) / per_seg;
     if (want > l.K) want = l.K;
     if (want < 1) want = 1;
