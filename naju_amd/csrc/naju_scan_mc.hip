@@ -88,6 +88,49 @@ __device__ __forceinline__ void ld4v(const TT* __restrict__ p, uint32_t i, float
   }
 }
 
+// Four consecutive elements of a stream as loaded: the raw bits (8 bytes
+// for 2-byte types, 16 for float), turned into floats only where they are
+// used. A conversion right after the load would make the wave wait for the
+// load there, so data loaded a sub-block ahead stays raw until its turn.
+template <typename TT>
+struct Raw4 {
+  static constexpr int NW = sizeof(TT) == 2 ? 2 : 4;
+  uint32_t w[NW];
+  __device__ __forceinline__ float get(int e) const {
+    if constexpr (sizeof(TT) == 4) {
+      return __builtin_bit_cast(float, w[e]);
+    } else {
+      const uint32_t x = w[e >> 1];
+      const uint16_t h = (e & 1) ? (uint16_t)(x >> 16) : (uint16_t)(x & 0xffffu);
+      return to_f32(__builtin_bit_cast(TT, h));
+    }
+  }
+};
+
+// Raw4 load of elements i .. i+3 at p (4-element aligned; VEC: one 8- or
+// 16-byte load) or of the elements at offsets o[0..3] (clamped edge lanes).
+template <typename TT>
+__device__ __forceinline__ void ld4r(const TT* __restrict__ p, uint32_t i, Raw4<TT>& r) {
+  // a clang vector type (not HIP's uint2 / uint4 structs, whose member
+  // reads are split into one 4-byte load each)
+  typedef uint32_t vw __attribute__((ext_vector_type(Raw4<TT>::NW)));
+  const vw v = *reinterpret_cast<const vw*>(p + i);
+#pragma unroll
+  for (int k = 0; k < Raw4<TT>::NW; ++k) r.w[k] = v[k];
+}
+template <typename TT>
+__device__ __forceinline__ void ld4r_at(const TT* __restrict__ p, const uint32_t (&o)[4], Raw4<TT>& r) {
+  if constexpr (sizeof(TT) == 2) {
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = __builtin_bit_cast(uint16_t, p[o[e]]);
+    r.w[0] = h[0] | (h[1] << 16), r.w[1] = h[2] | (h[3] << 16);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.w[e] = __builtin_bit_cast(uint32_t, p[o[e]]);
+  }
+}
+
 // LDS tiles of a sub-block's B and C, staged once per workgroup:
 //   Bn, C [t][n]  (row-major; pitch NP + 4 makes 16-byte reads of 16
 //                  different rows conflict-free),
@@ -109,7 +152,9 @@ struct McBC {
 // entries n0 .. n0+3 with n0 = (4 tid) % NP.
 template <int NP, bool MAP, typename TU, typename TG, typename TB>
 struct McIn {
-  float f[4], i[4], u[4], b[4], c[MAP ? 1 : 4];
+  Raw4<TG> f, i;
+  Raw4<TU> u;
+  Raw4<TB> b, c;
 
   __device__ __forceinline__ void load(const ScanArgs& a, int b_row, int64_t t0, int64_t dw, int rho, int cq,
                                        int tid, bool vec) {
@@ -122,18 +167,16 @@ struct McIn {
     const uint32_t off = (uint32_t)((rho < rows ? rho : rows - 1) * D);
     if (vec) {  // the wave's 16 channels lie inside [0, D), D % 4 == 0
       const uint32_t o = off + (uint32_t)(dw + cq);
-      ld4v<TG, true>((const TG*)a.fl + base, o, f);
-      ld4v<TG, true>((const TG*)a.il + base, o, i);
-      ld4v<TU, true>((const TU*)a.u + base, o, u);
+      ld4r<TG>((const TG*)a.fl + base, o, f);
+      ld4r<TG>((const TG*)a.il + base, o, i);
+      ld4r<TU>((const TU*)a.u + base, o, u);
     } else {
+      uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t dd = dw + cq + e < D ? dw + cq + e : D - 1;
-        const uint32_t o = off + (uint32_t)dd;
-        f[e] = to_f32(((const TG*)a.fl + base)[o]);
-        i[e] = to_f32(((const TG*)a.il + base)[o]);
-        u[e] = to_f32(((const TU*)a.u + base)[o]);
-      }
+      for (int e = 0; e < 4; ++e) o[e] = off + (uint32_t)(dw + cq + e < D ? dw + cq + e : D - 1);
+      ld4r_at<TG>((const TG*)a.fl + base, o, f);
+      ld4r_at<TG>((const TG*)a.il + base, o, i);
+      ld4r_at<TU>((const TU*)a.u + base, o, u);
     }
     if (tid < 4 * NP) {
       const int N = a.N;
@@ -141,15 +184,14 @@ struct McIn {
       const int64_t bb = ((int64_t)b_row * T + t0) * N;  // (t0, 0), uniform
       const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * N);
       if (N == NP) {
-        ld4v<TB, true>((const TB*)a.Bm + bb, ro + n0, b);
-        if constexpr (!MAP) ld4v<TB, true>((const TB*)a.Cm + bb, ro + n0, c);
+        ld4r<TB>((const TB*)a.Bm + bb, ro + n0, b);
+        if constexpr (!MAP) ld4r<TB>((const TB*)a.Cm + bb, ro + n0, c);
       } else {
+        uint32_t o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t o = ro + (uint32_t)(n0 + e < N ? n0 + e : N - 1);
-          b[e] = to_f32(((const TB*)a.Bm + bb)[o]);
-          if constexpr (!MAP) c[e] = to_f32(((const TB*)a.Cm + bb)[o]);
-        }
+        for (int e = 0; e < 4; ++e) o[e] = ro + (uint32_t)(n0 + e < N ? n0 + e : N - 1);
+        ld4r_at<TB>((const TB*)a.Bm + bb, o, b);
+        if constexpr (!MAP) ld4r_at<TB>((const TB*)a.Cm + bb, o, c);
       }
     }
   }
@@ -162,11 +204,11 @@ struct McIn {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool ok = rok && n0 + e < a.N;
-        const float vb = ok ? b[e] : 0.f;
+        const float vb = ok ? b.get(e) : 0.f;
         sh.Bt[buf][n0 + e][4 * (row & 3) + (row >> 2)] = vb;
         if constexpr (!MAP) {
           sh.Bn[buf][row][n0 + e] = vb;
-          sh.C[buf][row][n0 + e] = ok ? c[e] : 0.f;
+          sh.C[buf][row][n0 + e] = ok ? c.get(e) : 0.f;
         }
       }
     }
@@ -271,9 +313,9 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bool ok = rok && dw + cq + e < D;
-      s_t[wv][0][cq + e][rho] = ok ? sigm(cur.f[e]) : 1.f;
-      s_t[wv][1][cq + e][rho] = ok ? sigm(cur.i[e]) * cur.u[e] : 0.f;
-      uu[e] = ok ? cur.u[e] : 0.f;
+      s_t[wv][0][cq + e][rho] = ok ? sigm(cur.f.get(e)) : 1.f;
+      s_t[wv][1][cq + e][rho] = ok ? sigm(cur.i.get(e)) * cur.u.get(e) : 0.f;
+      uu[e] = ok ? cur.u.get(e) : 0.f;
     }
     __syncthreads();  // B / C of sb are staged; every wave is done with sb - 1
     // G[t][s] = C_t . B_s of the sub-block, in the layout of an A operand
@@ -534,7 +576,9 @@ struct McBwdLds {
 
 template <int NP, bool MAP, typename TU, typename TG, typename TB>
 struct McInB {
-  float f[4], dy[4], i[MAP ? 1 : 4], u[MAP ? 1 : 4], b[MAP ? 1 : 4], c[4];
+  Raw4<TG> f, i;
+  Raw4<TU> dy, u;
+  Raw4<TB> b, c;
 
   __device__ __forceinline__ void load(const ScanArgs& a, int b_row, int64_t t0, int64_t dw, int rho, int cq,
                                        int tid, bool vec) {
@@ -546,23 +590,21 @@ struct McInB {
     const uint32_t off = (uint32_t)((rho < rows ? rho : rows - 1) * D);
     if (vec) {
       const uint32_t o = off + (uint32_t)(dw + cq);
-      ld4v<TG, true>((const TG*)a.fl + base, o, f);
-      ld4v<TU, true>((const TU*)a.dy + base, o, dy);
+      ld4r<TG>((const TG*)a.fl + base, o, f);
+      ld4r<TU>((const TU*)a.dy + base, o, dy);
       if constexpr (!MAP) {
-        ld4v<TG, true>((const TG*)a.il + base, o, i);
-        ld4v<TU, true>((const TU*)a.u + base, o, u);
+        ld4r<TG>((const TG*)a.il + base, o, i);
+        ld4r<TU>((const TU*)a.u + base, o, u);
       }
     } else {
+      uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t dd = dw + cq + e < D ? dw + cq + e : D - 1;
-        const uint32_t o = off + (uint32_t)dd;
-        f[e] = to_f32(((const TG*)a.fl + base)[o]);
-        dy[e] = to_f32(((const TU*)a.dy + base)[o]);
-        if constexpr (!MAP) {
-          i[e] = to_f32(((const TG*)a.il + base)[o]);
-          u[e] = to_f32(((const TU*)a.u + base)[o]);
-        }
+      for (int e = 0; e < 4; ++e) o[e] = off + (uint32_t)(dw + cq + e < D ? dw + cq + e : D - 1);
+      ld4r_at<TG>((const TG*)a.fl + base, o, f);
+      ld4r_at<TU>((const TU*)a.dy + base, o, dy);
+      if constexpr (!MAP) {
+        ld4r_at<TG>((const TG*)a.il + base, o, i);
+        ld4r_at<TU>((const TU*)a.u + base, o, u);
       }
     }
     if (tid < 4 * NP) {
@@ -571,15 +613,14 @@ struct McInB {
       const int64_t bb = ((int64_t)b_row * T + t0) * N;
       const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * N);
       if (N == NP) {
-        ld4v<TB, true>((const TB*)a.Cm + bb, ro + n0, c);
-        if constexpr (!MAP) ld4v<TB, true>((const TB*)a.Bm + bb, ro + n0, b);
+        ld4r<TB>((const TB*)a.Cm + bb, ro + n0, c);
+        if constexpr (!MAP) ld4r<TB>((const TB*)a.Bm + bb, ro + n0, b);
       } else {
+        uint32_t o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t o = ro + (uint32_t)(n0 + e < N ? n0 + e : N - 1);
-          c[e] = to_f32(((const TB*)a.Cm + bb)[o]);
-          if constexpr (!MAP) b[e] = to_f32(((const TB*)a.Bm + bb)[o]);
-        }
+        for (int e = 0; e < 4; ++e) o[e] = ro + (uint32_t)(n0 + e < N ? n0 + e : N - 1);
+        ld4r_at<TB>((const TB*)a.Cm + bb, o, c);
+        if constexpr (!MAP) ld4r_at<TB>((const TB*)a.Bm + bb, o, b);
       }
     }
   }
@@ -592,10 +633,10 @@ struct McInB {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool ok = rok && n0 + e < a.N;
-        const float vc = ok ? c[e] : 0.f;
+        const float vc = ok ? c.get(e) : 0.f;
         sh.Ct[n0 + e][pr] = vc;
         if constexpr (!MAP) {
-          const float vb = ok ? b[e] : 0.f;
+          const float vb = ok ? b.get(e) : 0.f;
           sh.Bt[n0 + e][pr] = vb;
           sh.Bn[row][n0 + e] = vb;
           sh.C[row][n0 + e] = vc;
@@ -615,27 +656,30 @@ __device__ __forceinline__ void wr4(float* p, float a0, float a1, float a2, floa
 }
 
 // The checkpointed state entering sub-block sb of batch row b for channel
-// dcl (dok: the channel exists), in the D layout: x[m][r] = entry
-// 16m + 4g + r, zero past N and for channels past D.
+// dcl, in the D layout: x[m][r] = entry 16m + 4g + r (clamped in bounds;
+// the entries past N and the channels past D are zeroed where used, by
+// ckpt_val, so that a load a sub-block ahead does not wait for its data).
 template <int MT>
-__device__ __forceinline__ void load_ckpt(f4_t (&x)[MT], const ScanArgs& a, int b, int sb, int64_t dcl, bool dok,
-                                          int g) {
+__device__ __forceinline__ void load_ckpt(f4_t (&x)[MT], const ScanArgs& a, int b, int sb, int64_t dcl, int g) {
   const int N = a.N;
   const float* ck = a.ckpt + ((int64_t)b * a.Kc + sb) * a.D * N;  // uniform
   const uint32_t co = (uint32_t)(dcl * N);
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     const int n = 16 * m + 4 * g;
-    float x4[4];
     if ((N & 3) == 0) {
-      rd4(ck + (co + (uint32_t)(n < N ? n : N - 4)), x4);
+      const float4 v = *(const float4*)(ck + (co + (uint32_t)(n < N ? n : N - 4)));
+      x[m][0] = v.x, x[m][1] = v.y, x[m][2] = v.z, x[m][3] = v.w;
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x4[r] = ck[co + (uint32_t)(n + r < N ? n + r : N - 1)];
+      for (int r = 0; r < 4; ++r) x[m][r] = ck[co + (uint32_t)(n + r < N ? n + r : N - 1)];
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) x[m][r] = (dok && n + r < N) ? x4[r] : 0.f;
   }
+}
+// Entry 16m + 4g + r of a load_ckpt state, zero past N and for channels
+// past D.
+__device__ __forceinline__ float ckpt_val(const f4_t& xm, int r, int n, int N, bool dok) {
+  return (dok && n + r < N) ? xm[r] : 0.f;
 }
 
 // Four values of the load layout (row rho, channels cq .. cq+3) from a
@@ -705,16 +749,16 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
   float (*Tdy)[TP] = sh.gate[wv][1];
 
   // inputs of sub-blocks sb (cur) and sb - 1 (nxt), loaded one sub-block
-  // ahead; MAP (little work per sub-block) also those of sb - 2 (nx2)
-  In cur, nxt, nx2;
+  // ahead and kept raw until staged (two sets: cur's registers are free
+  // once staged, so nxt can take them without a copy)
+  In cur, nxt;
   // the checkpointed state entering the current (xc) and the next (xn)
   // sub-block, loaded one sub-block ahead like the inputs
   f4_t xc[MAP ? 1 : MT], xn[MAP ? 1 : MT];
   if (sb0 < sb1) {
     cur.load(a, b, (int64_t)(sb1 - 1) * Q, dw, rho, cq, tid, vec);
-    if constexpr (!MAP) load_ckpt<MT>(xc, a, b, sb1 - 1, dok ? d : D - 1, dok, g);
+    if constexpr (!MAP) load_ckpt<MT>(xc, a, b, sb1 - 1, dok ? d : D - 1, g);
   }
-  if (MAP && sb1 - 2 >= sb0) nxt.load(a, b, (int64_t)(sb1 - 2) * Q, dw, rho, cq, tid, vec);
   for (int sb = sb1 - 1; sb >= sb0; --sb) {
     // The lane's indices, recomputed every sub-block from an opaque copy of
     // the lane id (they shadow the ones above): otherwise every
@@ -738,21 +782,19 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bool ok = rok && e < ncq;
-      Tf[cq + e][rho] = ok ? sigm(cur.f[e]) : 1.f;
-      Tdy[cq + e][rho] = ok ? cur.dy[e] : 0.f;
+      Tf[cq + e][rho] = ok ? sigm(cur.f.get(e)) : 1.f;
+      Tdy[cq + e][rho] = ok ? cur.dy.get(e) : 0.f;
       if constexpr (!MAP) {
-        const float ig = ok ? sigm(cur.i[e]) : 0.f;
+        const float ig = ok ? sigm(cur.i.get(e)) : 0.f;
         sh.gate[wv][3][cq + e][rho] = ig;
-        sh.gate[wv][2][cq + e][rho] = ok ? ig * cur.u[e] : 0.f;
-        dDacc[e] = fmaf(ok ? cur.dy[e] : 0.f, ok ? cur.u[e] : 0.f, dDacc[e]);
+        sh.gate[wv][2][cq + e][rho] = ok ? ig * cur.u.get(e) : 0.f;
+        dDacc[e] = fmaf(ok ? cur.dy.get(e) : 0.f, ok ? cur.u.get(e) : 0.f, dDacc[e]);
       }
     }
     __syncthreads();  // staging visible
-    if constexpr (MAP) {
-      if (sb - 2 >= sb0) nx2.load(a, b, t0 - 2 * Q, dw, rho, cq, tid, vec);
-    } else if (sb - 1 >= sb0) {
+    if (sb - 1 >= sb0) {
       nxt.load(a, b, t0 - Q, dw, rho, cq, tid, vec);
-      load_ckpt<MT>(xn, a, b, sb - 1, dcl, dok, g);
+      if constexpr (!MAP) load_ckpt<MT>(xn, a, b, sb - 1, dcl, g);
     }
     asm volatile("" ::: "memory");
 
@@ -795,10 +837,11 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+          const float xv = ckpt_val(xc[m], e, 16 * m + 4 * g, N, dok);
           Gp = mma(b4[e], c4[e], Gp);
-          cx = mma(c4[e], xc[m][e], cx);
+          cx = mma(c4[e], xv, cx);
           bg = mma(b4[e], gh[m][e], bg);
-          gX = fmaf(gh[m][e], xc[m][e], gX);
+          gX = fmaf(gh[m][e], xv, gX);
         }
       }
       gX += __shfl_xor(gX, 16, 64);
@@ -1060,7 +1103,8 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const int n = 16 * m + 4 * g;
-          wr4(TX + j * P + n, xc[m][0], xc[m][1], xc[m][2], xc[m][3]);
+          wr4(TX + j * P + n, ckpt_val(xc[m], 0, n, N, dok), ckpt_val(xc[m], 1, n, N, dok),
+              ckpt_val(xc[m], 2, n, N, dok), ckpt_val(xc[m], 3, n, N, dok));
           wr4(TGh + j * P + n, gh[m][0], gh[m][1], gh[m][2], gh[m][3]);
         }
       }
@@ -1159,9 +1203,7 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
     // its share of the partial sums.
     if constexpr (MAP) __syncthreads();
     cur = nxt;
-    if constexpr (MAP) {
-      nxt = nx2;
-    } else {
+    if constexpr (!MAP) {
 #pragma unroll
       for (int m = 0; m < MT; ++m) xc[m] = xn[m];
     }
