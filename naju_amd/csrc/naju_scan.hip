@@ -56,41 +56,100 @@ using namespace naju_detail;
 // Out-of-range elements read as 0 and are not written.
 enum { kVecAll = 0, kVecLane = 1, kElem = 2 };
 
-template <typename T, int V, int MODE>
-__device__ __forceinline__ void ld_row(const T* __restrict__ p, int64_t d0, int64_t D, float (&o)[V]) {
-  typedef T vec_t __attribute__((ext_vector_type(V)));
-  if constexpr (MODE == kVecAll) {
-    const vec_t v = *reinterpret_cast<const vec_t*>(p + d0);
-#pragma unroll
-    for (int j = 0; j < V; ++j) o[j] = to_f32(v[j]);
-  } else if constexpr (MODE == kVecLane) {
-    if (d0 < D) {
-      const vec_t v = *reinterpret_cast<const vec_t*>(p + d0);
-#pragma unroll
-      for (int j = 0; j < V; ++j) o[j] = to_f32(v[j]);
+// V consecutive elements of a row as loaded: the raw bits (one 32-bit word
+// per two 2-byte elements), turned into floats where they are used. Chunk
+// rows are loaded long before pass 1 reaches them; kept raw, 2-byte rows take
+// half the registers of converted ones.
+template <typename T, int V>
+struct RawRow {
+  static constexpr int NW = (V * (int)sizeof(T) + 3) / 4;
+  uint32_t w[NW];
+  __device__ __forceinline__ float get(int j) const {
+    if constexpr (sizeof(T) == 4) {
+      return __builtin_bit_cast(float, w[j]);
     } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) o[j] = 0.f;
+      const uint32_t x = w[j >> 1];
+      const uint16_t h = (j & 1) ? (uint16_t)(x >> 16) : (uint16_t)(x & 0xffffu);
+      return to_f32(__builtin_bit_cast(T, h));
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) o[j] = (d0 + j < D) ? to_f32(p[d0 + j]) : 0.f;
   }
+};
+
+// ld_row into a RawRow from row pointer p (uniform: the row at the tile's
+// first channel) at lane element offset lo, channel d0 = tile start + lo.
+// The byte offset is a 32-bit lane value, so the load takes the row address
+// in scalar registers and one offset register shared by every row.
+// Out-of-range elements read as 0 (all-zero bits).
+template <typename T>
+__device__ __forceinline__ const T* at_lane(const T* p, uint32_t lo) {
+  return (const T*)((const char*)p + lo * (uint32_t)sizeof(T));
+}
+template <typename T>
+__device__ __forceinline__ T* at_lane(T* p, uint32_t lo) {
+  return (T*)((char*)p + lo * (uint32_t)sizeof(T));
+}
+
+// A uniform pointer held in scalar registers through an opaque copy: loads
+// at it plus a lane's 32-bit offset then use the scalar-base address form,
+// instead of the compiler deriving every row's 64-bit address from the
+// previous row's in vector registers.
+template <typename T>
+__device__ __forceinline__ T* sreg(T* p) {
+  uint64_t v = (uint64_t)p;
+  asm("s_mov_b64 %0, %1" : "=s"(v) : "s"(v));
+  // back through a global (address space 1) pointer, so the accesses stay
+  // global ones rather than flat ones
+  return (T*)(__attribute__((address_space(1))) T*)v;
 }
 
 template <typename T, int V, int MODE>
-__device__ __forceinline__ void st_row(T* __restrict__ p, int64_t d0, int64_t D, const float (&x)[V]) {
+__device__ __forceinline__ void ld_row_raw(const T* __restrict__ p, uint32_t lo, int64_t d0, int64_t D,
+                                           RawRow<T, V>& o) {
+  constexpr int NW = RawRow<T, V>::NW;
+  if constexpr (MODE != kElem && (V * sizeof(T)) % 4 == 0) {
+    // a clang vector type: HIP's uint2 / uint4 member reads become one
+    // 4-byte load each
+    typedef uint32_t vw __attribute__((ext_vector_type(NW)));
+    if (MODE == kVecAll || d0 < D) {
+      const vw v = *reinterpret_cast<const vw*>(at_lane(p, lo));
+#pragma unroll
+      for (int k = 0; k < NW; ++k) o.w[k] = v[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < NW; ++k) o.w[k] = 0u;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NW; ++k) o.w[k] = 0u;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const bool ok = MODE == kElem ? d0 + j < D : (MODE == kVecAll || d0 < D);
+      if constexpr (sizeof(T) == 4) {
+        o.w[j] = ok ? __builtin_bit_cast(uint32_t, at_lane(p, lo)[j]) : 0u;
+      } else {
+        const uint32_t h = ok ? (uint32_t)__builtin_bit_cast(uint16_t, at_lane(p, lo)[j]) : 0u;
+        o.w[j >> 1] |= (j & 1) ? h << 16 : h;
+      }
+    }
+  }
+}
+
+// st_row at row pointer p (uniform, the tile's first channel) and lane
+// element offset lo (channel d0 = tile start + lo).
+template <typename T, int V, int MODE>
+__device__ __forceinline__ void st_row_at(T* __restrict__ p, uint32_t lo, int64_t d0, int64_t D,
+                                          const float (&x)[V]) {
   typedef T vec_t __attribute__((ext_vector_type(V)));
   if constexpr (MODE == kElem) {
 #pragma unroll
     for (int j = 0; j < V; ++j)
-      if (d0 + j < D) p[d0 + j] = from_f32<T>(x[j]);
+      if (d0 + j < D) at_lane(p, lo)[j] = from_f32<T>(x[j]);
   } else {
     if (MODE == kVecAll || d0 < D) {
       vec_t v;
 #pragma unroll
       for (int j = 0; j < V; ++j) v[j] = from_f32<T>(x[j]);
-      *reinterpret_cast<vec_t*>(p + d0) = v;
+      *reinterpret_cast<vec_t*>(at_lane(p, lo)) = v;
     }
   }
 }
@@ -161,10 +220,10 @@ __global__ void epoch_bump_kernel(uint32_t* hdr) {
 // Also returns the launch's look-back tag in *s_tag (a.tag, or the device
 // epoch's tag when a.tag is 0: read next to the ticket, in the same round
 // trip; nothing changes the epoch while the launch runs).
-// Returns false (after recording it in the status word) if the counter held
-// a value outside [0, K): a workspace that was not zero-filled. The caller
-// then poisons its blockIdx chunk instead of computing it.
-__device__ __forceinline__ bool take_ticket(const ScanArgs& a, int tile, uint32_t* s_ticket, uint32_t* s_tag) {
+// Returns the ticket (uniform). A ticket outside [0, K) means a workspace
+// that was not zero-filled: it is recorded in the status word and the
+// caller poisons its blockIdx chunk instead of computing it.
+__device__ __forceinline__ uint32_t take_ticket(const ScanArgs& a, int tile, uint32_t* s_ticket, uint32_t* s_tag) {
   if (threadIdx.x == 0) {
     uint32_t* ctr = a.hdr + kCtrBase + (int64_t)tile * kCtrStride;
     uint32_t e = 0;
@@ -176,7 +235,7 @@ __device__ __forceinline__ bool take_ticket(const ScanArgs& a, int tile, uint32_
     *s_tag = a.tag != 0u ? a.tag : epoch_tag(e);
   }
   __syncthreads();
-  return *s_ticket < (uint32_t)a.K;
+  return __builtin_amdgcn_readfirstlane(*s_ticket);
 }
 
 // ------------------------------------------------ workgroup-wide look-back
@@ -203,13 +262,115 @@ struct LookShared {
   int ctl[2];       // done, number of predecessors consumed
 };
 
+// One round's polled words, as this wave loaded them: predecessor slot
+// p*W + wv of the round (p < P), V channel words of each kind.
+template <int V, int P>
+struct LookPoll {
+  uint64_t wi[P][V], wf[P][V], wz[P][V];
+};
+
+// Issue this wave's polls of the round whose first predecessor is `base`.
+template <int V, int W, int P>
+__device__ __forceinline__ void lb_issue(const ScanArgs& a, int base, int tile, int dir, int lane, int wv,
+                                         LookPoll<V, P>& q) {
+  constexpr int CH = 64 * V;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = base + dir * (p * W + wv);
+    const bool inr = c >= 0 && c < a.K;
+    const uint64_t* pi = a.incl + ((int64_t)c * a.n_tiles + tile) * CH + lane;
+    const uint64_t* pa = a.agg + ((int64_t)c * a.n_tiles + tile) * 2 * CH + lane;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      // values (not struct members) assigned on both paths, so the words
+      // stay in registers
+      uint64_t wi = 0, wf = 0, wz = 0;
+      if (inr) {
+        wi = ld_word(pi + j * 64);
+        wf = ld_word(pa + j * 64);
+        wz = ld_word(pa + CH + j * 64);
+      }
+      q.wi[p][j] = wi;
+      q.wf[p][j] = wf;
+      q.wz[p][j] = wz;
+    }
+  }
+}
+
+// Finish one round from its polled words: stage them in LDS, wave 0 walks
+// the window in order (aggregates composed into aF, aZ until the first
+// inclusive carry, which ends the walk into `out`; a predecessor that is
+// not ready ends the round). Returns true when the carry is known; else
+// advances base past the predecessors consumed.
+template <int V, int W, int P>
+__device__ __forceinline__ bool lb_consume(const ScanArgs& a, LookShared<V, W, P>& sh, int& base, int dir,
+                                           uint32_t tag, int lane, int wv, const LookPoll<V, P>& q, float (&aF)[V],
+                                           float (&aZ)[V], float (&out)[V], uint32_t& idle) {
+  constexpr int WP = W * P;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int slot = p * W + wv;
+    const int c = base + dir * slot;
+    const bool inr = c >= 0 && c < a.K;
+    bool iok = inr, aok = inr;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      iok = iok && word_ok(q.wi[p][j], tag);
+      aok = aok && word_ok(q.wf[p][j], tag) && word_ok(q.wz[p][j], tag);
+      sh.S[slot][j * 64 + lane] = word_val(q.wi[p][j]);
+      sh.F[slot][j * 64 + lane] = word_val(q.wf[p][j]);
+      sh.Z[slot][j * 64 + lane] = word_val(q.wz[p][j]);
+    }
+    iok = __all(iok);
+    aok = __all(aok);
+    if (lane == 0) sh.stat[slot] = iok ? 2 : (aok ? 1 : 0);
+  }
+  __syncthreads();
+  if (wv == 0) {
+    int consumed = 0, done = 0;
+    for (int slot = 0; slot < WP; ++slot) {
+      const int st = sh.stat[slot];
+      if (st == 2) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) out[j] = fmaf(aF[j], sh.S[slot][j * 64 + lane], aZ[j]);
+        done = 1;
+        break;
+      }
+      // strict: never compose aggregates, wait for the predecessor's
+      // inclusive carry (a fixed composition order)
+      if (st != 1 || a.strict) break;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        aZ[j] = fmaf(aF[j], sh.Z[slot][j * 64 + lane], aZ[j]);
+        aF[j] *= sh.F[slot][j * 64 + lane];
+      }
+      ++consumed;
+    }
+    if (!done && consumed == 0 && ++idle > kSpinLimit) {
+      // Bounded wait exceeded: record it and end with a NaN carry.
+      if (lane == 0) __hip_atomic_store(a.hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int j = 0; j < V; ++j) out[j] = __builtin_nanf("");
+      done = 1;
+    }
+    if (lane == 0) {
+      sh.ctl[0] = done;
+      sh.ctl[1] = consumed;
+    }
+  }
+  __syncthreads();
+  const int done = sh.ctl[0];
+  const int consumed = sh.ctl[1];
+  base += dir * consumed;
+  if (!done && consumed == 0) __builtin_amdgcn_s_sleep(2);
+  return done != 0;
+}
+
 // Carry entering chunk k (dir = -1: forward, predecessors k-1, k-2, ...;
 // dir = +1: backward, k+1, k+2, ...). Result valid in wave 0's lanes.
 template <int V, int W, int P>
-__device__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, int tile, int dir, uint32_t tag,
-                             int lane, int wv, float (&out)[V]) {
-  constexpr int CH = 64 * V;
-  constexpr int WP = W * P;
+__device__ __forceinline__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, int tile, int dir,
+                                             uint32_t tag, int lane, int wv, float (&out)[V]) {
   float aF[V], aZ[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
@@ -220,117 +381,44 @@ __device__ void wg_look_back(const ScanArgs& a, LookShared<V, W, P>& sh, int k, 
   int base = k + dir;
   uint32_t idle = 0;
   while (true) {
-#pragma unroll 1
-    for (int p = 0; p < P; ++p) {
-      const int slot = p * W + wv;
-      const int c = base + dir * slot;
-      const bool inr = c >= 0 && c < a.K;
-      bool iok = inr, aok = inr;
-      float S[V], F[V], Z[V];
-      if (inr) {
-        const uint64_t* pi = a.incl + ((int64_t)c * a.n_tiles + tile) * CH + lane;
-        const uint64_t* pa = a.agg + ((int64_t)c * a.n_tiles + tile) * 2 * CH + lane;
-        uint64_t wi[V], wf[V], wz[V];
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          wi[j] = ld_word(pi + j * 64);
-          wf[j] = ld_word(pa + j * 64);
-          wz[j] = ld_word(pa + CH + j * 64);
-        }
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          iok = iok && word_ok(wi[j], tag);
-          aok = aok && word_ok(wf[j], tag) && word_ok(wz[j], tag);
-          S[j] = word_val(wi[j]);
-          F[j] = word_val(wf[j]);
-          Z[j] = word_val(wz[j]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < V; ++j) S[j] = F[j] = Z[j] = 0.f;
-      }
-      iok = __all(iok);
-      aok = __all(aok);
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        sh.S[slot][j * 64 + lane] = S[j];
-        sh.F[slot][j * 64 + lane] = F[j];
-        sh.Z[slot][j * 64 + lane] = Z[j];
-      }
-      if (lane == 0) sh.stat[slot] = iok ? 2 : (aok ? 1 : 0);
-    }
-    __syncthreads();
-    if (wv == 0) {
-      int consumed = 0, done = 0;
-      for (int slot = 0; slot < WP; ++slot) {
-        const int st = sh.stat[slot];
-        if (st == 2) {
-#pragma unroll
-          for (int j = 0; j < V; ++j) out[j] = fmaf(aF[j], sh.S[slot][j * 64 + lane], aZ[j]);
-          done = 1;
-          break;
-        }
-        // strict: never compose aggregates, wait for the predecessor's
-        // inclusive carry (a fixed composition order)
-        if (st != 1 || a.strict) break;
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          aZ[j] = fmaf(aF[j], sh.Z[slot][j * 64 + lane], aZ[j]);
-          aF[j] *= sh.F[slot][j * 64 + lane];
-        }
-        ++consumed;
-      }
-      if (!done && consumed == 0 && ++idle > kSpinLimit) {
-        // Bounded wait exceeded: record it and end with a NaN carry.
-        if (lane == 0) __hip_atomic_store(a.hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int j = 0; j < V; ++j) out[j] = __builtin_nanf("");
-        done = 1;
-      }
-      if (lane == 0) {
-        sh.ctl[0] = done;
-        sh.ctl[1] = consumed;
-      }
-    }
-    __syncthreads();
-    const int done = sh.ctl[0];
-    const int consumed = sh.ctl[1];
-    if (done) break;
-    base += dir * consumed;
-    if (consumed == 0) __builtin_amdgcn_s_sleep(2);
+    LookPoll<V, P> q;
+    lb_issue<V, W, P>(a, base, tile, dir, lane, wv, q);
+    if (lb_consume<V, W, P>(a, sh, base, dir, tag, lane, wv, q, aF, aZ, out, idle)) break;
   }
 }
 
-// Rows [t0, t0+R) of one [batch,T,D] stream for this lane's channels
-// (rowbase = b*T + t0). ROWCHK: rows at or beyond T read as 0.
+// Rows [t0, t0+R) (rowbase = b*T + t0) of one [batch,T,D] stream, p at the
+// tile's first channel. ROWCHK: rows at or beyond T read as 0.
 template <typename T, int V, int R, int MODE, bool ROWCHK>
-__device__ __forceinline__ void ld_rows(const T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn, int64_t D,
-                                        int64_t d0, float (&o)[R][V]) {
+__device__ __forceinline__ void ld_rows_raw(const T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn, int64_t D,
+                                            uint32_t lo, int64_t d0, RawRow<T, V> (&o)[R]) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (!ROWCHK || t0 + r < Tn) {
-      ld_row<T, V, MODE>(p + (rowbase + r) * D, d0, D, o[r]);
+      ld_row_raw<T, V, MODE>(sreg(p + (rowbase + r) * D), lo, d0, D, o[r]);
     } else {
 #pragma unroll
-      for (int j = 0; j < V; ++j) o[r][j] = 0.f;
+      for (int k = 0; k < RawRow<T, V>::NW; ++k) o[r].w[k] = 0u;
     }
   }
 }
 
-template <typename T, int V, int R, int MODE, bool ROWCHK>
-__device__ __forceinline__ void st_rows(T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn, int64_t D,
-                                        int64_t d0, const float (&x)[R][V]) {
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (!ROWCHK || t0 + r < Tn) st_row<T, V, MODE>(p + (rowbase + r) * D, d0, D, x[r]);
-}
-
-// B_t or C_t of rows [t0, t0+R) of batch row b (N = 1: one value per row).
+// B_t and C_t of rows [t0, t0+R) into scalar registers: lane r < R loads
+// B_t0+r and lane R + r loads C_t0+r (one vector register for the wave),
+// then each value is read out of its lane. Held as vector registers, the
+// 2R values uniform across the wave would take 2R of them.
 template <typename T, int R, bool ROWCHK>
-__device__ __forceinline__ void ld_scalars(const T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn,
-                                           float (&o)[R]) {
+__device__ __forceinline__ void ld_bc(const T* __restrict__ pb, const T* __restrict__ pc, int64_t rowbase, int t0,
+                                      int64_t Tn, int lane, float (&bt)[R], float (&ct)[R]) {
+  static_assert(2 * R <= 64, "one lane per value");
+  const int r = lane < R ? lane : lane - R;
+  float v = 0.f;
+  if (lane < 2 * R && (!ROWCHK || t0 + r < Tn)) v = to_f32((lane < R ? pb : pc)[rowbase + r]);
 #pragma unroll
-  for (int r = 0; r < R; ++r) o[r] = (!ROWCHK || t0 + r < Tn) ? to_f32(p[rowbase + r]) : 0.f;
+  for (int q = 0; q < R; ++q) {
+    bt[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), q));
+    ct[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), R + q));
+  }
 }
 
 // ------------------------------------------------------------ N = 1 forward
@@ -344,8 +432,9 @@ __device__ __forceinline__ void ld_scalars(const T* __restrict__ p, int64_t rowb
 // bounds checks, all loads issued back to back; edge workgroups check.
 template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O, bool FULL>
 __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, int lane, int wv, uint32_t tag,
-                                            bool poison, float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
-                                            float (&s_in)[64 * V], LookShared<V, W, P>& s_lb) {
+                                            bool poison,
+                                            float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V], float (&s_in)[64 * V],
+                                            LookShared<V, W, P>& s_lb) {
   using TY = std::conditional_t<F32O, float, TU>;  // y dtype
   constexpr int CH = 64 * V;
   constexpr int L = W * R;
@@ -353,7 +442,9 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
-  const int64_t d0 = (int64_t)dtile * CH + lane * V;
+  const int64_t dbase = (int64_t)dtile * CH;  // the tile's first channel
+  const uint32_t lo = (uint32_t)(lane * V);
+  const int64_t d0 = dbase + lo;
   const int t0 = k * L + wv * R;
   const int64_t rowbase = (int64_t)b * T + t0;
 
@@ -366,13 +457,13 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
   }
 
   // ---- load the wave's R rows
-  float xu[R][V], xf[R][V], xi[R][V];
+  RawRow<TU, V> xu[R];
+  RawRow<TG, V> xf[R], xi[R];
   float Bt[R], Ct[R];
-  ld_rows<TU, V, R, M, !FULL>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
-  ld_rows<TG, V, R, M, !FULL>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
-  ld_rows<TG, V, R, M, !FULL>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
-  ld_scalars<TB, R, !FULL>((const TB*)a.Bm, rowbase, t0, T, Bt);
-  ld_scalars<TB, R, !FULL>((const TB*)a.Cm, rowbase, t0, T, Ct);
+  ld_rows_raw<TU, V, R, M, !FULL>((const TU*)a.u + dbase, rowbase, t0, T, D, lo, d0, xu);
+  ld_rows_raw<TG, V, R, M, !FULL>((const TG*)a.fl + dbase, rowbase, t0, T, D, lo, d0, xf);
+  ld_rows_raw<TG, V, R, M, !FULL>((const TG*)a.il + dbase, rowbase, t0, T, D, lo, d0, xi);
+  ld_bc<TB, R, !FULL>((const TB*)a.Bm, (const TB*)a.Cm, rowbase, t0, T, lane, Bt, Ct);
 
   // ---- pass 1: local scan from zero; keep y = yl + q * (carry) per element
   float F[V], Z[V];
@@ -388,13 +479,16 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const bool v = tv && dok[j];
-      const float f = v ? sigm(xf[r][j]) : 1.f;
-      const float ig = v ? sigm(xi[r][j]) : 0.f;
-      const float x = xu[r][j];
+      const float f = v ? sigm(xf[r].get(j)) : 1.f;
+      const float ig = v ? sigm(xi[r].get(j)) : 0.f;
+      const float x = xu[r].get(j);
       Z[j] = fmaf(f, Z[j], ig * Bt[r] * x);
       F[j] *= f;
       yl[r][j] = fmaf(Ct[r], Z[j], Dv[j] * x);
       q[r][j] = Ct[r] * F[j];
+      // formed here: otherwise the compiler moves parts of this row's
+      // arithmetic past the look-back and keeps more values live across it
+      asm volatile("" : "+v"(yl[r][j]), "+v"(q[r][j]));
     }
   }
 #pragma unroll
@@ -469,7 +563,9 @@ __device__ __forceinline__ void n1_fwd_body(const ScanArgs& a, int k, int tile, 
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < V; ++j) yl[r][j] = fmaf(q[r][j], s[j], yl[r][j]);
-  st_rows<TY, V, R, M, !FULL>((TY*)a.y, rowbase, t0, T, D, d0, yl);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (FULL || t0 + r < T) st_row_at<TY, V, M>((TY*)a.y + (rowbase + r) * D + dbase, lo, d0, D, yl[r]);
 }
 
 template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
@@ -483,14 +579,16 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
   __shared__ LookShared<V, W, P> s_lb;
 
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  // an out-of-range ticket (a workspace that was not zero-filled) poisons
-  // the chunk this workgroup's index names, so no output is left unwritten
-  const bool poison = !take_ticket(a, tile, &s_ticket, &s_tag);
-  const int k = poison ? (int)(blockIdx.x / (uint32_t)a.n_tiles) : (int)__builtin_amdgcn_readfirstlane(s_ticket);
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dtile = tile % a.n_dtiles;
+  const int kx = (int)(blockIdx.x / (uint32_t)a.n_tiles);
+  const uint32_t t = take_ticket(a, tile, &s_ticket, &s_tag);
+  // an out-of-range ticket (a workspace that was not zero-filled) poisons
+  // the chunk this workgroup's index names, so no output is left unwritten
+  const bool poison = t >= (uint32_t)a.K;
+  const int k = poison ? kx : (int)t;
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   if constexpr (VEC) {
     if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
       n1_fwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_in, s_lb);
@@ -509,7 +607,8 @@ __global__ __launch_bounds__(64 * W) void n1_fwd_kernel(const ScanArgs a) {
 // forward state entering the chunk comes from the forward's checkpoint.
 template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O, bool FULL>
 __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, int lane, int wv, uint32_t tag,
-                                            bool poison, float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
+                                            bool poison,
+                                            float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
                                             float (&s_Zb)[W][64 * V], float (&s_g)[64 * V],
                                             LookShared<V, W, P>& s_lb, float (&s_pq)[W][2 * R][64]) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
@@ -520,7 +619,9 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   const int b = tile / a.n_dtiles;
   const int dtile = tile - b * a.n_dtiles;
   const int64_t T = a.T, D = a.D;
-  const int64_t d0 = (int64_t)dtile * CH + lane * V;
+  const int64_t dbase = (int64_t)dtile * CH;  // the tile's first channel
+  const uint32_t lo = (uint32_t)(lane * V);
+  const int64_t d0 = dbase + lo;
   const int t0 = k * L + wv * R;
   const int64_t rowbase = (int64_t)b * T + t0;
 
@@ -532,14 +633,17 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
     Dv[j] = dok[j] ? a.Dsk[d0 + j] : 0.f;
   }
 
-  float xu[R][V], xf[R][V], xi[R][V], xg[R][V];
+  // rows as loaded (u and dy stay raw until used; the gate logits become
+  // gates in pass 1)
+  RawRow<TU, V> xu[R], xg[R];
+  RawRow<TG, V> lf[R], li[R];
+  float xf[R][V], xi[R][V];
   float Bt[R], Ct[R];
-  ld_rows<TU, V, R, M, !FULL>((const TU*)a.u, rowbase, t0, T, D, d0, xu);
-  ld_rows<TG, V, R, M, !FULL>((const TG*)a.fl, rowbase, t0, T, D, d0, xf);
-  ld_rows<TG, V, R, M, !FULL>((const TG*)a.il, rowbase, t0, T, D, d0, xi);
-  ld_rows<TU, V, R, M, !FULL>((const TU*)a.dy, rowbase, t0, T, D, d0, xg);
-  ld_scalars<TB, R, !FULL>((const TB*)a.Bm, rowbase, t0, T, Bt);
-  ld_scalars<TB, R, !FULL>((const TB*)a.Cm, rowbase, t0, T, Ct);
+  ld_rows_raw<TU, V, R, M, !FULL>((const TU*)a.u + dbase, rowbase, t0, T, D, lo, d0, xu);
+  ld_rows_raw<TG, V, R, M, !FULL>((const TG*)a.fl + dbase, rowbase, t0, T, D, lo, d0, lf);
+  ld_rows_raw<TG, V, R, M, !FULL>((const TG*)a.il + dbase, rowbase, t0, T, D, lo, d0, li);
+  ld_rows_raw<TU, V, R, M, !FULL>((const TU*)a.dy + dbase, rowbase, t0, T, D, lo, d0, xg);
+  ld_bc<TB, R, !FULL>((const TB*)a.Bm, (const TB*)a.Cm, rowbase, t0, T, lane, Bt, Ct);
   float s[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) s[j] = dok[j] ? a.ckpt[((int64_t)b * a.K + k) * D + d0 + j] : 0.f;
@@ -558,16 +662,23 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const bool v = tv && dok[j];
-      xf[r][j] = v ? sigm(xf[r][j]) : 1.f;  // f
-      xi[r][j] = v ? sigm(xi[r][j]) : 0.f;  // i
-      Z[j] = fmaf(xf[r][j], Z[j], xi[r][j] * Bt[r] * xu[r][j]);
+      xf[r][j] = v ? sigm(lf[r].get(j)) : 1.f;  // f
+      xi[r][j] = v ? sigm(li[r].get(j)) : 0.f;  // i
+      Z[j] = fmaf(xf[r][j], Z[j], xi[r][j] * Bt[r] * xu[r].get(j));
       F[j] *= xf[r][j];
+      // only the gates (and the raw rows) cross the look-back, not products
+      // that pass 2 would otherwise share with this pass
+      asm volatile("" : "+v"(xf[r][j]), "+v"(xi[r][j]));
     }
   }
 #pragma unroll
   for (int r = R - 1; r >= 0; --r)
 #pragma unroll
-    for (int j = 0; j < V; ++j) G[j] = xf[r][j] * fmaf(xg[r][j], Ct[r], G[j]);
+    for (int j = 0; j < V; ++j) G[j] = xf[r][j] * fmaf(xg[r].get(j), Ct[r], G[j]);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int k2 = 0; k2 < RawRow<TU, V>::NW; ++k2) asm volatile("" : "+v"(xu[r].w[k2]), "+v"(xg[r].w[k2]));
 #pragma unroll
   for (int j = 0; j < V; ++j) {
     s_F[wv][j * 64 + lane] = F[j];
@@ -638,7 +749,7 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      s[j] = fmaf(xf[r][j], s[j], xi[r][j] * Bt[r] * xu[r][j]);
+      s[j] = fmaf(xf[r][j], s[j], xi[r][j] * Bt[r] * xu[r].get(j));
       xs[r][j] = s[j];
     }
 
@@ -652,9 +763,10 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
 #pragma unroll
   for (int r = R - 1; r >= 0; --r) {
     float pb = 0.f, pc = 0.f;
+    float du[V], dfl[V], dil[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      const float f = xf[r][j], ig = xi[r][j], x = xu[r][j], gy = xg[r][j];
+      const float f = xf[r][j], ig = xi[r][j], x = xu[r].get(j), gy = xg[r].get(j);
       const float xprev = r > 0 ? xs[r - 1][j] : s0[j];
       const float xb = fmaf(gy, Ct[r], g[j]);
       const float iu = ig * x;
@@ -663,16 +775,20 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
       pc = fmaf(gy, xs[r][j], pc);
       dDs[j] = fmaf(gy, x, dDs[j]);
       g[j] = f * xb;
-      xf[r][j] = fmaf(-f, f, f) * (xb * xprev);  // dfl
-      xi[r][j] = fmaf(-ig, ig, ig) * (dws * x);  // dil
-      xu[r][j] = fmaf(ig, dws, Dv[j] * gy);      // du
+      dfl[j] = fmaf(-f, f, f) * (xb * xprev);
+      dil[j] = fmaf(-ig, ig, ig) * (dws * x);
+      du[j] = fmaf(ig, dws, Dv[j] * gy);
     }
     s_pq[wv][r][lane] = pb;
     s_pq[wv][R + r][lane] = pc;
+    // each row's gradients are stored as soon as they are formed
+    if (FULL || t0 + r < T) {
+      const int64_t ro = (rowbase + r) * D + dbase;
+      if (a.du) st_row_at<TDU, V, M>(sreg((TDU*)a.du + ro), lo, d0, D, du);
+      if (a.dfl) st_row_at<TDG, V, M>(sreg((TDG*)a.dfl + ro), lo, d0, D, dfl);
+      if (a.dil) st_row_at<TDG, V, M>(sreg((TDG*)a.dil + ro), lo, d0, D, dil);
+    }
   }
-  if (a.du) st_rows<TDU, V, R, M, !FULL>((TDU*)a.du, rowbase, t0, T, D, d0, xu);
-  if (a.dfl) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dfl, rowbase, t0, T, D, d0, xf);
-  if (a.dil) st_rows<TDG, V, R, M, !FULL>((TDG*)a.dil, rowbase, t0, T, D, d0, xi);
   if (a.partB || a.partC) {
     // partial sums over this tile's channels, stored [dtile][b*T + t]: the Q
     // lanes 64i/2R .. of entry i (row r of dB, i < R, or of dC) each add
@@ -729,23 +845,23 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   __shared__ __align__(16) float s_pq[W][2 * R][64];
 
   const int tile = (int)(blockIdx.x % (uint32_t)a.n_tiles);
-  // an out-of-range ticket poisons the chunk this workgroup's index names
-  const bool poison = !take_ticket(a, tile, &s_ticket, &s_tag);
-  const int k = poison ? (int)(blockIdx.x / (uint32_t)a.n_tiles)
-                       : a.K - 1 - (int)__builtin_amdgcn_readfirstlane(s_ticket);
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dtile = tile % a.n_dtiles;
+  const int kx = (int)(blockIdx.x / (uint32_t)a.n_tiles);
+  const uint32_t t = take_ticket(a, tile, &s_ticket, &s_tag);
+  // an out-of-range ticket (a workspace that was not zero-filled) poisons
+  // the chunk this workgroup's index names, so no output is left unwritten
+  const bool poison = t >= (uint32_t)a.K;
+  const int k = poison ? kx : a.K - 1 - (int)t;
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   if constexpr (VEC) {
     if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
-      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g,
-                                                           s_lb, s_pq);
+      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb, s_pq);
       return;
     }
   }
-  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb,
-                                                        s_pq);
+  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb, s_pq);
 }
 
 // Sum over q < n_parts of p[q*stride + i], in q order, with the loads of
@@ -2106,19 +2222,19 @@ size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 #define NAJU_F_R 16
 #endif
 #ifndef NAJU_F_W
-#define NAJU_F_W 4
+#define NAJU_F_W 8
 #endif
 #ifndef NAJU_F_P
 #define NAJU_F_P 1
 #endif
 #ifndef NAJU_B_V
-#define NAJU_B_V 1
+#define NAJU_B_V 2
 #endif
 #ifndef NAJU_B_R
-#define NAJU_B_R 16
+#define NAJU_B_R 8
 #endif
 #ifndef NAJU_B_W
-#define NAJU_B_W 4
+#define NAJU_B_W 8
 #endif
 #ifndef NAJU_B_P
 #define NAJU_B_P 1
