@@ -301,11 +301,44 @@ def main():
             print(f"bench: {name} {ex[name]['ms_per_step']} ms/step {ex[name]['GBs']} GB/s", file=sys.stderr,
                   flush=True)
         out["target_ms_c2_n1"] = tgt("c2")
+        ex["stream_reference"] = _stream_reference(dev)
+        print(f"bench: stream reference {ex['stream_reference']}", file=sys.stderr, flush=True)
         ex["c5_lm_step"] = _bench_lm(max(5, min(K, 10)), 3, None, line=False)
         print(f"bench: c5 {ex['c5_lm_step']['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
         out["configs"] = ex
     out["cpu_baseline"] = None if args.no_cpu else _cpu_baseline(args.config, N)
     print(json.dumps(out), flush=True)
+
+
+def _stream_reference(dev):
+    """What plain streaming reaches on this GPU: torch.addcmul over three bf16
+    input streams and one output stream (the forward's streams, contiguous,
+    no scan), at the c2 size (inputs fit the 256 MB last-level cache, so
+    repeated passes partly hit it) and at the c4 size (working set far above
+    it). GB/s of algorithmic traffic, median of 10 timed passes."""
+    import torch
+
+    res = {}
+    for name, (b, t, d) in (("c2_size", (8, 4096, 1024)), ("c4_size", (32, 8192, 4096))):
+        x = [torch.randn(b, t, d, device=dev, dtype=torch.bfloat16) for _ in range(3)]
+        y = torch.empty_like(x[0])
+        nbytes = 4 * x[0].numel() * 2
+        for _ in range(3):
+            torch.addcmul(x[0], x[1], x[2], out=y)
+        ts = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            torch.addcmul(x[0], x[1], x[2], out=y)
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ts.sort()
+        res[name] = round(nbytes / (ts[len(ts) // 2] * 1e-3) / 1e9, 1)
+        del x, y
+        torch.cuda.empty_cache()
+    res["unit"] = "GB/s"
+    return res
 
 
 def _step_bytes_of(config, N):
