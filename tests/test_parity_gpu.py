@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests._helpers import check_all, oracle_all, rand_inputs, run_abi, run_hip
+from tests._helpers import GRAD_KEYS, check_all, oracle_all, rand_inputs, run_abi, run_hip
 
 pytestmark = pytest.mark.gpu
 
@@ -74,6 +74,52 @@ def test_h0(gpu, dtype):
     assert "dh0" in g and g["dh0"].shape == (3, 192, 1)
     ry, rg = oracle_all(ins)
     check_all(y, g, ry, rg)
+
+
+# Odd D: a lane's two channels are not a whole vector, so both directions
+# take the element-wise load / store path (every channel checked against D);
+# with ragged T, h0 and partial channel tiles.
+@pytest.mark.parametrize("shape", [(2, 70, 33), (1, 129, 7), (3, 65, 131)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_n1_odd_channels_elementwise_path(gpu, shape, dtype):
+    b, T, D = shape
+    ins = rand_inputs(b, T, D, 1, seed=T * D, dtype=dtype, h0_std=0.3)
+    if dtype == torch.float32:
+        y, g = run_hip(ins, gpu)
+    else:
+        # bf16 inputs with float32 outputs: the kernels' arithmetic at the
+        # float32 bound. (With bf16 outputs, the storage rounding of the few
+        # dB / dC entries of these small shapes alone comes close to the bf16
+        # norm-wise tolerance.)
+        y, g = run_abi(ins, gpu, out_f32=True)
+    ry, rg = oracle_all(ins)
+    check_all(y, g, ry, rg)
+
+
+# Even D but streams that start one element past an aligned address: the
+# vector path needs every stream aligned to its vector width, so this also
+# runs element-wise (and the outputs, freshly allocated, are aligned).
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_n1_misaligned_streams(gpu, dtype):
+    from naju_amd import naju_scan_hip
+
+    b, T, D = 2, 97, 256
+    ins = rand_inputs(b, T, D, 1, seed=11, dtype=dtype, h0_std=0.2)
+    names = ["u", "f_logit", "i_logit", "B", "C", "D_skip", "h0"]
+    xs = {}
+    for k in names:
+        t = ins[k].to(gpu)
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=gpu)
+        buf[1:].copy_(t.reshape(-1))
+        xs[k] = buf[1:].view(t.shape).detach().requires_grad_(True)
+    # one element past an allocation: not aligned to two elements
+    assert xs["u"].data_ptr() % (2 * xs["u"].element_size()) != 0
+    y = naju_scan_hip(*[xs[k] for k in names[:6]], xs["h0"])
+    y.backward(ins["dy"].to(gpu))
+    torch.cuda.synchronize()
+    grads = {GRAD_KEYS[k]: xs[k].grad for k in names}
+    ry, rg = oracle_all(ins)
+    check_all(y, grads, ry, rg)
 
 
 def test_edge_gates_exact_zero_one(gpu):
