@@ -822,8 +822,13 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       float (*TGT)[TP] = (float (*)[TP])(pl + 1 * 16 * TP);  // G[s][t] at [t][s]
       float (*Tx1)[TP] = (float (*)[TP])(pl + 2 * 16 * TP);  // gathers, then row sums
       float (*Tx2)[TP] = (float (*)[TP])(pl + 3 * 16 * TP);
-      float (*TH)[TP] = (float (*)[TP])(pl + 4 * 16 * TP);   // H[t][p(r)]
-      float (*THT)[TP] = (float (*)[TP])(pl + 5 * 16 * TP);  // H[s][t] at [t][p(s)]
+      // H in the pool's last two tiles, past the dC / dB partials (which take
+      // its first 32 P floats) and the scratch tiles: other waves read it
+      // after the partial-sum barrier
+      constexpr int kPH = McBwdLds<NP, MAP>::POOL - 32 * TP;
+      static_assert(32 * P <= kPH && 7 * 16 * TP <= kPH, "H tiles clear of the partials and scratch tiles");
+      float (*TH)[TP] = (float (*)[TP])(pl + kPH);             // H[t][p(r)]
+      float (*THT)[TP] = (float (*)[TP])(pl + kPH + 16 * TP);  // H[s][t] at [t][p(s)]
       // ---- G[t][s] = C_t . B_s in the layout of an A operand whose MFMA row
       // i is time row arow(i): Gp[r] = G[arow(j)][4r + g] (k-step (q, r')
       // takes n = 16q + 4k + r'); C X and B ghat for the own rows (MFMA row
@@ -1014,11 +1019,11 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
           THT[j][4 * (s & 3) + (s >> 2)] = hv[0];
         }
         // row sums of all 16 rows, and column sums over the channel's lanes
-        // (group g's partials in pool tile 6 + g for g < 3, tile 3 for g = 3)
+        // (group g's partials in pool tile 4 + g for g < 3, tile 3 for g = 3)
 #pragma unroll
         for (int r = 0; r < 4; ++r) Tx1[j][4 * r + g] = rs[r];
         {
-          float* tc = pl + (g < 3 ? 6 + g : 3) * 16 * TP;
+          float* tc = pl + (g < 3 ? 4 + g : 3) * 16 * TP;
 #pragma unroll
           for (int q4 = 0; q4 < Q; q4 += 4) wr4(tc + j * TP + q4, cp[q4], cp[q4 + 1], cp[q4 + 2], cp[q4 + 3]);
         }
@@ -1030,9 +1035,9 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
           for (int r = 3; r >= 0; --r) {
             float r4[4], c0[4], c1[4], c2[4], c3[4], cs[4];
             rd4(&Tx1[j][4 * r], r4);
-            rd4(pl + 6 * 16 * TP + j * TP + 4 * r, c0);
-            rd4(pl + 7 * 16 * TP + j * TP + 4 * r, c1);
-            rd4(pl + 8 * 16 * TP + j * TP + 4 * r, c2);
+            rd4(pl + 4 * 16 * TP + j * TP + 4 * r, c0);
+            rd4(pl + 5 * 16 * TP + j * TP + 4 * r, c1);
+            rd4(pl + 6 * 16 * TP + j * TP + 4 * r, c2);
             rd4(pl + 3 * 16 * TP + j * TP + 4 * r, c3);
 #pragma unroll
             for (int e = 0; e < 4; ++e) cs[e] = (c0[e] + c1[e]) + (c2[e] + c3[e]);
@@ -1086,16 +1091,15 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       // and ghat (entering this sub-block) per channel and entry come through
       // this wave's pool as [16 channels][P] tiles, written in the D layout
       // and read transposed.
-      float (*TQ1)[TP] = (float (*)[TP])(pl + 6 * 16 * TP);  // (dy Pf)[t][d]
-      float (*TQ2)[TP] = (float (*)[TP])(pl + 7 * 16 * TP);  // (w Pe)[t][d]
+      // (tiles 0 and 1: the decay phase is done with them)
+      float (*TQ1)[TP] = (float (*)[TP])(pl + 0 * 16 * TP);  // (dy Pf)[t][d]
+      float (*TQ2)[TP] = (float (*)[TP])(pl + 1 * 16 * TP);  // (w Pe)[t][d]
 #pragma unroll
       for (int r = 0; r < 4; ++r) TQ1[4 * r + g][j] = q1[r], TQ2[4 * r + g][j] = q2[r];
       asm volatile("" ::: "memory");
-      float qv1[4], qv2[4], hq[4], htq[4];
+      float qv1[4], qv2[4];
       rd4(&TQ1[j][4 * g], qv1);
       rd4(&TQ2[j][4 * g], qv2);
-      rd4(&TH[j][4 * g], hq);
-      rd4(&THT[j][4 * g], htq);
       asm volatile("" ::: "memory");
       float* TX = pl;           // X [channel][n]
       float* TGh = pl + 16 * P;  // ghat [channel][n]
@@ -1109,22 +1113,17 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         }
       }
       asm volatile("" ::: "memory");
+      // the wave's channel part: X^T (dy Pf) and ghat^T (w Pe) over its 16
+      // channels (the H part, B^T H and C^T H^T, is formed once per
+      // workgroup from the waves' summed H after the partial-sum barrier)
       f4_t dCt[MT], dBt[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        float bt4[4], ct4[4];
-        rd4(&sh.Bt[16 * m + j][4 * g], bt4);
-        rd4(&sh.Ct[16 * m + j][4 * g], ct4);
         f4_t accC = {0.f, 0.f, 0.f, 0.f}, accB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           accC = mma(TX[(4 * g + e) * P + 16 * m + j], qv1[e], accC);
           accB = mma(TGh[(4 * g + e) * P + 16 * m + j], qv2[e], accB);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          accC = mma(bt4[e], hq[e], accC);
-          accB = mma(ct4[e], htq[e], accB);
         }
         dCt[m] = accC;
         dBt[m] = accB;
@@ -1148,39 +1147,43 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         wr4(pl + (1 * 16 + j) * P + 16 * m + 4 * g, dBt[m][0], dBt[m][1], dBt[m][2], dBt[m][3]);
       }
       __syncthreads();
-      {
-        // thread tid sums four consecutive entries n .. n+3 of row t of dC
-        // (qd = 0) or dB (qd = 1) over the waves, in wave order
-        constexpr int NQ = NP / 4;
-        constexpr int NE4 = 2 * 16 * NQ;
-        constexpr int NTH = 64 * kMcWB;
-        const int64_t btn = (int64_t)a.batch * T * N;
-        const int64_t pb = (int64_t)dtile * btn + ((int64_t)b * T + t0) * N;  // uniform
+      static_assert(2 * MT <= kMcWB, "one output tile per wave");
+      if (wv < 2 * MT) {
+        // wave w forms output tile w: dC (qd = 0) or dB (qd = 1) for entries
+        // n = 16m .. 16m+15 and the sub-block's 16 rows, in the MFMA output
+        // layout (lane (j, g) holds n = 16m + 4g + r of row t = j): the
+        // waves' channel parts summed in wave order, plus B^T (sum H) or
+        // C^T (sum H)^T with H summed over the waves in wave order
+        const int qd = wv / MT, m = wv - qd * MT;
+        float hs[4] = {0.f, 0.f, 0.f, 0.f}, acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < (NE4 + NTH - 1) / NTH; ++k) {
-          const int e4 = tid + NTH * k;
-          const int qd = e4 / (16 * NQ), t = (e4 / NQ) % 16, n = 4 * (e4 % NQ);
-          if ((NE4 % NTH == 0 || e4 < NE4) && t0 + t < T && n < N) {
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kMcWB; ++w) {
+          const float* pw = sh.pool[w];
+          float h4[4], v4[4];
+          rd4(pw + kPH + qd * 16 * TP + j * TP + 4 * g, h4);
+          rd4(pw + (qd * 16 + j) * P + 16 * m + 4 * g, v4);
 #pragma unroll
-            for (int w = 0; w < kMcWB; ++w) {
-              float v4[4];
-              rd4(&sh.pool[w][(qd * 16 + t) * P + n], v4);
+          for (int e = 0; e < 4; ++e) hs[e] += h4[e], acc[e] += v4[e];
+        }
+        float a4[4];
+        rd4(qd == 0 ? &sh.Bt[16 * m + j][4 * g] : &sh.Ct[16 * m + j][4 * g], a4);
+        f4_t hp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int e = 0; e < 4; ++e) acc[e] += v4[e];
-            }
-            float* dst = qd == 0 ? a.partC : a.partB;
-            if (dst) {
-              float* q = dst + pb;
-              const uint32_t o = (uint32_t)(t * N + n);
-              if ((N & 3) == 0) {
-                *(float4*)(q + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-              } else {
+        for (int e = 0; e < 4; ++e) hp = mma(a4[e], hs[e], hp);
+        float* dst = qd == 0 ? a.partC : a.partB;
+        const int n = 16 * m + 4 * g;
+        if (dst && t0 + j < T && n < N) {
+          const int64_t btn = (int64_t)a.batch * T * N;
+          float* q = dst + (int64_t)dtile * btn + ((int64_t)b * T + t0) * N;  // uniform
+          const uint32_t o = (uint32_t)(j * N + n);
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  if (n + e < N) q[o + e] = acc[e];
-              }
-            }
+          for (int r = 0; r < 4; ++r) acc[r] += hp[r];
+          if ((N & 3) == 0) {
+            *(float4*)(q + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < N) q[o + r] = acc[r];
           }
         }
       }
@@ -1196,12 +1199,9 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
       }
     }
-    // MAP: every wave is done with the staged C before it is restaged. The
-    // scan needs no barrier here: every read of the staged B / C happens
-    // before the partial-sum barrier above, and a wave writes its pool again
-    // only after the next staging barrier, which every wave reaches after
-    // its share of the partial sums.
-    if constexpr (MAP) __syncthreads();
+    // every wave is done with the staged B / C (and, in the scan, with the
+    // pools and H tiles its output tile reads) before they are restaged
+    __syncthreads();
     cur = nxt;
     if constexpr (!MAP) {
 #pragma unroll
