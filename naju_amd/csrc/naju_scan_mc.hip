@@ -42,6 +42,47 @@ __device__ __forceinline__ f4_t mma(float a, float b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Four values that are exact in the 2-byte stream type TT (B and C as
+// staged: converted from TT, zero rows included) packed as TT pairs.
+template <typename TT>
+__device__ __forceinline__ void pack4(const float (&x)[4], uint32_t (&w)[2]) {
+  if constexpr (__is_same(TT, bf16_t)) {
+    // the upper halves of the float bits (exact: the low halves are zero)
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      w[k] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, x[2 * k + 1]), __builtin_bit_cast(uint32_t, x[2 * k]),
+                                   0x07060302u);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 h = {(_Float16)x[2 * k], (_Float16)x[2 * k + 1]};
+      w[k] = __builtin_bit_cast(uint32_t, h);
+    }
+  }
+}
+
+// D += A B with K = 32 on the 16-bit matrix-core path, for operands exact in
+// TT (bf16 or f16): lane l supplies A[l%16][k] and B[k][l%16] for its eight
+// k of the product, a0 and b0 (then a1 and b1) packed by pack4 from the same
+// four k each, so that any assignment of the lane's values to k pairs A and
+// B alike. The products are exact in float32 and only the accumulation
+// rounds, as on the float32 path, at one instruction in place of eight.
+template <typename TT>
+__device__ __forceinline__ f4_t mma_k32(const uint32_t (&a0)[2], const uint32_t (&a1)[2], const uint32_t (&b0)[2],
+                                        const uint32_t (&b1)[2], f4_t c) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 av = {a0[0], a0[1], a1[0], a1[1]}, bv = {b0[0], b0[1], b1[0], b1[1]};
+  if constexpr (__is_same(TT, bf16_t)) {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, av), __builtin_bit_cast(v8, bv), c, 0, 0,
+                                                   0);
+  } else {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, av), __builtin_bit_cast(v8, bv), c, 0, 0, 0);
+  }
+}
+
 constexpr int Q = kMcQ;    // rows per sub-block
 constexpr int TP = Q + 4;  // pitch of the per-wave [channel][row] tiles
 
@@ -196,6 +237,20 @@ struct McIn {
     }
   }
 
+  // Waits for these loads here. Used on the first sub-block's inputs before
+  // the loop: the compiler's wait counting would otherwise still see them
+  // pending at their uses inside the loop, and since every other iteration
+  // has the next sub-block's loads issued after them, it would wait there
+  // for those too, leaving nothing in flight while the sub-block is worked.
+  __device__ __forceinline__ void settle() {
+#pragma unroll
+    for (int k = 0; k < Raw4<TG>::NW; ++k) asm volatile("" : "+v"(f.w[k]), "+v"(i.w[k]));
+#pragma unroll
+    for (int k = 0; k < Raw4<TU>::NW; ++k) asm volatile("" : "+v"(u.w[k]));
+#pragma unroll
+    for (int k = 0; k < Raw4<TB>::NW; ++k) asm volatile("" : "+v"(b.w[k]), "+v"(c.w[k]));
+  }
+
   // B (and C) into LDS buffer buf; zeros past T and past N
   __device__ __forceinline__ void stage(McBC<NP, MAP>& sh, int buf, const ScanArgs& a, int64_t t0, int tid) const {
     if (tid < 4 * NP) {
@@ -266,6 +321,9 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
         const int n = 16 * m + 4 * g + r;
         X[m][r] = (xin && dok && n < N) ? xin[d * N + n] : 0.f;
       }
+    // loaded before the loop, waited for here (as McIn::settle)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(X[m]));
     // the state entering the segment, kept for the backward's recompute
     if (!MAP && a.segst && seg > 0 && dok) {
       float* st = a.segst + (((int64_t)b * a.nseg + seg) * D + d) * N;
@@ -283,12 +341,14 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
   float Dvc[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) Dvc[e] = (!MAP && dw + cq + e < D) ? a.Dsk[dw + cq + e] : 0.f;
+  asm volatile("" : "+v"(Dvc[0]), "+v"(Dvc[1]), "+v"(Dvc[2]), "+v"(Dvc[3]));
 
   // inputs of sub-blocks sb (cur) and sb + 1 (nxt), loaded one sub-block
   // ahead of their use
   In cur, nxt;
   if (sb0 < sb1) {
     cur.load(a, b, (int64_t)sb0 * Q, dw, rho, cq, tid, vec);
+    cur.settle();
     cur.stage(sh, 0, a, (int64_t)sb0 * Q, tid);
   }
   for (int sb = sb0; sb < sb1; ++sb) {
@@ -323,7 +383,21 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
     // (the product B_(arow) C_(arow)^T transposed; k-step (q, r') takes
     // n = 16q + 4k + r')
     f4_t Gp = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (!MAP) {
+    if constexpr (!MAP && sizeof(TB) == 2 && NP >= 32) {
+      // B and C exact in TB: two 16-entry groups of n per K = 32 product
+#pragma unroll
+      for (int q = 0; q < NP / 16; q += 2) {
+        uint32_t pb[2][2], pc[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4 c4 = *(const float4*)&sh.C[buf][arow][16 * (q + h) + 4 * g];
+          const float4 b4 = *(const float4*)&sh.Bn[buf][arow][16 * (q + h) + 4 * g];
+          pack4<TB>({b4.x, b4.y, b4.z, b4.w}, pb[h]);
+          pack4<TB>({c4.x, c4.y, c4.z, c4.w}, pc[h]);
+        }
+        Gp = mma_k32<TB>(pb[0], pb[1], pc[0], pc[1], Gp);
+      }
+    } else if constexpr (!MAP) {
 #pragma unroll
       for (int q = 0; q < NP / 16; ++q) {
         const float4 c4 = *(const float4*)&sh.C[buf][arow][16 * q + 4 * g];
@@ -410,6 +484,13 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
         cx = mma(c4.y, X[m][1], cx);
         cx = mma(c4.z, X[m][2], cx);
         cx = mma(c4.w, X[m][3], cx);
+      }
+      // B / C of sb + 1 into the other buffer (free since the barrier
+      // above), before this sub-block's stores are issued: waiting for the
+      // next sub-block's loads after them would wait for the stores as well
+      if (sb + 1 < sb1) {
+        nxt.settle();
+        nxt.stage(sh, buf ^ 1, a, t0 + Q, tid);
       }
       // the state entering this sub-block is the backward's checkpoint
       if (a.ckpt && dok && sb % ck_sb == 0) {
@@ -501,9 +582,9 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
       X[m] = mma(bt.z, wp[2], X[m]);
       X[m] = mma(bt.w, wp[3], X[m]);
     }
-    // B / C of sb + 1 into the other buffer (free since the barrier above),
-    // as late as possible so that their loads have the whole sub-block to land
-    if (sb + 1 < sb1) nxt.stage(sh, buf ^ 1, a, t0 + Q, tid);
+    // the map's B of sb + 1 into the other buffer, as late as possible so
+    // that its loads have the whole sub-block to land
+    if (MAP && sb + 1 < sb1) nxt.stage(sh, buf ^ 1, a, t0 + Q, tid);
     cur = nxt;
   }
   if (!dok) return;
@@ -625,6 +706,16 @@ struct McInB {
     }
   }
 
+  // waits for these loads here (as McIn::settle)
+  __device__ __forceinline__ void settle() {
+#pragma unroll
+    for (int k = 0; k < Raw4<TG>::NW; ++k) asm volatile("" : "+v"(f.w[k]), "+v"(i.w[k]));
+#pragma unroll
+    for (int k = 0; k < Raw4<TU>::NW; ++k) asm volatile("" : "+v"(dy.w[k]), "+v"(u.w[k]));
+#pragma unroll
+    for (int k = 0; k < Raw4<TB>::NW; ++k) asm volatile("" : "+v"(b.w[k]), "+v"(c.w[k]));
+  }
+
   __device__ __forceinline__ void stage(McBwdLds<NP, MAP>& sh, const ScanArgs& a, int64_t t0, int tid) const {
     if (tid < 4 * NP) {
       const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
@@ -728,7 +819,8 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
   const bool vec = dw + 16 <= D && D % 4 == 0;
   const int rho = lane >> 2, cq = (lane & 3) * 4;
   const int ncq = (int)(D - dw - cq < 4 ? (D - dw - cq < 0 ? 0 : D - dw - cq) : 4);  // valid of cq .. cq+3
-  const float Dv = (!MAP && dok) ? a.Dsk[d] : 0.f;
+  float Dv = (!MAP && dok) ? a.Dsk[d] : 0.f;
+  asm volatile("" : "+v"(Dv));
 
   // adjoint carry in the D layout: gh[m][r] = entry 16m + 4g + r of channel j
   f4_t gh[MT];
@@ -741,6 +833,9 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         const int n = 16 * m + 4 * g + r;
         gh[m][r] = (gin && dok && n < N) ? gin[d * N + n] : 0.f;
       }
+    // loaded before the loop, waited for here (as McIn::settle)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(gh[m]));
   }
   float Fseg = 1.f;
   float dDacc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -757,7 +852,12 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
   f4_t xc[MAP ? 1 : MT], xn[MAP ? 1 : MT];
   if (sb0 < sb1) {
     cur.load(a, b, (int64_t)(sb1 - 1) * Q, dw, rho, cq, tid, vec);
-    if constexpr (!MAP) load_ckpt<MT>(xc, a, b, sb1 - 1, dok ? d : D - 1, g);
+    cur.settle();
+    if constexpr (!MAP) {
+      load_ckpt<MT>(xc, a, b, sb1 - 1, dok ? d : D - 1, g);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(xc[m]));
+    }
   }
   for (int sb = sb1 - 1; sb >= sb0; --sb) {
     // The lane's indices, recomputed every sub-block from an opaque copy of
@@ -835,15 +935,30 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
       // 4g + r = time row 4r + g) and ghat . X per channel from the same reads
       f4_t Gp = {0.f, 0.f, 0.f, 0.f}, cx = {0.f, 0.f, 0.f, 0.f}, bg = {0.f, 0.f, 0.f, 0.f};
       float gX = 0.f;
+      // (B and C exact in TB: G on the 16-bit path, two groups of n per
+      // product, the even group's values packed until the odd one's)
+      constexpr bool g16 = sizeof(TB) == 2 && NP >= 32;
+      uint32_t pb[2], pc[2];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         float c4[4], b4[4];
         rd4(&sh.C[arow][16 * m + 4 * g], c4);
         rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
+        if constexpr (g16) {
+          if (m & 1) {
+            uint32_t qb[2], qc[2];
+            pack4<TB>(b4, qb);
+            pack4<TB>(c4, qc);
+            Gp = mma_k32<TB>(pb, qb, pc, qc, Gp);
+          } else {
+            pack4<TB>(b4, pb);
+            pack4<TB>(c4, pc);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float xv = ckpt_val(xc[m], e, 16 * m + 4 * g, N, dok);
-          Gp = mma(b4[e], c4[e], Gp);
+          if constexpr (!g16) Gp = mma(b4[e], c4[e], Gp);
           cx = mma(c4[e], xv, cx);
           bg = mma(b4[e], gh[m][e], bg);
           gX = fmaf(gh[m][e], xv, gX);
@@ -1067,6 +1182,14 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         Tw[j][4 * r + g] = dil;
       }
       asm volatile("" ::: "memory");
+      // the next sub-block's loads are waited for here, before this
+      // sub-block's stores are issued: waiting for them after the stores
+      // (at the end of the sub-block) would wait for the stores as well
+      if (sb - 1 >= sb0) {
+        nxt.settle();
+#pragma unroll
+        for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(xn[m]));
+      }
       if (rok && ncq > 0) {
         const int64_t ob = ((int64_t)b * T + t0) * D;  // uniform
         const uint32_t o = (uint32_t)(rho * D + dw + cq);
