@@ -83,6 +83,49 @@ __device__ __forceinline__ f4_t mma_k32(const uint32_t (&a0)[2], const uint32_t 
   }
 }
 
+// x[k] = hi + mid + lo exactly, in three bf16 parts packed in pairs like
+// pack4: hi keeps the top 8 significant bits of x (truncated), mid the next
+// 8 of the remainder and lo the at most 8 left, so each part is exact in
+// bf16 and each difference exact in float32. (x = +-inf or nan gives nan
+// parts; the states and adjoints split here are finite for finite inputs.)
+__device__ __forceinline__ void split4_bf16(const float (&x)[4], uint32_t (&h)[2], uint32_t (&md)[2],
+                                            uint32_t (&lo)[2]) {
+  uint32_t hb[4], mb[4], lb[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    // x as rounded: the subtraction below must not be fused with the
+    // product that formed x (the parts would then sum to the unrounded
+    // product, differently wherever the compiler chose to fuse)
+    float xk = x[k];
+    asm volatile("" : "+v"(xk));
+    hb[k] = __builtin_bit_cast(uint32_t, xk) & 0xffff0000u;
+    const float r = xk - __builtin_bit_cast(float, hb[k]);
+    mb[k] = __builtin_bit_cast(uint32_t, r) & 0xffff0000u;
+    lb[k] = __builtin_bit_cast(uint32_t, r - __builtin_bit_cast(float, mb[k]));
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    h[k] = __builtin_amdgcn_perm(hb[2 * k + 1], hb[2 * k], 0x07060302u);
+    md[k] = __builtin_amdgcn_perm(mb[2 * k + 1], mb[2 * k], 0x07060302u);
+    lo[k] = __builtin_amdgcn_perm(lb[2 * k + 1], lb[2 * k], 0x07060302u);
+  }
+}
+
+// D += A B over the lane's four k (the k-steps of four 16x16x4 float32
+// products) with A exact in bf16 (a: packed by pack4) and B float32 given by
+// its split4_bf16 parts: hi and mid in one K = 32 product, lo (with zeros)
+// in a second. Each product is exact; the result matches the float32 path
+// up to the accumulation's rounding, at two instructions in place of four.
+// (The K = 16 form, v_mfma_f32_16x16x16_bf16, took the lo part at first and
+// gave run-to-run different results in this position on gfx950 with the
+// compiler's default scheduling; the K = 32 form is used throughout.)
+__device__ __forceinline__ f4_t mma_x3(const uint32_t (&a)[2], const uint32_t (&h)[2], const uint32_t (&md)[2],
+                                       const uint32_t (&lo)[2], f4_t c) {
+  c = mma_k32<bf16_t>(a, a, h, md, c);
+  const uint32_t z[2] = {0u, 0u};
+  return mma_k32<bf16_t>(a, z, lo, z, c);
+}
+
 constexpr int Q = kMcQ;    // rows per sub-block
 constexpr int TP = Q + 4;  // pitch of the per-wave [channel][row] tiles
 
@@ -573,14 +616,28 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
     float wp[4];
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) wp[s2] = pe[s2] * w_o[s2];
+    if constexpr (__is_same(TB, bf16_t)) {
+      // B exact in bf16: Pe w split in three bf16 parts (the 16-bit path)
+      uint32_t wh[2], wm[2], wl[2];
+      split4_bf16(wp, wh, wm, wl);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      X[m] *= Pall;
-      const float4 bt = *(const float4*)&sh.Bt[buf][16 * m + j][4 * g];
-      X[m] = mma(bt.x, wp[0], X[m]);
-      X[m] = mma(bt.y, wp[1], X[m]);
-      X[m] = mma(bt.z, wp[2], X[m]);
-      X[m] = mma(bt.w, wp[3], X[m]);
+      for (int m = 0; m < MT; ++m) {
+        X[m] *= Pall;
+        const float4 bt = *(const float4*)&sh.Bt[buf][16 * m + j][4 * g];
+        uint32_t ab[2];
+        pack4<TB>({bt.x, bt.y, bt.z, bt.w}, ab);
+        X[m] = mma_x3(ab, wh, wm, wl, X[m]);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        X[m] *= Pall;
+        const float4 bt = *(const float4*)&sh.Bt[buf][16 * m + j][4 * g];
+        X[m] = mma(bt.x, wp[0], X[m]);
+        X[m] = mma(bt.y, wp[1], X[m]);
+        X[m] = mma(bt.z, wp[2], X[m]);
+        X[m] = mma(bt.w, wp[3], X[m]);
+      }
     }
     // the map's B of sb + 1 into the other buffer, as late as possible so
     // that its loads have the whole sub-block to land
@@ -742,6 +799,36 @@ __device__ __forceinline__ void rd4(const float* p, float (&o)[4]) {
   const float4 v = *(const float4*)p;
   o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
 }
+
+// The adjoint carry's update ghat <- Pall ghat + C^T (Pf dy) for the lane's
+// entries (k-step e takes rows 4e + g; on the 16-bit path when C is bf16).
+template <typename TB, int MT>
+__device__ __forceinline__ void carry_update(f4_t (&gh)[MT], const float (*Ct)[TP], float Pall, const float (&pfdy)[4],
+                                             int j, int g) {
+  if constexpr (__is_same(TB, bf16_t)) {
+    uint32_t qh[2], qm[2], ql[2];
+    split4_bf16(pfdy, qh, qm, ql);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float ct4[4];
+      rd4(&Ct[16 * m + j][4 * g], ct4);
+      uint32_t ac[2];
+      pack4<TB>(ct4, ac);
+      gh[m] *= Pall;
+      gh[m] = mma_x3(ac, qh, qm, ql, gh[m]);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float ct4[4];
+      rd4(&Ct[16 * m + j][4 * g], ct4);
+      gh[m] *= Pall;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
+    }
+  }
+}
+
 __device__ __forceinline__ void wr4(float* p, float a0, float a1, float a2, float a3) {
   *(float4*)p = make_float4(a0, a1, a2, a3);
 }
@@ -1252,14 +1339,7 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         dBt[m] = accB;
       }
       // ---- carry update: ghat <- Pall ghat + C^T (Pf dy)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        float ct4[4];
-        rd4(&sh.Ct[16 * m + j][4 * g], ct4);
-        gh[m] *= Pall;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
-      }
+      carry_update<TB, MT>(gh, sh.Ct, Pall, pfdy, j, g);
       // ---- the wave's dC / dB [t][n] into its pool (its reads of the pool
       // are done; other waves read it after the barrier), then the workgroup
       // adds the waves' in wave order
@@ -1291,8 +1371,15 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         float a4[4];
         rd4(qd == 0 ? &sh.Bt[16 * m + j][4 * g] : &sh.Ct[16 * m + j][4 * g], a4);
         f4_t hp = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (__is_same(TB, bf16_t)) {
+          uint32_t ab[2], hh[2], hm[2], hl[2];
+          pack4<TB>(a4, ab);
+          split4_bf16(hs, hh, hm, hl);
+          hp = mma_x3(ab, hh, hm, hl, hp);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hp = mma(a4[e], hs[e], hp);
+          for (int e = 0; e < 4; ++e) hp = mma(a4[e], hs[e], hp);
+        }
         float* dst = qd == 0 ? a.partC : a.partB;
         const int n = 16 * m + 4 * g;
         if (dst && t0 + j < T && n < N) {
@@ -1313,14 +1400,7 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
     } else {
       // MAP: the adjoint map of the segment (ghat from zero, decay product)
       Fseg *= Pall;
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        float ct4[4];
-        rd4(&sh.Ct[16 * m + j][4 * g], ct4);
-        gh[m] *= Pall;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) gh[m] = mma(ct4[e], pfdy[e], gh[m]);
-      }
+      carry_update<TB, MT>(gh, sh.Ct, Pall, pfdy, j, g);
     }
     // every wave is done with the staged B / C (and, in the scan, with the
     // pools and H tiles its output tile reads) before they are restaged
