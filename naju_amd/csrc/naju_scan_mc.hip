@@ -1031,12 +1031,36 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         float c4[4], b4[4];
         rd4(&sh.C[arow][16 * m + 4 * g], c4);
         rd4(&sh.Bn[arow][16 * m + 4 * g], b4);
+        constexpr bool bx = g16 && __is_same(TB, bf16_t);
         if constexpr (g16) {
           if (m & 1) {
             uint32_t qb[2], qc[2];
             pack4<TB>(b4, qb);
             pack4<TB>(c4, qc);
             Gp = mma_k32<TB>(pb, qb, pc, qc, Gp);
+            if constexpr (bx) {
+              // C X and B ghat over the pair of entry groups m - 1, m: X and
+              // ghat split in three bf16 parts, three K = 32 products each
+              float xe[4], xo[4], ge4[4], go4[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                xe[e] = ckpt_val(xc[m - 1], e, 16 * (m - 1) + 4 * g, N, dok);
+                xo[e] = ckpt_val(xc[m], e, 16 * m + 4 * g, N, dok);
+                ge4[e] = gh[m - 1][e];
+                go4[e] = gh[m][e];
+              }
+              uint32_t h0[2], m0[2], l0[2], h1[2], m1[2], l1[2];
+              split4_bf16(xe, h0, m0, l0);
+              split4_bf16(xo, h1, m1, l1);
+              cx = mma_k32<TB>(pc, qc, h0, h1, cx);
+              cx = mma_k32<TB>(pc, qc, m0, m1, cx);
+              cx = mma_k32<TB>(pc, qc, l0, l1, cx);
+              split4_bf16(ge4, h0, m0, l0);
+              split4_bf16(go4, h1, m1, l1);
+              bg = mma_k32<TB>(pb, qb, h0, h1, bg);
+              bg = mma_k32<TB>(pb, qb, m0, m1, bg);
+              bg = mma_k32<TB>(pb, qb, l0, l1, bg);
+            }
           } else {
             pack4<TB>(b4, pb);
             pack4<TB>(c4, pc);
@@ -1046,8 +1070,10 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         for (int e = 0; e < 4; ++e) {
           const float xv = ckpt_val(xc[m], e, 16 * m + 4 * g, N, dok);
           if constexpr (!g16) Gp = mma(b4[e], c4[e], Gp);
-          cx = mma(c4[e], xv, cx);
-          bg = mma(b4[e], gh[m][e], bg);
+          if constexpr (!bx) {
+            cx = mma(c4[e], xv, cx);
+            bg = mma(b4[e], gh[m][e], bg);
+          }
           gX = fmaf(gh[m][e], xv, gX);
         }
       }
@@ -1086,21 +1112,44 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         }
         asm volatile("" ::: "memory");
         f4_t D1 = {0.f, 0.f, 0.f, 0.f}, D2 = D1, D3 = D1, R1 = D1, DH = D1, D4 = D1;
+        // the 0 / 1 masks are exact in bf16: the masked sums take the 16-bit
+        // path with the float32 operand split (mask_pk: four masks packed)
+        const auto mask_pk = [](bool m0, bool m1, bool m2, bool m3, uint32_t (&w)[2]) {
+          w[0] = (m0 ? 0x3f80u : 0u) | (m1 ? 0x3f800000u : 0u);
+          w[1] = (m2 ? 0x3f80u : 0u) | (m3 ? 0x3f800000u : 0u);
+        };
+        float v2[4], v3[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int s = 4 * e + g;
           const bool ge = s >= arow, le = s <= arow;
           D1 = mma(ge ? TGs[s][arow] : 0.f, ra[e], D1);
-          D2 = mma(ge ? 1.f : 0.f, ra[e] * cx[e], D2);
-          D3 = mma(le ? 1.f : 0.f, rb[e] * bg[e], D3);
+          v2[e] = ra[e] * cx[e];
+          v3[e] = rb[e] * bg[e];
           R1 = mma(le ? Gp[e] : 0.f, rb[e], R1);
           DH = mma(Ta[s][j], Tb[s][j], DH);
         }
+        uint32_t mge[2], mle[2], mgt[2];
+        mask_pk(g >= arow, 4 + g >= arow, 8 + g >= arow, 12 + g >= arow, mge);
+        mask_pk(g <= arow, 4 + g <= arow, 8 + g <= arow, 12 + g <= arow, mle);
+        mask_pk(g > arow, 4 + g > arow, 8 + g > arow, 12 + g > arow, mgt);
+        {
+          uint32_t h[2], md[2], lo[2];
+          split4_bf16(v2, h, md, lo);
+          D2 = mma_x3(mge, h, md, lo, D2);
+          split4_bf16(v3, h, md, lo);
+          D3 = mma_x3(mle, h, md, lo, D3);
+        }
+        {
+          float v4[4], v5[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int s = 4 * e + g;
-          D4 = mma(s >= arow ? 1.f : 0.f, ra[e] * R1[e], D4);
-          D4 = mma(s > arow ? 1.f : 0.f, -(rb[e] * D1[e]), D4);
+          for (int e = 0; e < 4; ++e) v4[e] = ra[e] * R1[e], v5[e] = -(rb[e] * D1[e]);
+          uint32_t h4[2], m4[2], l4[2], h5[2], m5[2], l5[2];
+          split4_bf16(v4, h4, m4, l4);
+          split4_bf16(v5, h5, m5, l5);
+          D4 = mma_k32<bf16_t>(mge, mgt, h4, h5, D4);
+          D4 = mma_k32<bf16_t>(mge, mgt, m4, m5, D4);
+          D4 = mma_k32<bf16_t>(mge, mgt, l4, l5, D4);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
