@@ -2262,19 +2262,39 @@ struct Layout {
 #define NAJU_GN_TARGET_WGS 1536  // two rounds of three 4-wave workgroups per CU
 #endif
 constexpr int kGnTargetWgs = NAJU_GN_TARGET_WGS;
-// The chunked matrix-core kernels' segment targets (workgroups per launch):
-// the forward runs four 4-wave workgroups per CU, the backward one 8-wave
-// workgroup per CU, whose per-segment start-up (the carry, the first loads)
-// favours longer segments.
-#ifndef NAJU_MC_FWD_TARGET
-#define NAJU_MC_FWD_TARGET 1024
+// The chunked matrix-core kernels' time segments: the forward holds up to
+// four 4-wave workgroups per CU and wants at least three (for latency
+// hiding); the backward holds one 8-wave workgroup per CU and wants two per
+// CU over the launch (measured at the C2 shape: 4, 8 and 12 segments took
+// 696, 689 and 709 us), so that one workgroup's start-up overlaps another's
+// tail.
+#ifndef NAJU_MC_FWD_MIN_PER_CU
+#define NAJU_MC_FWD_MIN_PER_CU 3
 #endif
-#ifndef NAJU_MC_BWD_TARGET
-#define NAJU_MC_BWD_TARGET 768
+#ifndef NAJU_MC_BWD_MIN_PER_CU
+#define NAJU_MC_BWD_MIN_PER_CU 2
 #endif
-constexpr int kMcFwdTarget = NAJU_MC_FWD_TARGET;
-constexpr int kMcBwdTarget = NAJU_MC_BWD_TARGET;
+constexpr int kCUs = 256;  // MI355X
 constexpr int kGcTargetWaves = 2048;
+
+// Segment count of a chunked matrix-core launch over n_tiles channel tiles
+// and K sub-blocks: the one whose busiest CU walks the fewest sub-blocks,
+// ceil(n_tiles s / CUs) ceil(K / s), among those that give every CU at
+// least min_per_cu workgroups; the fewest segments on a tie, since each one
+// past the first costs the segment-map pass over its rows and a start-up.
+int mc_nseg(int64_t n_tiles, int K, bool bwd) {
+  const int64_t min_wg = (int64_t)kCUs * (bwd ? NAJU_MC_BWD_MIN_PER_CU : NAJU_MC_FWD_MIN_PER_CU);
+  int best = K;
+  int64_t best_cost = -1;
+  for (int s = 1; s <= K; ++s) {
+    const int64_t wg = n_tiles * s;
+    if (wg < min_wg && s < K) continue;
+    const int64_t cost = (wg + kCUs - 1) / kCUs * ((K + s - 1) / s);
+    if (best_cost < 0 || cost < best_cost) best_cost = cost, best = s;
+    if (wg >= 8 * min_wg) break;
+  }
+  return best;
+}
 // gq_fwd_kernel serves a forward whose batch x channel-group grid holds at
 // least three 4-wave workgroups per CU (256 CUs); smaller grids take the
 // segmented gc_fwd_kernel, whose time segments supply the parallelism.
@@ -2381,9 +2401,8 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
     // workgroups): about kGnTargetWgs workgroups
     const int64_t per_seg = (mc || bwd) ? l.n_tiles : batch * ((D + 63) / 64);
     // (the 8-wave NP = 128 backward runs one workgroup per CU: 1024)
-    const int64_t target = mc ? (bwd ? kMcBwdTarget : kMcFwdTarget)
-                              : bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
-    int64_t want = (target + per_seg - 1) / per_seg;
+    const int64_t target = bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
+    int64_t want = mc ? mc_nseg(l.n_tiles, l.K, bwd) : (target + per_seg - 1) / per_seg;
     if (want > l.K) want = l.K;
     if (want < 1) want = 1;
     l.seg_sc = (int)((l.K + want - 1) / want);
