@@ -380,6 +380,9 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
   float Fseg = 1.f;
   // load role: row rho, channels cq .. cq+3 of the wave's 16
   const int rho = lane >> 2, cq = (lane & 3) * 4;
+  // channels of the load role inside [0, D) (0..4), formed once: past D a
+  // channel is the neutral step
+  const int ncq0 = (int)(D - dw - cq < 4 ? (D - dw - cq < 0 ? 0 : D - dw - cq) : 4);
   // D of the load role's channels (the D u term of y is added there)
   float Dvc[4];
 #pragma unroll
@@ -411,13 +414,18 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
     if (sb + 1 < sb1) nxt.load(a, b, t0 + Q, dw, rho, cq, tid, vec);
     // gates in the load layout, each element computed once; rows past T
     // and channels past D are the neutral step f = 1, w = u = 0
-    const bool rok = t0 + rho < T;
+    // (32-bit tests: rows left in the sub-block, uniform, and ncq0)
+    const int rl = (int)(T - t0 < Q ? T - t0 : Q);
+    const bool rok = rho < rl;
     float uu[4];  // u of the load role (0 past T / D), for the D u term
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const bool ok = rok && dw + cq + e < D;
-      s_t[wv][0][cq + e][rho] = ok ? sigm(cur.f.get(e)) : 1.f;
-      s_t[wv][1][cq + e][rho] = ok ? sigm(cur.i.get(e)) * cur.u.get(e) : 0.f;
+      const bool ok = rok && e < ncq0;
+      // both gates formed on every lane, then selected (no branch per element)
+      float sf = sigm(cur.f.get(e)), sw = sigm(cur.i.get(e)) * cur.u.get(e);
+      asm volatile("" : "+v"(sf), "+v"(sw));
+      s_t[wv][0][cq + e][rho] = ok ? sf : 1.f;
+      s_t[wv][1][cq + e][rho] = ok ? sw : 0.f;
       uu[e] = ok ? cur.u.get(e) : 0.f;
     }
     __syncthreads();  // B / C of sb are staged; every wave is done with sb - 1
