@@ -313,6 +313,36 @@ struct McIn {
   }
 };
 
+// The wave's 16 channels x 64 state entries (X in the D layout: lane (j, g)
+// value r of X[m] is entry 16m + 4g + r of channel j), stored as the
+// contiguous 4 KB run [channel][entry] at ckw. Stored straight from the D
+// layout, each store would write sixteen 64-byte pieces; transposed through
+// tt (16 x 36 floats of the wave's own LDS, free at the call), each store
+// writes eight whole 128-byte lines. Two halves of 32 entries per channel.
+// (MT = 4 only: the callers test N == 64)
+template <int MT>
+__device__ __forceinline__ void store_state64(float* ckw, const f4_t (&X)[MT], float* tt, int j, int g, int lane) {
+  static_assert(16 * 36 <= 2 * 16 * TP, "the transposition fits a wave's two gate tiles");
+  if constexpr (MT == 4) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        *(float4*)(tt + j * 36 + 16 * k + 4 * g) =
+            make_float4(X[2 * h + k][0], X[2 * h + k][1], X[2 * h + k][2], X[2 * h + k][3]);
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int c = 8 * s2 + (lane >> 3), q = 4 * (lane & 7);
+        const float4 v = *(const float4*)(tt + c * 36 + q);
+        *(float4*)(ckw + c * 64 + 32 * h + q) = v;
+      }
+    }
+    asm volatile("" ::: "memory");
+  }
+}
+
 // ------------------------------------------------------------------ forward
 //
 // One workgroup per (batch row, kMcDT channels, time segment); the segment's
@@ -545,31 +575,7 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
       }
       // the state entering this sub-block is the backward's checkpoint
       if (NP == 64 && N == 64 && a.ckpt && dw + 16 <= D && sb % ck_sb == 0) {
-        // The wave's 16 channels x 64 entries are one contiguous 4 KB run.
-        // Stored straight from the D layout, each store would write 16
-        // pieces of 64 bytes; transposed through the wave's own gate tiles
-        // (free here: f and w are in registers, y is staged after), each
-        // store writes eight whole 128-byte lines. Two halves of 32 entries
-        // per channel, [channel][entry] at pitch 36.
-        float* tt = &s_t[wv][0][0][0];
-        float* ckw = a.ckpt + (((int64_t)b * a.Kc + sb / ck_sb) * D + dw) * N;  // uniform
-        static_assert(16 * 36 <= 2 * 16 * TP, "the transposition fits the wave's gate tiles");
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          asm volatile("" ::: "memory");
-#pragma unroll
-          for (int k = 0; k < 2; ++k)
-            *(float4*)(tt + j * 36 + 16 * k + 4 * g) =
-                make_float4(X[2 * h + k][0], X[2 * h + k][1], X[2 * h + k][2], X[2 * h + k][3]);
-          asm volatile("" ::: "memory");
-#pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2) {
-            const int c = 8 * s2 + (lane_l >> 3), q = 4 * (lane_l & 7);
-            const float4 v = *(const float4*)(tt + c * 36 + q);
-            *(float4*)(ckw + c * 64 + 32 * h + q) = v;
-          }
-        }
-        asm volatile("" ::: "memory");
+        store_state64(a.ckpt + (((int64_t)b * a.Kc + sb / ck_sb) * D + dw) * N, X, &s_t[wv][0][0][0], j, g, lane_l);
       } else if (a.ckpt && dok && sb % ck_sb == 0) {
         float* ck = a.ckpt + (((int64_t)b * a.Kc + sb / ck_sb) * D + d) * N;
 #pragma unroll
@@ -630,7 +636,11 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
             X[m][r] = (dok && n < N) ? st[n] : 0.f;
           }
       }
-      if (a.recomp && dok) {
+      if (NP == 64 && N == 64 && a.recomp && dw + 16 <= D) {
+        // the state entering sb, as the scan's checkpoint holds it (the
+        // wave's gate tiles are free: f and w are in registers)
+        store_state64(a.ckpt + (((int64_t)b * a.Kc + sb) * D + dw) * N, X, &s_t[wv][0][0][0], j, g, lane_l);
+      } else if (a.recomp && dok) {
         // the state entering sb, as the scan's checkpoint holds it
         float* ck = a.ckpt + (((int64_t)b * a.Kc + sb) * D + d) * N;
 #pragma unroll
