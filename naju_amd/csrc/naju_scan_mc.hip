@@ -1009,14 +1009,20 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
     // ---- stage B / C; gates in the load layout (each element once; rows
     // past T and channels past D are the neutral step f = 1, i = w = dy = 0)
     cur.stage(sh, a, t0, tid);
-    const bool rok = t0 + rho < T;
+    const int rl = (int)(T - t0 < Q ? T - t0 : Q);  // rows left (uniform)
+    const bool rok = rho < rl;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bool ok = rok && e < ncq;
-      Tf[cq + e][rho] = ok ? sigm(cur.f.get(e)) : 1.f;
+      // gates formed on every lane, then selected (no branch per element)
+      float sf = sigm(cur.f.get(e));
+      asm volatile("" : "+v"(sf));
+      Tf[cq + e][rho] = ok ? sf : 1.f;
       Tdy[cq + e][rho] = ok ? cur.dy.get(e) : 0.f;
       if constexpr (!MAP) {
-        const float ig = ok ? sigm(cur.i.get(e)) : 0.f;
+        float si = sigm(cur.i.get(e));
+        asm volatile("" : "+v"(si));
+        const float ig = ok ? si : 0.f;
         sh.gate[wv][3][cq + e][rho] = ig;
         sh.gate[wv][2][cq + e][rho] = ok ? ig * cur.u.get(e) : 0.f;
         dDacc[e] = fmaf(ok ? cur.dy.get(e) : 0.f, ok ? cur.u.get(e) : 0.f, dDacc[e]);
