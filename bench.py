@@ -106,13 +106,21 @@ def _scan_case(L, config, N, dev, seed=0):
                                                                               dD, dh0, ws))
 
 
-def _time_case(case, steps, warmup, stream):
+def _time_case(case, steps, warmup, stream, min_warm_ms=0.0):
     """K steps back to back (wall clock between synchronisations), then K
-    more with HIP events on the launch stream around each call."""
+    more with HIP events on the launch stream around each call. Untimed
+    warmup: `warmup` steps, continued until min_warm_ms of wall time have
+    passed (the GPU's clocks ramp up over the first milliseconds of work: a
+    C2 N=1 step measures 0.192 ms after 10 warmup steps, 0.186 ms after 200)."""
     import torch
-    for _ in range(warmup):
+    t_w = time.perf_counter()
+    k = 0
+    while k < warmup or (time.perf_counter() - t_w) * 1e3 < min_warm_ms:
         case["fwd"]()
         case["bwd"]()
+        k += 1
+        if k >= warmup and min_warm_ms > 0 and k % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -141,7 +149,7 @@ def _config_entry(L, config, N, dev, steps, warmup, target_ms=None):
     elements/s and roofline fractions of the fused fwd+bwd step."""
     import torch
     case = _scan_case(L, config, N, dev)
-    t = _time_case(case, steps, warmup, torch.cuda.current_stream(dev))
+    t = _time_case(case, steps, warmup, torch.cuda.current_stream(dev), min_warm_ms=100.0)
     b, T, D, n = case["shape"]
     step_bytes = case["bytes_fwd"] + case["bytes_bwd"]
     gbs = step_bytes / (t["ms_step"] * 1e-3) / 1e9
@@ -176,7 +184,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default: 200 scan steps, 3 LM steps for --config c5)")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="c1-c4: the scan itself; c5: the LM training step (tokens/s)")
     ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
@@ -196,6 +205,8 @@ def main():
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
 
+    if args.warmup is None:
+        args.warmup = 3 if args.config == "c5" else 200
     if args.config == "c5":
         print(json.dumps(_bench_lm(args.steps, args.warmup, args.tune_gemms, line=True)), flush=True)
         return
