@@ -11,8 +11,13 @@ value = algorithmic bytes of fwd+bwd per step * K / wall time of K steps
 HIP events recorded on the launch stream inside the timed region. The same
 line carries the step timed after a 1 GiB cache-flush write, and (default
 c2, N = 1 run) a "configs" table: c1, c3 and c4 at N = 1 (c3 / c4 against the
-70%-of-HBM step times), c2 at N = 64 (VALU roofline) and the c5 LM training
-step (tokens/s). The cpu_baseline leg times the sequential torch-CPU
+70%-of-HBM step times), c2, c3 and c4 at N = 64 (HBM fraction and the
+roofline of the instructions the kernels issue) and the c5 LM training step
+(tokens/s and peak memory, at the default and a 128-row checkpoint
+interval); an "inference" table (the no-grad forward at c2, N = 1 and 64);
+and "reference_bench_shapes", the reference's own scan benchmark shapes
+(naju/tests/bench_scan.py) in fp32 and bf16: forward under no_grad, forward
++ backward, peak memory. The cpu_baseline leg times the sequential torch-CPU
 restatement of the reference's scan (oracle/scan_ref.py: scan_loop_torch,
 the algorithm of reference naju/scan.py:79-93) on the host cores: c1 forward
 and forward + backward at N = 1 and 64, and the benchmarked workload.
@@ -33,18 +38,37 @@ if _ROOT not in sys.path:
     sys.path.insert(0, _ROOT)
 
 HBM_PEAK_GBS = 8000.0
-VALU_PEAK_TFLOPS = 157.3 / 2  # fp32 FMA without packed-FP32 instructions
-MFMA_F32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA (v_mfma_f32_16x16x4_f32)
 
 
-def compute_roof(n):
-    """The compute bound of the general-N scan kernels at state size n:
-    9 <= n <= 64 run the chunked form on the fp32 matrix cores, the others on
-    the VALU. Work is counted as the recurrence's own 19n flop per element
-    (5n forward, 14n backward), whichever units do it."""
-    if 9 <= n <= 64:
-        return "mfma", MFMA_F32_PEAK_TFLOPS
-    return "valu", VALU_PEAK_TFLOPS
+CLOCK_GHZ = 2.4     # MI355X peak engine clock
+N_SIMDS = 256 * 4   # 256 CUs x 4 SIMDs
+
+
+def issue_roof(key, E, n, ms_step):
+    """The compute roofline of a general-N step from the instructions its
+    kernels issue (profiles/issue.json, rocprofv3 counters of the same
+    workload): every SIMD issuing its share of the VALU wave-instructions at
+    4 cycles each (16 lanes, no packed FP32) plus its matrix-core busy
+    cycles, back to back, at the peak clock. frac = that time / the measured
+    step; peak = the recurrence's 19n flop per element delivered at that
+    rate. None without a record for this workload."""
+    path = os.path.join(_ROOT, "profiles", "issue.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(key)
+    except (OSError, ValueError):
+        rec = None
+    if not rec:
+        return None
+    cyc = (4.0 * rec["valu_wave_insts_per_step"] + rec["mfma_busy_cycles_per_step"]) / N_SIMDS
+    t_issue_ms = cyc / (CLOCK_GHZ * 1e9) * 1e3
+    work = 19.0 * n * E
+    return {"bound": "instruction issue (VALU + matrix cores, serialised, at 2.4 GHz)",
+            "work": "19N flop per element", "unit": "TFLOP/s",
+            "achieved": round(work / (ms_step * 1e-3) / 1e12, 2),
+            "peak": round(work / (t_issue_ms * 1e-3) / 1e12, 2),
+            "issue_bound_ms": round(t_issue_ms, 5), "frac": round(t_issue_ms / ms_step, 4),
+            "source": "profiles/issue.json (" + rec.get("profile", "") + ")"}
 METRIC = "fwd+bwd scan GB/s (% of HBM peak) at B8 L4096 D1024; LM tokens/s"
 
 
@@ -86,6 +110,11 @@ def _scan_case(L, config, N, dev, seed=0):
         _lib.check(L.naju_scan_fwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(h0), p(y), p(ck), None,
                                    Bsz, T, D, N, *dts, 0, p(ws), ws_bytes, sh))
 
+    def fwd_infer():
+        # the forward as under no_grad: no checkpoint is written
+        _lib.check(L.naju_scan_fwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(h0), p(y), None, None,
+                                   Bsz, T, D, N, *dts, 0, p(ws), ws_bytes, sh))
+
     def bwd():
         _lib.check(L.naju_scan_bwd(p(u), p(fl), p(il), p(Bm), p(Cm), p(Dk), p(ck), p(dy), p(du), p(dfl),
                                    p(dil), p(dB), p(dC), p(dD), p(dh0), Bsz, T, D, N, *dts, 0, p(ws),
@@ -101,7 +130,7 @@ def _scan_case(L, config, N, dev, seed=0):
     bf = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=True, bwd=False)
     bb = algorithmic_bytes(Bsz, T, D, N, s_x, s_g, s_bc, has_h0, fwd=False, bwd=True)
     dname = {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[xdt]
-    return dict(fwd=fwd, bwd=bwd, status=status, bytes_fwd=bf, bytes_bwd=bb, E=Bsz * T * D, dtype=dname,
+    return dict(fwd=fwd, bwd=bwd, fwd_infer=fwd_infer, status=status, bytes_fwd=bf, bytes_bwd=bb, E=Bsz * T * D, dtype=dname,
                 shape=(Bsz, T, D, N), has_h0=has_h0, gate=cfg["gate"], _keep=(ins, y, ck, du, dfl, dil, dB, dC,
                                                                               dD, dh0, ws))
 
@@ -165,13 +194,7 @@ def _config_entry(L, config, N, dev, steps, warmup, target_ms=None):
         "roofline_frac_bwd": round(case["bytes_bwd"] / (t["bwd_avg"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
     if n > 1:
-        fl_bwd, fl_fwd = 14.0 * n * case["E"], 5.0 * n * case["E"]
-        bound, peak = compute_roof(n)
-        e["roofline_compute"] = {
-            "bound": bound, "peak": peak, "unit": "TFLOP/s", "work": "19N flop per element",
-            "bwd_achieved": round(fl_bwd / (t["bwd_avg"] * 1e-3) / 1e12, 2),
-            "fwd_achieved": round(fl_fwd / (t["fwd_avg"] * 1e-3) / 1e12, 2),
-            "frac_step": round((fl_bwd + fl_fwd) / (t["ms_step"] * 1e-3) / 1e12 / peak, 4)}
+        e["roofline_compute"] = issue_roof(f"{config}_N{n}", case["E"], n, t["ms_step"])
     if target_ms is not None:
         e["target_ms"] = target_ms
         e["meets_target"] = bool(t["ms_step"] <= target_ms)
@@ -191,7 +214,8 @@ def main():
     ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the other configurations (c1, c3, c4 at N=1; c2 at N=64; the c5 LM step)")
+                    help="skip the other configurations (c1, c3, c4 at N=1; c2-c4 at N=64; the c5 LM step), "
+                         "the inference entries and the reference's benchmark shapes")
     ap.add_argument("--no-flush", action="store_true",
                     help="skip the steps timed with a 1 GiB cache-flush write before each step")
     ap.add_argument("--tune-gemms", default=None, metavar="CSV",
@@ -268,17 +292,9 @@ def main():
         },
     }
     if N > 1:
-        # General N is compute-bound: the recurrence, readout and adjoint are
-        # about 19N flop per element (5N forward, 14N backward). 9 <= N <= 64
-        # runs on the fp32 matrix cores (157.3 TFLOP/s dense), other N on the
-        # VALU (packed-FP32 ops are disabled in this build: half of 157.3).
-        E = case["E"]
-        bound, peak = compute_roof(N)
-        ach = 14.0 * N * E / (t["bwd_avg"] * 1e-3) / 1e12
-        out["roofline_compute"] = {"kernel": "naju_scan_bwd call", "bound": bound, "achieved": round(ach, 2),
-                                   "peak": peak, "unit": "TFLOP/s", "work": "19N flop per element",
-                                   "frac": round(ach / peak, 4),
-                                   "fwd_achieved": round(5.0 * N * E / (t["fwd_avg"] * 1e-3) / 1e12, 2)}
+        # General N is compute-bound (about 19N flop per element against
+        # 22-44 bytes): the roofline of the instructions the kernels issue
+        out["roofline_compute"] = issue_roof(f"{args.config}_N{N}", case["E"], N, ms_step)
     if not args.no_flush:
         # the same step with a 1 GiB write before it: nothing of the step's
         # inputs is left in the 256 MB last-level cache
@@ -307,7 +323,8 @@ def main():
         tgt = lambda c: round(_step_bytes_of(c, 1) / (TARGET_FRAC * HBM_PEAK_GBS * 1e9) * 1e3, 4)  # noqa: E731
         ex = {}
         for name, cfg, n, target in (("c1_n1", "c1", 1, None), ("c3_n1", "c3", 1, tgt("c3")),
-                                     ("c4_n1", "c4", 1, tgt("c4")), ("c2_n64", "c2", 64, None)):
+                                     ("c4_n1", "c4", 1, tgt("c4")), ("c2_n64", "c2", 64, None),
+                                     ("c3_n64", "c3", 64, None), ("c4_n64", "c4", 64, None)):
             ex[name] = _config_entry(L, cfg, n, dev, ks, ws, target)
             print(f"bench: {name} {ex[name]['ms_per_step']} ms/step {ex[name]['GBs']} GB/s", file=sys.stderr,
                   flush=True)
@@ -316,9 +333,138 @@ def main():
         print(f"bench: stream reference {ex['stream_reference']}", file=sys.stderr, flush=True)
         ex["c5_lm_step"] = _bench_lm(max(5, min(K, 10)), 3, None, line=False)
         print(f"bench: c5 {ex['c5_lm_step']['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
+        ex["c5_lm_step_ckpt128"] = _bench_lm(max(5, min(K, 10)), 3, None, line=False, ckpt_rows=128)
+        print(f"bench: c5 (128-row checkpoint interval) {ex['c5_lm_step_ckpt128']['tokens_per_s']} tokens/s",
+              file=sys.stderr, flush=True)
         out["configs"] = ex
+        out["inference"] = {name: _inference_entry(L, cfg, n, dev, ks)
+                            for name, cfg, n in (("c2_n1", "c2", 1), ("c2_n64", "c2", 64))}
+        print(f"bench: inference {out['inference']}", file=sys.stderr, flush=True)
+        out["reference_bench_shapes"] = _reference_bench(dev)
+        print("bench: reference bench shapes done", file=sys.stderr, flush=True)
     out["cpu_baseline"] = None if args.no_cpu else _cpu_baseline(args.config, N)
     print(json.dumps(out), flush=True)
+
+
+def _inference_entry(L, config, N, dev, steps):
+    """The no-grad forward (naju_scan_fwd with no checkpoint, what
+    naju_scan_hip runs under torch.no_grad; the role of the reference's
+    inference backend, naju/cuda/bw.py:36-38): GB/s of the forward's
+    algorithmic bytes (read u, f_logit, i_logit, B, C, h0; write y) and % of
+    HBM peak, HIP events around each call on the launch stream after at least
+    100 ms of warmup."""
+    import torch
+    case = _scan_case(L, config, N, dev)
+    stream = torch.cuda.current_stream(dev)
+    t_w = time.perf_counter()
+    while (time.perf_counter() - t_w) < 0.1:
+        for _ in range(8):
+            case["fwd_infer"]()
+        torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record(stream)
+        case["fwd_infer"]()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ts = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+    ms = sum(ts) / len(ts)
+    b, T, D, n = case["shape"]
+    gbs = case["bytes_fwd"] / (ms * 1e-3) / 1e9
+    out = {"workload": f"naju scan forward, no grad (no checkpoint): {config} B={b} L={T} D={D} N={n} "
+                       f"{case['dtype']} streams" + (" with h0" if case["has_h0"] else ""),
+           "steps": steps, "ms_avg": round(ms, 5), "ms_median": round(ts[len(ts) // 2], 5),
+           "algorithmic_bytes": case["bytes_fwd"], "GBs": round(gbs, 1),
+           "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+           "elements_per_s": round(case["E"] / (ms * 1e-3), 1)}
+    del case
+    torch.cuda.empty_cache()
+    return out
+
+
+# The reference's own scan benchmark shapes (naju/tests/bench_scan.py:112):
+# (batch, T, d_inner, N)
+REF_BENCH_SHAPES = ((8, 2048, 512, 64), (8, 8192, 512, 64), (2, 32768, 512, 64))
+
+
+def _reference_bench(dev, iters=30, warmup=10):
+    """The reference's scan benchmark (naju/tests/bench_scan.py:24-80) run
+    on these kernels through the backend callable naju_scan_hip, as it runs
+    each of its backends: its input recipe (u ~ N(0,1), f_logit ~ N(0,1)+2,
+    i_logit ~ N(0,1)-1, B, C ~ N(0,1)/sqrt(N), D_skip ~ 0.01 N(0,1)), in
+    float32 (its default) and bfloat16 (its --dtype bf16); forward under
+    no_grad and forward + backward (y.backward(dy)), CUDA events around each
+    call after `warmup` calls, median / p10 / p90 of `iters`; peak memory =
+    torch.cuda.max_memory_allocated over the run, inputs included, with this
+    package's workspace cache emptied first (so its workspace counts). The
+    training step also at the 128-row checkpoint interval (the memory-light
+    mode). GB/s and % of HBM use the algorithmic bytes of the pass (fwd: read
+    u, f_logit, i_logit, B, C; write y)."""
+    import torch
+    from naju_amd import naju_scan_hip
+    from naju_amd import scan as scan_mod
+    from naju_amd.workloads import algorithmic_bytes
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ts.sort()
+        n = len(ts)
+        return ts[n // 2], ts[max(0, n // 10)], ts[min(n - 1, 9 * n // 10)]
+
+    res = {}
+    for dtype, dname in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        for (b, T, D, N) in REF_BENCH_SHAPES:
+            s = 4 if dtype == torch.float32 else 2
+            entry = {}
+            for mode, rows in (("fwd", None), ("fwd+bwd", None), ("fwd+bwd ckpt128", 128)):
+                scan_mod._WS._bufs.clear()
+                scan_mod._WS._status.clear()
+                torch.cuda.synchronize()
+                torch.cuda.empty_cache()
+                base = torch.cuda.memory_allocated(dev)
+                torch.cuda.reset_peak_memory_stats(dev)
+                g = torch.Generator(device=dev).manual_seed(0)
+
+                def r(*shape):
+                    return torch.randn(*shape, generator=g, device=dev)
+                ins = [r(b, T, D), r(b, T, D) + 2.0, r(b, T, D) - 1.0, r(b, T, N) / N ** 0.5, r(b, T, N) / N ** 0.5,
+                       r(D) * 0.01]
+                ins = [x.to(dtype) for x in ins]
+                if mode == "fwd":
+                    with torch.no_grad():
+                        med, p10, p90 = timed(lambda: naju_scan_hip(*ins))
+                    nbytes = algorithmic_bytes(b, T, D, N, s, s, s, False, fwd=True, bwd=False)
+                else:
+                    xs = [x.requires_grad_(True) for x in ins]
+                    dy = torch.randn(b, T, D, device=dev, dtype=dtype, generator=g)
+
+                    def step():
+                        naju_scan_hip(*xs, ckpt_rows=rows).backward(dy)
+                        for x in xs:
+                            x.grad = None
+                    med, p10, p90 = timed(step)
+                    nbytes = algorithmic_bytes(b, T, D, N, s, s, s, False)
+                peak = torch.cuda.max_memory_allocated(dev) - base
+                gbs = nbytes / (med * 1e-3) / 1e9
+                entry[mode] = {"ms_median": round(med, 4), "ms_p10": round(p10, 4), "ms_p90": round(p90, 4),
+                               "peak_GiB": round(peak / 2 ** 30, 3), "Mtok_per_s": round(b * T / (med * 1e-3) / 1e6, 2),
+                               "GBs": round(gbs, 1), "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2)}
+                del ins
+            res[f"{dname} B={b} T={T} d_inner={D} N={N}"] = entry
+    scan_mod._WS._bufs.clear()
+    scan_mod._WS._status.clear()
+    torch.cuda.empty_cache()
+    return res
 
 
 def _stream_reference(dev):
@@ -360,14 +506,25 @@ def _step_bytes_of(config, N):
     return algorithmic_bytes(c["batch"], c["T"], c["D"], N, s, s, s, c["h0_std"] > 0)
 
 
-def _bench_lm(steps, warmup, tune_gemms=None, line=True):
+def _bench_lm(steps, warmup, tune_gemms=None, line=True, ckpt_rows=None):
     """Benchmark configuration c5: one training step of the Naju LM (12 layers,
     d_model 768, vocab 50257, N = 64) on a batch of 8 x 2048 uniformly random
     token ids: bf16 autocast forward, cross-entropy (the fused HIP kernels of
     naju_amd.xent on the bf16 logits), backward, gradient
     clipping at 1.0 and an AdamW step, with every mixer's scan on the HIP
     kernels. value = tokens per second. line=True: the whole bench line;
-    else the entry of the per-configuration table."""
+    else the entry of the per-configuration table. ckpt_rows: the scans'
+    checkpoint interval (NAJU_CKPT_ROWS for the run; None = the default).
+    peak_GiB: torch.cuda.max_memory_allocated over the timed steps."""
+    if ckpt_rows:
+        os.environ["NAJU_CKPT_ROWS"] = str(int(ckpt_rows))
+    try:
+        return _bench_lm_run(steps, warmup, tune_gemms, line, ckpt_rows)
+    finally:
+        os.environ.pop("NAJU_CKPT_ROWS", None)
+
+
+def _bench_lm_run(steps, warmup, tune_gemms, line, ckpt_rows):
     import torch
     from naju_amd.mixer import NajuLM, build_optimizer
     from naju_amd.xent import cross_entropy
@@ -406,17 +563,20 @@ def _bench_lm(steps, warmup, tune_gemms=None, line=True):
     # meanwhile); the objects alive after the warmup are moved out of its way
     gc.collect()
     gc.freeze()
+    torch.cuda.reset_peak_memory_stats(dev)
     K = steps
     t0 = time.perf_counter()
     for _ in range(K):
         loss = step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / K
+    peak_gib = round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 3)
     gc.unfreeze()
     tokens = Bsz * T
     tflops = 6.0 * n_params * tokens / dt / 1e12
     workload = ("naju LM training step c5: 12 layers, d_model 768, vocab 50257, N=64, "
-                "batch 8 x seq 2048, AdamW + clip 1.0")
+                "batch 8 x seq 2048, AdamW + clip 1.0"
+                + (f", scan checkpoint every {ckpt_rows} rows" if ckpt_rows else ""))
     roof = {"kernel": "whole training step (6 x parameters x tokens)", "bound": "mfma",
             "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
             "frac": round(tflops / 2500.0, 4), "traffic": None}
@@ -426,7 +586,7 @@ def _bench_lm(steps, warmup, tune_gemms=None, line=True):
     if not line:
         return {"workload": workload, "steps": K, "ms_per_step": round(dt * 1e3, 3),
                 "tokens_per_s": round(tokens / dt, 1), "model_TFLOPs": round(tflops, 1),
-                "roofline": roof, "loss_last": loss_last,
+                "roofline": roof, "loss_last": loss_last, "peak_GiB": peak_gib,
                 "gemm_choices": os.path.basename(tuned) if tuned else "library default"}
     return {
         "metric": METRIC, "value": round(tokens / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
@@ -435,7 +595,7 @@ def _bench_lm(steps, warmup, tune_gemms=None, line=True):
         "data": "synthetic (uniform random token ids; random init)",
         "config": {"workload": workload, "parameters": n_params, "parallelism": "single GPU",
                    "gemm_choices": os.path.basename(tuned) if tuned else "library default"},
-        "loss_last": loss_last, "roofline": roof, "cpu_baseline": None,
+        "loss_last": loss_last, "peak_GiB": peak_gib, "roofline": roof, "cpu_baseline": None,
     }
 
 

@@ -37,24 +37,23 @@
  *     results repeat to float32 rounding only. N > 1 is always bitwise
  *     deterministic.
  *   NAJU_CKPT_ROWS(r) (bits 8-15): the forward's checkpoint interval for
- *     N > 1, r rows (a multiple of 16, up to 4080; 0 = the default). The
- *     checkpoint holds the state every r rows (batch*ceil(T/r)*D*N floats).
+ *     N > 1, r rows (32, 64 or 128; 0 = the default). The checkpoint holds
+ *     the state every r rows (batch*ceil(T/r)*D*N floats).
  *     The default is 16 rows for 9 <= N <= 64 (the state entering every
  *     sub-block of the matrix-core backward) and 32 rows otherwise; a longer
  *     interval is the memory-light mode of the reference's recompute backend
  *     (naju/cuda/__init__.py:9-12, CK = 32 in naju/cuda/naju_cuda.cu:25):
- *     the checkpoint then also holds the state entering each of the
- *     forward's time segments after the first (a few [batch,D,N] blocks),
- *     and the backward first recomputes the state at every 16-row sub-block
- *     from it into its workspace (one forward-like pass over u, f_logit,
- *     i_logit and B), so the memory held between forward and backward
- *     shrinks about r/16-fold at the cost of that pass. Every gradient is
- *     bitwise the one of the default interval. Served for 9 <= N <= 64 by
- *     naju_scan_fwd (not by naju_scan_fwd_noalloc when its scratch forces
- *     fewer time segments); other N accept only their default
- *     (NAJU_ERR_UNSUPPORTED otherwise). The backward must be given the
- *     forward's flags value for these bits, and the size queries below have
- *     _ex forms that take it.
+ *     the forward's time segments always start at multiples of 128 rows
+ *     (so the checkpoint holds every state a recompute starts from, and
+ *     nothing else), and the backward first recomputes the state at every
+ *     16-row sub-block from it into its workspace (one forward-like pass
+ *     over u, f_logit, i_logit and B), so the memory held between forward
+ *     and backward shrinks r/16-fold at the cost of that pass. Every output
+ *     is bitwise the one of the default interval.
+ *     Served for 9 <= N <= 64 by naju_scan_fwd and naju_scan_fwd_noalloc;
+ *     other N accept only their default (NAJU_ERR_UNSUPPORTED otherwise).
+ *     The backward must be given the forward's flags value for these bits,
+ *     and the size queries below have _ex forms that take it.
  *
  * Workspace: naju_scan_workspace_bytes() bytes of device memory that MUST be
  * zero-filled once before its first use; every call leaves it reusable
@@ -195,9 +194,24 @@ int naju_scan_fwd_noalloc(const void* u, const void* f_logit,
  * bounded wait and the affected outputs were set to NaN; 2 = a ticket
  * counter held a value out of range (a workspace that was not zero-filled
  * before first use), and the affected workgroups wrote NaN outputs. No
- * counterpart in the reference (its kernels have no cross-workgroup waits). */
+ * counterpart in the reference (its kernels have no cross-workgroup waits).
+ * Only the N = 1 kernels hand carries between workgroups, so only N = 1
+ * calls can set a nonzero status. Test hook: the environment variable
+ * NAJU_DEBUG_SPIN_LIMIT, read at every call, lowers the bound on a hand-off's
+ * idle polling rounds (default about a second of polling); 0 makes every
+ * hand-off give up at once, so status 1 can be produced while every kernel
+ * exits normally. */
 int naju_scan_workspace_status(const void* workspace, void* stream,
                                uint32_t* status);
+
+/* naju_scan_workspace_status for the static scratch of
+ * naju_scan_fwd_noalloc on the current HIP device (synchronises `stream`):
+ * reads its status word and, when it is nonzero, clears it and rewinds the
+ * scratch's ticket counters, so later naju_scan_fwd_noalloc calls on this
+ * device start clean. Status 0 before the first naju_scan_fwd_noalloc call
+ * on the device. No counterpart in the reference; it is the recovery path
+ * of callers that cannot allocate (they never hold a workspace pointer). */
+int naju_scan_noalloc_status(void* stream, uint32_t* status);
 
 #ifdef __cplusplus
 }

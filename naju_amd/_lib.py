@@ -35,6 +35,7 @@ EXPORTED = (
     "naju_scan_bwd",
     "naju_scan_workspace_status",
     "naju_scan_fwd_noalloc",
+    "naju_scan_noalloc_status",
     "naju_mixer_last_error",
     "naju_dwconv_fwd",
     "naju_dwconv_workspace_bytes",
@@ -98,6 +99,8 @@ def lib():
     L.naju_scan_fwd_noalloc.restype = I
     L.naju_scan_workspace_status.argtypes = [P, P, ctypes.POINTER(ctypes.c_uint32)]
     L.naju_scan_workspace_status.restype = I
+    L.naju_scan_noalloc_status.argtypes = [P, ctypes.POINTER(ctypes.c_uint32)]
+    L.naju_scan_noalloc_status.restype = I
     L.naju_mixer_last_error.argtypes = []
     L.naju_mixer_last_error.restype = ctypes.c_char_p
     # x, x_ld, w, bias, add, add_ld, y, batch, T, C, K, act, x_dt, add_dt, y_dt, stream

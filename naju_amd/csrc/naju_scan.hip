@@ -38,6 +38,7 @@
 #include <mutex>
 #include <type_traits>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "naju_scan.h"
@@ -346,7 +347,7 @@ __device__ __forceinline__ bool lb_consume(const ScanArgs& a, LookShared<V, W, P
       }
       ++consumed;
     }
-    if (!done && consumed == 0 && ++idle > kSpinLimit) {
+    if (!done && consumed == 0 && ++idle > a.spin_limit) {
       // Bounded wait exceeded: record it and end with a NaN carry.
       if (lane == 0) __hip_atomic_store(a.hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
@@ -377,6 +378,16 @@ __device__ __forceinline__ void wg_look_back(const ScanArgs& a, LookShared<V, W,
     aF[j] = 1.f;
     aZ[j] = 0.f;
     out[j] = 0.f;
+  }
+  if (a.spin_limit == 0u) {
+    // the host asked every hand-off to give up at once (a test hook): the
+    // failure path of an exceeded wait, taken without polling
+    if (wv == 0) {
+      if (lane == 0) __hip_atomic_store(a.hdr + HDR_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int j = 0; j < V; ++j) out[j] = __builtin_nanf("");
+    }
+    return;
   }
   int base = k + dir;
   uint32_t idle = 0;
@@ -2210,6 +2221,18 @@ int fail(int code, const char* fmt, ...) {
 
 size_t dsize(int dt) { return dt == NAJU_DTYPE_F32 ? 4 : 2; }
 
+// The look-back's bound on idle rounds: kSpinLimit, or a smaller value from
+// the environment variable NAJU_DEBUG_SPIN_LIMIT (read at every call). A
+// test hook: 0 makes every carry hand-off give up at once, so the failure
+// path (NaN outputs, status word 1) runs while every kernel exits normally.
+uint32_t spin_limit() {
+  const char* s = getenv("NAJU_DEBUG_SPIN_LIMIT");
+  if (!s || !*s) return kSpinLimit;
+  char* end = nullptr;
+  const unsigned long v = strtoul(s, &end, 10);
+  return (end && *end == 0 && v < kSpinLimit) ? (uint32_t)v : kSpinLimit;
+}
+
 // Tile geometry of the N = 1 kernels, per direction: V channels per lane,
 // R rows per wave, W waves per workgroup (chunk L = W*R rows), P look-back
 // slots polled per wave and round (window W*P chunks). The checkpoint holds
@@ -2275,22 +2298,31 @@ constexpr int kGnTargetWgs = NAJU_GN_TARGET_WGS;
 #define NAJU_MC_BWD_MIN_PER_CU 2
 #endif
 constexpr int kCUs = 256;  // MI355X
+// The matrix-core forward's time segments are whole multiples of this many
+// sub-blocks (128 rows), so that they start at interval boundaries of every
+// served checkpoint interval (32, 64 and 128 rows).
+constexpr int kMcSegUnit = 8;
 constexpr int kGcTargetWaves = 2048;
 
-// Segment count of a chunked matrix-core launch over n_tiles channel tiles
-// and K sub-blocks: the one whose busiest CU walks the fewest sub-blocks,
-// ceil(n_tiles s / CUs) ceil(K / s), among those that give every CU at
-// least min_per_cu workgroups; the fewest segments on a tie, since each one
-// past the first costs the segment-map pass over its rows and a start-up.
-int mc_nseg(int64_t n_tiles, int K, bool bwd) {
+// Sub-blocks per time segment of a chunked matrix-core launch over n_tiles
+// channel tiles and K sub-blocks: the segmentation whose busiest CU walks
+// the fewest sub-blocks, ceil(n_tiles s / CUs) * (sub-blocks per segment),
+// among those that give every CU at least min_per_cu workgroups; the fewest
+// segments on a tie, since each one past the first costs the segment-map
+// pass over its rows and a start-up. Segments are a multiple of `unit`
+// sub-blocks long (the forward with a checkpoint interval of unit
+// sub-blocks: every segment then starts where an interval does).
+int mc_seg_sc(int64_t n_tiles, int K, bool bwd, int unit) {
   const int64_t min_wg = (int64_t)kCUs * (bwd ? NAJU_MC_BWD_MIN_PER_CU : NAJU_MC_FWD_MIN_PER_CU);
   int best = K;
   int64_t best_cost = -1;
   for (int s = 1; s <= K; ++s) {
-    const int64_t wg = n_tiles * s;
+    const int sc = ((K + s - 1) / s + unit - 1) / unit * unit;
+    const int ns = unit == 1 ? s : (K + sc - 1) / sc;
+    const int64_t wg = n_tiles * ns;
     if (wg < min_wg && s < K) continue;
-    const int64_t cost = (wg + kCUs - 1) / kCUs * ((K + s - 1) / s);
-    if (best_cost < 0 || cost < best_cost) best_cost = cost, best = s;
+    const int64_t cost = (wg + kCUs - 1) / kCUs * sc;
+    if (best_cost < 0 || cost < best_cost) best_cost = cost, best = sc;
     if (wg >= 8 * min_wg) break;
   }
   return best;
@@ -2315,12 +2347,14 @@ int64_t gn_ck_rows(int64_t N) { return use_mc(N, true) ? kMcQ : kGnCK; }
 // default: the backward's chunk at N = 1, gn_ck_rows at N > 1), or -1 when
 // the shape does not serve it: longer intervals than the default only on the
 // matrix-core path, whose backward recomputes the states between.
-int64_t seg_states(int64_t batch, int64_t T, int64_t D, int64_t N, int rows);
 int ckpt_rows(int flags, int64_t N) {
   const int r = ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16;
   const int def = N == 1 ? kBChunk : (int)gn_ck_rows(N);
   if (r == 0 || r == def) return def;
-  return (N > 1 && use_mc(N, true)) ? r : -1;
+  // 2, 4, ... kMcSegUnit sub-blocks: intervals that divide the forward's
+  // segment unit
+  const bool served = r > kMcQ && r <= kMcQ * kMcSegUnit && (kMcQ * kMcSegUnit) % r == 0;
+  return (N > 1 && use_mc(N, true) && served) ? r : -1;
 }
 int gq_channels(int64_t N);
 int gn_bwd_dt(int np);
@@ -2358,18 +2392,14 @@ void place_regions(Layout& l, int64_t batch, int64_t T, int64_t D, int64_t N, bo
 
 // cap: at N > 1, fewer time segments (down to one) until the workspace fits
 // in cap bytes; the N = 1 layout has no such freedom.
-Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd,
-                   size_t cap, int ck_rows);
-
-// The checkpoint's segment-start states (a checkpoint interval longer than
-// the matrix-core sub-block): batch * nseg * D * N floats for the forward's
-// (uncapped) segmentation, 0 otherwise.
-int64_t seg_states(int64_t batch, int64_t T, int64_t D, int64_t N, int rows) {
-  if (N == 1 || !use_mc(N, false) || rows <= kMcQ) return 0;
-  const Layout f = make_layout(batch, T, D, N, 0, 0, false, SIZE_MAX, rows);
-  return f.nseg > 1 ? batch * f.nseg * D * N : 0;
-}
-
+// cap: at N > 1, fewer time segments (down to one) until the workspace fits
+// in cap bytes; the N = 1 layout has no such freedom. ck_rows: the
+// checkpoint interval (0 = the default; it sizes the backward's recomputed
+// states). The matrix-core forward's time segments are a multiple of
+// kMcSegUnit sub-blocks long, for every interval: every segment then starts
+// at an interval boundary of each served interval, so the checkpoint holds
+// every state the backward's recompute starts from, and the segmentation
+// (hence every output bit) does not depend on the interval.
 Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int g_dt, bool bwd,
                    size_t cap = SIZE_MAX, int ck_rows = 0) {
   Layout l{};
@@ -2395,23 +2425,29 @@ Layout make_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int x_dt, int
   l.n_tiles = (int)(batch * l.n_dtiles);
   l.nseg = 1;
   l.seg_sc = l.K;
+  // sub-blocks per segment must be a multiple of this (the matrix-core
+  // forward: kMcSegUnit, whatever the checkpoint interval)
+  const int unit = (mc && !bwd) ? kMcSegUnit : 1;
   if (N > 1 && l.n_tiles > 0 && l.K > 0 && (mc || bwd || !gq_ok(N, batch, D))) {
-    // forward (lanes over channels): about kGcTargetWaves waves; backward
-    // (8-wave workgroups over 64 channels) and the chunked kernels (4-wave
-    // workgroups): about kGnTargetWgs workgroups
-    const int64_t per_seg = (mc || bwd) ? l.n_tiles : batch * ((D + 63) / 64);
-    // (the 8-wave NP = 128 backward runs one workgroup per CU: 1024)
-    const int64_t target = bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
-    int64_t want = mc ? mc_nseg(l.n_tiles, l.K, bwd) : (target + per_seg - 1) / per_seg;
-    if (want > l.K) want = l.K;
-    if (want < 1) want = 1;
-    l.seg_sc = (int)((l.K + want - 1) / want);
+    if (mc) {
+      l.seg_sc = mc_seg_sc(l.n_tiles, l.K, bwd, unit);
+    } else {
+      // forward (lanes over channels): about kGcTargetWaves waves; backward
+      // (8-wave workgroups over 64 channels): about kGnTargetWgs workgroups
+      const int64_t per_seg = bwd ? l.n_tiles : batch * ((D + 63) / 64);
+      // (the 8-wave NP = 128 backward runs one workgroup per CU: 1024)
+      const int64_t target = bwd ? (np_of(N) <= 64 ? kGnTargetWgs : 1024) : kGcTargetWaves;
+      int64_t want = (target + per_seg - 1) / per_seg;
+      if (want > l.K) want = l.K;
+      if (want < 1) want = 1;
+      l.seg_sc = (int)((l.K + want - 1) / want);
+    }
     l.nseg = (l.K + l.seg_sc - 1) / l.seg_sc;
   }
   place_regions(l, batch, T, D, N, bwd);
   while (l.total > cap && l.nseg > 1) {
     const int want = l.nseg / 2;
-    l.seg_sc = (l.K + want - 1) / want;
+    l.seg_sc = ((l.K + want - 1) / want + unit - 1) / unit * unit;
     l.nseg = (l.K + l.seg_sc - 1) / l.seg_sc;
     place_regions(l, batch, T, D, N, bwd);
   }
@@ -2588,12 +2624,10 @@ int64_t naju_scan_ckpt_elems_ex(int64_t batch, int64_t T, int64_t D, int64_t N, 
                                 int bc_dtype, int flags) {
   if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return -1;
   const int rows = ckpt_rows(flags, N);
-  if (rows < 0) return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+  if (rows < 0) return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld (served: 32, 64 and 128 rows at 9 <= N <= 64)",
                             ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N), -1;
   // N = 1: one state per backward chunk; N > 1: the state every `rows` rows
-  // (with a longer interval than the default, also the state entering every
-  // forward time segment after the first)
-  if (N > 1) return batch * ((T + rows - 1) / rows) * D * N + seg_states(batch, T, D, N, rows);
+  if (N > 1) return batch * ((T + rows - 1) / rows) * D * N;
   const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, true);
   return batch * (int64_t)l.K * D * N;
 }
@@ -2607,7 +2641,7 @@ size_t naju_scan_workspace_bytes_ex(int64_t batch, int64_t T, int64_t D, int64_t
                                     int bc_dtype, int flags) {
   if (check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype) != NAJU_OK) return 0;
   const int rows = ckpt_rows(flags, N);
-  if (rows < 0) return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+  if (rows < 0) return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld (served: 32, 64 and 128 rows at 9 <= N <= 64)",
                             ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N), 0;
   const size_t f = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, SIZE_MAX, rows).total;
   const size_t b = make_layout(batch, T, D, N, x_dtype, gate_dtype, true, SIZE_MAX, rows).total;
@@ -2636,7 +2670,7 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
     return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
   const int ck_rows = ckpt_rows(flags, N);
   if (ck_rows < 0)
-    return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+    return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld (served: 32, 64 and 128 rows at 9 <= N <= 64)",
                 ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N);
   const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
@@ -2650,7 +2684,7 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
   }
   if (!u || !f_logit || !i_logit || !B || !C || !D_skip || !y)
     return fail(NAJU_ERR_INVALID, "null input/output pointer (u, f_logit, i_logit, B, C, D_skip and y are required)");
-  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, cap);
+  const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, cap, ck_rows);
   if (!workspace || workspace_bytes < l.total)
     return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", l.total,
                 workspace ? workspace_bytes : (size_t)0);
@@ -2695,14 +2729,6 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
       a.n_tiles = l.n_tiles;
       a.ck_rows = ck_rows;
       a.Kc = (int)((T + a.ck_rows - 1) / a.ck_rows);
-      if (ck_rows > kMcQ && l.nseg > 1) {
-        // the segment-start states follow the interval states in ckpt; the
-        // backward's recompute assumes the uncapped segmentation
-        if (l.nseg != make_layout(batch, T, D, N, x_dtype, gate_dtype, false, SIZE_MAX, ck_rows).nseg)
-          return fail(NAJU_ERR_UNSUPPORTED, "a checkpoint interval above %d rows needs the full workspace "
-                      "(use naju_scan_fwd)", kMcQ);
-        a.segst = ckpt ? ckpt + (int64_t)batch * a.Kc * D * N : nullptr;
-      }
       if ((int64_t)l.n_tiles * l.nseg > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "problem too large");
       hipError_t e = hipSuccess;
       if (l.nseg > 1) {
@@ -2744,6 +2770,7 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
   if (tg < 0) return fail(NAJU_ERR_LAUNCH, "epoch launch failed");
   a.tag = (uint32_t)tg;
   a.strict = (flags & NAJU_FLAG_DETERMINISTIC) != 0;
+  a.spin_limit = spin_limit();
   a.ck_rows = kBChunk;
   a.Kc = (int)((T + kBChunk - 1) / kBChunk);
   kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, false);
@@ -2824,7 +2851,8 @@ int naju_scan_fwd_noalloc(const void* u, const void* f_logit, const void* i_logi
   const int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
   if (batch > 0 && T > 0 && D > 0) {
-    const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, kScratchBytes);
+    const int rows = ckpt_rows(flags, N);
+    const Layout l = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, kScratchBytes, rows < 0 ? 0 : rows);
     if (l.total > kScratchBytes)
       return fail(NAJU_ERR_WORKSPACE,
                   "naju_scan_fwd_noalloc: this shape needs %zu bytes of scratch, the static maximum is %zu "
@@ -2850,7 +2878,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
   const int ck_rows = ckpt_rows(flags, N);
   if (ck_rows < 0)
-    return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld",
+    return fail(NAJU_ERR_UNSUPPORTED, "checkpoint interval %d rows is not served at N=%lld (served: 32, 64 and 128 rows at 9 <= N <= 64)",
                 ((flags & NAJU_CKPT_MASK) >> NAJU_CKPT_SHIFT) * 16, (long long)N);
   const int out_f32 = flags & NAJU_FLAG_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
@@ -2929,10 +2957,6 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
         r.recomp = 1;
         r.ck_src = ckpt;
         r.Kc_src = (int)((T + ck_rows - 1) / ck_rows);
-        const Layout lf = make_layout(batch, T, D, N, x_dtype, gate_dtype, false, SIZE_MAX, ck_rows);
-        r.seg_sc_f = lf.seg_sc;
-        r.nseg_f = lf.nseg;
-        r.segst = (float*)ckpt + (int64_t)batch * r.Kc_src * D * N;
         r.ckpt = (float*)(ws + l.off_dense);
         r.Kc = (int)((T + kMcQ - 1) / kMcQ);
         r.seg_sc = ck_rows / kMcQ;
@@ -2973,6 +2997,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
     if (tg < 0) return fail(NAJU_ERR_LAUNCH, "epoch launch failed");
     a.tag = (uint32_t)tg;
     a.strict = (flags & NAJU_FLAG_DETERMINISTIC) != 0;
+    a.spin_limit = spin_limit();
     kern_t k = pick_n1_all(vec, out_f32 != 0, x_dtype, gate_dtype, bc_dtype, true);
     rc = launch(k, (unsigned)wgs, 64 * kBW, st, a);
     if (rc) return rc;
@@ -3018,6 +3043,24 @@ int naju_scan_workspace_status(const void* workspace, void* stream, uint32_t* st
       return fail(NAJU_ERR_LAUNCH, "could not clear the workspace header");
   }
   return NAJU_OK;
+}
+
+int naju_scan_noalloc_status(void* stream, uint32_t* status) {
+  g_err[0] = 0;
+  if (!status) return fail(NAJU_ERR_INVALID, "null status pointer");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(NAJU_ERR_LAUNCH, "no current HIP device (or device index >= %d)", kMaxDevices);
+  void* p = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch_ptr[dev];
+  }
+  if (!p) {  // no naju_scan_fwd_noalloc call on this device yet
+    *status = 0;
+    return NAJU_OK;
+  }
+  return naju_scan_workspace_status(p, stream, status);
 }
 
 }  // extern "C"

@@ -397,15 +397,6 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
     // loaded before the loop, waited for here (as McIn::settle)
 #pragma unroll
     for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(X[m]));
-    // the state entering the segment, kept for the backward's recompute
-    if (!MAP && a.segst && seg > 0 && dok) {
-      float* st = a.segst + (((int64_t)b * a.nseg + seg) * D + d) * N;
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (16 * m + 4 * g + r < N) st[16 * m + 4 * g + r] = X[m][r];
-    }
   }
   float Fseg = 1.f;
   // load role: row rho, channels cq .. cq+3 of the wave's 16
@@ -624,18 +615,6 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(3))) 
       }
     } else {
       Fseg *= Pall;
-      if (a.recomp && sb != sb0 && sb % a.seg_sc_f == 0) {
-        // a forward segment starts here: the forward's state came from the
-        // carry over the segments, not from stepping
-        const float* st = a.segst + (((int64_t)b * a.nseg_f + sb / a.seg_sc_f) * D + (dok ? d : D - 1)) * N;
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int n = 16 * m + 4 * g + r;
-            X[m][r] = (dok && n < N) ? st[n] : 0.f;
-          }
-      }
       if (NP == 64 && N == 64 && a.recomp && dw + 16 <= D) {
         // the state entering sb, as the scan's checkpoint holds it (the
         // wave's gate tiles are free: f and w are in registers)

@@ -107,23 +107,22 @@ struct ScanArgs {
   // recompute of the state entering every sub-block (into ckpt, Kc of them)
   // from the forward's checkpoint ck_src (Kc_src intervals, one segment
   // each) instead of a segment map.
+  // (With a checkpoint interval longer than the sub-block the forward's time
+  // segments start at interval boundaries, so every state the recompute
+  // starts from is a checkpoint entry.)
   const float* ck_src;
   int Kc_src;
   int recomp;
-  // With a checkpoint interval longer than the sub-block: the state entering
-  // each forward time segment s >= 1 ([batch][nseg_f][D][N], after the
-  // interval states in the checkpoint), written by the forward and restored
-  // by the recompute at those sub-blocks (the forward's segmentation:
-  // seg_sc_f sub-blocks per segment, nseg_f segments).
-  float* segst;
-  int seg_sc_f;
-  int nseg_f;
   // N = 1: this launch's look-back tag. Nonzero: a host tag (odd, new for
   // every eager launch). Zero: the launch was recorded into a HIP graph, and
   // the tag comes from the device epoch, which the one-thread
   // epoch_bump_kernel recorded right before it advances on every replay.
   uint32_t tag;
   int strict;    // N = 1: take carries from the immediate predecessor's inclusive carry only
+  // N = 1: idle look-back rounds before a hand-off gives up (kSpinLimit;
+  // 0 = give up at once, a test hook that makes every hand-off fail while
+  // every kernel still exits normally)
+  uint32_t spin_limit;
 };
 
 // Lane exchange for the butterfly steps below: the value of the partner lane

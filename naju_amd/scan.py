@@ -19,8 +19,13 @@ Public surface, mirroring /root/reference/naju/scan.py:
   with this package: the call raises until one is registered under that
   name (the tests register the oracle's loop).
 * ``workspace_status(device=None)`` -- reads (and clears) the status word of
-  the current stream's workspace; ``NAJU_CHECK_STATUS=1`` makes every call
-  check it and raise on a failed cross-workgroup hand-off.
+  the current stream's workspace. After every N = 1 call (the only kernels
+  that hand carries between workgroups) the wrapper copies that word to
+  pinned host memory asynchronously; the next call or backward on the same
+  stream reads the copy once it has landed (no synchronisation) and raises
+  ``NajuScanError`` when a hand-off failed, clearing the word so the
+  workspace is usable again. ``NAJU_CHECK_STATUS=1`` checks synchronously
+  after every call instead.
 * ``register(name="hip", scan_module=None)`` -- inserts ``naju_scan_hip`` into
   the reference's ``naju.scan._BACKEND_CACHE``. ``_get`` returns cached entries
   before it validates names (scan.py:55-57) and ``resolve_backend`` lower-cases
@@ -51,10 +56,12 @@ def _ptr(t):
 class _Workspace:
     """One zero-filled workspace per (device, stream), grown on demand. The
     kernels return it to a reusable state after every call, so it is zeroed
-    only when (re)allocated."""
+    only when (re)allocated. Per workspace also a pinned host copy of its
+    status word and the event that marks when the copy has landed."""
 
     def __init__(self):
         self._bufs = {}
+        self._status = {}
 
     def get(self, device, stream, nbytes):
         key = (device.index, stream)
@@ -103,6 +110,39 @@ def _check_status(dev):
         st = workspace_status(dev)
         if st:
             raise _lib.NajuScanError(st, _STATUS_MSG.get(st, f"status {st}"))
+
+
+def _watch_status(dev, stream, ws):
+    """Queue an asynchronous copy of the workspace's status word (word 0) to
+    pinned host memory behind the call just issued on `stream`, and mark its
+    landing with an event. Not while the stream is being captured into a
+    graph (the copy would be recorded too)."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    key = (dev.index, stream)
+    ent = _WS._status.get(key)
+    if ent is None:
+        ent = (torch.zeros(1, dtype=torch.int32, pin_memory=True), torch.cuda.Event())
+        _WS._status[key] = ent
+    ent[0].copy_(ws[:4].view(torch.int32), non_blocking=True)
+    ent[1].record()
+
+
+def _raise_pending(dev, stream):
+    """Raise NajuScanError if the last landed status copy of this stream's
+    workspace is nonzero (a failed hand-off in an earlier call: its outputs
+    were NaN). Does not wait for a copy still in flight: the word stays set
+    on the device until cleared, so a later copy shows it. On raising, the
+    word is cleared (synchronously), so the workspace is usable again."""
+    ent = _WS._status.get((dev.index, stream))
+    if ent is None or not ent[1].query():
+        return
+    st = int(ent[0][0])
+    if st:
+        ent[0].zero_()
+        workspace_status(dev)  # clears the word and rewinds the counters
+        raise _lib.NajuScanError(st, "an earlier scan call on this stream failed: "
+                                 + _STATUS_MSG.get(st, f"status {st}"))
 
 
 def _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0):
@@ -166,12 +206,15 @@ class NajuScanHip(torch.autograd.Function):
         nbytes = L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags)
         if nbytes == 0 and Bsz * T * D > 0:
             _lib.check(_lib.ERR_UNSUPPORTED if "interval" in _lib.last_error() else _lib.ERR_INVALID)
+        _raise_pending(dev, stream)
         ws = _WS.get(dev, stream, nbytes)
         y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
         hT = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_hT else None
         _lib.check(L.naju_scan_fwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
             _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
+        if N == 1:
+            _watch_status(dev, stream, ws)
         _check_status(dev)
         if need_grad:
             ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
@@ -200,25 +243,39 @@ class NajuScanHip(torch.autograd.Function):
         dh0 = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_h0 else None
         L = _lib.lib()
         stream = _stream_handle(dev)
+        _raise_pending(dev, stream)
         ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags))
         _lib.check(L.naju_scan_bwd(
             _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
             _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
             Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
+        if N == 1:
+            _watch_status(dev, stream, ws)
         _check_status(dev)
         grads = [du, dfl, dil, dB, dC, dD]
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
         return (*grads, dh0, None, None)
 
 
+def _default_ckpt_rows(N):
+    """The checkpoint interval of calls that name none: NAJU_CKPT_ROWS from
+    the environment where it is served (9 <= N <= 64), else the default. It
+    lets unmodified NajuMixer / NajuLM code run the memory-light mode, as
+    NAJU_SCAN_BACKEND=cuda selects the reference's recompute backend."""
+    v = os.environ.get("NAJU_CKPT_ROWS", "")
+    return int(v) if v and 9 <= N <= 64 else 0
+
+
 def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False, ckpt_rows=None):
     """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module
     doc); (y, hT) with return_final_state=True. ckpt_rows: the checkpoint
-    interval kept for the backward (None = the default; a longer interval,
-    a multiple of 16 served at 9 <= N <= 64, is the memory-light mode: the
-    backward recomputes the states between, with bitwise the same
-    gradients)."""
-    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state), int(ckpt_rows or 0))
+    interval kept for the backward (None = NAJU_CKPT_ROWS from the
+    environment where served, else the default; 32, 64 or 128 rows, served
+    at 9 <= N <= 64, is the memory-light mode: the backward recomputes the
+    states between, with bitwise the same outputs)."""
+    if ckpt_rows is None:
+        ckpt_rows = _default_ckpt_rows(B.shape[-1])
+    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state), int(ckpt_rows))
 
 
 def resolve_backend(backend=None):

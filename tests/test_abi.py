@@ -375,21 +375,30 @@ def test_checkpoint_interval_size_queries_and_checks():
     base = L.naju_scan_ckpt_elems(B_, T, D, 64, BF16, F32, BF16)
     assert L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, 0) == base
     assert L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, fl(16)) == base
-    for rows in (32, 48, 64, 128, 4080):
+    for rows in (32, 64, 128):
+        # the interval states only: the forward's time segments start at
+        # interval boundaries, so no other state is kept
         n = L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, fl(rows))
-        # the interval states, then the state entering each of the forward's
-        # time segments (a whole number of [batch, D, N] blocks, fewer than
-        # the intervals here)
-        states = B_ * (-(-T // rows)) * D * 64
-        assert n >= states and (n - states) % (B_ * D * 64) == 0 and n - states < B_ * 64 * D * 64
+        assert n == B_ * (-(-T // rows)) * D * 64
+    # intervals that do not divide the forward's 128-row segment unit
+    for rows in (48, 96, 256, 4080):
+        assert L.naju_scan_ckpt_elems_ex(B_, T, D, 64, BF16, F32, BF16, fl(rows)) == -1
+        assert b"interval" in L.naju_scan_last_error()
+    # a longer interval is always lighter than the default, also on small
+    # grids whose forward takes many time segments (one per 16-row sub-block
+    # here: 2 channel tiles, 63 sub-blocks)
+    small = L.naju_scan_ckpt_elems(1, 1000, 128, 64, BF16, F32, BF16)
+    assert small == 1 * 63 * 128 * 64
+    for rows in (32, 64, 128):
+        n = L.naju_scan_ckpt_elems_ex(1, 1000, 128, 64, BF16, F32, BF16, fl(rows))
+        assert n == -(-1000 // rows) * 128 * 64 and n < small
     ws0 = L.naju_scan_workspace_bytes_ex(B_, T, D, 64, BF16, F32, BF16, 0)
     assert ws0 == L.naju_scan_workspace_bytes(B_, T, D, 64, BF16, F32, BF16)
     ws64 = L.naju_scan_workspace_bytes_ex(B_, T, D, 64, BF16, F32, BF16, fl(64))
     # the recomputed states: one float per (b, 16-row sub-block, d, n)
     assert ws64 >= ws0 + B_ * (T // 16) * D * 64 * 4
     # ragged T: the last interval is partial
-    n = L.naju_scan_ckpt_elems_ex(2, 300, 96, 33, F32, F32, F32, fl(64))
-    assert n >= 2 * 5 * 96 * 33 and (n - 2 * 5 * 96 * 33) % (2 * 96 * 33) == 0
+    assert L.naju_scan_ckpt_elems_ex(2, 300, 96, 33, F32, F32, F32, fl(64)) == 2 * 5 * 96 * 33
     # other N: only the default interval (32 rows at N <= 8 and N > 64, the
     # backward's chunk at N = 1)
     assert L.naju_scan_ckpt_elems_ex(2, 300, 96, 4, F32, F32, F32, fl(32)) == 2 * 10 * 96 * 4
@@ -410,3 +419,24 @@ def test_checkpoint_interval_size_queries_and_checks():
         fl(24)
     with pytest.raises(ValueError):
         fl(4096)
+
+
+def test_noalloc_status_host_checks():
+    """naju_scan_noalloc_status rejects a null status pointer on the host."""
+    L = _lib.lib()
+    assert L.naju_scan_noalloc_status(None, None) == _lib.ERR_INVALID
+    assert b"status" in L.naju_scan_last_error()
+
+
+def test_env_checkpoint_interval_default(monkeypatch):
+    """NAJU_CKPT_ROWS sets the interval of calls that name none, where it is
+    served (9 <= N <= 64); other N keep their default."""
+    from naju_amd import scan as scan_mod
+    monkeypatch.delenv("NAJU_CKPT_ROWS", raising=False)
+    assert scan_mod._default_ckpt_rows(64) == 0
+    monkeypatch.setenv("NAJU_CKPT_ROWS", "128")
+    assert scan_mod._default_ckpt_rows(64) == 128
+    assert scan_mod._default_ckpt_rows(9) == 128
+    assert scan_mod._default_ckpt_rows(1) == 0
+    assert scan_mod._default_ckpt_rows(8) == 0
+    assert scan_mod._default_ckpt_rows(65) == 0

@@ -1,6 +1,7 @@
-"""GPU parity at the full sizes of benchmark configurations c3 and c4
-(naju_amd.workloads.CONFIGS, N = 1), against
-the fp64 oracle run over channel slices on the host's cores.
+"""GPU parity at the full sizes of benchmark configurations c2-c4
+(naju_amd.workloads.CONFIGS) at N = 1 and at the mixer's N = 64, and of one
+c5 scan layer, against the fp64 oracle run over channel slices on the
+host's cores.
 
 Config 3 (B=1, T=131072, D=2048, fp32, retention near 1): EVERY output is
 checked against the oracle. The oracle runs on 64-channel slices; y, du, dfl,
@@ -175,6 +176,47 @@ def test_full_size_c2_n64_batch_row(gpu):
     ins = config_inputs("c2", N=64, seed=12, device=gpu)
     y, g = run_hip(ins, gpu)
     _check_row0(ins, y, g, 64)
+
+
+def test_full_size_c4_n64_exact_decay_batch_row(gpu):
+    """Benchmark configuration c4's recipe at the mixer's N = 64 (32 x 8192 x
+    4096, bf16, 10% of the gates exactly 0 and 10% exactly 1), full size.
+    Nearly every 16-row x 16-channel block then holds a hard reset, so the
+    matrix-core kernels take their exact-decay (Horner) path at NP = 64
+    almost everywhere. Batch row 0 of every output in full, dB and dC (sums
+    over all 4096 channels) included; dD over the whole batch."""
+    from naju_amd.workloads import config_inputs
+    print("c4 N=64 full size, seed 44", flush=True)
+    ins = config_inputs("c4", N=64, seed=44, device=gpu)
+    # share of (16 rows x 16 channels) blocks of batch row 0 with a zero gate
+    z = torch.isneginf(ins["f_logit"][0]).view(8192 // 16, 16, 4096 // 16, 16).any(dim=3).any(dim=1)
+    assert float(z.float().mean()) > 0.999
+    y, g = run_hip(ins, gpu)
+    _check_row0(ins, y, g, 256)
+
+
+def test_full_size_c3_n64_every_output(gpu):
+    """Benchmark configuration c3 at N = 64 (1 x 131072 x 2048 fp32,
+    retention near 1: the state carries over the whole 131072 rows), full
+    size: every element of every output against the oracle over 64-channel
+    slices, dB and dC as the slice-ordered sums of the slices' partial sums."""
+    from naju_amd.workloads import config_inputs
+    print("c3 N=64 full size, seed 33", flush=True)
+    ins = config_inputs("c3", N=64, seed=33, device=gpu)
+    y, g = run_hip(ins, gpu)
+    inp = {k: _host(ins[k]) for k in ("u", "f_logit", "i_logit", "dy", "B", "C", "D_skip")}
+    out = {"y": _host(y), "du": _host(g["du"]), "dfl": _host(g["dfl"]), "dil": _host(g["dil"])}
+    del ins
+    tot, dB, dC, dD = _slices_vs_oracle(inp, out, 64)
+    for k in ("y", "du", "dfl", "dil"):
+        tot[k].check(k, torch.float32)
+    for k, ref in (("dB", dB), ("dC", dC)):
+        e = _Err()
+        e.add(_host(g[k]), ref)
+        e.check(k, torch.float32)
+    e = _Err()
+    e.add(_host(g["dD"]), dD)
+    e.check("dD", torch.float32)
 
 
 def test_full_size_c5_scan_layer(gpu):
