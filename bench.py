@@ -421,46 +421,51 @@ def _reference_bench(dev, iters=30, warmup=10):
         n = len(ts)
         return ts[n // 2], ts[max(0, n // 10)], ts[min(n - 1, 9 * n // 10)]
 
+    def one(b, T, D, N, dtype, mode, rows):
+        # everything of the measurement is local, so it is freed on return
+        s = 4 if dtype == torch.float32 else 2
+        scan_mod._WS._bufs.clear()
+        scan_mod._WS._status.clear()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        base = torch.cuda.memory_allocated(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
+        g = torch.Generator(device=dev).manual_seed(0)
+
+        def r(*shape, add=0.0, scale=1.0):
+            # one float32 temporary at a time
+            return (torch.randn(*shape, generator=g, device=dev) * scale + add).to(dtype)
+        ins = [r(b, T, D), r(b, T, D, add=2.0), r(b, T, D, add=-1.0), r(b, T, N, scale=N ** -0.5),
+               r(b, T, N, scale=N ** -0.5), r(D, scale=0.01)]
+        in_bytes = sum(x.numel() * x.element_size() for x in ins)
+        if mode == "fwd":
+            with torch.no_grad():
+                med, p10, p90 = timed(lambda: naju_scan_hip(*ins))
+            nbytes = algorithmic_bytes(b, T, D, N, s, s, s, False, fwd=True, bwd=False)
+        else:
+            for x in ins:
+                x.requires_grad_(True)
+            dy = torch.randn(b, T, D, device=dev, generator=g).to(dtype)
+
+            def step():
+                naju_scan_hip(*ins, ckpt_rows=rows).backward(dy)
+                for x in ins:
+                    x.grad = None
+            med, p10, p90 = timed(step)
+            nbytes = algorithmic_bytes(b, T, D, N, s, s, s, False)
+        peak = torch.cuda.max_memory_allocated(dev) - base
+        gbs = nbytes / (med * 1e-3) / 1e9
+        return {"ms_median": round(med, 4), "ms_p10": round(p10, 4), "ms_p90": round(p90, 4),
+                "peak_GiB": round(peak / 2 ** 30, 3), "inputs_GiB": round(in_bytes / 2 ** 30, 3),
+                "Mtok_per_s": round(b * T / (med * 1e-3) / 1e6, 2),
+                "GBs": round(gbs, 1), "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2)}
+
     res = {}
     for dtype, dname in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
         for (b, T, D, N) in REF_BENCH_SHAPES:
-            s = 4 if dtype == torch.float32 else 2
-            entry = {}
-            for mode, rows in (("fwd", None), ("fwd+bwd", None), ("fwd+bwd ckpt128", 128)):
-                scan_mod._WS._bufs.clear()
-                scan_mod._WS._status.clear()
-                torch.cuda.synchronize()
-                torch.cuda.empty_cache()
-                base = torch.cuda.memory_allocated(dev)
-                torch.cuda.reset_peak_memory_stats(dev)
-                g = torch.Generator(device=dev).manual_seed(0)
-
-                def r(*shape):
-                    return torch.randn(*shape, generator=g, device=dev)
-                ins = [r(b, T, D), r(b, T, D) + 2.0, r(b, T, D) - 1.0, r(b, T, N) / N ** 0.5, r(b, T, N) / N ** 0.5,
-                       r(D) * 0.01]
-                ins = [x.to(dtype) for x in ins]
-                if mode == "fwd":
-                    with torch.no_grad():
-                        med, p10, p90 = timed(lambda: naju_scan_hip(*ins))
-                    nbytes = algorithmic_bytes(b, T, D, N, s, s, s, False, fwd=True, bwd=False)
-                else:
-                    xs = [x.requires_grad_(True) for x in ins]
-                    dy = torch.randn(b, T, D, device=dev, dtype=dtype, generator=g)
-
-                    def step():
-                        naju_scan_hip(*xs, ckpt_rows=rows).backward(dy)
-                        for x in xs:
-                            x.grad = None
-                    med, p10, p90 = timed(step)
-                    nbytes = algorithmic_bytes(b, T, D, N, s, s, s, False)
-                peak = torch.cuda.max_memory_allocated(dev) - base
-                gbs = nbytes / (med * 1e-3) / 1e9
-                entry[mode] = {"ms_median": round(med, 4), "ms_p10": round(p10, 4), "ms_p90": round(p90, 4),
-                               "peak_GiB": round(peak / 2 ** 30, 3), "Mtok_per_s": round(b * T / (med * 1e-3) / 1e6, 2),
-                               "GBs": round(gbs, 1), "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2)}
-                del ins
-            res[f"{dname} B={b} T={T} d_inner={D} N={N}"] = entry
+            res[f"{dname} B={b} T={T} d_inner={D} N={N}"] = {
+                mode: one(b, T, D, N, dtype, mode, rows)
+                for mode, rows in (("fwd", None), ("fwd+bwd", None), ("fwd+bwd ckpt128", 128))}
     scan_mod._WS._bufs.clear()
     scan_mod._WS._status.clear()
     torch.cuda.empty_cache()

@@ -215,7 +215,7 @@ def test_noalloc_graph_capture_replays(gpu, N, shape, dtype):
     torch.cuda.synchronize()
     for rep in range(4):
         ins = rand_inputs(*shape, N, seed=200 * rep + N, dtype=dtype, h0_std=0.2)
-        for k in ("u", "f_logit", "i_logit", "B", "C", "h0"):
+        for k in ("u", "f_logit", "i_logit", "B", "C", "D_skip", "h0"):
             t[k].copy_(ins[k].to(gpu))
         for o in (y, ck, hT):
             o.fill_(float("nan"))
