@@ -294,20 +294,24 @@ struct McIn {
     for (int k = 0; k < Raw4<TB>::NW; ++k) asm volatile("" : "+v"(b.w[k]), "+v"(c.w[k]));
   }
 
-  // B (and C) into LDS buffer buf; zeros past T and past N
+  // B (and C) into LDS buffer buf; zeros past T and past N. (Each 16 lanes
+  // read one 64-entry row of B and C, coalesced; the backward's staging takes
+  // another lane map, which the forward measured slower with.)
   __device__ __forceinline__ void stage(McBC<NP, MAP>& sh, int buf, const ScanArgs& a, int64_t t0, int tid) const {
     if (tid < 4 * NP) {
       const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
       const bool rok = t0 + row < a.T;
+      float vb[4], vc[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool ok = rok && n0 + e < a.N;
-        const float vb = ok ? b.get(e) : 0.f;
-        sh.Bt[buf][n0 + e][4 * (row & 3) + (row >> 2)] = vb;
-        if constexpr (!MAP) {
-          sh.Bn[buf][row][n0 + e] = vb;
-          sh.C[buf][row][n0 + e] = ok ? c.get(e) : 0.f;
-        }
+        vb[e] = ok ? b.get(e) : 0.f;
+        if constexpr (!MAP) vc[e] = ok ? c.get(e) : 0.f;
+        sh.Bt[buf][n0 + e][4 * (row & 3) + (row >> 2)] = vb[e];
+      }
+      if constexpr (!MAP) {
+        *(float4*)&sh.Bn[buf][row][n0] = make_float4(vb[0], vb[1], vb[2], vb[3]);
+        *(float4*)&sh.C[buf][row][n0] = make_float4(vc[0], vc[1], vc[2], vc[3]);
       }
     }
   }
@@ -770,7 +774,7 @@ struct McInB {
     }
     if (tid < 4 * NP) {
       const int N = a.N;
-      const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
+      const int row = tid % kMcQ, n0 = 4 * (tid / kMcQ);
       const int64_t bb = ((int64_t)b_row * T + t0) * N;
       const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * N);
       if (N == NP) {
@@ -796,22 +800,31 @@ struct McInB {
     for (int k = 0; k < Raw4<TB>::NW; ++k) asm volatile("" : "+v"(b.w[k]), "+v"(c.w[k]));
   }
 
+  // B and C into LDS. Thread tid < 4 NP takes row tid % 16, entries n0 ..
+  // n0+3 with n0 = 4 (tid / 16): a half-wave holds all 16 rows of two
+  // groups of entries, so the transposed tiles' 4-byte writes fall on 32
+  // different banks, and each [t][n] tile takes one 16-byte write per lane
+  // (the forward's row-per-16-lanes map costs 14 and 6 extra LDS cycles per
+  // write there, about 1.4% of this kernel).
   __device__ __forceinline__ void stage(McBwdLds<NP, MAP>& sh, const ScanArgs& a, int64_t t0, int tid) const {
     if (tid < 4 * NP) {
-      const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
+      const int row = tid % kMcQ, n0 = 4 * (tid / kMcQ);
       const bool rok = t0 + row < a.T;
       const int pr = 4 * (row & 3) + (row >> 2);
+      float vb[4], vc[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool ok = rok && n0 + e < a.N;
-        const float vc = ok ? c.get(e) : 0.f;
-        sh.Ct[n0 + e][pr] = vc;
+        vc[e] = ok ? c.get(e) : 0.f;
+        sh.Ct[n0 + e][pr] = vc[e];
         if constexpr (!MAP) {
-          const float vb = ok ? b.get(e) : 0.f;
-          sh.Bt[n0 + e][pr] = vb;
-          sh.Bn[row][n0 + e] = vb;
-          sh.C[row][n0 + e] = vc;
+          vb[e] = ok ? b.get(e) : 0.f;
+          sh.Bt[n0 + e][pr] = vb[e];
         }
+      }
+      if constexpr (!MAP) {
+        *(float4*)&sh.Bn[row][n0] = make_float4(vb[0], vb[1], vb[2], vb[3]);
+        *(float4*)&sh.C[row][n0] = make_float4(vc[0], vc[1], vc[2], vc[3]);
       }
     }
   }
