@@ -103,7 +103,8 @@ __device__ __forceinline__ T* sreg(T* p) {
   return (T*)(__attribute__((address_space(1))) T*)v;
 }
 
-template <typename T, int V, int MODE>
+// NT: a non-temporal load (a stream read once per call).
+template <typename T, int V, int MODE, bool NT = false>
 __device__ __forceinline__ void ld_row_raw(const T* __restrict__ p, uint32_t lo, int64_t d0, int64_t D,
                                            RawRow<T, V>& o) {
   constexpr int NW = RawRow<T, V>::NW;
@@ -112,7 +113,8 @@ __device__ __forceinline__ void ld_row_raw(const T* __restrict__ p, uint32_t lo,
     // 4-byte load each
     typedef uint32_t vw __attribute__((ext_vector_type(NW)));
     if (MODE == kVecAll || d0 < D) {
-      const vw v = *reinterpret_cast<const vw*>(at_lane(p, lo));
+      const vw v = NT ? __builtin_nontemporal_load(reinterpret_cast<const vw*>(at_lane(p, lo)))
+                      : *reinterpret_cast<const vw*>(at_lane(p, lo));
 #pragma unroll
       for (int k = 0; k < NW; ++k) o.w[k] = v[k];
     } else {
@@ -136,7 +138,13 @@ __device__ __forceinline__ void ld_row_raw(const T* __restrict__ p, uint32_t lo,
 }
 
 // st_row at row pointer p (uniform, the tile's first channel) and lane
-// element offset lo (channel d0 = tile start + lo).
+// element offset lo (channel d0 = tile start + lo). The rows stored here are
+// the N = 1 kernels' outputs (y; du, dfl, dil), written once per call and
+// not read again by the scan: non-temporal stores, so they do not take the
+// caches' room from the input streams, which the backward reads again after
+// the forward (at config 2 the step went from 187 to 165 us with them, with
+// the dy loads below from 165 to 150; at configs 3 and 4, whose streams far
+// exceed the last-level cache, 3-5% per step).
 template <typename T, int V, int MODE>
 __device__ __forceinline__ void st_row_at(T* __restrict__ p, uint32_t lo, int64_t d0, int64_t D,
                                           const float (&x)[V]) {
@@ -144,13 +152,13 @@ __device__ __forceinline__ void st_row_at(T* __restrict__ p, uint32_t lo, int64_
   if constexpr (MODE == kElem) {
 #pragma unroll
     for (int j = 0; j < V; ++j)
-      if (d0 + j < D) at_lane(p, lo)[j] = from_f32<T>(x[j]);
+      if (d0 + j < D) __builtin_nontemporal_store(from_f32<T>(x[j]), at_lane(p, lo) + j);
   } else {
     if (MODE == kVecAll || d0 < D) {
       vec_t v;
 #pragma unroll
       for (int j = 0; j < V; ++j) v[j] = from_f32<T>(x[j]);
-      *reinterpret_cast<vec_t*>(at_lane(p, lo)) = v;
+      __builtin_nontemporal_store(v, reinterpret_cast<vec_t*>(at_lane(p, lo)));
     }
   }
 }
@@ -400,13 +408,13 @@ __device__ __forceinline__ void wg_look_back(const ScanArgs& a, LookShared<V, W,
 
 // Rows [t0, t0+R) (rowbase = b*T + t0) of one [batch,T,D] stream, p at the
 // tile's first channel. ROWCHK: rows at or beyond T read as 0.
-template <typename T, int V, int R, int MODE, bool ROWCHK>
+template <typename T, int V, int R, int MODE, bool ROWCHK, bool NT = false>
 __device__ __forceinline__ void ld_rows_raw(const T* __restrict__ p, int64_t rowbase, int t0, int64_t Tn, int64_t D,
                                             uint32_t lo, int64_t d0, RawRow<T, V> (&o)[R]) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (!ROWCHK || t0 + r < Tn) {
-      ld_row_raw<T, V, MODE>(sreg(p + (rowbase + r) * D), lo, d0, D, o[r]);
+      ld_row_raw<T, V, MODE, NT>(sreg(p + (rowbase + r) * D), lo, d0, D, o[r]);
     } else {
 #pragma unroll
       for (int k = 0; k < RawRow<T, V>::NW; ++k) o[r].w[k] = 0u;
@@ -653,7 +661,8 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   ld_rows_raw<TU, V, R, M, !FULL>((const TU*)a.u + dbase, rowbase, t0, T, D, lo, d0, xu);
   ld_rows_raw<TG, V, R, M, !FULL>((const TG*)a.fl + dbase, rowbase, t0, T, D, lo, d0, lf);
   ld_rows_raw<TG, V, R, M, !FULL>((const TG*)a.il + dbase, rowbase, t0, T, D, lo, d0, li);
-  ld_rows_raw<TU, V, R, M, !FULL>((const TU*)a.dy + dbase, rowbase, t0, T, D, lo, d0, xg);
+  // dy is read once per call (non-temporal loads, like the output stores)
+  ld_rows_raw<TU, V, R, M, !FULL, true>((const TU*)a.dy + dbase, rowbase, t0, T, D, lo, d0, xg);
   ld_bc<TB, R, !FULL>((const TB*)a.Bm, (const TB*)a.Cm, rowbase, t0, T, lane, Bt, Ct);
   float s[V];
 #pragma unroll
