@@ -7,7 +7,9 @@ default workload is benchmark configuration c2 (naju_amd.workloads.CONFIGS): B=8
 streams with fp32 state, N=1 (B=C=1), h0 ~ N(0, 0.1^2), dy ~ N(0,1).
 
 value = algorithmic bytes of fwd+bwd per step * K / wall time of K steps
-(GB/s). The roofline object reports the dominant kernel (the backward) from
+(GB/s), after W untimed warmup steps continued until at least WARM_MS of
+warmup have passed (the GPU's clocks ramp over the first milliseconds of
+work). The roofline object reports the dominant kernel (the backward) from
 HIP events recorded on the launch stream inside the timed region. The same
 line carries the step timed after a 1 GiB cache-flush write, and (default
 c2, N = 1 run) a "configs" table: c1, c3 and c4 at N = 1 (c3 / c4 against the
@@ -84,6 +86,8 @@ def _dt_size(dt):
 # rooflines of the per-config lines: %-of-HBM targets from the survey's
 # measurement plan (70% of 8 TB/s on the fused fwd+bwd at N = 1)
 TARGET_FRAC = 0.70
+# minimum wall time of the headline's untimed warmup (besides its W steps)
+WARM_MS = 100.0
 
 
 def _scan_case(L, config, N, dev, seed=0):
@@ -146,8 +150,13 @@ def _time_case(case, steps, warmup, stream, min_warm_ms=0.0):
     passed (the GPU's clocks ramp up over the first milliseconds of work: a
     C2 N=1 step measures 0.192 ms after 10 warmup steps, 0.186 ms after 200)."""
     import torch
+    # the first step (code loading, first-touch allocations) is not counted
+    # towards min_warm_ms
+    case["fwd"]()
+    case["bwd"]()
+    torch.cuda.synchronize()
     t_w = time.perf_counter()
-    k = 0
+    k = 1
     while k < warmup or (time.perf_counter() - t_w) * 1e3 < min_warm_ms:
         case["fwd"]()
         case["bwd"]()
@@ -155,6 +164,7 @@ def _time_case(case, steps, warmup, stream, min_warm_ms=0.0):
         if k >= warmup and min_warm_ms > 0 and k % 8 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+    n_warm = k
     t0 = time.perf_counter()
     for _ in range(steps):
         case["fwd"]()
@@ -174,7 +184,7 @@ def _time_case(case, steps, warmup, stream, min_warm_ms=0.0):
     if case["status"]() != 0:
         raise RuntimeError("workspace status nonzero: a carry hand-off timed out")
     return dict(ms_step=ms_step, fwd_avg=sum(t_fwd) / steps, bwd_avg=sum(t_bwd) / steps,
-                fwd_med=t_fwd[len(t_fwd) // 2], bwd_med=t_bwd[len(t_bwd) // 2])
+                fwd_med=t_fwd[len(t_fwd) // 2], bwd_med=t_bwd[len(t_bwd) // 2], warmup_run=n_warm)
 
 
 def _config_entry(L, config, N, dev, steps, warmup, target_ms=None):
@@ -212,7 +222,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed warmup steps (default: 200 scan steps, 3 LM steps for --config c5)")
+                    help="untimed warmup steps (default: 200 scan steps, 3 LM steps for --config c5); "
+                         "the scan's warmup also lasts at least WARM_MS = 100 ms")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="c1-c4: the scan itself; c5: the LM training step (tokens/s)")
     ap.add_argument("--N", type=int, default=1, help="state size (d_state)")
@@ -255,7 +266,9 @@ def main():
     N = args.N
     case = _scan_case(L, args.config, N, dev)
     stream = torch.cuda.current_stream(dev)
-    t = _time_case(case, args.steps, args.warmup, stream)
+    # at least W warmup steps, and at least 100 ms of them: the clocks ramp
+    # over the first milliseconds of work whatever W is
+    t = _time_case(case, args.steps, args.warmup, stream, min_warm_ms=WARM_MS)
     Bsz, T, D, _ = case["shape"]
     bytes_fwd, bytes_bwd = case["bytes_fwd"], case["bytes_bwd"]
     bytes_step = bytes_fwd + bytes_bwd
@@ -269,6 +282,8 @@ def main():
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "warmup_steps_run": t["warmup_run"],
+        "warmup_min_ms": WARM_MS,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
