@@ -629,7 +629,8 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
                                             bool poison,
                                             float (&s_F)[W][64 * V], float (&s_Z)[W][64 * V],
                                             float (&s_Zb)[W][64 * V], float (&s_g)[64 * V],
-                                            LookShared<V, W, P>& s_lb, float (&s_pq)[W][2 * R][64]) {
+                                            float (&s_dD)[W][64 * V], LookShared<V, W, P>& s_lb,
+                                            float (&s_pq)[W][2 * R][64]) {
   using TDU = std::conditional_t<F32O, float, TU>;  // du dtype
   using TDG = std::conditional_t<F32O, float, TG>;  // dfl, dil dtype
   constexpr int CH = 64 * V;
@@ -695,6 +696,15 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   for (int r = R - 1; r >= 0; --r)
 #pragma unroll
     for (int j = 0; j < V; ++j) G[j] = xf[r][j] * fmaf(xg[r].get(j), Ct[r], G[j]);
+  // this wave's dD terms sum_t dy u (they need no scan): summed over the
+  // workgroup by wave 0 behind the barrier below
+  float dDs[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) dDs[j] = 0.f;
+#pragma unroll
+  for (int r = R - 1; r >= 0; --r)
+#pragma unroll
+    for (int j = 0; j < V; ++j) dDs[j] = fmaf(xg[r].get(j), xu[r].get(j), dDs[j]);
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -704,6 +714,7 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
     s_F[wv][j * 64 + lane] = F[j];
     s_Z[wv][j * 64 + lane] = Z[j];
     s_Zb[wv][j * 64 + lane] = G[j];
+    s_dD[wv][j * 64 + lane] = dDs[j];
   }
   __syncthreads();
 
@@ -735,6 +746,15 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
       for (int j = 0; j < V; ++j) {
         st_word(my_agg + j * 64, A[j], tag);
         st_word(my_agg + CH + j * 64, Zb[j], tag);
+      }
+    }
+    if (a.partD) {
+      // the chunk's dD partial: the waves' sums in wave order
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float acc = 0.f;
+        for (int w = 0; w < W; ++w) acc += s_dD[w][j * 64 + lane];
+        if (dok[j]) a.partD[((int64_t)b * a.K + k) * D + d0 + j] = acc;
       }
     }
   }
@@ -777,9 +797,6 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
   // f(1-f) and i(1-i) as fma(-f, f, f), exactly 0 at f in {0, 1}.
   // This lane's terms of the dB / dC sums of row r go to s_pq[wv][r] /
   // s_pq[wv][R + r] (in LDS rather than registers: 2R fewer live VGPRs).
-  float dDs[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) dDs[j] = 0.f;
 #pragma unroll
   for (int r = R - 1; r >= 0; --r) {
     float pb = 0.f, pc = 0.f;
@@ -793,7 +810,6 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
       const float dws = xb * Bt[r];
       pb = fmaf(xb, iu, pb);
       pc = fmaf(gy, xs[r][j], pc);
-      dDs[j] = fmaf(gy, x, dDs[j]);
       g[j] = f * xb;
       dfl[j] = fmaf(-f, f, f) * (xb * xprev);
       dil[j] = fmaf(-ig, ig, ig) * (dws * x);
@@ -836,20 +852,6 @@ __device__ __forceinline__ void n1_bwd_body(const ScanArgs& a, int k, int tile, 
       if (dst) dst[(int64_t)dtile * a.batch * T + (int64_t)b * T + t] = acc;
     }
   }
-  if (a.partD) {
-    __syncthreads();  // every wave has read s_Z for its carry
-#pragma unroll
-    for (int j = 0; j < V; ++j) s_Z[wv][j * 64 + lane] = dDs[j];
-    __syncthreads();
-    if (wv == 0) {
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        float acc = 0.f;
-        for (int w = 0; w < W; ++w) acc += s_Z[w][j * 64 + lane];
-        if (dok[j]) a.partD[((int64_t)b * a.K + k) * D + d0 + j] = acc;
-      }
-    }
-  }
 }
 
 template <typename TU, typename TG, typename TB, int V, int R, int W, int P, bool VEC, bool F32O>
@@ -861,6 +863,7 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   __shared__ float s_Z[W][CH];
   __shared__ float s_Zb[W][CH];
   __shared__ float s_g[CH];
+  __shared__ float s_dD[W][CH];
   __shared__ LookShared<V, W, P> s_lb;
   __shared__ __align__(16) float s_pq[W][2 * R][64];
 
@@ -877,11 +880,13 @@ __global__ __launch_bounds__(64 * W) void n1_bwd_kernel(const ScanArgs a) {
   const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   if constexpr (VEC) {
     if ((int64_t)(k + 1) * L <= a.T && (int64_t)(dtile + 1) * CH <= a.D) {
-      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb, s_pq);
+      n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, true>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_dD,
+                                                             s_lb, s_pq);
       return;
     }
   }
-  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_lb, s_pq);
+  n1_bwd_body<TU, TG, TB, V, R, W, P, VEC, F32O, false>(a, k, tile, lane, wv, tag, poison, s_F, s_Z, s_Zb, s_g, s_dD,
+                                                        s_lb, s_pq);
 }
 
 // Sum over q < n_parts of p[q*stride + i], in q order, with the loads of
