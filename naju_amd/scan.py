@@ -133,7 +133,10 @@ def _raise_pending(dev, stream):
     workspace is nonzero (a failed hand-off in an earlier call: its outputs
     were NaN). Does not wait for a copy still in flight: the word stays set
     on the device until cleared, so a later copy shows it. On raising, the
-    word is cleared (synchronously), so the workspace is usable again."""
+    word is cleared (synchronously), so the workspace is usable again.
+    Nothing is queried while the stream is being captured into a graph."""
+    if torch.cuda.is_current_stream_capturing():
+        return
     ent = _WS._status.get((dev.index, stream))
     if ent is None or not ent[1].query():
         return
