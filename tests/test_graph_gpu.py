@@ -127,3 +127,39 @@ def test_graph_back_to_back_replays_with_new_inputs(gpu, N, shape, dtype):
         assert ref_status() == 0
         for k, v in got[rep].items():
             assert torch.equal(v, ref_bufs[k]), f"replay {rep}: {k} differs from an eager call on its inputs"
+
+
+@pytest.mark.parametrize("N,shape,dtype", [(1, (2, 1000, 256), torch.bfloat16), (16, (2, 300, 128), torch.float32)])
+def test_wrapper_inference_forward_captures(gpu, N, shape, dtype):
+    """naju_scan_hip's no-grad forward captured into a graph through the
+    Python wrapper: its asynchronous status watching stays out of the capture
+    (no copy recorded, no event queried while capturing), and every replay on
+    new inputs equals an eager call on them bitwise (with torch's
+    deterministic mode on, which selects fixed-order N = 1 carries)."""
+    from naju_amd import naju_scan_hip
+    names = ("u", "f_logit", "i_logit", "B", "C", "D_skip", "h0")
+    ins = rand_inputs(*shape, N, seed=90 + N, dtype=dtype, h0_std=0.2)
+    t = {k: ins[k].to(gpu) for k in names}
+    s = torch.cuda.Stream(gpu)
+    was = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True)
+    try:
+        with torch.no_grad(), torch.cuda.stream(s):
+            naju_scan_hip(*[t[k] for k in names])  # the workspace exists before capture
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                y = naju_scan_hip(*[t[k] for k in names])
+        torch.cuda.synchronize()
+        for rep in range(3):
+            new = rand_inputs(*shape, N, seed=200 + 10 * rep + N, dtype=dtype, h0_std=0.2)
+            for k in names:
+                t[k].copy_(new[k].to(gpu))
+            g.replay()
+            torch.cuda.synchronize()
+            with torch.no_grad():
+                ref = naju_scan_hip(*[new[k].to(gpu) for k in names])
+            torch.cuda.synchronize()
+            assert torch.equal(y, ref), f"replay {rep} differs from an eager call on its inputs"
+    finally:
+        torch.use_deterministic_algorithms(was)
