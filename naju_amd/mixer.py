@@ -33,6 +33,7 @@ from torch.utils.checkpoint import checkpoint
 
 from naju_amd import gradsink
 from naju_amd.dwconv import dwconv
+from naju_amd.linear import compute_dtype, linear
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
 from naju_amd.rmsnorm import supported as rmsnorm_supported
@@ -66,6 +67,14 @@ class RMSNorm(nn.Module):
 def _out_dtype(x):
     dev = x.device.type
     return torch.get_autocast_dtype(dev) if torch.is_autocast_enabled(dev) else x.dtype
+
+
+def _linear(x, weight):
+    """F.linear(x, weight) (no bias); on CUDA in 16-bit compute with the
+    split-K float32 weight gradient of naju_amd.linear."""
+    if compute_dtype(x) is not None:
+        return linear(x, weight)
+    return F.linear(x, weight)
 
 
 def _causal_dwconv(x, conv):
@@ -149,7 +158,7 @@ class NajuMixer(nn.Module):
         return F.silu(_causal_dwconv(x, self.conv1d))
 
     def forward(self, u):
-        xz = self.in_proj(u)
+        xz = _linear(u, self.in_proj.weight)
         if xz.is_cuda:
             # x feeds the content convolution and z the readout; both write
             # their gradients straight into one buffer for in_proj
@@ -164,7 +173,7 @@ class NajuMixer(nn.Module):
             # the convolutions read their slices in place
             di, N = self.d_inner, self.d_state
             w = torch.cat([self.f_proj.weight, self.i_proj.weight, self.x_proj.weight], 0)
-            p_f, p_i, Bm, Cm = gradsink.split(F.linear(h, w), [di, di, N, N])
+            p_f, p_i, Bm, Cm = gradsink.split(_linear(h, w), [di, di, N, N])
             f_logit = self._gate_logit(h, None, self.f_conv, self.f_bias, p=p_f)
             i_logit = self._gate_logit(h, None, self.i_conv, self.i_bias, p=p_i)
         else:
@@ -179,7 +188,7 @@ class NajuMixer(nn.Module):
             y = readout(cx, h, z, self.D, self._cx_scale, out_dtype=_out_dtype(h))
         else:
             y = (cx * self._cx_scale + self.D * h) * F.silu(z)
-        return self.out_proj(y)
+        return _linear(y, self.out_proj.weight)
 
 
 class NajuBlock(nn.Module):

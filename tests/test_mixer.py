@@ -155,3 +155,13 @@ def test_build_optimizer_groups():
     mult = math.sqrt(16)
     assert g["lr"] == pytest.approx(1e-3 * mult) and g["weight_decay"] == pytest.approx(0.1 / mult)
     assert g["eps"] == pytest.approx(1e-8 / mult) and len(g["params"]) == 4
+
+
+def test_linear_token_parts_rule():
+    """The split-K weight gradient's token parts (naju_amd.linear._parts)."""
+    from naju_amd.linear import _parts
+    assert _parts(16384, 768, 1536) == 8
+    assert _parts(16384, 3200, 1536) == 2
+    assert _parts(16384, 3072, 768) == 4
+    assert _parts(666, 40, 96) == 1          # too few tokens per part
+    assert _parts(16384, 50257, 768) == 1    # many output tiles already
