@@ -55,8 +55,13 @@ size_t naju_dwconv_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K);
  * pre-activation is recomputed from x. The gradient of add is dy itself;
  * dadd (act = 0 only, nullable) receives it in dadd_dtype with dadd_ld
  * elements between rows, so that it lands in place in a wider gradient
- * buffer (one slice of a fused projection's gradient). Deterministic
- * (fixed-order sums). The autograd of the reference's Conv1d + slice. */
+ * buffer (one slice of a fused projection's gradient). act may carry
+ * NAJU_DWCONV_ACCUM_DX: dx then receives dx + (the gradient), rounded once
+ * to dx_dtype, so that x's gradient from several consumers collects in one
+ * buffer without separate additions (no reference counterpart: autograd
+ * adds them there). Deterministic (fixed-order sums). The autograd of the
+ * reference's Conv1d + slice. */
+#define NAJU_DWCONV_ACCUM_DX 2
 int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
                     int64_t dx_ld, float* dw, float* dbias, void* dadd, int64_t dadd_ld, int64_t batch, int64_t T,
                     int64_t C, int K, int act, int x_dtype, int dy_dtype, int dx_dtype, int dadd_dtype,

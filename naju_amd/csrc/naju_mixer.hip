@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int
                                                              const float* bias, const void* dy, void* dx,
                                                              int64_t ld_dx, void* dadd, int64_t ld_dadd, float* part,
                                                              int64_t T, int64_t C, int x_dt, int dy_dt, int dx_dt,
-                                                             int dadd_dt) {
+                                                             int dadd_dt, int acc) {
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (c >= C) return;
   const int64_t b = blockIdx.z;
@@ -135,7 +135,10 @@ __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int
       float g = wr[K - 1] * dz;
 #pragma unroll
       for (int j = 0; j < K - 1; ++j) g = fmaf(wr[j], gz[K - 2 - j], g);
-      if (dx) stv(dx, dx_dt, (b * T + t) * ld_dx + c, g);
+      if (dx) {
+        const int64_t o = (b * T + t) * ld_dx + c;
+        stv(dx, dx_dt, o, acc ? ldv(dx, dx_dt, o) + g : g);
+      }
       if (dadd) stv(dadd, dadd_dt, (b * T + t) * ld_dadd + c, dz);
 #pragma unroll
       for (int j = 0; j < K; ++j) dw[j] = fmaf(dz, xv[j], dw[j]);
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, 
                                                       const float* __restrict__ w, const float* __restrict__ bias,
                                                       const TDY* __restrict__ dy, TX* __restrict__ dx, int64_t ld_dx,
                                                       TX* __restrict__ dadd, int64_t ld_dadd,
-                                                      float* __restrict__ part, int64_t T, int64_t C) {
+                                                      float* __restrict__ part, int64_t T, int64_t C, int acc) {
   constexpr int K = 4;
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
   if (c0 >= C) return;
@@ -390,7 +393,17 @@ __global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, 
         for (int k = 0; k < K; ++k) dw[j][k] = fmaf(dz[j], xv[k][j], dw[j][k]);
         db[j] += dz[j];
       }
-      if (dx) st8(dx + (b * T + t) * ld_dx + c0, g);
+      if (dx) {
+        TX* q = dx + (b * T + t) * ld_dx + c0;
+        if (acc) {
+          // dx += g: one rounding to TX of the sum
+          float o[kVec];
+          ld8(q, o);
+#pragma unroll
+          for (int j = 0; j < kVec; ++j) g[j] += o[j];
+        }
+        st8(q, g);
+      }
       if (!SILU && dadd) st8(dadd + (b * T + t) * ld_dadd + c0, dz);
     }
 #pragma unroll
@@ -530,11 +543,16 @@ int fail(int code, const char* fmt, ...) {
 
 bool dt_ok(int dt) { return dt == NAJU_DTYPE_F32 || dt == NAJU_DTYPE_BF16 || dt == NAJU_DTYPE_F16; }
 
-int check(int64_t batch, int64_t T, int64_t C, int K, int act, int64_t x_ld) {
+// act: 0 (identity) or 1 (SiLU); the backward also takes
+// NAJU_DWCONV_ACCUM_DX in it (acc_ok).
+int check(int64_t batch, int64_t T, int64_t C, int K, int act, int64_t x_ld, bool acc_ok = false) {
   if (batch < 0 || T < 0 || C < 0) return fail(NAJU_ERR_INVALID, "negative shape");
   if (x_ld < C) return fail(NAJU_ERR_INVALID, "x_ld (%lld) must be >= C (%lld)", (long long)x_ld, (long long)C);
   if (K < 1 || K > kMaxK) return fail(NAJU_ERR_UNSUPPORTED, "kernel size K must be in [1, %d], got %d", kMaxK, K);
-  if (act != 0 && act != 1) return fail(NAJU_ERR_INVALID, "act must be 0 (identity) or 1 (SiLU)");
+  const int a = acc_ok ? (act & ~NAJU_DWCONV_ACCUM_DX) : act;
+  if (a != 0 && a != 1)
+    return fail(NAJU_ERR_INVALID, acc_ok ? "act must be 0 (identity) or 1 (SiLU), optionally | NAJU_DWCONV_ACCUM_DX"
+                                         : "act must be 0 (identity) or 1 (SiLU)");
   if (batch > 65535 || (T + kRows - 1) / kRows > 65535 || C > (1ll << 30))
     return fail(NAJU_ERR_UNSUPPORTED, "shape too large (batch <= 65535, T <= %d)", 65535 * kRows);
   return NAJU_OK;
@@ -543,7 +561,7 @@ int check(int64_t batch, int64_t T, int64_t C, int K, int act, int64_t x_ld) {
 typedef void (*fwd_t)(const void*, int64_t, const float*, const float*, const void*, int64_t, void*, int64_t, int64_t,
                       int, int, int);
 typedef void (*bwd_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, void*, int64_t,
-                      float*, int64_t, int64_t, int, int, int, int);
+                      float*, int64_t, int64_t, int, int, int, int, int);
 
 template <int K>
 fwd_t pick_fwd_k(bool silu) {
@@ -583,8 +601,7 @@ int64_t n_tblocks(int64_t T) { return (T + kRows - 1) / kRows; }
 typedef void (*dwf_vec_t)(const void*, int64_t, const float*, const float*, const void*, int64_t, void*, int64_t,
                           int64_t);
 typedef void (*dwb_vec_t)(const void*, int64_t, const float*, const float*, const void*, void*, int64_t, void*,
-                          int64_t, float*, int64_t,
-                          int64_t);
+                          int64_t, float*, int64_t, int64_t, int);
 
 template <typename TX>
 dwf_vec_t dwf_vec_for(int y_dt, bool silu, bool add) {
@@ -624,6 +641,7 @@ dwb_vec_t dwb_vec_for(int dy_dt, bool silu) {
 dwb_vec_t pick_bwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* dy, void* dx,
                        int64_t dx_ld, const void* dadd, int64_t dadd_ld, int64_t T, int64_t C, int K, int act,
                        int x_dt, int dy_dt, int dx_dt, int dadd_dt) {
+  // act: the activation only (the accumulate bit is taken off by the caller)
   if (K != 4 || C % kVec || x_ld % kVec || dx_ld % kVec || (dadd && dadd_ld % kVec) ||
       (T + kVRowsB - 1) / kVRowsB > 65535)
     return nullptr;
@@ -972,8 +990,10 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
                     int64_t C, int K, int act, int x_dtype, int dy_dtype, int dx_dtype, int dadd_dtype,
                     void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
-  int rc = check(batch, T, C, K, act, x_ld);
+  int rc = check(batch, T, C, K, act, x_ld, true);
   if (rc) return rc;
+  const int acc = (act & NAJU_DWCONV_ACCUM_DX) ? 1 : 0;
+  act &= ~NAJU_DWCONV_ACCUM_DX;
   if (!dt_ok(x_dtype) || !dt_ok(dy_dtype) || !dt_ok(dx_dtype) || (dadd && !dt_ok(dadd_dtype)))
     return fail(NAJU_ERR_INVALID, "unknown dtype code");
   if (dx && dx_ld < C) return fail(NAJU_ERR_INVALID, "dx_ld (%lld) must be >= C (%lld)", (long long)dx_ld, (long long)C);
@@ -1000,12 +1020,12 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
                                   dx_dtype, dadd_dtype)) {
     const int64_t ntb = (T + kVRowsB - 1) / kVRowsB;
     const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)ntb, (unsigned)batch);
-    hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C);
+    hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C, acc);
     nblk = batch * ntb;
   } else {
     const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
     hipLaunchKernelGGL(pick_bwd(K, act == 1), grid, dim3(kThreads), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd,
-                       dadd_ld, part, T, C, x_dtype, dy_dtype, dx_dtype, dadd_dtype);
+                       dadd_ld, part, T, C, x_dtype, dy_dtype, dx_dtype, dadd_dtype, acc);
     nblk = batch * n_tblocks(T);
   }
   const hipError_t e = hipGetLastError();

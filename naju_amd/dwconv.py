@@ -19,9 +19,11 @@ and a missing library raises.
 import torch
 
 from naju_amd import _lib
-from naju_amd.gradsink import sink_of
+from naju_amd.gradsink import acc_sink_of, sink_of
 
 _DT = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16}
+# naju_dwconv_bwd: dx += the gradient (include/naju_mixer.h)
+_ACCUM_DX = 2
 
 
 class _Workspace:
@@ -57,7 +59,7 @@ def _rows(x):
 
 class _DwConv(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, bias, add, silu, out_dtype, x_sink, add_sink):
+    def forward(ctx, x, w, bias, add, silu, out_dtype, x_sink, add_sink, x_acc):
         B, T, C = x.shape
         K = w.shape[1]
         x, ldx = _rows(x)
@@ -75,6 +77,9 @@ class _DwConv(torch.autograd.Function):
         ctx.add_dtype = None if add is None else add.dtype
         # pieces of a gradsink.split(): their gradients go into its buffer
         ctx.x_sink, ctx.add_sink = x_sink, add_sink
+        # x is a gradsink.fanout() alias: dx is written into, or added to,
+        # the fan-out's buffer
+        ctx.x_acc = x_acc
         return y
 
     @staticmethod
@@ -87,10 +92,17 @@ class _DwConv(torch.autograd.Function):
         dy = dy.contiguous()
         need_x, need_w, need_b, need_add = ctx.needs_input_grad[:4]
         dx = None
+        act = int(ctx.silu)
+        dx_ret = None
         if need_x:
             if ctx.x_sink is not None:
                 sink, col = ctx.x_sink
                 dx = sink.slice(col, C)
+            elif ctx.x_acc is not None:
+                dx, accumulate = ctx.x_acc.target()
+                if accumulate:
+                    act |= _ACCUM_DX
+                dx_ret = ctx.x_acc.marker()
             else:
                 dx = torch.empty((B, T, C), dtype=x.dtype, device=x.device)
         dw = torch.empty((C, K), dtype=torch.float32, device=x.device) if need_w else None
@@ -109,11 +121,11 @@ class _DwConv(torch.autograd.Function):
             _lib.check_mixer(L.naju_dwconv_bwd(
                 _ptr(x), x.stride(1), _ptr(w), _ptr(bias), _ptr(dy), _ptr(dx), dx.stride(1) if dx is not None else C,
                 _ptr(dw), _ptr(db), _ptr(dadd), dadd.stride(1) if dadd is not None else C, B, T, C, K,
-                int(ctx.silu), _DT[x.dtype], _DT[dy.dtype], _DT[x.dtype],
+                act, _DT[x.dtype], _DT[dy.dtype], _DT[x.dtype],
                 _DT[dadd.dtype] if dadd is not None else 0, _ptr(ws), ws.numel(), stream))
         if dadd is None and need_add and ctx.add_dtype is not None:
             dadd = dy.to(ctx.add_dtype)
-        return dx, dw, db, dadd, None, None, None, None
+        return dx if dx_ret is None else dx_ret, dw, db, dadd, None, None, None, None, None
 
 
 def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
@@ -133,11 +145,13 @@ def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
     if add is not None:
         if add.shape != x.shape:
             raise ValueError(f"add must have x's shape {tuple(x.shape)}, got {tuple(add.shape)}")
-    x_sink, add_sink = sink_of(x), sink_of(add)
+    x_sink, add_sink, x_acc = sink_of(x), sink_of(add), acc_sink_of(x)
     if x.dtype not in _DT:
-        x, x_sink = x.float(), None
+        x, x_sink, x_acc = x.float(), None, None
+    if x_acc is not None and (x.stride(2) != 1 or x.stride(0) != x.shape[1] * x.stride(1) or x.stride(1) != C):
+        x_acc = None  # the fan-out's buffer is contiguous: dx must be too
     if add is not None and add.dtype not in _DT:
         add, add_sink = add.float(), None
     if out_dtype is None:
         out_dtype = x.dtype
-    return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype, x_sink, add_sink)
+    return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype, x_sink, add_sink, x_acc)

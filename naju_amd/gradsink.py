@@ -68,3 +68,73 @@ def split(t, sizes):
 def sink_of(t):
     """(sink, first column) of a piece returned by split(), else None."""
     return getattr(t, "_naju_sink", None) if t is not None else None
+
+
+class AccumSink:
+    """One gradient buffer that the consumers of one tensor fill in turn,
+    instead of each returning its own gradient for autograd to add: the
+    first to call target() writes the buffer, the later ones add into it
+    (kernels and GEMMs with an accumulating form), and each returns
+    marker() -- a zero of the tensor's shape without storage -- in place of
+    its gradient. A consumer without an accumulating form returns its
+    gradient as usual, and the fan-out adds it."""
+
+    def __init__(self, like):
+        self.shape, self.dtype, self.device = like.shape, like.dtype, like.device
+        self.buf = None
+        self._zero = torch.zeros((), dtype=like.dtype, device=like.device)
+
+    def target(self):
+        """(buffer, accumulate): the buffer, and whether it already holds an
+        earlier consumer's gradient (add into it) or not (write it)."""
+        if self.buf is None:
+            self.buf = torch.empty(self.shape, dtype=self.dtype, device=self.device)
+            return self.buf, False
+        return self.buf, True
+
+    def marker(self):
+        return self._zero.expand(self.shape)
+
+    def is_marker(self, g):
+        return g.data_ptr() == self._zero.data_ptr() and all(s == 0 for s in g.stride())
+
+
+class _Fanout(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, t, n, sink):
+        ctx.set_materialize_grads(False)
+        ctx.sink = sink
+        return tuple(t.view_as(t) for _ in range(n))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        sink = ctx.sink
+        buf, sink.buf = sink.buf, None  # a later backward through the same graph allocates anew
+        own = buf is not None
+        for g in grads:
+            if g is None or sink.is_marker(g):
+                continue
+            if buf is None:
+                buf = g
+            elif own:
+                buf.add_(g)
+            else:
+                buf = buf + g
+        return buf, None, None
+
+
+def fanout(t, n):
+    """n aliases of t, each for one consumer, tagged with one AccumSink:
+    consumers that know the sink (acc_sink_of) leave their gradients in its
+    buffer, and the fan-out's backward returns that buffer as t's gradient
+    (plus any gradient returned the usual way)."""
+    sink = AccumSink(t)
+    outs = _Fanout.apply(t, int(n), sink)
+    for o in outs:
+        o._naju_acc = sink
+    return outs
+
+
+def acc_sink_of(t):
+    """The AccumSink of an alias returned by fanout(), else None."""
+    return getattr(t, "_naju_acc", None) if t is not None else None

@@ -18,6 +18,8 @@ otherwise).
 import torch
 import torch.nn.functional as F
 
+from naju_amd.gradsink import acc_sink_of
+
 # output tiles (128 x 128) times parts kept at or below this: about two
 # waves of workgroups over the 256 compute units
 _TILE_BUDGET = 640
@@ -52,11 +54,14 @@ def weight_grad(dy, x):
 
 class _Linear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, dtype):
+    def forward(ctx, x, weight, dtype, x_acc):
         xb = x if x.dtype == dtype else x.to(dtype)
         wb = weight.to(dtype)
         ctx.save_for_backward(xb, wb)
         ctx.x_dtype, ctx.w_dtype = x.dtype, weight.dtype
+        # x is a gradsink.fanout() alias (in the compute dtype): dx is
+        # written into, or added to, the fan-out's buffer
+        ctx.x_acc = x_acc if xb is x else None
         return F.linear(xb, wb)
 
     @staticmethod
@@ -68,14 +73,23 @@ class _Linear(torch.autograd.Function):
             dy2 = dy2.to(wb.dtype)
         dx = dw = None
         if ctx.needs_input_grad[0]:
-            dx = torch.mm(dy2, wb).view(*dy.shape[:-1], n_in)
-            if dx.dtype != ctx.x_dtype:
-                dx = dx.to(ctx.x_dtype)
+            if ctx.x_acc is not None:
+                buf, accumulate = ctx.x_acc.target()
+                b2 = buf.view(-1, n_in)
+                if accumulate:
+                    b2.addmm_(dy2, wb)
+                else:
+                    torch.mm(dy2, wb, out=b2)
+                dx = ctx.x_acc.marker()
+            else:
+                dx = torch.mm(dy2, wb).view(*dy.shape[:-1], n_in)
+                if dx.dtype != ctx.x_dtype:
+                    dx = dx.to(ctx.x_dtype)
         if ctx.needs_input_grad[1]:
             dw = weight_grad(dy2.contiguous(), xb.reshape(-1, n_in))
             if dw.dtype != ctx.w_dtype:
                 dw = dw.to(ctx.w_dtype)
-        return dx, dw, None
+        return dx, dw, None, None
 
 
 def compute_dtype(x):
@@ -94,4 +108,7 @@ def linear(x, weight):
     dt = compute_dtype(x)
     if dt is None:
         raise ValueError("naju_amd.linear.linear serves CUDA tensors computed in float16 / bfloat16")
-    return _Linear.apply(x, weight, dt)
+    x_acc = acc_sink_of(x)
+    if x_acc is not None and not x.is_contiguous():
+        x_acc = None
+    return _Linear.apply(x, weight, dt, x_acc)

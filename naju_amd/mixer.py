@@ -37,7 +37,8 @@ from naju_amd.linear import compute_dtype, linear
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
 from naju_amd.rmsnorm import supported as rmsnorm_supported
-from naju_amd.scan import naju_scan
+from naju_amd import scan as _scan
+from naju_amd.scan import naju_scan, naju_scan_hip
 
 
 class RMSNorm(nn.Module):
@@ -67,6 +68,12 @@ class RMSNorm(nn.Module):
 def _out_dtype(x):
     dev = x.device.type
     return torch.get_autocast_dtype(dev) if torch.is_autocast_enabled(dev) else x.dtype
+
+
+def _hip_scan(backend):
+    """naju_scan_hip when `backend` resolves to it, else None."""
+    fn = _scan._get(_scan.resolve_backend(backend))
+    return fn if fn is naju_scan_hip else None
 
 
 def _linear(x, weight):
@@ -166,6 +173,17 @@ class NajuMixer(nn.Module):
         else:
             x, z = xz.chunk(2, dim=-1)
         h = self._content(x)
+        # h feeds five consumers (projection GEMM, two gate convolutions,
+        # scan, readout). With the HIP scan, their gradients collect in one
+        # buffer instead of four additions: the scan's du comes first and
+        # also carries the readout's D h term (du_skip = D / s), and the
+        # convolutions and the GEMM add into it in place
+        fold = (h.is_cuda and not self.gate_rank and torch.is_grad_enabled() and h.requires_grad
+                and _hip_scan(self.scan_backend) is not None)
+        if fold:
+            h_g, h_f, h_i, h_s, h_r = gradsink.fanout(h, 5)
+        else:
+            h_g = h_f = h_i = h_s = h_r = h
         if h.is_cuda and not self.gate_rank:
             # f_proj, i_proj and x_proj in one GEMM over h (the same weights:
             # each output column is the same product), so h's gradient from
@@ -173,19 +191,23 @@ class NajuMixer(nn.Module):
             # the convolutions read their slices in place
             di, N = self.d_inner, self.d_state
             w = torch.cat([self.f_proj.weight, self.i_proj.weight, self.x_proj.weight], 0)
-            p_f, p_i, Bm, Cm = gradsink.split(_linear(h, w), [di, di, N, N])
-            f_logit = self._gate_logit(h, None, self.f_conv, self.f_bias, p=p_f)
-            i_logit = self._gate_logit(h, None, self.i_conv, self.i_bias, p=p_i)
+            p_f, p_i, Bm, Cm = gradsink.split(_linear(h_g, w), [di, di, N, N])
+            f_logit = self._gate_logit(h_f, None, self.f_conv, self.f_bias, p=p_f)
+            i_logit = self._gate_logit(h_i, None, self.i_conv, self.i_bias, p=p_i)
         else:
             Bm, Cm = self.x_proj(h).split(self.d_state, dim=-1)
             f_logit = self._gate_logit(h, self.f_proj, self.f_conv, self.f_bias)
             i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)
         # the scan reads out the state only; the D skip is applied here
-        cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
+        if fold:
+            cx = naju_scan_hip(h_s, f_logit, i_logit, Bm, Cm, self.D_zero,
+                               du_skip=self.D.detach() * (1.0 / self._cx_scale))
+        else:
+            cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
         if h.is_cuda:
             # one kernel each way; the output takes the autocast dtype the
             # out_proj GEMM consumes
-            y = readout(cx, h, z, self.D, self._cx_scale, out_dtype=_out_dtype(h))
+            y = readout(cx, h_r, z, self.D, self._cx_scale, out_dtype=_out_dtype(h), dh_elsewhere=fold)
         else:
             y = (cx * self._cx_scale + self.D * h) * F.silu(z)
         return _linear(y, self.out_proj.weight)

@@ -28,7 +28,7 @@ def _rows_of(t):
 
 class _Readout(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, cx, h, z, Dv, scale, out_dtype, z_sink):
+    def forward(ctx, cx, h, z, Dv, scale, out_dtype, z_sink, dh_elsewhere):
         B, T, C = h.shape
         z, z_ld = _rows_of(z)
         y = torch.empty((B, T, C), dtype=out_dtype, device=h.device)
@@ -40,6 +40,7 @@ class _Readout(torch.autograd.Function):
         ctx.save_for_backward(cx, h, z, Dv)
         ctx.scale = float(scale)
         ctx.z_sink = z_sink  # z is a piece of a gradsink.split(): dz goes into its buffer
+        ctx.dh_elsewhere = dh_elsewhere
         return y
 
     @staticmethod
@@ -51,6 +52,7 @@ class _Readout(torch.autograd.Function):
         dy = dy.contiguous()
         need_cx, need_h, need_z, need_D = ctx.needs_input_grad[:4]
         dcx = torch.empty((B, T, C), dtype=cx.dtype, device=h.device) if need_cx else None
+        need_h = need_h and not ctx.dh_elsewhere
         dh = torch.empty((B, T, C), dtype=h.dtype, device=h.device) if need_h else None
         dz = None
         if need_z:
@@ -70,10 +72,13 @@ class _Readout(torch.autograd.Function):
                 _ptr(dz), dz.stride(1) if dz is not None else C, _ptr(dD), B * T, C, _DT[cx.dtype], _DT[h.dtype],
                 _DT[z.dtype], _DT[dy.dtype], _DT[cx.dtype], _DT[h.dtype], _DT[z.dtype], _ptr(ws), ws.numel(),
                 stream))
-        return dcx, dh, dz, dD, None, None, None
+        return dcx, dh, dz, dD, None, None, None, None
 
 
-def readout(cx, h, z, D, scale, out_dtype=None):
+def readout(cx, h, z, D, scale, out_dtype=None, dh_elsewhere=False):
+    """dh_elsewhere: h's gradient through the D h term is formed by another
+    consumer of h (the scan's backward with du_skip = D / scale), so this
+    backward leaves it out and returns no gradient for h."""
     if not h.is_cuda:
         raise RuntimeError("naju_amd.readout runs on the HIP kernels only: h must be a CUDA tensor")
     if h.dim() != 3 or cx.shape != h.shape or z.shape != h.shape:
@@ -89,4 +94,4 @@ def readout(cx, h, z, D, scale, out_dtype=None):
     Dv = D if D.dtype == torch.float32 else D.float()
     if out_dtype is None:
         out_dtype = torch.promote_types(torch.promote_types(cx.dtype, h.dtype), Dv.dtype)
-    return _Readout.apply(cx, h, z, Dv.contiguous(), float(scale), out_dtype, z_sink)
+    return _Readout.apply(cx, h, z, Dv.contiguous(), float(scale), out_dtype, z_sink, bool(dh_elsewhere))

@@ -43,6 +43,7 @@ import os
 import torch
 
 from naju_amd import _lib
+from naju_amd.gradsink import acc_sink_of
 
 _BACKEND_CACHE = {}
 
@@ -190,7 +191,7 @@ class NajuScanHip(torch.autograd.Function):
     """Autograd wrapper of naju_scan_fwd / naju_scan_bwd (include/naju_scan.h)."""
 
     @staticmethod
-    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False, ckpt_rows=0):
+    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False, ckpt_rows=0, du_skip=None):
         Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
         out_dtype = u.dtype
         u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0)
@@ -220,9 +221,15 @@ class NajuScanHip(torch.autograd.Function):
             _watch_status(dev, stream, ws)
         _check_status(dev)
         if need_grad:
-            ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt)
+            # du_skip: the skip coefficient of du's D dy term in place of
+            # D_skip (naju_scan_hip's doc)
+            D_b = D_ if du_skip is None else du_skip.detach().float().contiguous()
+            ctx.save_for_backward(u_, fl_, il_, B_, C_, D_, ckpt, D_b)
             ctx.meta = (Bsz, T, D, N, dts, flags, h0 is not None,
                         (u.dtype, f_logit.dtype, i_logit.dtype, B.dtype, C.dtype, D_skip.dtype))
+            # u is a gradsink.fanout() alias: du goes into the fan-out's
+            # buffer when it is the first gradient there
+            ctx.u_acc = acc_sink_of(u) if u_ is u else None
         y = y if y.dtype == out_dtype else y.to(out_dtype)
         if want_hT:
             ctx.mark_non_differentiable(hT)
@@ -231,12 +238,18 @@ class NajuScanHip(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy, *_unused_dhT):
-        u_, fl_, il_, B_, C_, D_, ckpt = ctx.saved_tensors
+        u_, fl_, il_, B_, C_, D_, ckpt, D_b = ctx.saved_tensors
         Bsz, T, D, N, dts, flags, has_h0, in_dtypes = ctx.meta
         ng = ctx.needs_input_grad
         dev = u_.device
         dy = dy.to(u_.dtype).contiguous()
-        du = torch.empty_like(u_) if ng[0] else None
+        du = du_ret = None
+        if ng[0]:
+            if ctx.u_acc is not None and ctx.u_acc.buf is None:
+                du, _ = ctx.u_acc.target()
+                du_ret = ctx.u_acc.marker()
+            else:
+                du = torch.empty_like(u_)
         dfl = torch.empty_like(fl_) if ng[1] else None
         dil = torch.empty_like(il_) if ng[2] else None
         dB = torch.empty_like(B_) if ng[3] else None
@@ -249,7 +262,7 @@ class NajuScanHip(torch.autograd.Function):
         _raise_pending(dev, stream)
         ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags))
         _lib.check(L.naju_scan_bwd(
-            _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(ckpt), _ptr(dy),
+            _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_b), _ptr(ckpt), _ptr(dy),
             _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
             Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
         if N == 1:
@@ -257,7 +270,9 @@ class NajuScanHip(torch.autograd.Function):
         _check_status(dev)
         grads = [du, dfl, dil, dB, dC, dD]
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
-        return (*grads, dh0, None, None)
+        if du_ret is not None:
+            grads[0] = du_ret
+        return (*grads, dh0, None, None, None)
 
 
 def _default_ckpt_rows(N):
@@ -269,16 +284,25 @@ def _default_ckpt_rows(N):
     return int(v) if v and 9 <= N <= 64 else 0
 
 
-def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False, ckpt_rows=None):
+def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False, ckpt_rows=None,
+                  du_skip=None):
     """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module
     doc); (y, hT) with return_final_state=True. ckpt_rows: the checkpoint
     interval kept for the backward (None = NAJU_CKPT_ROWS from the
     environment where served, else the default; 32, 64 or 128 rows, served
     at 9 <= N <= 64, is the memory-light mode: the backward recomputes the
-    states between, with bitwise the same outputs)."""
+    states between, with bitwise the same outputs).
+
+    du_skip ([D], no gradient): the backward forms du = i dws + du_skip dy
+    instead of i dws + D_skip dy (the forward still adds D_skip u to y). A
+    caller that multiplies y by s and adds D u itself (the mixer's readout,
+    naju/mixer.py:123-124, called with D_skip = 0) passes du_skip = D / s:
+    then du already holds the gradient of that D u term, which the caller's
+    own backward can leave out (one gradient fewer to add)."""
     if ckpt_rows is None:
         ckpt_rows = _default_ckpt_rows(B.shape[-1])
-    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state), int(ckpt_rows))
+    return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state), int(ckpt_rows),
+                             du_skip)
 
 
 def resolve_backend(backend=None):

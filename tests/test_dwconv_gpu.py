@@ -196,3 +196,52 @@ def test_gradsink_split_matches_plain_split(gpu):
         grads.append(t.grad.clone())
     assert torch.equal(grads[0], grads[1])
     assert torch.count_nonzero(grads[0][..., 3 * C:]) == 0
+
+
+@pytest.mark.parametrize("C,dtype", [(1536, torch.bfloat16), (100, torch.bfloat16), (96, torch.float32)])
+def test_bwd_accumulates_dx_in_place(gpu, C, dtype):
+    """naju_dwconv_bwd with NAJU_DWCONV_ACCUM_DX adds the gradient to what dx
+    holds (one rounding of the sum to dx's dtype): a buffer holding g0 comes
+    back as g0 + dx, on the vector path (C a multiple of 8, bf16) and the
+    element path, dw and dbias unchanged by the flag."""
+    import ctypes
+    from naju_amd import _lib
+    from naju_amd.dwconv import _DT, _WS
+    L = _lib.lib()
+    g = torch.Generator(device=gpu).manual_seed(C)
+    B, T, K = 2, 300, 4
+    x = torch.randn(B, T, C, generator=g, device=gpu).to(dtype)
+    w = torch.randn(C, K, generator=g, device=gpu)
+    bias = torch.randn(C, generator=g, device=gpu)
+    dy = torch.randn(B, T, C, generator=g, device=gpu)
+    g0 = torch.randn(B, T, C, generator=g, device=gpu).to(dtype)
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    ws = _WS.get(gpu, st, L.naju_dwconv_workspace_bytes(B, T, C, K))
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    def bwd(dx, act, dw, db):
+        _lib.check_mixer(L.naju_dwconv_bwd(p(x), C, p(w), p(bias), p(dy), p(dx), C, p(dw), p(db), None, C, B, T, C,
+                                           K, act, _DT[dtype], _DT[torch.float32], _DT[dx.dtype], 0, p(ws),
+                                           ws.numel(), st))
+
+    for act in (0, 1):
+        # the gradient alone, in float32 (element path)
+        ref = torch.empty(B, T, C, dtype=torch.float32, device=gpu)
+        dw0, db0 = torch.empty(C, K, device=gpu), torch.empty(C, device=gpu)
+        bwd(ref, act, dw0, db0)
+        acc = g0.clone()
+        dw1, db1 = torch.empty(C, K, device=gpu), torch.empty(C, device=gpu)
+        bwd(acc, act | 2, dw1, db1)
+        # the same call without the flag (same kernel path): same dw, dbias
+        plain = torch.empty_like(g0)
+        dw2, db2 = torch.empty(C, K, device=gpu), torch.empty(C, device=gpu)
+        bwd(plain, act, dw2, db2)
+        torch.cuda.synchronize()
+        want = (g0.float() + ref).to(dtype)
+        # the vector kernel forms the same gradient up to float32 rounding,
+        # so the sum may land one rounding step of dtype apart
+        tol = 2.0 ** -7 if dtype == torch.bfloat16 else 1e-6
+        assert float(((acc.float() - want.float()).abs() / want.float().abs().clamp_min(1e-3)).max()) <= tol, act
+        assert torch.equal(dw1, dw2) and torch.equal(db1, db2)
+    with pytest.raises(_lib.NajuScanError, match="act must be"):
+        bwd(acc, 4, None, None)

@@ -225,3 +225,37 @@ def test_lm_c5_full_size_training_steps(gpu):
     assert all(math.isfinite(v) for v in losses)
     assert math.log(V) - 0.2 < losses[0] < math.log(V) + 2.0, losses
     assert losses[-1] < losses[0] - 0.5 and abs(losses[-1] - math.log(V)) < 0.2, losses
+
+
+def test_mixer_gradient_fanout_matches_autograd_sums(gpu):
+    """With the HIP scan the mixer collects h's gradient (projection GEMM,
+    two gate convolutions, scan, readout) in one buffer: the scan writes its
+    du, which also carries the readout's D h term (du_skip = D / s), and the
+    convolutions and the GEMM add into it. Against the same mixer whose
+    scan is reached through another backend name (autograd then sums the
+    five gradients), under bf16 autocast at the C5 layer's width: every
+    gradient agrees to bf16 rounding."""
+    import copy
+    from naju_amd import scan as scan_mod
+    from naju_amd.mixer import NajuMixer
+    scan_mod._BACKEND_CACHE["hip_plain"] = lambda *a: scan_mod.naju_scan_hip(*a)
+    try:
+        torch.manual_seed(3)
+        ma = NajuMixer(768, d_state=64, scan_backend="hip").to(gpu)
+        mb = copy.deepcopy(ma)
+        mb.scan_backend = "hip_plain"
+        u = torch.randn(2, 512, 768, device=gpu)
+        gy = torch.randn(2, 512, 768, device=gpu)
+        outs = []
+        for m in (ma, mb):
+            ui = u.clone().requires_grad_(True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = m(ui)
+            y.float().backward(gy)
+            outs.append((y.detach().float(), ui.grad))
+        assert torch.equal(outs[0][0], outs[1][0])
+        assert _rel(outs[0][1], outs[1][1]) < 1e-2
+        for (n, pa), pb in zip(ma.named_parameters(), mb.parameters()):
+            assert _rel(pa.grad, pb.grad) < 1e-2, n
+    finally:
+        scan_mod._BACKEND_CACHE.pop("hip_plain", None)
