@@ -1,4 +1,6 @@
-"""Splits whose consumers write their gradients in place.
+"""Gradient routing without extra copies or additions.
+
+split(): splits whose consumers write their gradients in place.
 
 Autograd's backward of ``t.split(sizes, -1)`` concatenates the pieces'
 gradients into a new tensor of t's shape: one more read and write of t's
@@ -10,6 +12,13 @@ The split's backward then returns that buffer itself, copying in only the
 pieces whose gradient arrived in another tensor (a piece that also had
 other consumers, whose gradients autograd summed elsewhere, or one whose
 consumer does not use the sink) and zero-filling pieces without a gradient.
+
+fanout(): aliases of one tensor for several consumers whose gradients
+collect in one buffer: the first consumer to get there writes it, later ones
+add into it in place (the depthwise convolution with NAJU_DWCONV_ACCUM_DX, a
+GEMM with addmm_), and the fan-out returns the buffer as the tensor's
+gradient, where autograd would otherwise add the consumers' separate
+gradients one by one (one read-read-write pass of the tensor per addition).
 """
 import torch
 
