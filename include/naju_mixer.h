@@ -112,6 +112,33 @@ int naju_rmsnorm_bwd(const void* x, const float* w, const float* rstd, const voi
                      int64_t n_rows, int64_t d, int x_dtype, int dy_dtype, int dx_dtype, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* naju_rmsnorm_bwd with dx = dres + (the norm's gradient), dres [n_rows, d]
+ * in x's dtype (nullable; not dx itself): the pre-norm block's residual
+ * stream feeds both the norm and the residual add (naju/mixer.py:138-144),
+ * and this adds the two gradients in the norm's pass instead of a separate
+ * addition. No reference counterpart (autograd adds them there). */
+int naju_rmsnorm_bwd_add(const void* x, const float* w, const float* rstd, const void* dy, const void* dres,
+                         void* dx, float* dw, int64_t n_rows, int64_t d, int x_dtype, int dy_dtype, int dx_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* The pre-norm block's residual add with dropout, u + Dropout(p)(mix)
+ * (naju/mixer.py:131-144: NajuBlock's self.drop and residual), in one pass:
+ * out = u + (keep_i ? (mix_i / (1 - p) rounded to mix_dtype) : 0), n
+ * elements, u and out float32, mix in mix_dtype. keep_i is a pure function
+ * of (*seed, i) (a SplitMix64 draw per pair of elements, kept with
+ * probability 1 - p), so the backward draws the same mask again and no mask
+ * is stored; seed is a device pointer (the caller draws it from its own
+ * generator, e.g. torch's, without a host synchronisation) and may be NULL
+ * when p = 0. */
+int naju_residual_dropout_fwd(const float* u, const void* mix, const int64_t* seed, float p, float* out, int64_t n,
+                              int mix_dtype, void* stream);
+
+/* Backward of the dropout in naju_residual_dropout_fwd with the same seed
+ * and p: dmix = keep_i ? g_i / (1 - p) : 0 (rounded once to mix_dtype) from
+ * the float32 gradient g of out (which is also u's gradient, unchanged). */
+int naju_dropout_bwd(const float* g, const int64_t* seed, float p, void* dmix, int64_t n, int mix_dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,6 +46,9 @@ EXPORTED = (
     "naju_rmsnorm_fwd",
     "naju_rmsnorm_workspace_bytes",
     "naju_rmsnorm_bwd",
+    "naju_rmsnorm_bwd_add",
+    "naju_residual_dropout_fwd",
+    "naju_dropout_bwd",
     "naju_loss_last_error",
     "naju_xent_workspace_bytes",
     "naju_xent_fwd",
@@ -129,6 +132,12 @@ def lib():
     # x, w, rstd, dy, dx, dw, n_rows, d, x_dt, dy_dt, dx_dt, ws, ws_bytes, stream
     L.naju_rmsnorm_bwd.argtypes = [P] * 6 + [I64, I64, I, I, I, P, SZ, P]
     L.naju_rmsnorm_bwd.restype = I
+    L.naju_rmsnorm_bwd_add.argtypes = [P] * 7 + [I64, I64, I, I, I, P, SZ, P]
+    L.naju_rmsnorm_bwd_add.restype = I
+    L.naju_residual_dropout_fwd.argtypes = [P, P, P, F, P, I64, I, P]
+    L.naju_residual_dropout_fwd.restype = I
+    L.naju_dropout_bwd.argtypes = [P, P, F, P, I64, I, P]
+    L.naju_dropout_bwd.restype = I
     L.naju_loss_last_error.argtypes = []
     L.naju_loss_last_error.restype = ctypes.c_char_p
     L.naju_xent_workspace_bytes.argtypes = [I64]

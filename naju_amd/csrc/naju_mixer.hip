@@ -779,6 +779,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_vec(const TX* __r
                                                                    const float* __restrict__ w,
                                                                    const float* __restrict__ rstd,
                                                                    const TDY* __restrict__ dy, TX* __restrict__ dx,
+                                                                   const TX* __restrict__ dres,
                                                                    float* __restrict__ part, int64_t n_rows,
                                                                    int64_t d) {
   constexpr int RPW = norm_rpw<G>();
@@ -834,6 +835,13 @@ __global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_vec(const TX* __r
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = fmaf(wr[g][e] * gv[i][g][e], rs[i], -xv[i][g][e] * k);
+        if (dres) {
+          // dx = dres + the norm's gradient (the residual stream's other use)
+          float q[4];
+          ld4(dres + r * d + c, q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] += q[e];
+        }
         st4(dx + r * d + c, o);
       }
     }
@@ -886,12 +894,12 @@ void norm_fwd_launch(int G, dim3 grid, hipStream_t st, const void* x, const floa
 
 template <typename TX, typename TDY>
 void norm_bwd_launch(int G, dim3 grid, hipStream_t st, const void* x, const float* w, const float* rstd,
-                     const void* dy, void* dx, float* part, int64_t n, int64_t d) {
+                     const void* dy, void* dx, const void* dres, float* part, int64_t n, int64_t d) {
   const dim3 blk(64 * kNormWaves);
 #define NAJU_NORM_B(GG)                                                                                          \
   case GG:                                                                                                      \
     hipLaunchKernelGGL((rmsnorm_bwd_vec<TX, TDY, GG>), grid, blk, 0, st, (const TX*)x, w, rstd, (const TDY*)dy,  \
-                       (TX*)dx, part, n, d);                                                                     \
+                       (TX*)dx, (const TX*)dres, part, n, d);                                                    \
     break;
   switch (G) {
     NAJU_NORM_B(1)
@@ -918,13 +926,13 @@ bool norm_fwd_dt(int y_dt, int G, dim3 grid, hipStream_t st, const void* x, cons
 
 template <typename TX>
 bool norm_bwd_dt(int dy_dt, int G, dim3 grid, hipStream_t st, const void* x, const float* w, const float* rstd,
-                 const void* dy, void* dx, float* part, int64_t n, int64_t d) {
+                 const void* dy, void* dx, const void* dres, float* part, int64_t n, int64_t d) {
   if (dy_dt == NAJU_DTYPE_F32)
-    norm_bwd_launch<TX, float>(G, grid, st, x, w, rstd, dy, dx, part, n, d);
+    norm_bwd_launch<TX, float>(G, grid, st, x, w, rstd, dy, dx, dres, part, n, d);
   else if (dy_dt == NAJU_DTYPE_BF16)
-    norm_bwd_launch<TX, bf16_t>(G, grid, st, x, w, rstd, dy, dx, part, n, d);
+    norm_bwd_launch<TX, bf16_t>(G, grid, st, x, w, rstd, dy, dx, dres, part, n, d);
   else
-    norm_bwd_launch<TX, f16_t>(G, grid, st, x, w, rstd, dy, dx, part, n, d);
+    norm_bwd_launch<TX, f16_t>(G, grid, st, x, w, rstd, dy, dx, dres, part, n, d);
   return true;
 }
 
@@ -944,6 +952,119 @@ int norm_check(int64_t n_rows, int64_t d, int x_dt, std::initializer_list<int> d
       return fail(NAJU_ERR_UNSUPPORTED, "pointers must be 16-byte aligned");
   return NAJU_OK;
 }
+
+
+// ------------------------------------------------- residual add with dropout
+//
+// The pre-norm block's u + Dropout(mix) (reference naju/mixer.py:131-144) in
+// one pass, and the dropout's backward in one pass. The keep decision of
+// element i is a pure function of (seed, i), drawn again by the backward,
+// so no mask is stored: a SplitMix64 output (Steele, Lea and Flood, "Fast
+// splittable pseudorandom number generators", OOPSLA 2014) of the 64-bit
+// word seed + (i / 2 + 1) * 0x9E3779B97F4A7C15, whose upper and lower
+// 32-bit halves decide elements 2m and 2m + 1: kept when the half is at or
+// above p * 2^32. Kept elements are scaled by 1 / (1 - p) and rounded to
+// mix's dtype first, as the reference's Dropout output is.
+struct DropKeep {
+  uint32_t thr;  // keep when the 32-bit draw is >= thr
+  float scale;   // 1 / (1 - p)
+};
+
+DropKeep drop_keep(float p) {
+  DropKeep k;
+  const double t = (double)p * 4294967296.0;
+  k.thr = t >= 4294967295.0 ? 0xffffffffu : (uint32_t)t;
+  k.scale = 1.f / (1.f - p);
+  return k;
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// keep bits of elements 2m and 2m + 1 (bit 0: element 2m)
+__device__ __forceinline__ uint32_t drop_pair(uint64_t seed, int64_t m, uint32_t thr) {
+  const uint64_t z = splitmix64(seed + (uint64_t)(m + 1) * 0x9E3779B97F4A7C15ull);
+  return ((uint32_t)z >= thr ? 1u : 0u) | ((uint32_t)(z >> 32) >= thr ? 2u : 0u);
+}
+
+template <typename TM>
+__device__ __forceinline__ float drop_val(float v, bool keep, float scale) {
+  return keep ? (float)(TM)(v * scale) : 0.f;
+}
+
+// out = u + dropout(mix); VEC: 8 elements per thread (n % 8 == 0, 16-byte
+// aligned), else one. seed == nullptr: p = 0, every element kept.
+template <typename TM, bool VEC>
+__global__ __launch_bounds__(256) void residual_dropout_kernel(const float* __restrict__ u,
+                                                               const TM* __restrict__ mix,
+                                                               const int64_t* __restrict__ seed, DropKeep dk,
+                                                               float* __restrict__ out, int64_t n) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint64_t s = seed ? (uint64_t)seed[0] : 0ull;
+  if constexpr (VEC) {
+    const int64_t i0 = t * kVec;
+    if (i0 >= n) return;
+    float uv[kVec], mv[kVec];
+    ld8f(u + i0, uv);
+    ld8(mix + i0, mv);
+    uint32_t keep = 0xffu;
+    if (seed) {
+      keep = 0u;
+#pragma unroll
+      for (int q = 0; q < kVec / 2; ++q) keep |= drop_pair(s, i0 / 2 + q, dk.thr) << (2 * q);
+    }
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) uv[j] += seed ? drop_val<TM>(mv[j], (keep >> j) & 1u, dk.scale) : mv[j];
+    *(float4*)(out + i0) = make_float4(uv[0], uv[1], uv[2], uv[3]);
+    *(float4*)(out + i0 + 4) = make_float4(uv[4], uv[5], uv[6], uv[7]);
+  } else {
+    if (t >= n) return;
+    const float mv = (float)mix[t];
+    float o = u[t];
+    if (seed) {
+      const bool keep = (drop_pair(s, t / 2, dk.thr) >> (t & 1)) & 1u;
+      o += drop_val<TM>(mv, keep, dk.scale);
+    } else {
+      o += mv;
+    }
+    out[t] = o;
+  }
+}
+
+// dmix = dropout'(g): g * scale where kept, 0 where dropped, rounded once to
+// mix's dtype.
+template <typename TM, bool VEC>
+__global__ __launch_bounds__(256) void dropout_bwd_kernel(const float* __restrict__ g,
+                                                          const int64_t* __restrict__ seed, DropKeep dk,
+                                                          TM* __restrict__ dmix, int64_t n) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint64_t s = seed ? (uint64_t)seed[0] : 0ull;
+  if constexpr (VEC) {
+    const int64_t i0 = t * kVec;
+    if (i0 >= n) return;
+    float gv[kVec];
+    ld8f(g + i0, gv);
+    if (seed) {
+      uint32_t keep = 0u;
+#pragma unroll
+      for (int q = 0; q < kVec / 2; ++q) keep |= drop_pair(s, i0 / 2 + q, dk.thr) << (2 * q);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) gv[j] = ((keep >> j) & 1u) ? gv[j] * dk.scale : 0.f;
+    }
+    st8(dmix + i0, gv);
+  } else {
+    if (t >= n) return;
+    float v = g[t];
+    if (seed) v = ((drop_pair(s, t / 2, dk.thr) >> (t & 1)) & 1u) ? v * dk.scale : 0.f;
+    dmix[t] = (TM)v;
+  }
+}
+
+typedef void (*resdrop_t)(const float*, const void*, const int64_t*, DropKeep, float*, int64_t);
+typedef void (*dropbwd_t)(const float*, const int64_t*, DropKeep, void*, int64_t);
 
 }  // namespace
 
@@ -1160,8 +1281,15 @@ size_t naju_rmsnorm_workspace_bytes(int64_t n_rows, int64_t d) {
 int naju_rmsnorm_bwd(const void* x, const float* w, const float* rstd, const void* dy, void* dx, float* dw,
                      int64_t n_rows, int64_t d, int x_dtype, int dy_dtype, int dx_dtype, void* workspace,
                      size_t workspace_bytes, void* stream) {
+  return naju_rmsnorm_bwd_add(x, w, rstd, dy, nullptr, dx, dw, n_rows, d, x_dtype, dy_dtype, dx_dtype, workspace,
+                              workspace_bytes, stream);
+}
+
+int naju_rmsnorm_bwd_add(const void* x, const float* w, const float* rstd, const void* dy, const void* dres,
+                         void* dx, float* dw, int64_t n_rows, int64_t d, int x_dtype, int dy_dtype, int dx_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
-  int rc = norm_check(n_rows, d, x_dtype, {dy_dtype, dx_dtype}, {x, w, dy, dx, workspace});
+  int rc = norm_check(n_rows, d, x_dtype, {dy_dtype, dx_dtype}, {x, w, dy, dx, dres, workspace});
   if (rc) return rc;
   if (dx_dtype != x_dtype) return fail(NAJU_ERR_UNSUPPORTED, "dx must have x's dtype");
   if (d == 0) return NAJU_OK;
@@ -1172,6 +1300,7 @@ int naju_rmsnorm_bwd(const void* x, const float* w, const float* rstd, const voi
   }
   if (!x || !w || !rstd || !dy || !dx)
     return fail(NAJU_ERR_INVALID, "null pointer (x, w, rstd, dy and dx are required)");
+  if (dres && dres == dx) return fail(NAJU_ERR_INVALID, "dres must not be dx");
   const size_t need = naju_rmsnorm_workspace_bytes(n_rows, d);
   if (dw && (!workspace || workspace_bytes < need))
     return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
@@ -1180,13 +1309,67 @@ int naju_rmsnorm_bwd(const void* x, const float* w, const float* rstd, const voi
   const int64_t nblk = norm_blocks(n_rows, G);
   float* part = dw ? (float*)workspace : nullptr;
   if (x_dtype == NAJU_DTYPE_F32)
-    norm_bwd_dt<float>(dy_dtype, G, dim3((unsigned)nblk), st, x, w, rstd, dy, dx, part, n_rows, d);
+    norm_bwd_dt<float>(dy_dtype, G, dim3((unsigned)nblk), st, x, w, rstd, dy, dx, dres, part, n_rows, d);
   else
-    norm_bwd_dt<bf16_t>(dy_dtype, G, dim3((unsigned)nblk), st, x, w, rstd, dy, dx, part, n_rows, d);
+    norm_bwd_dt<bf16_t>(dy_dtype, G, dim3((unsigned)nblk), st, x, w, rstd, dy, dx, dres, part, n_rows, d);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   if (dw) return launch_fold(part, nblk, d, 0, nullptr, dw, st);
   return NAJU_OK;
+}
+
+int naju_residual_dropout_fwd(const float* u, const void* mix, const int64_t* seed, float p, float* out, int64_t n,
+                              int mix_dtype, void* stream) {
+  g_err[0] = 0;
+  if (n < 0) return fail(NAJU_ERR_INVALID, "negative size");
+  if (!dt_ok(mix_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (!(p >= 0.f && p < 1.f)) return fail(NAJU_ERR_INVALID, "p must be in [0, 1)");
+  if (n == 0) return NAJU_OK;
+  if (!u || !mix || !out || (p > 0.f && !seed))
+    return fail(NAJU_ERR_INVALID, "null pointer (u, mix and out are required; seed when p > 0)");
+  const DropKeep dk = drop_keep(p);
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = n % kVec == 0 && al16(u) && al16(mix) && al16(out);
+  const int64_t units = vec ? n / kVec : n;
+  const dim3 grid((unsigned)((units + 255) / 256));
+  if (grid.x == 0 || (units + 255) / 256 > 0x7fffffffll) return fail(NAJU_ERR_UNSUPPORTED, "too many elements");
+  resdrop_t k;
+  if (mix_dtype == NAJU_DTYPE_F32)
+    k = vec ? (resdrop_t)residual_dropout_kernel<float, true> : (resdrop_t)residual_dropout_kernel<float, false>;
+  else if (mix_dtype == NAJU_DTYPE_BF16)
+    k = vec ? (resdrop_t)residual_dropout_kernel<bf16_t, true> : (resdrop_t)residual_dropout_kernel<bf16_t, false>;
+  else
+    k = vec ? (resdrop_t)residual_dropout_kernel<f16_t, true> : (resdrop_t)residual_dropout_kernel<f16_t, false>;
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, st, u, mix, p > 0.f ? seed : nullptr, dk, out, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NAJU_OK : fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+}
+
+int naju_dropout_bwd(const float* g, const int64_t* seed, float p, void* dmix, int64_t n, int mix_dtype,
+                     void* stream) {
+  g_err[0] = 0;
+  if (n < 0) return fail(NAJU_ERR_INVALID, "negative size");
+  if (!dt_ok(mix_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (!(p >= 0.f && p < 1.f)) return fail(NAJU_ERR_INVALID, "p must be in [0, 1)");
+  if (n == 0) return NAJU_OK;
+  if (!g || !dmix || (p > 0.f && !seed))
+    return fail(NAJU_ERR_INVALID, "null pointer (g and dmix are required; seed when p > 0)");
+  const DropKeep dk = drop_keep(p);
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = n % kVec == 0 && al16(g) && al16(dmix);
+  const int64_t units = vec ? n / kVec : n;
+  const dim3 grid((unsigned)((units + 255) / 256));
+  if ((units + 255) / 256 > 0x7fffffffll) return fail(NAJU_ERR_UNSUPPORTED, "too many elements");
+  dropbwd_t k;
+  if (mix_dtype == NAJU_DTYPE_F32)
+    k = vec ? (dropbwd_t)dropout_bwd_kernel<float, true> : (dropbwd_t)dropout_bwd_kernel<float, false>;
+  else if (mix_dtype == NAJU_DTYPE_BF16)
+    k = vec ? (dropbwd_t)dropout_bwd_kernel<bf16_t, true> : (dropbwd_t)dropout_bwd_kernel<bf16_t, false>;
+  else
+    k = vec ? (dropbwd_t)dropout_bwd_kernel<f16_t, true> : (dropbwd_t)dropout_bwd_kernel<f16_t, false>;
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, st, g, p > 0.f ? seed : nullptr, dk, dmix, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NAJU_OK : fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
 }
 
 }  // extern "C"

@@ -79,6 +79,18 @@ def sink_of(t):
     return getattr(t, "_naju_sink", None) if t is not None else None
 
 
+_ZEROS = {}
+
+
+def _zero(dtype, device):
+    """A cached 0-dim zero per (dtype, device): the storage of every marker."""
+    key = (dtype, device)
+    z = _ZEROS.get(key)
+    if z is None:
+        z = _ZEROS[key] = torch.zeros((), dtype=dtype, device=device)
+    return z
+
+
 class AccumSink:
     """One gradient buffer that the consumers of one tensor fill in turn,
     instead of each returning its own gradient for autograd to add: the
@@ -91,7 +103,7 @@ class AccumSink:
     def __init__(self, like):
         self.shape, self.dtype, self.device = like.shape, like.dtype, like.device
         self.buf = None
-        self._zero = torch.zeros((), dtype=like.dtype, device=like.device)
+        self._zero = _zero(like.dtype, like.device)
 
     def target(self):
         """(buffer, accumulate): the buffer, and whether it already holds an

@@ -36,7 +36,10 @@ from naju_amd.dwconv import dwconv
 from naju_amd.linear import compute_dtype, linear
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
+from naju_amd.rmsnorm import rms_norm_fork
 from naju_amd.rmsnorm import supported as rmsnorm_supported
+from naju_amd.residual import residual_dropout
+from naju_amd.residual import supported as residual_supported
 from naju_amd import scan as _scan
 from naju_amd.scan import naju_scan, naju_scan_hip
 
@@ -227,9 +230,25 @@ class NajuBlock(nn.Module):
         # the norm's output feeds in_proj only: take it in that GEMM's dtype
         return self.drop(self.mixer(self.norm(u, out_dtype=_out_dtype(u))))
 
+    def _fused(self, u):
+        # the norm and the residual read u; their gradients meet in the
+        # norm's backward pass, and the residual add and the dropout are one
+        # pass each way (naju_amd.residual)
+        u_res, h = rms_norm_fork(u, self.norm.weight, self.norm.eps, out_dtype=_out_dtype(u))
+        mix = self.mixer(h)
+        if not residual_supported(u_res, mix):
+            return u_res + self.drop(mix)
+        return residual_dropout(u_res, mix, self.drop.p if self.training else 0.0)
+
     def forward(self, u):
+        # CUDA float32 residual streams that the fused kernels serve
+        fused = u.is_cuda and u.dtype == torch.float32 and rmsnorm_supported(u)
         if self.use_ckpt and torch.is_grad_enabled():
+            if fused:
+                return checkpoint(self._fused, u, use_reentrant=False)
             return u + checkpoint(self._branch, u, use_reentrant=False)
+        if fused:
+            return self._fused(u)
         return u + self._branch(u)
 
 
