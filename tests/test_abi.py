@@ -23,7 +23,7 @@ def header_functions():
     names = set()
     for h in HEADERS:
         txt = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(naju_(?:scan|dwconv|mixer|readout|rmsnorm|loss|xent)_\w+)\s*\(", txt))
+        names |= set(re.findall(r"\b(naju_\w+)\s*\(", txt))
     return sorted(names)
 
 
