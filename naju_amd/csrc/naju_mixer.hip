@@ -12,7 +12,9 @@
 // as it is. The backward walks its block in reverse with a window of the
 // next K-1 output gradients, recomputing the pre-activation from x when the
 // activation is SiLU, and writes per-block partial sums of dw and dbias that
-// a second kernel folds in a fixed order (deterministic).
+// a second kernel folds in a fixed order (deterministic). The K = 4 kernels
+// (the mixer's) load every row a thread needs before using the first, so a
+// wave waits for memory once per block rather than once per row.
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -48,7 +50,10 @@ __device__ __forceinline__ void stv(void* p, int dt, int64_t i, float v) {
     ((f16_t*)p)[i] = (f16_t)v;
 }
 
-__device__ __forceinline__ float silu(float z) { return z / (1.f + __expf(-z)); }
+// sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an
+// IEEE divide, whose expansion made the SiLU kernels instruction-bound
+__device__ __forceinline__ float sigmoid_f(float z) { return __builtin_amdgcn_rcpf(1.f + __expf(-z)); }
+__device__ __forceinline__ float silu(float z) { return z * sigmoid_f(z); }
 
 // grid: (ceil(C / kThreads), ceil(T / kRows), batch)
 template <int K, bool SILU>
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void dwconv_bwd_kernel(const void* x, int
       float z = bc;
 #pragma unroll
       for (int j = 0; j < K; ++j) z = fmaf(wr[j], xv[j], z);
-      const float sg = 1.f / (1.f + __expf(-z));
+      const float sg = sigmoid_f(z);
       dz *= sg * fmaf(z, 1.f - sg, 1.f);  // d silu / dz = s (1 + z (1 - s))
     }
     if (t < t1) {
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, c
     const float zz = ldv(z, z_dt, r * z_ld + c);
     const float hh = ldv(h, h_dt, o);
     const float g = ldv(dy, dy_dt, o);
-    const float sg = 1.f / (1.f + __expf(-zz));
+    const float sg = sigmoid_f(zz);
     const float gs = g * (zz * sg);  // dy * SiLU(z)
     if (dcx) stv(dcx, dcx_dt, o, gs * scale);
     if (dh) stv(dh, dh_dt, o, gs * dv);
@@ -219,14 +224,14 @@ __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, c
 
 // ------------------------------------------------ vector fast paths (K = 4)
 //
-// The same operations with 8 channels per thread and 16-byte accesses (one
-// wave moves 1 KB per load instruction instead of 128 B), kVRows rows per
-// thread with all row loads issued together, one wave per block. Used when
-// C and the row strides are multiples of 8 and the pointers 16-byte
-// aligned; the scalar kernels above serve every other case.
+// The same operations on several channels per thread with 8- or 16-byte
+// accesses (the readout: 8 channels, kVRows rows per thread, one wave per
+// block; the convolutions: kCV channels, below). Used when C and the row
+// strides are multiples of 8 and the pointers 16-byte aligned; the scalar
+// kernels above serve every other case.
 constexpr int kVec = 8;
 constexpr int kVRows = 16;
-constexpr int kVRowsB = 32;  // rows per block of the vector conv backward (a longer reverse walk per halo)
+constexpr int kVRowsB = 32;  // rows per block of the vector conv backward (one dw / dbias partial row each)
 
 template <typename T>
 __device__ __forceinline__ void ld8(const T* p, float (&o)[kVec]) {
@@ -248,182 +253,208 @@ __device__ __forceinline__ void ld8f(const float* p, float (&o)[kVec]) {
   o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
 }
 
-// grid: (ceil(C / (64 * kVec)), ceil(T / kVRows), batch), 64 threads. A
-// thread walks its rows in order with the last K-1 inputs in registers.
+// The K = 4 vector kernels: kCV channels per thread (8- or 16-byte
+// accesses), every row a thread needs loaded before the first is used, so a
+// wave waits for memory once per block instead of once per row.
+constexpr int kCV = 4;    // channels per thread
+constexpr int kCRF = 16;  // forward: rows per thread (one wave per workgroup)
+constexpr int kCRB = 8;  // backward: rows per wave
+constexpr int kCWB = 4;  // backward: waves per workgroup, one block of kCWB * kCRB rows
+static_assert(kCWB * kCRB == kVRowsB, "one partial row per kVRowsB rows");
+
+template <typename T>
+using cvec_t = T __attribute__((ext_vector_type(kCV)));
+
+template <typename T>
+__device__ __forceinline__ cvec_t<T> ldc(const T* p) {
+  return *(const cvec_t<T>*)p;
+}
+template <typename T>
+__device__ __forceinline__ void stc(T* p, const float (&x)[kCV]) {
+  cvec_t<T> v;
+#pragma unroll
+  for (int j = 0; j < kCV; ++j) v[j] = (T)x[j];
+  *(cvec_t<T>*)p = v;
+}
+
+// grid: (ceil(C / (64 * kCV)), ceil(T / kCRF), batch), 64 threads: rows
+// t0 .. t0 + kCRF - 1 of kCV channels; x rows t0-3 .. and the add rows are
+// loaded first (rows outside [0, T) from a clamped row, then zeroed or
+// skipped).
 template <typename TX, typename TY, bool SILU, bool ADD>
 __global__ __launch_bounds__(64) void dwconv4_fwd_vec(const TX* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ w, const float* __restrict__ bias,
                                                       const TX* __restrict__ add, int64_t ld_add,
                                                       TY* __restrict__ y, int64_t T, int64_t C) {
-  constexpr int K = 4;
-  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  constexpr int K = 4, V = kCV, R = kCRF;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * V;
   if (c0 >= C) return;
   const int64_t b = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.y * kVRows;
-  const int64_t t1 = t0 + kVRows < T ? t0 + kVRows : T;
-  float wr[kVec][K], bc[kVec];
+  const int64_t t0 = (int64_t)blockIdx.y * R;
+  const TX* xb = x + b * T * ldx + c0;
+  cvec_t<TX> xr[R + K - 1], ar[R];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) {
+  for (int i = 0; i < R + K - 1; ++i) {
+    int64_t t = t0 - (K - 1) + i;
+    t = t < 0 ? 0 : (t < T ? t : T - 1);
+    xr[i] = ldc(xb + t * ldx);
+  }
+  if (ADD) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = t0 + r < T ? t0 + r : T - 1;
+      ar[r] = ldc(add + (b * T + t) * ld_add + c0);
+    }
+  }
+  float wr[V][K], bc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
     const float4 q = *(const float4*)(w + (c0 + j) * K);
     wr[j][0] = q.x, wr[j][1] = q.y, wr[j][2] = q.z, wr[j][3] = q.w;
+    bc[j] = bias ? bias[c0 + j] : 0.f;
   }
-  if (bias) {
-    ld8f(bias + c0, bc);
-  } else {
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) bc[j] = 0.f;
-  }
-  const TX* xb = x + b * T * ldx + c0;
-  float xw[K - 1][kVec];  // rows t-3, t-2, t-1 entering row t
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r;
+    if (t >= T) break;
+    float acc[V];
 #pragma unroll
-  for (int r = 0; r < K - 1; ++r) {
-    const int64_t t = t0 - (K - 1) + r;
-    if (t >= 0) {
-      ld8(xb + t * ldx, xw[r]);
-    } else {
+    for (int j = 0; j < V; ++j) {
+      float a = fmaf(wr[j][K - 1], (float)xr[r + K - 1][j], bc[j]);
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) xw[r][j] = 0.f;
-    }
-  }
-#pragma unroll 4
-  for (int64_t t = t0; t < t1; ++t) {
-    float xt[kVec], acc[kVec];
-    ld8(xb + t * ldx, xt);
-    const int64_t o = (b * T + t) * C + c0;
-    float ad[kVec];
-    if (ADD) ld8(add + (b * T + t) * ld_add + c0, ad);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      float a = fmaf(wr[j][K - 1], xt[j], bc[j]);
-#pragma unroll
-      for (int k = 0; k < K - 1; ++k) a = fmaf(wr[j][k], xw[k][j], a);
-      if (ADD) a += ad[j];
+      for (int k = 0; k < K - 1; ++k)
+        if (t - (K - 1) + k >= 0) a = fmaf(wr[j][k], (float)xr[r + k][j], a);
+      if (ADD) a += (float)ar[r][j];
       acc[j] = SILU ? silu(a) : a;
-      xw[0][j] = xw[1][j];
-      xw[1][j] = xw[2][j];
-      xw[2][j] = xt[j];
     }
-    st8(y + o, acc);
+    stc(y + (b * T + t) * C + c0, acc);
   }
 }
 
-// Backward of dwconv4_fwd_vec without add (the reverse walk of
-// dwconv_bwd_kernel with 8 channels per thread); part [batch * nTB][C][K+1].
+// Backward of dwconv4_fwd_vec without add; part [batch * nTB][C][K+1].
+// grid: (ceil(C / (64 * kCV)), ceil(T / (kCWB * kCRB)), batch), kCWB waves:
+// wave w takes rows tw = t0 + w * kCRB .. + kCRB - 1 and loads dy rows
+// tw .. tw + kCRB + 2, x rows tw - 3 .. (tw + kCRB + 2 with SiLU, whose
+// derivative needs the pre-activation of those rows) and, when adding, the
+// dx rows, all before the first is used. The waves' dw / dbias sums are
+// added in wave order through LDS into the block's partial row.
 template <typename TX, typename TDY, bool SILU>
-__global__ __launch_bounds__(64) void dwconv4_bwd_vec(const TX* __restrict__ x, int64_t ldx,
-                                                      const float* __restrict__ w, const float* __restrict__ bias,
-                                                      const TDY* __restrict__ dy, TX* __restrict__ dx, int64_t ld_dx,
-                                                      TX* __restrict__ dadd, int64_t ld_dadd,
-                                                      float* __restrict__ part, int64_t T, int64_t C, int acc) {
-  constexpr int K = 4;
-  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
-  if (c0 >= C) return;
+__global__ __launch_bounds__(64 * kCWB) void dwconv4_bwd_vec(const TX* __restrict__ x, int64_t ldx,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             const TDY* __restrict__ dy, TX* __restrict__ dx,
+                                                             int64_t ld_dx, TX* __restrict__ dadd, int64_t ld_dadd,
+                                                             float* __restrict__ part, int64_t T, int64_t C, int acc) {
+  constexpr int K = 4, V = kCV, R = kCRB;
+  constexpr int NZ = R + K - 1;                 // dz rows tw .. tw + R + 2
+  constexpr int NX = SILU ? R + 2 * (K - 1) : R + K - 1;  // x rows tw - 3 ..
+  __shared__ float s_red[kCWB][(K + 1) * V][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + lane) * V;
+  const bool cok = c0 < C;
+  const int64_t cc = cok ? c0 : 0;  // in-bounds channel for the loads of idle lanes
   const int64_t b = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.y * kVRowsB;
-  const int64_t t1 = t0 + kVRowsB < T ? t0 + kVRowsB : T;
-  float wr[kVec][K], bc[kVec];
+  const int64_t tw = (int64_t)blockIdx.y * (kCWB * R) + wv * R;
+  const TX* xb = x + b * T * ldx + cc;
+  cvec_t<TDY> gr[NZ];
+  cvec_t<TX> xr[NX], dr[R];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) {
-    const float4 q = *(const float4*)(w + (c0 + j) * K);
-    wr[j][0] = q.x, wr[j][1] = q.y, wr[j][2] = q.z, wr[j][3] = q.w;
+  for (int i = 0; i < NZ; ++i) {
+    const int64_t t = tw + i < T ? tw + i : T - 1;
+    gr[i] = ldc(dy + (b * T + t) * C + cc);
   }
-  if (bias) {
-    ld8f(bias + c0, bc);
-  } else {
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) bc[j] = 0.f;
+  for (int i = 0; i < NX; ++i) {
+    int64_t t = tw - (K - 1) + i;
+    t = t < 0 ? 0 : (t < T ? t : T - 1);
+    xr[i] = ldc(xb + t * ldx);
   }
-  const TX* xb = x + b * T * ldx + c0;
-  const int64_t tstart = (t1 - 1 + (K - 1)) < (T - 1) ? (t1 - 1 + (K - 1)) : (T - 1);
-  // windows entering row t: gz[k] = dz[t+1+k] (k < K-1), xv[k] = x[t-(K-1)+k]
-  float gz[K - 1][kVec], xv[K][kVec];
+  if (dx && acc) {
 #pragma unroll
-  for (int k = 0; k < K - 1; ++k)
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) gz[k][j] = 0.f;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int64_t t = tstart - (K - 1) + k;
-    if (t >= 0) {
-      ld8(xb + t * ldx, xv[k]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) xv[k][j] = 0.f;
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = tw + r < T ? tw + r : T - 1;
+      dr[r] = ldc(dx + (b * T + t) * ld_dx + cc);
     }
   }
-  float dw[kVec][K], db[kVec];
+  float wr[V][K], bc[V];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) {
+  for (int j = 0; j < V; ++j) {
+    const float4 q = *(const float4*)(w + (cc + j) * K);
+    wr[j][0] = q.x, wr[j][1] = q.y, wr[j][2] = q.z, wr[j][3] = q.w;
+    bc[j] = bias ? bias[cc + j] : 0.f;
+  }
+  // x row i as floats, zero outside [0, T)
+  auto xv = [&](int i, int j) -> float {
+    const int64_t t = tw - (K - 1) + i;
+    return (t >= 0 && t < T) ? (float)xr[i][j] : 0.f;
+  };
+  // dz of rows tw + i (zero at and beyond T)
+  float dz[NZ][V];
+#pragma unroll
+  for (int i = 0; i < NZ; ++i) {
+    const bool tv = tw + i < T;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      float g = tv ? (float)gr[i][j] : 0.f;
+      if (SILU) {
+        float z = bc[j];
+#pragma unroll
+        for (int k = 0; k < K; ++k) z = fmaf(wr[j][k], xv(i + k, j), z);
+        const float sg = sigmoid_f(z);
+        g *= sg * fmaf(z, 1.f - sg, 1.f);
+      }
+      dz[i][j] = g;
+    }
+  }
+  float dw[V][K], db[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
     db[j] = 0.f;
 #pragma unroll
     for (int k = 0; k < K; ++k) dw[j][k] = 0.f;
   }
-#pragma unroll 4
-  for (int64_t t = tstart; t >= t0; --t) {
-    float dz[kVec], xn[kVec];
-    ld8(dy + (b * T + t) * C + c0, dz);
-    // the row entering the x window next; loaded from a clamped (in-bounds)
-    // row without a branch, so the loads of later iterations can be issued
-    // early, and zeroed when it lies outside the block's window
-    const int64_t tn = t - K;
-    ld8(xb + (tn >= 0 ? tn : 0) * ldx, xn);
-    if (!(tn >= 0 && t - 1 >= t0)) {
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) xn[j] = 0.f;
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = tw + r;
+    if (t >= T) break;
+    float g[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      float a = wr[j][K - 1] * dz[r][j];
+#pragma unroll
+      for (int k = 0; k < K - 1; ++k) a = fmaf(wr[j][k], dz[r + K - 1 - k][j], a);
+      g[j] = a;
+#pragma unroll
+      for (int k = 0; k < K; ++k) dw[j][k] = fmaf(dz[r][j], xv(r + k, j), dw[j][k]);
+      db[j] += dz[r][j];
     }
-    if (SILU) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        float z = bc[j];
-#pragma unroll
-        for (int k = 0; k < K; ++k) z = fmaf(wr[j][k], xv[k][j], z);
-        const float sg = 1.f / (1.f + __expf(-z));
-        dz[j] *= sg * fmaf(z, 1.f - sg, 1.f);
-      }
-    }
-    if (t < t1) {
-      float g[kVec];
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        float a = wr[j][K - 1] * dz[j];
-#pragma unroll
-        for (int k = 0; k < K - 1; ++k) a = fmaf(wr[j][k], gz[K - 2 - k][j], a);
-        g[j] = a;
-#pragma unroll
-        for (int k = 0; k < K; ++k) dw[j][k] = fmaf(dz[j], xv[k][j], dw[j][k]);
-        db[j] += dz[j];
-      }
+    if (cok) {
       if (dx) {
-        TX* q = dx + (b * T + t) * ld_dx + c0;
         if (acc) {
-          // dx += g: one rounding to TX of the sum
-          float o[kVec];
-          ld8(q, o);
 #pragma unroll
-          for (int j = 0; j < kVec; ++j) g[j] += o[j];
+          for (int j = 0; j < V; ++j) g[j] += (float)dr[r][j];
         }
-        st8(q, g);
+        stc(dx + (b * T + t) * ld_dx + c0, g);
       }
-      if (!SILU && dadd) st8(dadd + (b * T + t) * ld_dadd + c0, dz);
-    }
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      gz[2][j] = gz[1][j];
-      gz[1][j] = gz[0][j];
-      gz[0][j] = dz[j];
-      xv[3][j] = xv[2][j];
-      xv[2][j] = xv[1][j];
-      xv[1][j] = xv[0][j];
-      xv[0][j] = xn[j];
+      if (!SILU && dadd) stc(dadd + (b * T + t) * ld_dadd + c0, dz[r]);
     }
   }
   if (part) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) s_red[wv][j * (K + 1) + k][lane] = dw[j][k];
+      s_red[wv][j * (K + 1) + K][lane] = db[j];
+    }
+    __syncthreads();
+    // wave w sums entries e = w, w + kCWB, ... over the waves in wave order
     float* pp = part + (((int64_t)b * gridDim.y + blockIdx.y) * C + c0) * (K + 1);
+    for (int e = wv; e < (K + 1) * V; e += kCWB) {
+      float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) pp[j * (K + 1) + k] = dw[j][k];
-      pp[j * (K + 1) + K] = db[j];
+      for (int u = 0; u < kCWB; ++u) s += s_red[u][e][lane];
+      if (cok) pp[e] = s;
     }
   }
 }
@@ -479,7 +510,7 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
     float o0[kVec], o1[kVec], o2[kVec];
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const float sg = 1.f / (1.f + __expf(-zz[j]));
+      const float sg = sigmoid_f(zz[j]);
       const float gs = g[j] * (zz[j] * sg);
       o0[j] = gs * scale;
       o1[j] = gs * dv[j];
@@ -615,12 +646,12 @@ dwf_vec_t dwf_vec_for(int y_dt, bool silu, bool add) {
 
 // The K = 4 vector kernel for these arguments, or nullptr (scalar path):
 // x and add in one dtype, y in that dtype or float32, C, x_ld and add_ld
-// multiples of 8, 16-byte aligned pointers, T / kVRows blocks within the
+// multiples of 8, 16-byte aligned pointers, T / kCRF blocks within the
 // grid limit.
 dwf_vec_t pick_fwd_vec(const void* x, int64_t x_ld, const float* w, const float* bias, const void* add,
                        int64_t add_ld, void* y, int64_t T, int64_t C, int K, int act, int x_dt, int add_dt,
                        int y_dt) {
-  if (K != 4 || C % kVec || x_ld % kVec || (add && add_ld % kVec) || (T + kVRows - 1) / kVRows > 65535)
+  if (K != 4 || C % kVec || x_ld % kVec || (add && add_ld % kVec) || (T + kCRF - 1) / kCRF > 65535)
     return nullptr;
   if (!al16(x) || !al16(w) || !al16(y) || (bias && !al16(bias)) || (add && !al16(add))) return nullptr;
   if (add && add_dt != x_dt) return nullptr;
@@ -1086,7 +1117,7 @@ int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (batch == 0 || T == 0 || C == 0) return NAJU_OK;
   if (!x || !w || !y) return fail(NAJU_ERR_INVALID, "null pointer (x, w and y are required)");
   if (dwf_vec_t kv = pick_fwd_vec(x, x_ld, w, bias, add, add_ld, y, T, C, K, act, x_dtype, add_dtype, y_dtype)) {
-    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)((T + kVRows - 1) / kVRows),
+    const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)((T + kCRF - 1) / kCRF),
                     (unsigned)batch);
     hipLaunchKernelGGL(kv, grid, dim3(64), 0, (hipStream_t)stream, x, x_ld, w, bias, add, add_ld, y, T, C);
   } else {
@@ -1140,8 +1171,8 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (dwb_vec_t kv = pick_bwd_vec(x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, T, C, K, act, x_dtype, dy_dtype,
                                   dx_dtype, dadd_dtype)) {
     const int64_t ntb = (T + kVRowsB - 1) / kVRowsB;
-    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)ntb, (unsigned)batch);
-    hipLaunchKernelGGL(kv, grid, dim3(64), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C, acc);
+    const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)ntb, (unsigned)batch);
+    hipLaunchKernelGGL(kv, grid, dim3(64 * kCWB), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C, acc);
     nblk = batch * ntb;
   } else {
     const dim3 grid((unsigned)((C + kThreads - 1) / kThreads), (unsigned)n_tblocks(T), (unsigned)batch);
