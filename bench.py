@@ -535,8 +535,8 @@ def _bench_lm(steps, warmup, tune_gemms=None, line=True, ckpt_rows=None):
     d_model 768, vocab 50257, N = 64) on a batch of 8 x 2048 uniformly random
     token ids: bf16 autocast forward, cross-entropy (the fused HIP kernels of
     naju_amd.xent on the bf16 logits), backward, gradient
-    clipping at 1.0 and an AdamW step, with every mixer's scan on the HIP
-    kernels. value = tokens per second. line=True: the whole bench line;
+    clipping at 1.0 and an AdamW step (one fused HIP pass for both,
+    naju_amd.optim), with every mixer's scan on the HIP kernels. value = tokens per second. line=True: the whole bench line;
     else the entry of the per-configuration table. ckpt_rows: the scans'
     checkpoint interval (NAJU_CKPT_ROWS for the run; None = the default).
     peak_GiB: torch.cuda.max_memory_allocated over the timed steps."""
@@ -551,6 +551,7 @@ def _bench_lm(steps, warmup, tune_gemms=None, line=True, ckpt_rows=None):
 def _bench_lm_run(steps, warmup, tune_gemms, line, ckpt_rows):
     import torch
     from naju_amd.mixer import NajuLM, build_optimizer
+    from naju_amd.optim import AdamW as NajuAdamW
     from naju_amd.xent import cross_entropy
     from naju_amd import gemm_tuning
     dev = torch.device("cuda", 0)
@@ -575,8 +576,12 @@ def _bench_lm_run(steps, warmup, tune_gemms, line, ckpt_rows):
             loss = cross_entropy(logits.view(-1, V), y.view(-1))
         opt.zero_grad(set_to_none=True)
         loss.backward()
-        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
-        opt.step()
+        if isinstance(opt, NajuAdamW):
+            # clip_grad_norm_(params, 1.0) + step(), the clip inside the update
+            opt.step(max_grad_norm=1.0)
+        else:
+            torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+            opt.step()
         return loss
 
     for _ in range(warmup):

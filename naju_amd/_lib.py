@@ -1,5 +1,5 @@
 """ctypes binding of the C ABI declared in include/naju_scan.h,
-include/naju_mixer.h and include/naju_loss.h.
+include/naju_mixer.h, include/naju_loss.h and include/naju_optim.h.
 
 The library is naju_amd/libnaju_scan.so (built by naju_amd/build.py). Nothing
 here falls back to another implementation: if the library is missing or a
@@ -53,6 +53,10 @@ EXPORTED = (
     "naju_xent_workspace_bytes",
     "naju_xent_fwd",
     "naju_xent_bwd",
+    "naju_optim_last_error",
+    "naju_grad_norm_workspace_bytes",
+    "naju_grad_norm",
+    "naju_adamw_step",
 )
 
 _lib = None
@@ -148,6 +152,16 @@ def lib():
     # x, x_ld, target, n_rows, n_cols, x_dt, ignore_index, lse, scale, dloss, dx, dx_ld, dx_dt, stream
     L.naju_xent_bwd.argtypes = [P, I64, P, I64, I64, I, I64, P, P, P, P, I64, I, P]
     L.naju_xent_bwd.restype = I
+    L.naju_optim_last_error.argtypes = []
+    L.naju_optim_last_error.restype = ctypes.c_char_p
+    L.naju_grad_norm_workspace_bytes.argtypes = [I64]
+    L.naju_grad_norm_workspace_bytes.restype = SZ
+    # tensors, chunk_tensor, n_tensors, n_chunks, max_norm, norm, coef, ws, ws_bytes, stream
+    L.naju_grad_norm.argtypes = [P, P, I, I64, ctypes.c_float, P, P, P, SZ, P]
+    L.naju_grad_norm.restype = I
+    # tensors, chunk_tensor, n_tensors, n_chunks, groups (host), n_groups, grad_coef, stream
+    L.naju_adamw_step.argtypes = [P, P, I, I64, P, I, P, P]
+    L.naju_adamw_step.restype = I
     _lib = L
     return _lib
 
@@ -167,6 +181,13 @@ def check_mixer(rc):
     """check() for the calls of include/naju_mixer.h."""
     if rc != OK:
         raise NajuScanError(rc, lib().naju_mixer_last_error().decode(errors="replace"))
+    return rc
+
+
+def check_optim(rc):
+    """check() for the calls of include/naju_optim.h."""
+    if rc != OK:
+        raise NajuScanError(rc, lib().naju_optim_last_error().decode(errors="replace"))
     return rc
 
 

@@ -10,7 +10,8 @@ import sys
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_PKG)
 LIB_PATH = os.path.join(_PKG, "libnaju_scan.so")
-SOURCES = [os.path.join(_PKG, "csrc", n) for n in ("naju_scan.hip", "naju_scan_mc.hip", "naju_mixer.hip", "naju_loss.hip")]
+SOURCES = [os.path.join(_PKG, "csrc", n)
+           for n in ("naju_scan.hip", "naju_scan_mc.hip", "naju_mixer.hip", "naju_loss.hip", "naju_optim.hip")]
 
 # Packed-FP32 VALU ops are disabled for all device code: only plain fp32
 # arithmetic is emitted.

@@ -34,6 +34,7 @@ from torch.utils.checkpoint import checkpoint
 from naju_amd import gradsink
 from naju_amd.dwconv import dwconv
 from naju_amd.linear import compute_dtype, linear
+from naju_amd.optim import AdamW as NajuAdamW
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
 from naju_amd.rmsnorm import rms_norm_fork
@@ -281,14 +282,19 @@ def build_optimizer(model, lr, weight_decay=0.1, fused=None):
     lr * sqrt(d_inner), weight_decay / sqrt(d_inner) and eps 1e-8 / sqrt(d_inner)
     (reference naju/optim.py:30-52).
 
-    ``fused`` (default: True when every parameter is a CUDA tensor) selects
-    torch's single-kernel AdamW update instead of its multi-kernel foreach
-    one: the same update rule, one read and write of each optimizer tensor."""
+    ``fused`` (default: True when every parameter is a CUDA tensor) selects a
+    single-pass update: naju_amd.optim.AdamW (the HIP multi-tensor kernels,
+    whose ``step(max_grad_norm=...)`` also clips) when every parameter is
+    float32, else torch's fused AdamW. The same update rule as the
+    reference's torch.optim.AdamW either way."""
     if fused is None:
         fused = all(p.is_cuda for p in model.parameters())
+    opt_cls, kw = torch.optim.AdamW, {"fused": fused}
+    if fused and all(p.dtype == torch.float32 for p in model.parameters()):
+        opt_cls, kw = NajuAdamW, {}
     mixers = [m for m in model.modules() if isinstance(m, NajuMixer) and m.gate_reparam]
     if not mixers:
-        return torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay, fused=fused)
+        return opt_cls(model.parameters(), lr=lr, weight_decay=weight_decay, **kw)
     widths = {m.d_inner for m in mixers}
     if len(widths) != 1:
         raise ValueError(f"mixed d_inner across gate_reparam mixers: {widths}")
@@ -296,7 +302,7 @@ def build_optimizer(model, lr, weight_decay=0.1, fused=None):
     gate = {id(p) for m in mixers for p in (m.f_proj.weight, m.i_proj.weight)}
     rest = [p for p in model.parameters() if id(p) not in gate]
     gate_params = [p for p in model.parameters() if id(p) in gate]
-    return torch.optim.AdamW(
+    return opt_cls(
         [{"params": rest},
          {"params": gate_params, "lr": lr * mult, "weight_decay": weight_decay / mult, "eps": 1e-8 / mult}],
-        lr=lr, weight_decay=weight_decay, fused=fused)
+        lr=lr, weight_decay=weight_decay, **kw)

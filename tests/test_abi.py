@@ -15,7 +15,7 @@ import torch
 from naju_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("naju_scan.h", "naju_mixer.h", "naju_loss.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("naju_scan.h", "naju_mixer.h", "naju_loss.h", "naju_optim.h")]
 F32, BF16, F16 = 0, 1, 2
 
 

@@ -92,10 +92,12 @@ def test_lm_train_step_reduces_loss(gpu):
 
 def test_lm_step_fused_loss_and_optimizer_match_reference_loop(gpu):
     """The C5 step's pieces: naju_amd.xent.cross_entropy on the bf16 logits
-    and build_optimizer's fused AdamW against the reference loop's
-    cross_entropy on the float32 upcast and torch's foreach AdamW
-    (evals/lm/train.py:70-79), from the same weights and batch."""
+    and build_optimizer's AdamW with the clip inside its update
+    (naju_amd.optim, step(max_grad_norm=1.0)) against the reference loop's
+    cross_entropy on the float32 upcast, clip_grad_norm_ and torch's foreach
+    AdamW (evals/lm/train.py:70-80), from the same weights and batch."""
     from naju_amd.mixer import build_optimizer
+    from naju_amd.optim import AdamW as NajuAdamW
     from naju_amd.xent import cross_entropy
     dev = torch.device("cuda", 0)
     V = 97
@@ -105,7 +107,7 @@ def test_lm_step_fused_loss_and_optimizer_match_reference_loop(gpu):
     mb.load_state_dict(ma.state_dict())
     oa = build_optimizer(ma, lr=1e-3)
     ob = torch.optim.AdamW(mb.parameters(), lr=1e-3, weight_decay=0.1, foreach=True)
-    assert oa.defaults["fused"]
+    assert isinstance(oa, NajuAdamW)
     ids = torch.randint(0, V, (3, 40), device=dev)
     for step in range(3):
         losses = []
@@ -117,8 +119,11 @@ def test_lm_step_fused_loss_and_optimizer_match_reference_loop(gpu):
                     torch.nn.functional.cross_entropy(logits.float(), tgt)
             o.zero_grad(set_to_none=True)
             loss.backward()
-            torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
-            o.step()
+            if fused:
+                o.step(max_grad_norm=1.0)
+            else:
+                torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
+                o.step()
             losses.append(float(loss.detach()))
         assert abs(losses[0] - losses[1]) < 2e-3 * abs(losses[1]), (step, losses)
     for (n, pa), pb in zip(ma.named_parameters(), mb.parameters()):
@@ -218,9 +223,9 @@ def test_lm_c5_full_size_training_steps(gpu):
         del logits
         opt.zero_grad(set_to_none=True)
         loss.backward()
-        gn = torch.nn.utils.clip_grad_norm_(lm.parameters(), 1.0)
-        assert torch.isfinite(gn), "non-finite gradient norm"
-        opt.step()
+        # the bench's step: clip at 1.0 inside the fused AdamW update
+        opt.step(max_grad_norm=1.0)
+        assert torch.isfinite(opt.grad_norm), "non-finite gradient norm"
         losses.append(float(loss.detach()))
     assert all(math.isfinite(v) for v in losses)
     assert math.log(V) - 0.2 < losses[0] < math.log(V) + 2.0, losses
