@@ -460,6 +460,33 @@ __global__ __launch_bounds__(64 * kCWB) void dwconv4_bwd_vec(const TX* __restric
 }
 
 // grid: (ceil(C / (64 * kVec)), ceil(n_rows / kVRows)), 64 threads
+// Rows of a readout block are taken kRB at a time: in a whole batch every
+// load of the kRB rows is issued before the first is used, so a wave waits
+// for memory once per kRB rows (the block's last, partial batch goes row by
+// row).
+constexpr int kRB = 8;
+static_assert(kVRows % kRB == 0, "whole row batches per block");
+
+template <typename T>
+using v8_t = T __attribute__((ext_vector_type(kVec)));
+
+template <typename T>
+__device__ __forceinline__ v8_t<T> ld8r(const T* p) {
+  return *(const v8_t<T>*)p;
+}
+
+// An empty asm that takes v's registers as in-out operands: every load
+// feeding v is complete there, and nothing that uses v moves above it.
+template <typename T>
+__device__ __forceinline__ void pin8(v8_t<T>& v) {
+  static_assert(sizeof(v8_t<T>) % 4 == 0, "whole registers");
+  uint32_t w[sizeof(v8_t<T>) / 4];
+  __builtin_memcpy(w, &v, sizeof(w));
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(w) / 4); ++i) asm volatile("" : "+v"(w[i]));
+  __builtin_memcpy(&v, w, sizeof(w));
+}
+
 template <typename T>
 __global__ __launch_bounds__(64) void readout_fwd_vec(const T* __restrict__ cx, const T* __restrict__ h,
                                                       const T* __restrict__ z, int64_t z_ld,
@@ -470,17 +497,33 @@ __global__ __launch_bounds__(64) void readout_fwd_vec(const T* __restrict__ cx, 
   const int64_t r0 = (int64_t)blockIdx.y * kVRows;
   float dv[kVec];
   ld8f(Dv + c0, dv);
+  auto one = [&](const v8_t<T>& xa, const v8_t<T>& xh, const v8_t<T>& xz, int64_t row) {
+    float a[kVec];
 #pragma unroll
-  for (int r = 0; r < kVRows; ++r) {
-    const int64_t row = r0 + r;
-    if (row >= n_rows) break;
-    float a[kVec], hh[kVec], zz[kVec];
-    ld8(cx + row * C + c0, a);
-    ld8(h + row * C + c0, hh);
-    ld8(z + row * z_ld + c0, zz);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) a[j] = fmaf(a[j], scale, dv[j] * hh[j]) * silu(zz[j]);
+    for (int j = 0; j < kVec; ++j) a[j] = fmaf((float)xa[j], scale, dv[j] * (float)xh[j]) * silu((float)xz[j]);
     st8(y + row * C + c0, a);
+  };
+  for (int rb = 0; rb < kVRows; rb += kRB) {
+    const int64_t b0 = r0 + rb;
+    if (b0 + kRB <= n_rows) {
+      // a whole batch: straight-line loads, then the rows
+      v8_t<T> xa[kRB], xh[kRB], xz[kRB];
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) {
+        xa[r] = ld8r(cx + (b0 + r) * C + c0);
+        xh[r] = ld8r(h + (b0 + r) * C + c0);
+        xz[r] = ld8r(z + (b0 + r) * z_ld + c0);
+      }
+      // (keeps the compiler from sinking the loads into the rows' code)
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) pin8(xa[r]), pin8(xh[r]), pin8(xz[r]);
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) one(xa[r], xh[r], xz[r], b0 + r);
+    } else {
+      for (int64_t row = b0; row < n_rows; ++row)
+        one(ld8r(cx + row * C + c0), ld8r(h + row * C + c0), ld8r(z + row * z_ld + c0), row);
+      break;
+    }
   }
 }
 
@@ -498,29 +541,43 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
   ld8f(Dv + c0, dv);
 #pragma unroll
   for (int j = 0; j < kVec; ++j) dd[j] = 0.f;
-#pragma unroll
-  for (int r = 0; r < kVRows; ++r) {
-    const int64_t row = r0 + r;
-    if (row >= n_rows) break;
-    float cc[kVec], hh[kVec], zz[kVec], g[kVec];
-    ld8(cx + row * C + c0, cc);
-    ld8(h + row * C + c0, hh);
-    ld8(z + row * z_ld + c0, zz);
-    ld8(dy + row * C + c0, g);
+  auto one = [&](const v8_t<T>& xc, const v8_t<T>& xh, const v8_t<T>& xz, const v8_t<T>& xg, int64_t row) {
     float o0[kVec], o1[kVec], o2[kVec];
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const float sg = sigmoid_f(zz[j]);
-      const float gs = g[j] * (zz[j] * sg);
+      const float zz = (float)xz[j], g = (float)xg[j], hh = (float)xh[j];
+      const float sg = sigmoid_f(zz);
+      const float gs = g * (zz * sg);
       o0[j] = gs * scale;
       o1[j] = gs * dv[j];
-      dd[j] = fmaf(gs, hh[j], dd[j]);
-      const float a = fmaf(cc[j], scale, dv[j] * hh[j]);
-      o2[j] = g[j] * a * sg * fmaf(zz[j], 1.f - sg, 1.f);
+      dd[j] = fmaf(gs, hh, dd[j]);
+      const float a = fmaf((float)xc[j], scale, dv[j] * hh);
+      o2[j] = g * a * sg * fmaf(zz, 1.f - sg, 1.f);
     }
     if (dcx) st8(dcx + row * C + c0, o0);
     if (dh) st8(dh + row * C + c0, o1);
     if (dz) st8(dz + row * dz_ld + c0, o2);
+  };
+  for (int rb = 0; rb < kVRows; rb += kRB) {
+    const int64_t b0 = r0 + rb;
+    if (b0 + kRB <= n_rows) {
+      // a whole batch: straight-line loads, then the rows
+      v8_t<T> xc[kRB], xh[kRB], xz[kRB], xg[kRB];
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) {
+        xc[r] = ld8r(cx + (b0 + r) * C + c0);
+        xh[r] = ld8r(h + (b0 + r) * C + c0);
+        xz[r] = ld8r(z + (b0 + r) * z_ld + c0);
+        xg[r] = ld8r(dy + (b0 + r) * C + c0);
+      }
+#pragma unroll
+      for (int r = 0; r < kRB; ++r) one(xc[r], xh[r], xz[r], xg[r], b0 + r);
+    } else {
+      for (int64_t row = b0; row < n_rows; ++row)
+        one(ld8r(cx + row * C + c0), ld8r(h + row * C + c0), ld8r(z + row * z_ld + c0), ld8r(dy + row * C + c0),
+            row);
+      break;
+    }
   }
   if (part) {
     float* pp = part + (int64_t)blockIdx.y * C + c0;
@@ -817,32 +874,58 @@ __global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_vec(const TX* __r
   __shared__ float s_acc[kNormWaves][G * 256];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t r0 = ((int64_t)blockIdx.x * kNormWaves + wv) * RPW;
-  float wr[G][4], acc[G][4], xv[RPW][G][4], gv[RPW][G][4], rs[RPW];
+  float wr[G][4], acc[G][4], xv[RPW][G][4], gv[RPW][G][4], qv[RPW][G][4], rs[RPW];
+  // Every load is unconditional, from a clamped in-bounds row and column
+  // (d % 4 == 0, so column d - 4 exists), and lanes or rows outside the
+  // matrix take zeros afterwards: loads behind per-lane branches were each
+  // waited for at the end of their branch.
+  const int64_t rlast = n_rows - 1;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t c = ((int64_t)g * 64 + lane) * 4;
+    const int64_t cc = c < d ? c : d - 4;
+    ld4(w + cc, wr[g]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
-    if (c < d) {
-      ld4(w + c, wr[g]);
-    } else {
+    for (int e = 0; e < 4; ++e) {
+      acc[g][e] = 0.f;
+      wr[g][e] = c < d ? wr[g][e] : 0.f;
+    }
+  }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) wr[g][e] = 0.f;
+  for (int i = 0; i < RPW; ++i) {
+    const int64_t rr = r0 + i < n_rows ? r0 + i : rlast;
+    rs[i] = rstd[rr];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t c = ((int64_t)g * 64 + lane) * 4;
+      const int64_t cc = c < d ? c : d - 4;
+      ld4(x + rr * d + cc, xv[i][g]);
+      ld4(dy + rr * d + cc, gv[i][g]);
+    }
+  }
+  if (dres) {
+    // the residual gradient with the other loads, before any is used
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int64_t rr = r0 + i < n_rows ? r0 + i : rlast;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int64_t c = ((int64_t)g * 64 + lane) * 4;
+        ld4(dres + rr * d + (c < d ? c : d - 4), qv[i][g]);
+      }
     }
   }
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const bool rv = r0 + i < n_rows;
-    rs[i] = rv ? rstd[r0 + i] : 0.f;
+    rs[i] = rv ? rs[i] : 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const int64_t c = ((int64_t)g * 64 + lane) * 4;
-      if (rv && c < d) {
-        ld4(x + (r0 + i) * d + c, xv[i][g]);
-        ld4(dy + (r0 + i) * d + c, gv[i][g]);
-      } else {
+      const bool ok = rv && ((int64_t)g * 64 + lane) * 4 < d;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xv[i][g][e] = gv[i][g][e] = 0.f;
+      for (int e = 0; e < 4; ++e) {
+        xv[i][g][e] = ok ? xv[i][g][e] : 0.f;
+        gv[i][g][e] = ok ? gv[i][g][e] : 0.f;
       }
     }
   }
@@ -868,10 +951,8 @@ __global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_vec(const TX* __r
         for (int e = 0; e < 4; ++e) o[e] = fmaf(wr[g][e] * gv[i][g][e], rs[i], -xv[i][g][e] * k);
         if (dres) {
           // dx = dres + the norm's gradient (the residual stream's other use)
-          float q[4];
-          ld4(dres + r * d + c, q);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] += q[e];
+          for (int e = 0; e < 4; ++e) o[e] += qv[i][g][e];
         }
         st4(dx + r * d + c, o);
       }
