@@ -599,8 +599,24 @@ __global__ __launch_bounds__(1024) void fold_cols_kernel(const float* __restrict
   const int64_t i = (int64_t)blockIdx.x * 64 + lane;
   float acc = 0.f;
   if (i < ncol) {
-#pragma unroll 4
-    for (int64_t q = wv; q < nblk; q += 16) acc += part[q * ncol + i];
+    // kU blocks per round, all loaded (from an in-bounds block past the
+    // end) before the first is added; added in block order
+    constexpr int kU = 16;
+    for (int64_t q0 = wv; q0 < nblk; q0 += 16 * kU) {
+      float v[kU];
+#pragma unroll
+      for (int k = 0; k < kU; ++k) {
+        const int64_t q = q0 + 16 * k;
+        v[k] = part[(q < nblk ? q : q0) * ncol + i];
+      }
+#pragma unroll
+      for (int k = 0; k < kU; ++k) asm volatile("" : "+v"(v[k]));
+#pragma unroll
+      for (int k = 0; k < kU; ++k) {
+        const float t = acc + v[k];
+        acc = q0 + 16 * k < nblk ? t : acc;
+      }
+    }
   }
   s[wv][lane] = acc;
   __syncthreads();
