@@ -139,6 +139,12 @@ int naju_residual_dropout_fwd(const float* u, const void* mix, const int64_t* se
 int naju_dropout_bwd(const float* g, const int64_t* seed, float p, void* dmix, int64_t n, int mix_dtype,
                      void* stream);
 
+/* out[i] = sum over s < n_parts of parts[s * n + i], added in s order, all
+ * float32 (1 <= n_parts <= 16): the split-K weight gradient's sum of its
+ * token parts (naju_amd/linear.py). No reference counterpart: the reference
+ * forms the weight gradient as one GEMM. */
+int naju_sum_parts(const float* parts, int n_parts, int64_t n, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,7 @@ EXPORTED = (
     "naju_rmsnorm_bwd_add",
     "naju_residual_dropout_fwd",
     "naju_dropout_bwd",
+    "naju_sum_parts",
     "naju_loss_last_error",
     "naju_xent_workspace_bytes",
     "naju_xent_fwd",
@@ -142,6 +143,8 @@ def lib():
     L.naju_residual_dropout_fwd.restype = I
     L.naju_dropout_bwd.argtypes = [P, P, F, P, I64, I, P]
     L.naju_dropout_bwd.restype = I
+    L.naju_sum_parts.argtypes = [P, I, I64, P, P]
+    L.naju_sum_parts.restype = I
     L.naju_loss_last_error.argtypes = []
     L.naju_loss_last_error.restype = ctypes.c_char_p
     L.naju_xent_workspace_bytes.argtypes = [I64]

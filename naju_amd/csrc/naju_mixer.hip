@@ -633,6 +633,34 @@ __global__ __launch_bounds__(1024) void fold_cols_kernel(const float* __restrict
   }
 }
 
+// out = sum of the n_parts rows of parts [n_parts][n], in row order. The
+// vector kernel (S parts, n % 4 == 0, 16-byte aligned pointers) gives a
+// thread four consecutive entries and loads them from all S parts before
+// adding; other cases take one entry per thread.
+constexpr int kMaxParts = 16;
+template <int S>
+__global__ __launch_bounds__(256) void sum_parts_vec(const float4* __restrict__ parts, int64_t n4,
+                                                     float4* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n4) return;
+  float4 v[S];
+#pragma unroll
+  for (int q = 0; q < S; ++q) v[q] = parts[(int64_t)q * n4 + t];
+  float4 a = v[0];
+#pragma unroll
+  for (int q = 1; q < S; ++q) a.x += v[q].x, a.y += v[q].y, a.z += v[q].z, a.w += v[q].w;
+  out[t] = a;
+}
+
+__global__ __launch_bounds__(256) void sum_parts_any(const float* __restrict__ parts, int n_parts, int64_t n,
+                                                     float* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n) return;
+  float a = parts[t];
+  for (int q = 1; q < n_parts; ++q) a += parts[(int64_t)q * n + t];
+  out[t] = a;
+}
+
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 thread_local char g_err[256] = "";
@@ -1498,6 +1526,35 @@ int naju_dropout_bwd(const float* g, const int64_t* seed, float p, void* dmix, i
   hipLaunchKernelGGL(k, grid, dim3(256), 0, st, g, p > 0.f ? seed : nullptr, dk, dmix, n);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? NAJU_OK : fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+}
+
+int naju_sum_parts(const float* parts, int n_parts, int64_t n, float* out, void* stream) {
+  g_err[0] = 0;
+  if (n < 0) return fail(NAJU_ERR_INVALID, "negative size");
+  if (n_parts < 1 || n_parts > kMaxParts) return fail(NAJU_ERR_INVALID, "n_parts must be in [1, %d]", kMaxParts);
+  if (n == 0) return NAJU_OK;
+  if (!parts || !out) return fail(NAJU_ERR_INVALID, "null pointer");
+  if ((n + 255) / 256 > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "too many entries (%lld)", (long long)n);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t n4 = n / 4;
+  const dim3 g4((unsigned)((n4 + 255) / 256));
+  const bool vec = n % 4 == 0 && al16(parts) && al16(out);
+  const float4* p4 = (const float4*)parts;
+  float4* o4 = (float4*)out;
+  if (vec && n_parts == 2) {
+    hipLaunchKernelGGL(sum_parts_vec<2>, g4, dim3(256), 0, st, p4, n4, o4);
+  } else if (vec && n_parts == 4) {
+    hipLaunchKernelGGL(sum_parts_vec<4>, g4, dim3(256), 0, st, p4, n4, o4);
+  } else if (vec && n_parts == 8) {
+    hipLaunchKernelGGL(sum_parts_vec<8>, g4, dim3(256), 0, st, p4, n4, o4);
+  } else if (vec && n_parts == 16) {
+    hipLaunchKernelGGL(sum_parts_vec<16>, g4, dim3(256), 0, st, p4, n4, o4);
+  } else {
+    hipLaunchKernelGGL(sum_parts_any, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, parts, n_parts, n, out);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
 }
 
 }  // extern "C"

@@ -9,7 +9,7 @@ the output is small (768 x 1536 for out_proj: 72 tiles of 128 x 128 for 256
 compute units), so a single GEMM leaves most of the GPU idle. Here the
 tokens are split into S equal parts, the S partial products run as one
 batched GEMM with float32 output, and the parts are added in float32
-(fixed order). dW comes out in float32, the parameters' dtype, without the
+in part order (naju_sum_parts). dW comes out in float32, the parameters' dtype, without the
 bfloat16 rounding and the cast back that autocast's backward applies.
 
 CUDA tensors in float16 / bfloat16 only (the callers fall back to nn.Linear
@@ -18,6 +18,7 @@ otherwise).
 import torch
 import torch.nn.functional as F
 
+from naju_amd import _lib
 from naju_amd.gradsink import acc_sink_of
 
 # output tiles (128 x 128) times parts kept at or below this: about two
@@ -49,7 +50,12 @@ def weight_grad(dy, x):
         return torch.mm(dy.t(), x, out_dtype=torch.float32)
     # the left operand is the transposed view, the right one is contiguous
     part = torch.bmm(dy.view(s, K // s, M).transpose(1, 2), x.view(s, K // s, N), out_dtype=torch.float32)
-    return part.sum(0)
+    # the parts added in part order (one pass over them, naju_sum_parts)
+    out = torch.empty(M, N, dtype=torch.float32, device=dy.device)
+    L = _lib.lib()
+    _lib.check_mixer(L.naju_sum_parts(part.data_ptr(), s, M * N, out.data_ptr(),
+                                      torch.cuda.current_stream(dy.device).cuda_stream))
+    return out
 
 
 class _Linear(torch.autograd.Function):

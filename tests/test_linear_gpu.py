@@ -46,3 +46,26 @@ def test_linear_matches_autocast_and_float64(gpu, shape, n_out):
     err = float((wh.grad.double() - dw64).abs().max() / dw64.abs().max())
     assert err <= 1e-5, err
 
+
+
+@pytest.mark.parametrize("n_parts,n,offset", [(2, 4096, 0), (4, 1000, 0), (8, 768 * 1536, 0), (16, 64, 0),
+                                              (3, 999, 0), (8, 1024, 1)])
+def test_sum_parts_adds_in_part_order(gpu, n_parts, n, offset):
+    """naju_sum_parts: the float32 sum of the parts in part order, bitwise
+    (the vector kernels for 2, 4, 8, 16 aligned parts, the element kernel
+    for other counts, sizes and an unaligned start)."""
+    from naju_amd import _lib
+    g = torch.Generator(device=gpu).manual_seed(n_parts * 7 + n)
+    buf = torch.randn(n_parts * n + offset, generator=g, device=gpu)
+    parts = buf[offset:].view(n_parts, n)
+    out = torch.empty(n, device=gpu)
+    L = _lib.lib()
+    _lib.check_mixer(L.naju_sum_parts(parts.data_ptr(), n_parts, n, out.data_ptr(),
+                                      torch.cuda.current_stream(gpu).cuda_stream))
+    ref = parts[0].clone()
+    for q in range(1, n_parts):
+        ref += parts[q]
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    with pytest.raises(_lib.NajuScanError):
+        _lib.check_mixer(L.naju_sum_parts(parts.data_ptr(), 17, n, out.data_ptr(), 0))
