@@ -139,6 +139,36 @@ int naju_residual_dropout_fwd(const float* u, const void* mix, const int64_t* se
 int naju_dropout_bwd(const float* g, const int64_t* seed, float p, void* dmix, int64_t n, int mix_dtype,
                      void* stream);
 
+/* The mixer's two gate convolutions over one input in one pass (x read
+ * once): y0 = add0 + bias0 + conv(x, w0) and y1 = add1 + bias1 + conv(x, w1),
+ * each as naju_dwconv_fwd with act = 0. Served for K = 4, C and the row
+ * strides (x_ld, add_ld) multiples of 8, 16-byte aligned pointers, add in x's
+ * dtype, y in x's dtype or float32 (else NAJU_ERR_UNSUPPORTED, and the
+ * caller makes the two single calls). Both adds share add_ld (slices of one
+ * projection output); bias0 / bias1 may be NULL. */
+int naju_dwconv_pair_fwd(const void* x, int64_t x_ld, const float* w0, const float* bias0, const void* add0,
+                         const float* w1, const float* bias1, const void* add1, int64_t add_ld, void* y0, void* y1,
+                         int64_t batch, int64_t T, int64_t C, int K, int x_dtype, int y_dtype, void* stream);
+
+/* Bytes of workspace naju_dwconv_pair_bwd needs (both weights' partial
+ * sums); no zero-fill needed. */
+size_t naju_dwconv_pair_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K);
+
+/* Backward of naju_dwconv_pair_fwd: dx = conv0^T(dy0) + conv1^T(dy1) (x's
+ * gradient from both, rounded once to x's dtype; with accumulate != 0 dx
+ * receives dx + that sum), dw0 / dbias0 / dw1 / dbias1 (each nullable; fixed
+ * order, deterministic), and the adds' gradients dy0, dy1 written in x's
+ * dtype into dadd0 / dadd1 (nullable, row stride dadd_ld). dy0, dy1 are
+ * [batch, T, C] contiguous in x's dtype or float32. Same shapes served as
+ * the forward. No reference counterpart as one call: the reference's two
+ * Conv1d modules and autograd's sum of their input gradients
+ * (naju/mixer.py:108-110). */
+int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const float* w1, const void* dy0,
+                         const void* dy1, void* dx, int64_t dx_ld, float* dw0, float* dbias0, float* dw1,
+                         float* dbias1, void* dadd0, void* dadd1, int64_t dadd_ld, int64_t batch, int64_t T,
+                         int64_t C, int K, int accumulate, int x_dtype, int dy_dtype, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* out[i] = sum over s < n_parts of parts[s * n + i], added in s order, all
  * float32 (1 <= n_parts <= 16): the split-K weight gradient's sum of its
  * token parts (naju_amd/linear.py). No reference counterpart: the reference

@@ -50,6 +50,9 @@ EXPORTED = (
     "naju_residual_dropout_fwd",
     "naju_dropout_bwd",
     "naju_sum_parts",
+    "naju_dwconv_pair_fwd",
+    "naju_dwconv_pair_workspace_bytes",
+    "naju_dwconv_pair_bwd",
     "naju_loss_last_error",
     "naju_xent_workspace_bytes",
     "naju_xent_fwd",
@@ -145,6 +148,16 @@ def lib():
     L.naju_dropout_bwd.restype = I
     L.naju_sum_parts.argtypes = [P, I, I64, P, P]
     L.naju_sum_parts.restype = I
+    # x, x_ld, w0, bias0, add0, w1, bias1, add1, add_ld, y0, y1, batch, T, C, K, x_dt, y_dt, stream
+    L.naju_dwconv_pair_fwd.argtypes = [P, I64] + [P] * 6 + [I64, P, P] + [I64] * 3 + [I] * 3 + [P]
+    L.naju_dwconv_pair_fwd.restype = I
+    L.naju_dwconv_pair_workspace_bytes.argtypes = [I64] * 3 + [I]
+    L.naju_dwconv_pair_workspace_bytes.restype = SZ
+    # x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dw0, db0, dw1, db1, dadd0, dadd1, dadd_ld, batch, T, C, K,
+    # accumulate, x_dt, dy_dt, ws, ws_bytes, stream
+    L.naju_dwconv_pair_bwd.argtypes = ([P, I64] + [P] * 5 + [I64] + [P] * 6 + [I64] * 4 + [I] * 4
+                                       + [P, SZ, P])
+    L.naju_dwconv_pair_bwd.restype = I
     L.naju_loss_last_error.argtypes = []
     L.naju_loss_last_error.restype = ctypes.c_char_p
     L.naju_xent_workspace_bytes.argtypes = [I64]

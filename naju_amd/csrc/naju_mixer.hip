@@ -459,6 +459,207 @@ __global__ __launch_bounds__(64 * kCWB) void dwconv4_bwd_vec(const TX* __restric
   }
 }
 
+// ---- the two gate convolutions of a mixer over one input (K = 4, add, no
+// activation): y0 = add0 + b0 + conv(x, w0) and y1 = add1 + b1 + conv(x, w1)
+// in one pass, x read once. The forward takes the layout of
+// dwconv4_fwd_vec; the backward that of dwconv4_bwd_vec with kPW waves of
+// kPR rows, x's gradient conv0^T(dy0) + conv1^T(dy1) formed (and added to
+// dx) with one rounding, and each weight's partial row in its own part
+// array.
+constexpr int kPR = 8;  // backward rows per wave
+constexpr int kPW = 4;  // backward waves per workgroup
+static_assert(kPW * kPR == kVRowsB, "one partial row per kVRowsB rows");
+
+template <typename TX, typename TY>
+__global__ __launch_bounds__(64) void dwconv4_pair_fwd_vec(const TX* __restrict__ x, int64_t ldx,
+                                                           const float* __restrict__ w0,
+                                                           const float* __restrict__ b0,
+                                                           const float* __restrict__ w1,
+                                                           const float* __restrict__ b1,
+                                                           const TX* __restrict__ add0, const TX* __restrict__ add1,
+                                                           int64_t ld_add, TY* __restrict__ y0, TY* __restrict__ y1,
+                                                           int64_t T, int64_t C) {
+  constexpr int K = 4, V = kCV, R = kCRF;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * V;
+  if (c0 >= C) return;
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * R;
+  const TX* xb = x + b * T * ldx + c0;
+  cvec_t<TX> xr[R + K - 1], a0[R], a1[R];
+#pragma unroll
+  for (int i = 0; i < R + K - 1; ++i) {
+    int64_t t = t0 - (K - 1) + i;
+    t = t < 0 ? 0 : (t < T ? t : T - 1);
+    xr[i] = ldc(xb + t * ldx);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r < T ? t0 + r : T - 1;
+    a0[r] = ldc(add0 + (b * T + t) * ld_add + c0);
+    a1[r] = ldc(add1 + (b * T + t) * ld_add + c0);
+  }
+  float wr0[V][K], wr1[V][K], bc0[V], bc1[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const float4 q0 = *(const float4*)(w0 + (c0 + j) * K);
+    const float4 q1 = *(const float4*)(w1 + (c0 + j) * K);
+    wr0[j][0] = q0.x, wr0[j][1] = q0.y, wr0[j][2] = q0.z, wr0[j][3] = q0.w;
+    wr1[j][0] = q1.x, wr1[j][1] = q1.y, wr1[j][2] = q1.z, wr1[j][3] = q1.w;
+    bc0[j] = b0 ? b0[c0 + j] : 0.f;
+    bc1[j] = b1 ? b1[c0 + j] : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = t0 + r;
+    if (t >= T) break;
+    float o0[V], o1[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float xt = (float)xr[r + K - 1][j];
+      float s0 = fmaf(wr0[j][K - 1], xt, bc0[j]), s1 = fmaf(wr1[j][K - 1], xt, bc1[j]);
+#pragma unroll
+      for (int k = 0; k < K - 1; ++k)
+        if (t - (K - 1) + k >= 0) {
+          const float xv = (float)xr[r + k][j];
+          s0 = fmaf(wr0[j][k], xv, s0);
+          s1 = fmaf(wr1[j][k], xv, s1);
+        }
+      o0[j] = s0 + (float)a0[r][j];
+      o1[j] = s1 + (float)a1[r][j];
+    }
+    stc(y0 + (b * T + t) * C + c0, o0);
+    stc(y1 + (b * T + t) * C + c0, o1);
+  }
+}
+
+template <typename TX, typename TDY>
+__global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __restrict__ x, int64_t ldx,
+                                                                 const float* __restrict__ w0,
+                                                                 const float* __restrict__ w1,
+                                                                 const TDY* __restrict__ dy0,
+                                                                 const TDY* __restrict__ dy1,
+                                                                 TX* __restrict__ dx, int64_t ld_dx,
+                                                                 TX* __restrict__ dadd0, TX* __restrict__ dadd1,
+                                                                 int64_t ld_dadd, float* __restrict__ part0,
+                                                                 float* __restrict__ part1, int64_t T, int64_t C,
+                                                                 int acc) {
+  constexpr int K = 4, V = kCV, R = kPR;
+  constexpr int NZ = R + K - 1;  // dy rows tw .. tw + R + 2
+  constexpr int NX = R + K - 1;  // x rows tw - 3 .. tw + R - 1
+  __shared__ float s_red[kPW][(K + 1) * V][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + lane) * V;
+  const bool cok = c0 < C;
+  const int64_t cc = cok ? c0 : 0;
+  const int64_t b = blockIdx.z;
+  const int64_t tw = (int64_t)blockIdx.y * (kPW * R) + wv * R;
+  const TX* xb = x + b * T * ldx + cc;
+  cvec_t<TDY> g0[NZ], g1[NZ];
+  cvec_t<TX> xr[NX], dr[R];
+#pragma unroll
+  for (int i = 0; i < NZ; ++i) {
+    const int64_t t = tw + i < T ? tw + i : T - 1;
+    g0[i] = ldc(dy0 + (b * T + t) * C + cc);
+    g1[i] = ldc(dy1 + (b * T + t) * C + cc);
+  }
+#pragma unroll
+  for (int i = 0; i < NX; ++i) {
+    int64_t t = tw - (K - 1) + i;
+    t = t < 0 ? 0 : (t < T ? t : T - 1);
+    xr[i] = ldc(xb + t * ldx);
+  }
+  if (dx && acc) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = tw + r < T ? tw + r : T - 1;
+      dr[r] = ldc(dx + (b * T + t) * ld_dx + cc);
+    }
+  }
+  float wr0[V][K], wr1[V][K];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const float4 q0 = *(const float4*)(w0 + (cc + j) * K);
+    const float4 q1 = *(const float4*)(w1 + (cc + j) * K);
+    wr0[j][0] = q0.x, wr0[j][1] = q0.y, wr0[j][2] = q0.z, wr0[j][3] = q0.w;
+    wr1[j][0] = q1.x, wr1[j][1] = q1.y, wr1[j][2] = q1.z, wr1[j][3] = q1.w;
+  }
+  // dy of rows tw + i (zero at and beyond T), x of row tw - 3 + i (zero
+  // outside [0, T))
+  auto d0 = [&](int i, int j) -> float { return tw + i < T ? (float)g0[i][j] : 0.f; };
+  auto d1 = [&](int i, int j) -> float { return tw + i < T ? (float)g1[i][j] : 0.f; };
+  auto xv = [&](int i, int j) -> float {
+    const int64_t t = tw - (K - 1) + i;
+    return (t >= 0 && t < T) ? (float)xr[i][j] : 0.f;
+  };
+  float dw0[V][K], dw1[V][K], db0[V], db1[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    db0[j] = db1[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) dw0[j][k] = dw1[j][k] = 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = tw + r;
+    if (t >= T) break;
+    float g[V], e0[V], e1[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      float a0 = wr0[j][K - 1] * d0(r, j), a1 = wr1[j][K - 1] * d1(r, j);
+#pragma unroll
+      for (int k = 0; k < K - 1; ++k) {
+        a0 = fmaf(wr0[j][k], d0(r + K - 1 - k, j), a0);
+        a1 = fmaf(wr1[j][k], d1(r + K - 1 - k, j), a1);
+      }
+      g[j] = a0 + a1;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        dw0[j][k] = fmaf(d0(r, j), xv(r + k, j), dw0[j][k]);
+        dw1[j][k] = fmaf(d1(r, j), xv(r + k, j), dw1[j][k]);
+      }
+      db0[j] += d0(r, j);
+      db1[j] += d1(r, j);
+      e0[j] = d0(r, j);
+      e1[j] = d1(r, j);
+    }
+    if (cok) {
+      if (dx) {
+        if (acc) {
+#pragma unroll
+          for (int j = 0; j < V; ++j) g[j] += (float)dr[r][j];
+        }
+        stc(dx + (b * T + t) * ld_dx + c0, g);
+      }
+      if (dadd0) stc(dadd0 + (b * T + t) * ld_dadd + c0, e0);
+      if (dadd1) stc(dadd1 + (b * T + t) * ld_dadd + c0, e1);
+    }
+  }
+  // the waves' sums in wave order, one weight after the other through the
+  // same LDS
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    float* part = q == 0 ? part0 : part1;
+    if (!part) continue;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) s_red[wv][j * (K + 1) + k][lane] = q == 0 ? dw0[j][k] : dw1[j][k];
+      s_red[wv][j * (K + 1) + K][lane] = q == 0 ? db0[j] : db1[j];
+    }
+    __syncthreads();
+    float* pp = part + (((int64_t)b * gridDim.y + blockIdx.y) * C + c0) * (K + 1);
+    for (int e = wv; e < (K + 1) * V; e += kPW) {
+      float s = 0.f;
+#pragma unroll
+      for (int u = 0; u < kPW; ++u) s += s_red[u][e][lane];
+      if (cok) pp[e] = s;
+    }
+    __syncthreads();
+  }
+}
+
+
 // grid: (ceil(C / (64 * kVec)), ceil(n_rows / kVRows)), 64 threads
 // Rows of a readout block are taken kRB at a time: in a whole batch every
 // load of the kRB rows is issued before the first is used, so a wave waits
@@ -1554,6 +1755,152 @@ int naju_sum_parts(const float* parts, int n_parts, int64_t n, float* out, void*
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+}  // extern "C"
+
+// ---- the gate pair (dwconv4_pair_*): host side
+namespace {
+bool pair_ok(int64_t T, int64_t C, int K, std::initializer_list<int64_t> lds, std::initializer_list<const void*> ptrs) {
+  if (K != 4 || C % kVec || (T + kCRF - 1) / kCRF > 65535 || (T + kVRowsB - 1) / kVRowsB > 65535) return false;
+  for (int64_t ld : lds)
+    if (ld % kVec) return false;
+  for (const void* p : ptrs)
+    if (p && !al16(p)) return false;
+  return true;
+}
+
+template <typename TX, typename TY>
+void pair_fwd_launch(dim3 grid, hipStream_t st, const void* x, int64_t x_ld, const float* w0, const float* b0,
+                     const float* w1, const float* b1, const void* add0, const void* add1, int64_t add_ld, void* y0,
+                     void* y1, int64_t T, int64_t C) {
+  hipLaunchKernelGGL((dwconv4_pair_fwd_vec<TX, TY>), grid, dim3(64), 0, st, (const TX*)x, x_ld, w0, b0, w1, b1,
+                     (const TX*)add0, (const TX*)add1, add_ld, (TY*)y0, (TY*)y1, T, C);
+}
+
+template <typename TX>
+void pair_fwd_dt(int y_dt, dim3 grid, hipStream_t st, const void* x, int64_t x_ld, const float* w0, const float* b0,
+                 const float* w1, const float* b1, const void* add0, const void* add1, int64_t add_ld, void* y0,
+                 void* y1, int64_t T, int64_t C) {
+  if (y_dt == NAJU_DTYPE_F32)
+    pair_fwd_launch<TX, float>(grid, st, x, x_ld, w0, b0, w1, b1, add0, add1, add_ld, y0, y1, T, C);
+  else
+    pair_fwd_launch<TX, TX>(grid, st, x, x_ld, w0, b0, w1, b1, add0, add1, add_ld, y0, y1, T, C);
+}
+
+template <typename TX, typename TDY>
+void pair_bwd_launch(dim3 grid, hipStream_t st, const void* x, int64_t x_ld, const float* w0, const float* w1,
+                     const void* dy0, const void* dy1, void* dx, int64_t dx_ld, void* dadd0, void* dadd1,
+                     int64_t dadd_ld, float* part0, float* part1, int64_t T, int64_t C, int acc) {
+  hipLaunchKernelGGL((dwconv4_pair_bwd_vec<TX, TDY>), grid, dim3(64 * kPW), 0, st, (const TX*)x, x_ld, w0, w1,
+                     (const TDY*)dy0, (const TDY*)dy1, (TX*)dx, dx_ld, (TX*)dadd0, (TX*)dadd1, dadd_ld, part0, part1,
+                     T, C, acc);
+}
+
+template <typename TX>
+void pair_bwd_dt(int dy_dt, dim3 grid, hipStream_t st, const void* x, int64_t x_ld, const float* w0,
+                 const float* w1, const void* dy0, const void* dy1, void* dx, int64_t dx_ld, void* dadd0,
+                 void* dadd1, int64_t dadd_ld, float* part0, float* part1, int64_t T, int64_t C, int acc) {
+  if (dy_dt == NAJU_DTYPE_F32 && !std::is_same<TX, float>::value)
+    pair_bwd_launch<TX, float>(grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0, part1,
+                               T, C, acc);
+  else
+    pair_bwd_launch<TX, TX>(grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0, part1, T,
+                            C, acc);
+}
+}  // namespace
+
+extern "C" {
+
+int naju_dwconv_pair_fwd(const void* x, int64_t x_ld, const float* w0, const float* bias0, const void* add0,
+                         const float* w1, const float* bias1, const void* add1, int64_t add_ld, void* y0, void* y1,
+                         int64_t batch, int64_t T, int64_t C, int K, int x_dtype, int y_dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check(batch, T, C, K, 0, x_ld);
+  if (rc) return rc;
+  if (add_ld < C) return fail(NAJU_ERR_INVALID, "add_ld (%lld) must be >= C (%lld)", (long long)add_ld, (long long)C);
+  if (!dt_ok(x_dtype) || !dt_ok(y_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (y_dtype != x_dtype && y_dtype != NAJU_DTYPE_F32)
+    return fail(NAJU_ERR_UNSUPPORTED, "y must have x's dtype or float32");
+  if (batch == 0 || T == 0 || C == 0) return NAJU_OK;
+  if (!x || !w0 || !w1 || !add0 || !add1 || !y0 || !y1)
+    return fail(NAJU_ERR_INVALID, "null pointer (x, both weights, adds and outputs are required)");
+  if (!pair_ok(T, C, K, {x_ld, add_ld}, {x, w0, w1, bias0, bias1, add0, add1, y0, y1}))
+    return fail(NAJU_ERR_UNSUPPORTED,
+                "the pair kernels need K = 4, C and the row strides multiples of 8 and 16-byte aligned pointers");
+  const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)((T + kCRF - 1) / kCRF), (unsigned)batch);
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == NAJU_DTYPE_BF16)
+    pair_fwd_dt<bf16_t>(y_dtype, grid, st, x, x_ld, w0, bias0, w1, bias1, add0, add1, add_ld, y0, y1, T, C);
+  else if (x_dtype == NAJU_DTYPE_F16)
+    pair_fwd_dt<f16_t>(y_dtype, grid, st, x, x_ld, w0, bias0, w1, bias1, add0, add1, add_ld, y0, y1, T, C);
+  else
+    pair_fwd_dt<float>(y_dtype, grid, st, x, x_ld, w0, bias0, w1, bias1, add0, add1, add_ld, y0, y1, T, C);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+size_t naju_dwconv_pair_workspace_bytes(int64_t batch, int64_t T, int64_t C, int K) {
+  const size_t one = naju_dwconv_workspace_bytes(batch, T, C, K);
+  return one ? 2 * one : 0;
+}
+
+int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const float* w1, const void* dy0,
+                         const void* dy1, void* dx, int64_t dx_ld, float* dw0, float* dbias0, float* dw1,
+                         float* dbias1, void* dadd0, void* dadd1, int64_t dadd_ld, int64_t batch, int64_t T,
+                         int64_t C, int K, int accumulate, int x_dtype, int dy_dtype, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check(batch, T, C, K, 0, x_ld);
+  if (rc) return rc;
+  if (dx && dx_ld < C) return fail(NAJU_ERR_INVALID, "dx_ld (%lld) must be >= C (%lld)", (long long)dx_ld, (long long)C);
+  if ((dadd0 || dadd1) && dadd_ld < C)
+    return fail(NAJU_ERR_INVALID, "dadd_ld (%lld) must be >= C (%lld)", (long long)dadd_ld, (long long)C);
+  if (!dt_ok(x_dtype) || !dt_ok(dy_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (dy_dtype != x_dtype && dy_dtype != NAJU_DTYPE_F32)
+    return fail(NAJU_ERR_UNSUPPORTED, "dy must have x's dtype or float32");
+  hipStream_t st = (hipStream_t)stream;
+  if (C == 0) return NAJU_OK;
+  const bool sums = dw0 || dbias0 || dw1 || dbias1;
+  if (batch == 0 || T == 0) {
+    // empty sums: the folds over zero blocks write the zeros
+    if (dw0 || dbias0) {
+      if ((rc = launch_fold(nullptr, 0, C, K, dw0, dbias0, st))) return rc;
+    }
+    if (dw1 || dbias1) return launch_fold(nullptr, 0, C, K, dw1, dbias1, st);
+    return NAJU_OK;
+  }
+  if (!x || !w0 || !w1 || !dy0 || !dy1) return fail(NAJU_ERR_INVALID, "null pointer (x, weights and dy are required)");
+  if (!pair_ok(T, C, K, {x_ld, dx ? dx_ld : C, (dadd0 || dadd1) ? dadd_ld : C},
+               {x, w0, w1, dy0, dy1, dx, dadd0, dadd1}))
+    return fail(NAJU_ERR_UNSUPPORTED,
+                "the pair kernels need K = 4, C and the row strides multiples of 8 and 16-byte aligned pointers");
+  const size_t one = naju_dwconv_workspace_bytes(batch, T, C, K);
+  if (sums && (!workspace || workspace_bytes < 2 * one))
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", 2 * one,
+                workspace ? workspace_bytes : (size_t)0);
+  // the second part array starts 16-byte aligned (one = rows * C * (K+1) floats + 256, C % 8 == 0)
+  float* part0 = (dw0 || dbias0) ? (float*)workspace : nullptr;
+  float* part1 = (dw1 || dbias1) ? (float*)((char*)workspace + one) : nullptr;
+  const int64_t ntb = (T + kVRowsB - 1) / kVRowsB;
+  const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)ntb, (unsigned)batch);
+  const int acc = accumulate ? 1 : 0;
+  if (x_dtype == NAJU_DTYPE_BF16)
+    pair_bwd_dt<bf16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
+                        part1, T, C, acc);
+  else if (x_dtype == NAJU_DTYPE_F16)
+    pair_bwd_dt<f16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
+                       part1, T, C, acc);
+  else
+    pair_bwd_dt<float>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
+                       part1, T, C, acc);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  const int64_t nblk = batch * ntb;
+  if (part0 && (rc = launch_fold(part0, nblk, C, K, dw0, dbias0, st))) return rc;
+  if (part1) return launch_fold(part1, nblk, C, K, dw1, dbias1, st);
   return NAJU_OK;
 }
 

@@ -155,3 +155,103 @@ def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
     if out_dtype is None:
         out_dtype = x.dtype
     return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype, x_sink, add_sink, x_acc)
+
+
+class _DwConvPair(torch.autograd.Function):
+    """The mixer's two gate convolutions over one input in one pass each way
+    (naju_dwconv_pair_fwd / _bwd): y0 = add0 + b0 + conv(x, w0), y1 = add1 +
+    b1 + conv(x, w1); x's gradient from both formed with one rounding."""
+
+    @staticmethod
+    def forward(ctx, x, w0, b0, add0, w1, b1, add1, out_dtype, sinks, x_acc):
+        B, T, C = x.shape
+        K = w0.shape[1]
+        ldx, ld_add = x.stride(1), add0.stride(1)
+        y0 = torch.empty((B, T, C), dtype=out_dtype, device=x.device)
+        y1 = torch.empty_like(y0)
+        L = _lib.lib()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check_mixer(L.naju_dwconv_pair_fwd(
+            _ptr(x), ldx, _ptr(w0), _ptr(b0), _ptr(add0), _ptr(w1), _ptr(b1), _ptr(add1), ld_add, _ptr(y0), _ptr(y1),
+            B, T, C, K, _DT[x.dtype], _DT[out_dtype], stream))
+        ctx.save_for_backward(x, w0, w1)
+        ctx.has_b = (b0 is not None, b1 is not None)
+        ctx.sinks, ctx.x_acc = sinks, x_acc
+        return y0, y1
+
+    @staticmethod
+    def backward(ctx, dy0, dy1):
+        x, w0, w1 = ctx.saved_tensors
+        B, T, C = x.shape
+        K = w0.shape[1]
+        if dy1.dtype != dy0.dtype:
+            dy0, dy1 = dy0.float(), dy1.float()
+        dy0, dy1 = dy0.contiguous(), dy1.contiguous()
+        need = ctx.needs_input_grad
+        dx = dx_ret = None
+        acc = 0
+        if need[0]:
+            if ctx.x_acc is not None:
+                dx, accumulate = ctx.x_acc.target()
+                acc = int(accumulate)
+                dx_ret = ctx.x_acc.marker()
+            else:
+                dx = torch.empty((B, T, C), dtype=x.dtype, device=x.device)
+        f32 = dict(dtype=torch.float32, device=x.device)
+        dw0 = torch.empty((C, K), **f32) if need[1] else None
+        db0 = torch.empty((C,), **f32) if need[2] and ctx.has_b[0] else None
+        dw1 = torch.empty((C, K), **f32) if need[4] else None
+        db1 = torch.empty((C,), **f32) if need[5] and ctx.has_b[1] else None
+        # the adds' gradients are dy0, dy1: written into the split's buffer
+        # in x's dtype (pair_supported checked that the adds are pieces of
+        # one gradsink.split with x's dtype)
+        (s0, col0), (s1, col1) = ctx.sinks
+        dadd0 = s0.slice(col0, C) if need[3] else None
+        dadd1 = s1.slice(col1, C) if need[6] else None
+        ld_dadd = (dadd0 if dadd0 is not None else dadd1).stride(1) if (dadd0 is not None or dadd1 is not None) else C
+        L = _lib.lib()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        nbytes = L.naju_dwconv_pair_workspace_bytes(B, T, C, K)
+        ws = _WS.get(x.device, stream, nbytes)
+        _lib.check_mixer(L.naju_dwconv_pair_bwd(
+            _ptr(x), x.stride(1), _ptr(w0), _ptr(w1), _ptr(dy0), _ptr(dy1), _ptr(dx),
+            dx.stride(1) if dx is not None else C, _ptr(dw0), _ptr(db0), _ptr(dw1), _ptr(db1), _ptr(dadd0),
+            _ptr(dadd1), ld_dadd, B, T, C, K, acc, _DT[x.dtype], _DT[dy0.dtype], _ptr(ws), ws.numel(), stream))
+        return (dx if dx_ret is None else dx_ret, dw0, db0, dadd0, dw1, db1, dadd1, None, None, None)
+
+
+def pair_supported(x, w0, add0, w1, add1):
+    """Whether dwconv_pair serves these tensors: CUDA [B, T, C] x with C and
+    its row stride multiples of 8, kernel size 4, and adds that are pieces
+    of one gradsink.split (one row stride, x's dtype), 16-byte aligned."""
+    if not (x.is_cuda and x.dim() == 3 and x.dtype in _DT and add0.shape == x.shape and add1.shape == x.shape):
+        return False
+    C = x.shape[2]
+    if C % 8 or w0.numel() != 4 * C or w1.numel() != 4 * C:
+        return False
+    s0, s1 = sink_of(add0), sink_of(add1)
+    if s0 is None or s1 is None or s0[0] is not s1[0]:
+        return False
+    if add0.dtype != x.dtype or add1.dtype != x.dtype or add0.stride() != add1.stride():
+        return False
+    for t in (x, add0, add1):
+        if t.stride(2) != 1 or t.stride(0) != t.shape[1] * t.stride(1) or t.stride(1) % 8 or t.data_ptr() % 16:
+            return False
+    return True
+
+
+def dwconv_pair(x, w0, b0, add0, w1, b1, add1, out_dtype):
+    """(add0 + b0 + conv(x, w0), add1 + b1 + conv(x, w1)) in one pass each
+    way, for what pair_supported accepts: the two gate logits of the mixer,
+    each as dwconv(x, w, b, add=add, out_dtype=out_dtype) computes it."""
+    C = x.shape[2]
+    ws = []
+    for w in (w0, w1):
+        w = w.reshape(C, -1)
+        ws.append((w if w.dtype == torch.float32 else w.float()).contiguous())
+    bs = [None if b is None else b.float().contiguous() for b in (b0, b1)]
+    x_acc = acc_sink_of(x)
+    if x_acc is not None and x.stride(1) != C:
+        x_acc = None
+    return _DwConvPair.apply(x, ws[0], bs[0], add0, ws[1], bs[1], add1, out_dtype,
+                             (sink_of(add0), sink_of(add1)), x_acc)

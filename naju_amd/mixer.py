@@ -32,7 +32,7 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from naju_amd import gradsink
-from naju_amd.dwconv import dwconv
+from naju_amd.dwconv import dwconv, dwconv_pair, pair_supported
 from naju_amd.linear import compute_dtype, linear
 from naju_amd.optim import AdamW as NajuAdamW
 from naju_amd.readout import readout
@@ -184,7 +184,15 @@ class NajuMixer(nn.Module):
         # convolutions and the GEMM add into it in place
         fold = (h.is_cuda and not self.gate_rank and torch.is_grad_enabled() and h.requires_grad
                 and _hip_scan(self.scan_backend) is not None)
-        if fold:
+        # the two gate convolutions as one pass over h each way (their logits
+        # take the projection slices in place; not with gate_reparam, whose
+        # rescaled projection is a new tensor)
+        pair = (h.is_cuda and not self.gate_rank and not self.gate_reparam and self.d_inner % 8 == 0
+                and self.f_conv.weight.shape[-1] == 4 and self.i_conv.weight.shape[-1] == 4)
+        if fold and pair:
+            h_g, h_f, h_s, h_r = gradsink.fanout(h, 4)
+            h_i = h_f
+        elif fold:
             h_g, h_f, h_i, h_s, h_r = gradsink.fanout(h, 5)
         else:
             h_g = h_f = h_i = h_s = h_r = h
@@ -196,8 +204,13 @@ class NajuMixer(nn.Module):
             di, N = self.d_inner, self.d_state
             w = torch.cat([self.f_proj.weight, self.i_proj.weight, self.x_proj.weight], 0)
             p_f, p_i, Bm, Cm = gradsink.split(_linear(h_g, w), [di, di, N, N])
-            f_logit = self._gate_logit(h_f, None, self.f_conv, self.f_bias, p=p_f)
-            i_logit = self._gate_logit(h_i, None, self.i_conv, self.i_bias, p=p_i)
+            if pair and pair_supported(h_f, self.f_conv.weight, p_f, self.i_conv.weight, p_i):
+                f_logit, i_logit = dwconv_pair(
+                    h_f, self.f_conv.weight, self.f_bias, p_f, self.i_conv.weight, self.i_bias, p_i,
+                    out_dtype=torch.promote_types(_out_dtype(h), self.f_bias.dtype))
+            else:
+                f_logit = self._gate_logit(h_f, None, self.f_conv, self.f_bias, p=p_f)
+                i_logit = self._gate_logit(h_i, None, self.i_conv, self.i_bias, p=p_i)
         else:
             Bm, Cm = self.x_proj(h).split(self.d_state, dim=-1)
             f_logit = self._gate_logit(h, self.f_proj, self.f_conv, self.f_bias)

@@ -245,3 +245,57 @@ def test_bwd_accumulates_dx_in_place(gpu, C, dtype):
         assert torch.equal(dw1, dw2) and torch.equal(db1, db2)
     with pytest.raises(_lib.NajuScanError, match="act must be"):
         bwd(acc, 4, None, None)
+
+
+@pytest.mark.parametrize("dtype,T", [(torch.bfloat16, 2048), (torch.bfloat16, 77), (torch.float32, 100)])
+def test_gate_pair_matches_two_single_convolutions(gpu, dtype, T):
+    """naju_dwconv_pair_fwd / _bwd (the mixer's two gate convolutions over one
+    input, adds taken in place from one projection output) against two
+    dwconv calls: the logits, dw, dbias and the adds' gradients bitwise; x's
+    gradient (both convolutions' transposes summed, one rounding, added to
+    what the fan-out buffer holds) against float64."""
+    from naju_amd import gradsink
+    from naju_amd.dwconv import dwconv, dwconv_pair, pair_supported
+    B, C, K = 2, 1536 if T == 2048 else 264, 4
+    g = torch.Generator(device=gpu).manual_seed(T)
+    x0 = torch.randn(B, T, C, generator=g, device=gpu).to(dtype)
+    P0 = torch.randn(B, T, 2 * C + 16, generator=g, device=gpu).to(dtype)
+    ws = [torch.randn(C, 1, K, generator=g, device=gpu) / K for _ in range(2)]
+    bs = [torch.randn(C, generator=g, device=gpu) for _ in range(2)]
+    dys = [torch.randn(B, T, C, generator=g, device=gpu) for _ in range(2)]
+    g_prev = torch.randn(B, T, C, generator=g, device=gpu).to(dtype)
+
+    def run(paired):
+        x = x0.clone().requires_grad_(True)
+        P = P0.clone().requires_grad_(True)
+        w = [t.clone().requires_grad_(True) for t in ws]
+        b = [t.clone().requires_grad_(True) for t in bs]
+        # x feeds the pair and one more consumer (as h in the mixer): its
+        # gradient collects in a fan-out buffer that another gradient fills first
+        xa, xo = gradsink.fanout(x, 2)
+        p0, p1, _ = gradsink.split(P, [C, C, 16])
+        if paired:
+            assert pair_supported(xa, w[0], p0, w[1], p1)
+            y0, y1 = dwconv_pair(xa, w[0], b[0], p0, w[1], b[1], p1, out_dtype=torch.float32)
+        else:
+            y0 = dwconv(xa, w[0], b[0], add=p0, out_dtype=torch.float32)
+            y1 = dwconv(xa, w[1], b[1], add=p1, out_dtype=torch.float32)
+        loss = (y0 * dys[0]).sum() + (y1 * dys[1]).sum() + (xo.float() * g_prev.float()).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        return y0.detach(), y1.detach(), x.grad, P.grad, [t.grad for t in w], [t.grad for t in b]
+
+    y0p, y1p, dxp, dPp, dwp, dbp = run(True)
+    y0s, y1s, dxs, dPs, dws, dbs = run(False)
+    assert torch.equal(y0p, y0s) and torch.equal(y1p, y1s)
+    assert torch.equal(dPp, dPs)
+    for a, c in zip(dwp + dbp, dws + dbs):
+        assert torch.equal(a, c)
+    # x's gradient against float64: g_prev + conv0^T(dy0) + conv1^T(dy1)
+    want = g_prev.double()
+    for w, dy in zip(ws, dys):
+        xr = x0.double().requires_grad_(True)
+        yr = F.conv1d(xr.transpose(1, 2), w.double(), padding=K - 1, groups=C)[..., :T].transpose(1, 2)
+        want = want + torch.autograd.grad(yr, xr, dy.double())[0]
+    tol = 2.0 ** -7 if dtype == torch.bfloat16 else 1e-5
+    assert _rel(dxp, want) < tol
