@@ -56,6 +56,23 @@ int naju_xent_bwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_
                   int64_t ignore_index, const float* lse, const float* scale, const float* dloss, void* dx,
                   int64_t dx_ld, int dx_dtype, void* stream);
 
+/* Forward and gradient in one pass over the logits, for a caller that will
+ * take the gradient (autograd's loss.backward()): naju_xent_fwd's outputs,
+ * and dx written as naju_xent_bwd writes it for dloss = 1. Each row is read
+ * twice by its workgroup (the second time mostly from the caches) instead of
+ * a second full pass in the backward. No reference counterpart (the
+ * reference's loss is torch's, forward then backward). */
+int naju_xent_fwd_grad(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols,
+                       int x_dtype, int64_t ignore_index, float* lse, float* loss, float* scale, void* dx,
+                       int64_t dx_ld, int dx_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The backward after naju_xent_fwd_grad: when dloss[0] is 1 the dx that call
+ * wrote is the gradient and nothing is done (each workgroup reads dloss and
+ * returns); otherwise dx is rewritten as naju_xent_bwd writes it. */
+int naju_xent_bwd_if_scaled(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols,
+                            int x_dtype, int64_t ignore_index, const float* lse, const float* scale,
+                            const float* dloss, void* dx, int64_t dx_ld, int dx_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

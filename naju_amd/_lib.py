@@ -57,6 +57,8 @@ EXPORTED = (
     "naju_xent_workspace_bytes",
     "naju_xent_fwd",
     "naju_xent_bwd",
+    "naju_xent_fwd_grad",
+    "naju_xent_bwd_if_scaled",
     "naju_optim_last_error",
     "naju_grad_norm_workspace_bytes",
     "naju_grad_norm",
@@ -168,6 +170,11 @@ def lib():
     # x, x_ld, target, n_rows, n_cols, x_dt, ignore_index, lse, scale, dloss, dx, dx_ld, dx_dt, stream
     L.naju_xent_bwd.argtypes = [P, I64, P, I64, I64, I, I64, P, P, P, P, I64, I, P]
     L.naju_xent_bwd.restype = I
+    # x, x_ld, target, n_rows, n_cols, x_dt, ignore_index, lse, loss, scale, dx, dx_ld, dx_dt, ws, ws_bytes, stream
+    L.naju_xent_fwd_grad.argtypes = [P, I64, P, I64, I64, I, I64, P, P, P, P, I64, I, P, SZ, P]
+    L.naju_xent_fwd_grad.restype = I
+    L.naju_xent_bwd_if_scaled.argtypes = [P, I64, P, I64, I64, I, I64, P, P, P, P, I64, I, P]
+    L.naju_xent_bwd_if_scaled.restype = I
     L.naju_optim_last_error.argtypes = []
     L.naju_optim_last_error.restype = ctypes.c_char_p
     L.naju_grad_norm_workspace_bytes.argtypes = [I64]

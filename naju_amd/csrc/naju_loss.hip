@@ -77,13 +77,13 @@ __device__ __forceinline__ int64_t head_elems(const T* p, int64_t n) {
   return h < n ? h : n;
 }
 
-// grid: n_rows workgroups of kThreads.
+// Forward of row blockIdx.x by the workgroup: lse, the row's loss and
+// validity; the lse also into *s_l (LDS, visible after a barrier).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void xent_fwd_kernel(const T* __restrict__ x, int64_t ld,
-                                                            const int64_t* __restrict__ target, int64_t n_cols,
-                                                            int64_t ignore, float* __restrict__ lse,
-                                                            float* __restrict__ row_loss,
-                                                            float* __restrict__ row_valid) {
+__device__ __forceinline__ void xent_row_fwd(const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ target,
+                                             int64_t n_cols, int64_t ignore, float* __restrict__ lse,
+                                             float* __restrict__ row_loss, float* __restrict__ row_valid,
+                                             float* s_l) {
   constexpr int E = 16 / sizeof(T);
   typedef T vec_t __attribute__((ext_vector_type(E)));
   const int64_t r = blockIdx.x;
@@ -138,6 +138,7 @@ __global__ __launch_bounds__(kThreads) void xent_fwd_kernel(const T* __restrict_
     for (int w = 1; w < kWaves; ++w) ms_merge(M, S, sm[w], ss[w]);
     const float l = M + logf(S);
     lse[r] = l;
+    *s_l = l;
     const int64_t t = target[r];
     float loss = 0.f, valid = 0.f;
     if (t != ignore) {
@@ -147,6 +148,17 @@ __global__ __launch_bounds__(kThreads) void xent_fwd_kernel(const T* __restrict_
     row_loss[r] = loss;
     row_valid[r] = valid;
   }
+}
+
+// grid: n_rows workgroups of kThreads.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void xent_fwd_kernel(const T* __restrict__ x, int64_t ld,
+                                                            const int64_t* __restrict__ target, int64_t n_cols,
+                                                            int64_t ignore, float* __restrict__ lse,
+                                                            float* __restrict__ row_loss,
+                                                            float* __restrict__ row_valid) {
+  __shared__ float s_l;
+  xent_row_fwd<T>(x, ld, target, n_cols, ignore, lse, row_loss, row_valid, &s_l);
 }
 
 // One workgroup: loss = sum(row_loss) / sum(row_valid), scale = 1 / count,
@@ -177,26 +189,15 @@ __global__ __launch_bounds__(1024) void xent_mean_kernel(const float* __restrict
   }
 }
 
-// grid: n_rows workgroups of kThreads.
-// dx[c] = g * (exp(x[c] - lse) - [c == t]), g = dloss * scale (0 if ignored).
+// Row r of the gradient: dx[c] = g * (exp(x[c] - lse) - [c == t]), 0 for an
+// ignored row (t == ignore); g is NaN for a target outside [0, n_cols).
 template <typename T, typename TD>
-__global__ __launch_bounds__(kThreads) void xent_bwd_kernel(const T* __restrict__ x, int64_t ld,
-                                                            const int64_t* __restrict__ target, int64_t n_cols,
-                                                            int64_t ignore, const float* __restrict__ lse,
-                                                            const float* __restrict__ scale,
-                                                            const float* __restrict__ dloss, TD* __restrict__ dx,
-                                                            int64_t dld) {
-  const int64_t r = blockIdx.x;
-  const int tid = threadIdx.x;
-  const T* p = x + r * ld;
-  TD* d = dx + r * dld;
-  const int64_t t = target[r];
+__device__ __forceinline__ void grad_row(const T* __restrict__ p, TD* __restrict__ d, int64_t t, int64_t n_cols,
+                                         int64_t ignore, float g, float l, int tid) {
   if (t == ignore) {
     for (int64_t c = tid; c < n_cols; c += kThreads) d[c] = fromf<TD>(0.f);
     return;
   }
-  const float g = (t >= 0 && t < n_cols) ? dloss[0] * scale[0] : __builtin_nanf("");
-  const float l = lse[r];
   auto grad = [&](float v, int64_t c) {
     const float e = exp2_((v - l) * kLog2e) * g;
     return c == t ? e - g : e;
@@ -241,6 +242,60 @@ __global__ __launch_bounds__(kThreads) void xent_bwd_kernel(const T* __restrict_
   }
 }
 
+// grid: n_rows workgroups of kThreads. g = dloss * scale. With if_scaled
+// (the forward already wrote dx for dloss = 1) a workgroup returns at once
+// when dloss is 1.
+template <typename T, typename TD>
+__global__ __launch_bounds__(kThreads) void xent_bwd_kernel(const T* __restrict__ x, int64_t ld,
+                                                            const int64_t* __restrict__ target, int64_t n_cols,
+                                                            int64_t ignore, const float* __restrict__ lse,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ dloss, TD* __restrict__ dx,
+                                                            int64_t dld, int if_scaled) {
+  if (if_scaled && dloss[0] == 1.f) return;
+  const int64_t r = blockIdx.x;
+  const int64_t t = target[r];
+  const float g = (t >= 0 && t < n_cols) ? dloss[0] * scale[0] : __builtin_nanf("");
+  grad_row<T, TD>(x + r * ld, dx + r * dld, t, n_cols, ignore, g, t == ignore ? 0.f : lse[r], threadIdx.x);
+}
+
+// One workgroup: scale = 1 / (number of rows with target != ignore), the
+// count summed in float64 in a fixed order (the value xent_mean_kernel gives).
+__global__ __launch_bounds__(1024) void xent_count_kernel(const int64_t* __restrict__ target, int64_t n,
+                                                          int64_t ignore, float* __restrict__ scale) {
+  __shared__ double sc[1024];
+  const int t = threadIdx.x;
+  double c = 0.0;
+  for (int64_t i = t; i < n; i += 1024) c += target[i] != ignore ? 1.0 : 0.0;
+  sc[t] = c;
+  __syncthreads();
+  for (int w = 512; w >= 1; w >>= 1) {
+    if (t < w) sc[t] += sc[t + w];
+    __syncthreads();
+  }
+  if (t == 0) scale[0] = sc[0] > 0.0 ? (float)(1.0 / sc[0]) : 0.f;
+}
+
+// grid: n_rows workgroups of kThreads: the forward of row r (as
+// xent_fwd_kernel), then its gradient for dloss = 1 (as xent_bwd_kernel),
+// the row read a second time (from the caches when it is still there).
+template <typename T, typename TD>
+__global__ __launch_bounds__(kThreads) void xent_fwd_grad_kernel(const T* __restrict__ x, int64_t ld,
+                                                                 const int64_t* __restrict__ target, int64_t n_cols,
+                                                                 int64_t ignore, float* __restrict__ lse,
+                                                                 float* __restrict__ row_loss,
+                                                                 float* __restrict__ row_valid,
+                                                                 const float* __restrict__ scale,
+                                                                 TD* __restrict__ dx, int64_t dld) {
+  __shared__ float s_l;
+  xent_row_fwd<T>(x, ld, target, n_cols, ignore, lse, row_loss, row_valid, &s_l);
+  __syncthreads();
+  const int64_t r = blockIdx.x;
+  const int64_t t = target[r];
+  const float g = (t >= 0 && t < n_cols) ? 1.f * scale[0] : __builtin_nanf("");
+  grad_row<T, TD>(x + r * ld, dx + r * dld, t, n_cols, ignore, g, s_l, threadIdx.x);
+}
+
 // ------------------------------------------------------------------ host side
 
 thread_local char g_err[256] = "";
@@ -281,21 +336,41 @@ void launch_fwd(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int
 
 template <typename T, typename TD>
 void launch_bwd(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
-                const float* lse, const float* scale, const float* dloss, void* dx, int64_t dld, hipStream_t st) {
+                const float* lse, const float* scale, const float* dloss, void* dx, int64_t dld, int if_scaled,
+                hipStream_t st) {
   xent_bwd_kernel<T, TD><<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse,
-                                                                          scale, dloss, (TD*)dx, dld);
+                                                                          scale, dloss, (TD*)dx, dld, if_scaled);
 }
 
 template <typename T>
 void launch_bwd_dt(int dx_dt, const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols,
                    int64_t ignore, const float* lse, const float* scale, const float* dloss, void* dx, int64_t dld,
-                   hipStream_t st) {
+                   int if_scaled, hipStream_t st) {
   if (dx_dt == NAJU_DTYPE_F32)
-    launch_bwd<T, float>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, st);
+    launch_bwd<T, float>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, if_scaled, st);
   else if (dx_dt == NAJU_DTYPE_BF16)
-    launch_bwd<T, bf16_t>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, st);
+    launch_bwd<T, bf16_t>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, if_scaled, st);
   else
-    launch_bwd<T, f16_t>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, st);
+    launch_bwd<T, f16_t>(x, ld, tgt, rows, cols, ignore, lse, scale, dloss, dx, dld, if_scaled, st);
+}
+
+template <typename T, typename TD>
+void launch_fwd_grad(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
+                     float* lse, float* rl, float* rv, const float* scale, void* dx, int64_t dld, hipStream_t st) {
+  xent_fwd_grad_kernel<T, TD><<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>((const T*)x, ld, tgt, cols, ignore,
+                                                                               lse, rl, rv, scale, (TD*)dx, dld);
+}
+
+template <typename T>
+void launch_fwd_grad_dt(int dx_dt, const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols,
+                        int64_t ignore, float* lse, float* rl, float* rv, const float* scale, void* dx, int64_t dld,
+                        hipStream_t st) {
+  if (dx_dt == NAJU_DTYPE_F32)
+    launch_fwd_grad<T, float>(x, ld, tgt, rows, cols, ignore, lse, rl, rv, scale, dx, dld, st);
+  else if (dx_dt == NAJU_DTYPE_BF16)
+    launch_fwd_grad<T, bf16_t>(x, ld, tgt, rows, cols, ignore, lse, rl, rv, scale, dx, dld, st);
+  else
+    launch_fwd_grad<T, f16_t>(x, ld, tgt, rows, cols, ignore, lse, rl, rv, scale, dx, dld, st);
 }
 
 }  // namespace
@@ -333,9 +408,10 @@ int naju_xent_fwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_
   return launched();
 }
 
-int naju_xent_bwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols, int x_dtype,
+namespace {
+int xent_bwd_impl(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols, int x_dtype,
                   int64_t ignore_index, const float* lse, const float* scale, const float* dloss, void* dx,
-                  int64_t dx_ld, int dx_dtype, void* stream) {
+                  int64_t dx_ld, int dx_dtype, int if_scaled, void* stream) {
   g_err[0] = 0;
   int rc = check_shape(x_ld, n_rows, n_cols, x_dtype);
   if (rc) return rc;
@@ -347,13 +423,67 @@ int naju_xent_bwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_
     return fail(NAJU_ERR_INVALID, "null pointer (x, target, lse, scale, dloss and dx are required)");
   hipStream_t st = (hipStream_t)stream;
   if (x_dtype == NAJU_DTYPE_F32)
-    launch_bwd_dt<float>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld, st);
+    launch_bwd_dt<float>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld,
+                         if_scaled, st);
   else if (x_dtype == NAJU_DTYPE_BF16)
     launch_bwd_dt<bf16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld,
-                          st);
+                          if_scaled, st);
   else
-    launch_bwd_dt<f16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld, st);
+    launch_bwd_dt<f16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, scale, dloss, dx, dx_ld,
+                         if_scaled, st);
   return launched();
+}
+}  // namespace
+
+int naju_xent_bwd(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols, int x_dtype,
+                  int64_t ignore_index, const float* lse, const float* scale, const float* dloss, void* dx,
+                  int64_t dx_ld, int dx_dtype, void* stream) {
+  return xent_bwd_impl(x, x_ld, target, n_rows, n_cols, x_dtype, ignore_index, lse, scale, dloss, dx, dx_ld, dx_dtype,
+                       0, stream);
+}
+
+int naju_xent_fwd_grad(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols,
+                       int x_dtype, int64_t ignore_index, float* lse, float* loss, float* scale, void* dx,
+                       int64_t dx_ld, int dx_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_shape(x_ld, n_rows, n_cols, x_dtype);
+  if (rc) return rc;
+  if (dx_ld < n_cols) return fail(NAJU_ERR_INVALID, "dx_ld (%lld) must be >= n_cols (%lld)", (long long)dx_ld,
+                                  (long long)n_cols);
+  if (!dt_ok(dx_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
+  if (!loss || !scale) return fail(NAJU_ERR_INVALID, "null pointer (loss and scale are required)");
+  if (n_rows > 0 && (!x || !target || !lse || !dx))
+    return fail(NAJU_ERR_INVALID, "null pointer (x, target, lse and dx)");
+  if (n_rows > 0 && n_cols == 0) return fail(NAJU_ERR_INVALID, "n_cols must be positive when there are rows");
+  if (!workspace || workspace_bytes < ws_bytes(n_rows))
+    return fail(NAJU_ERR_WORKSPACE, "workspace of %zu bytes needed", ws_bytes(n_rows));
+  hipStream_t st = (hipStream_t)stream;
+  float* rl = (float*)workspace;
+  float* rv = rl + n_rows;
+  // the gradient's scale first (the count of valid rows), then the rows
+  xent_count_kernel<<<1, 1024, 0, st>>>(target, n_rows, ignore_index, scale);
+  if ((rc = launched())) return rc;
+  if (n_rows > 0) {
+    if (x_dtype == NAJU_DTYPE_F32)
+      launch_fwd_grad_dt<float>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, rl, rv, scale, dx,
+                                dx_ld, st);
+    else if (x_dtype == NAJU_DTYPE_BF16)
+      launch_fwd_grad_dt<bf16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, rl, rv, scale, dx,
+                                 dx_ld, st);
+    else
+      launch_fwd_grad_dt<f16_t>(dx_dtype, x, x_ld, target, n_rows, n_cols, ignore_index, lse, rl, rv, scale, dx,
+                                dx_ld, st);
+    if ((rc = launched())) return rc;
+  }
+  xent_mean_kernel<<<1, 1024, 0, st>>>(rl, rv, n_rows, loss, scale);
+  return launched();
+}
+
+int naju_xent_bwd_if_scaled(const void* x, int64_t x_ld, const int64_t* target, int64_t n_rows, int64_t n_cols,
+                            int x_dtype, int64_t ignore_index, const float* lse, const float* scale,
+                            const float* dloss, void* dx, int64_t dx_ld, int dx_dtype, void* stream) {
+  return xent_bwd_impl(x, x_ld, target, n_rows, n_cols, x_dtype, ignore_index, lse, scale, dloss, dx, dx_ld, dx_dtype,
+                       1, stream);
 }
 
 }  // extern "C"

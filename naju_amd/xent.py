@@ -56,9 +56,20 @@ class _CrossEntropy(torch.autograd.Function):
         stream = torch.cuda.current_stream(dev).cuda_stream
         nbytes = L.naju_xent_workspace_bytes(rows)
         ws = _WS.get(dev, stream, nbytes)
-        _lib.check_loss(L.naju_xent_fwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype],
-                                        ignore_index, lse.data_ptr(), loss.data_ptr(), scale.data_ptr(),
-                                        ws.data_ptr(), ws.numel(), stream))
+        ctx.dx = None
+        if ctx.needs_input_grad[0]:
+            # the gradient (for dloss = 1) in the same pass over the logits;
+            # the backward keeps it when dloss is 1
+            dx = torch.empty((rows, cols), dtype=x.dtype, device=dev)
+            _lib.check_loss(L.naju_xent_fwd_grad(
+                x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype], ignore_index, lse.data_ptr(),
+                loss.data_ptr(), scale.data_ptr(), dx.data_ptr(), dx.stride(0), _DT[x.dtype], ws.data_ptr(),
+                ws.numel(), stream))
+            ctx.dx = dx
+        else:
+            _lib.check_loss(L.naju_xent_fwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype],
+                                            ignore_index, lse.data_ptr(), loss.data_ptr(), scale.data_ptr(),
+                                            ws.data_ptr(), ws.numel(), stream))
         ctx.save_for_backward(x, target, lse, scale)
         ctx.ignore_index = ignore_index
         return loss
@@ -68,12 +79,19 @@ class _CrossEntropy(torch.autograd.Function):
         x, target, lse, scale = ctx.saved_tensors
         rows, cols = x.shape
         dloss = dloss.detach().float().contiguous()
-        dx = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
         L = _lib.lib()
         stream = torch.cuda.current_stream(x.device).cuda_stream
-        _lib.check_loss(L.naju_xent_bwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype],
-                                        ctx.ignore_index, lse.data_ptr(), scale.data_ptr(), dloss.data_ptr(),
-                                        dx.data_ptr(), dx.stride(0), _DT[x.dtype], stream))
+        if ctx.dx is not None:
+            # the forward's gradient, rewritten only when dloss is not 1
+            # (taken once: a second backward of a retained graph recomputes)
+            dx, ctx.dx = ctx.dx, None
+            bwd = L.naju_xent_bwd_if_scaled
+        else:
+            dx = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+            bwd = L.naju_xent_bwd
+        _lib.check_loss(bwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype], ctx.ignore_index,
+                            lse.data_ptr(), scale.data_ptr(), dloss.data_ptr(), dx.data_ptr(), dx.stride(0),
+                            _DT[x.dtype], stream))
         return dx, None, None
 
 

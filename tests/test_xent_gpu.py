@@ -130,3 +130,40 @@ def test_xent_deterministic_and_matches_lm_shape(gpu):
     lt = lt.detach()
     assert abs(float(outs[0][0]) - float(lt)) <= 2e-6 * float(lt)
     assert _rel(outs[0][1], xt.grad) < 2e-3
+
+
+@pytest.mark.parametrize("dloss", [1.0, 0.5])
+def test_xent_gradient_from_forward_matches_two_passes(gpu, dloss):
+    """With logits that require grad the forward also writes the gradient
+    (naju_xent_fwd_grad) and the backward keeps it when dloss is 1
+    (naju_xent_bwd_if_scaled), else rewrites it: bitwise what
+    naju_xent_fwd + naju_xent_bwd give, with ignored rows; a retained graph's
+    second backward recomputes."""
+    from naju_amd import _lib
+    L = _lib.lib()
+    rows, cols = 96, 50257
+    g = torch.Generator(device=gpu).manual_seed(11)
+    x = (torch.randn(rows, cols, generator=g, device=gpu) * 3).to(torch.bfloat16)
+    t = torch.randint(0, cols, (rows,), generator=g, device=gpu)
+    t[::7] = -100
+    xg = x.clone().requires_grad_(True)
+    loss = cross_entropy(xg, t)
+    (loss * dloss).backward(retain_graph=True)
+    g1 = xg.grad.clone()
+    (loss * dloss).backward()
+    # the two-pass calls
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    lse = torch.empty(rows, device=gpu)
+    loss2, scale = torch.empty((), device=gpu), torch.empty((), device=gpu)
+    ws = torch.empty(L.naju_xent_workspace_bytes(rows), dtype=torch.uint8, device=gpu)
+    _lib.check_loss(L.naju_xent_fwd(x.data_ptr(), cols, t.data_ptr(), rows, cols, _lib.DT_BF16, -100, lse.data_ptr(),
+                                    loss2.data_ptr(), scale.data_ptr(), ws.data_ptr(), ws.numel(), st))
+    dl = torch.full((), dloss, device=gpu)
+    dx = torch.empty_like(x)
+    _lib.check_loss(L.naju_xent_bwd(x.data_ptr(), cols, t.data_ptr(), rows, cols, _lib.DT_BF16, -100, lse.data_ptr(),
+                                    scale.data_ptr(), dl.data_ptr(), dx.data_ptr(), cols, _lib.DT_BF16, st))
+    torch.cuda.synchronize()
+    assert torch.equal(loss.detach(), loss2)
+    assert torch.equal(g1, dx)
+    assert torch.equal(xg.grad, dx + dx)
+    assert torch.count_nonzero(dx[::7]) == 0
