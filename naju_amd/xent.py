@@ -46,7 +46,7 @@ _WS = _Workspace()
 
 class _CrossEntropy(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, target, ignore_index):
+    def forward(ctx, x, target, ignore_index, want_grad):
         rows, cols = x.shape
         dev = x.device
         lse = torch.empty(rows, dtype=torch.float32, device=dev)
@@ -57,7 +57,7 @@ class _CrossEntropy(torch.autograd.Function):
         nbytes = L.naju_xent_workspace_bytes(rows)
         ws = _WS.get(dev, stream, nbytes)
         ctx.dx = None
-        if ctx.needs_input_grad[0]:
+        if want_grad:
             # the gradient (for dloss = 1) in the same pass over the logits;
             # the backward keeps it when dloss is 1
             dx = torch.empty((rows, cols), dtype=x.dtype, device=dev)
@@ -92,7 +92,7 @@ class _CrossEntropy(torch.autograd.Function):
         _lib.check_loss(bwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype], ctx.ignore_index,
                             lse.data_ptr(), scale.data_ptr(), dloss.data_ptr(), dx.data_ptr(), dx.stride(0),
                             _DT[x.dtype], stream))
-        return dx, None, None
+        return dx, None, None, None
 
 
 def cross_entropy(logits, target, ignore_index=-100):
@@ -107,4 +107,7 @@ def cross_entropy(logits, target, ignore_index=-100):
     if logits.stride(1) != 1 or logits.stride(0) < logits.shape[1]:
         logits = logits.contiguous()
     target = target.to(device=logits.device, dtype=torch.int64).contiguous()
-    return _CrossEntropy.apply(logits, target, int(ignore_index))
+    # a backward will follow (a graph is being recorded): the forward also
+    # writes the gradient
+    want_grad = torch.is_grad_enabled() and logits.requires_grad
+    return _CrossEntropy.apply(logits, target, int(ignore_index), want_grad)
