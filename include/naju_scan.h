@@ -166,6 +166,24 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit,
                   int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* naju_scan_fwd / naju_scan_bwd with B and C read from rows bc_ld elements
+ * apart (and dB, dC written to rows dbc_ld apart) instead of N: the mixer's
+ * B and C are column slices of one projection output [batch, T, width], so
+ * the scan reads them, and writes their gradients, in place. Served on the
+ * matrix-core path (9 <= N <= 64) with bc_ld, dbc_ld multiples of 4 and
+ * pointers aligned to four elements; elsewhere a stride other than N returns
+ * NAJU_ERR_UNSUPPORTED. Every output is bitwise the contiguous call's. No
+ * reference counterpart (the reference's backends take contiguous B, C). */
+int naju_scan_fwd_strided(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                          const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch,
+                          int64_t T, int64_t D, int64_t N, int64_t bc_ld, int x_dtype, int gate_dtype, int bc_dtype,
+                          int flags, void* workspace, size_t workspace_bytes, void* stream);
+int naju_scan_bwd_strided(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                          const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil,
+                          void* dB, void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N,
+                          int64_t bc_ld, int64_t dbc_ld, int x_dtype, int gate_dtype, int bc_dtype, int flags,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free forward: naju_scan_fwd with the caller's workspace
  * replaced by a static device array of NAJU_NOALLOC_SCRATCH_BYTES per GPU
  * (each GPU the library runs on holds it until the process ends; its

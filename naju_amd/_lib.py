@@ -33,6 +33,8 @@ EXPORTED = (
     "naju_scan_workspace_bytes_ex",
     "naju_scan_fwd",
     "naju_scan_bwd",
+    "naju_scan_fwd_strided",
+    "naju_scan_bwd_strided",
     "naju_scan_workspace_status",
     "naju_scan_fwd_noalloc",
     "naju_scan_noalloc_status",
@@ -107,6 +109,11 @@ def lib():
     # ws_bytes, stream
     L.naju_scan_bwd.argtypes = [P] * 15 + [I64] * 4 + [I] * 4 + [P, SZ, P]
     L.naju_scan_bwd.restype = I
+    # the same with the B / C row stride after N (and the dB / dC one after it)
+    L.naju_scan_fwd_strided.argtypes = [P] * 10 + [I64] * 5 + [I] * 4 + [P, SZ, P]
+    L.naju_scan_fwd_strided.restype = I
+    L.naju_scan_bwd_strided.argtypes = [P] * 15 + [I64] * 6 + [I] * 4 + [P, SZ, P]
+    L.naju_scan_bwd_strided.restype = I
     # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, flags, stream
     L.naju_scan_fwd_noalloc.argtypes = [P] * 10 + [I64] * 4 + [I] * 4 + [P]
     L.naju_scan_fwd_noalloc.restype = I

@@ -917,7 +917,11 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
                                                     const float* __restrict__ partC, int n_parts, int64_t btn,
                                                     void* dB, void* dC, int bc_dt, int n_bc_blocks,
                                                     const float* __restrict__ partD, int64_t n_rows, int64_t D,
-                                                    float* __restrict__ dD, int bc_split) {
+                                                    float* __restrict__ dD, int bc_split, int64_t N,
+                                                    int64_t ld_out) {
+  // entry i of the [batch * T][N] sums lands at row i / N, column i % N of
+  // dB / dC, whose rows are ld_out elements apart
+  auto out = [&](int64_t i) { return ld_out == N ? i : (i / N) * ld_out + (i - (i / N) * N); };
   __shared__ float s_acc[16][64];
   __shared__ float4 s_b4[16][64], s_c4[16][64];
   if ((int)blockIdx.x < n_bc_blocks) {
@@ -960,8 +964,8 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (dB) st_any(dB, bc_dt, 4 * i4 + e, (&tb.x)[e]);
-          if (dC) st_any(dC, bc_dt, 4 * i4 + e, (&tc.x)[e]);
+          if (dB) st_any(dB, bc_dt, out(4 * i4 + e), (&tb.x)[e]);
+          if (dC) st_any(dC, bc_dt, out(4 * i4 + e), (&tc.x)[e]);
         }
       }
       return;
@@ -1002,15 +1006,15 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (dB) st_any(dB, bc_dt, 4 * i4 + e, sb[e]);
-          if (dC) st_any(dC, bc_dt, 4 * i4 + e, sc[e]);
+          if (dB) st_any(dB, bc_dt, out(4 * i4 + e), sb[e]);
+          if (dC) st_any(dC, bc_dt, out(4 * i4 + e), sc[e]);
         }
       }
       return;
     }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < btn; i += stride) {
-      if (dB) st_any(dB, bc_dt, i, sum_parts(partB, n_parts, btn, i));
-      if (dC) st_any(dC, bc_dt, i, sum_parts(partC, n_parts, btn, i));
+      if (dB) st_any(dB, bc_dt, out(i), sum_parts(partB, n_parts, btn, i));
+      if (dC) st_any(dC, bc_dt, out(i), sum_parts(partC, n_parts, btn, i));
     }
     return;
   }
@@ -2671,15 +2675,33 @@ size_t naju_scan_workspace_bytes(int64_t batch, int64_t T, int64_t D, int64_t N,
 
 namespace {
 
+// B / C (or dB / dC) with rows ld elements apart: ld = N always; another
+// ld only on the matrix-core path (9 <= N <= 64), a multiple of 4 with both
+// pointers aligned to four elements (the staging loads of the kernels).
+int check_bc_ld(const void* p, const void* q, int64_t N, int dt, int64_t ld, bool bwd) {
+  if (ld == N) return NAJU_OK;
+  if (ld < N) return fail(NAJU_ERR_INVALID, "B / C row stride (%lld) must be >= N (%lld)", (long long)ld, (long long)N);
+  if (N <= 1 || !use_mc(N, bwd))
+    return fail(NAJU_ERR_UNSUPPORTED, "a B / C row stride other than N is served at 9 <= N <= 64 only");
+  // the kernels address a sub-block's rows with 32-bit offsets
+  if (ld > (1 << 24)) return fail(NAJU_ERR_UNSUPPORTED, "B / C row stride (%lld) above 2^24", (long long)ld);
+  const size_t a4 = 4 * dsize(dt);
+  if (ld % 4 || (p && !aligned(p, a4)) || (q && !aligned(q, a4)))
+    return fail(NAJU_ERR_UNSUPPORTED, "strided B / C need a row stride that is a multiple of 4 and %zu-byte "
+                "aligned pointers", a4);
+  return NAJU_OK;
+}
+
 // The forward of naju_scan_fwd and naju_scan_fwd_noalloc. cap bounds the
 // layout (time segments at N > 1) to the bytes available.
 int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                   const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch, int64_t T,
                   int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
-                  size_t workspace_bytes, void* stream, size_t cap) {
+                  size_t workspace_bytes, void* stream, size_t cap, int64_t ldbc) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
+  if ((rc = check_bc_ld(B, C, N, bc_dtype, ldbc, false))) return rc;
   if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC | NAJU_CKPT_MASK))
     return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
   const int ck_rows = ckpt_rows(flags, N);
@@ -2724,6 +2746,7 @@ int scan_fwd_impl(const void* u, const void* f_logit, const void* i_logit, const
   a.incl = (uint64_t*)(ws + l.off_incl);
   a.T = T;
   a.D = D;
+  a.ldbc = ldbc;
   a.N = (int)N;
   a.batch = (int)batch;
   a.bc_dt = bc_dtype;
@@ -2854,7 +2877,15 @@ int naju_scan_fwd(const void* u, const void* f_logit, const void* i_logit, const
                   int64_t D, int64_t N, int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
                   size_t workspace_bytes, void* stream) {
   return scan_fwd_impl(u, f_logit, i_logit, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dtype, gate_dtype,
-                       bc_dtype, flags, workspace, workspace_bytes, stream, SIZE_MAX);
+                       bc_dtype, flags, workspace, workspace_bytes, stream, SIZE_MAX, N);
+}
+
+int naju_scan_fwd_strided(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                          const float* D_skip, const float* h0, void* y, float* ckpt, float* hT, int64_t batch,
+                          int64_t T, int64_t D, int64_t N, int64_t bc_ld, int x_dtype, int gate_dtype, int bc_dtype,
+                          int flags, void* workspace, size_t workspace_bytes, void* stream) {
+  return scan_fwd_impl(u, f_logit, i_logit, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dtype, gate_dtype,
+                       bc_dtype, flags, workspace, workspace_bytes, stream, SIZE_MAX, bc_ld);
 }
 
 int naju_scan_fwd_noalloc(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
@@ -2877,17 +2908,22 @@ int naju_scan_fwd_noalloc(const void* u, const void* f_logit, const void* i_logi
   void* ws = scratch_for_current_device(st);
   if (!ws) return NAJU_ERR_LAUNCH;
   return scan_fwd_impl(u, f_logit, i_logit, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dtype, gate_dtype,
-                       bc_dtype, flags, ws, kScratchBytes, stream, kScratchBytes);
+                       bc_dtype, flags, ws, kScratchBytes, stream, kScratchBytes, N);
 }
 
-int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
-                  const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil, void* dB,
-                  void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
-                  int gate_dtype, int bc_dtype, int flags, void* workspace, size_t workspace_bytes,
-                  void* stream) {
+static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                         const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil,
+                         void* dB, void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N,
+                         int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
+                         size_t workspace_bytes, void* stream, int64_t ldbc, int64_t lddbc) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
+  if ((rc = check_bc_ld(B, C, N, bc_dtype, ldbc, true))) return rc;
+  if ((rc = check_bc_ld(dB, dC, N, (flags & NAJU_FLAG_OUT_F32) ? (int)NAJU_DTYPE_F32 : bc_dtype, lddbc, true)))
+    return rc;
+  if (lddbc != N && batch * T > 0 && D == 0)
+    return fail(NAJU_ERR_UNSUPPORTED, "strided dB / dC need D > 0");
   if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC | NAJU_CKPT_MASK))
     return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
   const int ck_rows = ckpt_rows(flags, N);
@@ -2943,6 +2979,7 @@ int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const
   a.partD = dD ? (float*)(ws + l.off_partD) : nullptr;
   a.T = T;
   a.D = D;
+  a.ldbc = ldbc;
   a.N = (int)N;
   a.batch = (int)batch;
   a.bc_dt = bc_dtype;
@@ -3031,10 +3068,28 @@ fold:
     const int n_d = dD ? (int)((D + 63) / 64) : 0;
     hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
                        btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD,
-                       batch * (int64_t)(N == 1 ? l.K : l.nseg), D, dD, bc_split);
+                       batch * (int64_t)(N == 1 ? l.K : l.nseg), D, dD, bc_split, N, lddbc);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;
+}
+
+int naju_scan_bwd(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                  const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil, void* dB,
+                  void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N, int x_dtype,
+                  int gate_dtype, int bc_dtype, int flags, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  return scan_bwd_impl(u, f_logit, i_logit, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N,
+                       x_dtype, gate_dtype, bc_dtype, flags, workspace, workspace_bytes, stream, N, N);
+}
+
+int naju_scan_bwd_strided(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                          const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil,
+                          void* dB, void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N,
+                          int64_t bc_ld, int64_t dbc_ld, int x_dtype, int gate_dtype, int bc_dtype, int flags,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return scan_bwd_impl(u, f_logit, i_logit, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N,
+                       x_dtype, gate_dtype, bc_dtype, flags, workspace, workspace_bytes, stream, bc_ld, dbc_ld);
 }
 
 int naju_scan_workspace_status(const void* workspace, void* stream, uint32_t* status) {

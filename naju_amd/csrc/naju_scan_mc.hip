@@ -265,8 +265,8 @@ struct McIn {
     if (tid < 4 * NP) {
       const int N = a.N;
       const int row = (4 * tid) / NP, n0 = (4 * tid) % NP;
-      const int64_t bb = ((int64_t)b_row * T + t0) * N;  // (t0, 0), uniform
-      const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * N);
+      const int64_t bb = ((int64_t)b_row * T + t0) * a.ldbc;  // (t0, 0), uniform
+      const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * a.ldbc);
       if (N == NP) {
         ld4r<TB>((const TB*)a.Bm + bb, ro + n0, b);
         if constexpr (!MAP) ld4r<TB>((const TB*)a.Cm + bb, ro + n0, c);
@@ -775,8 +775,8 @@ struct McInB {
     if (tid < 4 * NP) {
       const int N = a.N;
       const int row = tid % kMcQ, n0 = 4 * (tid / kMcQ);
-      const int64_t bb = ((int64_t)b_row * T + t0) * N;
-      const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * N);
+      const int64_t bb = ((int64_t)b_row * T + t0) * a.ldbc;
+      const uint32_t ro = (uint32_t)((row < rows ? row : rows - 1) * a.ldbc);
       if (N == NP) {
         ld4r<TB>((const TB*)a.Cm + bb, ro + n0, c);
         if constexpr (!MAP) ld4r<TB>((const TB*)a.Bm + bb, ro + n0, b);

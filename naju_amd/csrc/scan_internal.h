@@ -95,6 +95,7 @@ struct ScanArgs {
   uint64_t* incl;  // [K][n_tiles][CH]
   int64_t T;
   int64_t D;
+  int64_t ldbc;  // elements between rows of B and C (N unless strided; the matrix-core path only)
   int N;
   int batch;
   int bc_dt;

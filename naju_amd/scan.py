@@ -43,7 +43,7 @@ import os
 import torch
 
 from naju_amd import _lib
-from naju_amd.gradsink import acc_sink_of
+from naju_amd.gradsink import acc_sink_of, sink_of
 
 _BACKEND_CACHE = {}
 
@@ -149,9 +149,11 @@ def _raise_pending(dev, stream):
                                  + _STATUS_MSG.get(st, f"status {st}"))
 
 
-def _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0):
+def _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0, bc_strided=False):
     """Contiguous tensors in a dtype combination the kernels serve:
-    u in {f32,bf16,f16}; gates and B/C each f32 or u's dtype; D_skip, h0 f32."""
+    u in {f32,bf16,f16}; gates and B/C each f32 or u's dtype; D_skip, h0 f32.
+    bc_strided: B and C stay as they are when their dtype is served (the
+    strided scan calls read their rows in place)."""
     if u.dtype not in _DT:
         u = u.float()
     xd = u.dtype
@@ -164,8 +166,9 @@ def _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0):
     D_skip = D_skip.float()
     if h0 is not None:
         h0 = h0.float().contiguous()
-    return (u.contiguous(), f_logit.contiguous(), i_logit.contiguous(),
-            B.contiguous(), C.contiguous(), D_skip.contiguous(), h0)
+    if not bc_strided:
+        B, C = B.contiguous(), C.contiguous()
+    return (u.contiguous(), f_logit.contiguous(), i_logit.contiguous(), B, C, D_skip.contiguous(), h0)
 
 
 def _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0):
@@ -187,6 +190,21 @@ def _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0):
     return Bsz, T, D, N
 
 
+def _bc_pair(B, C, N):
+    """B and C as the scan reads them, and their row stride: on the
+    matrix-core path (9 <= N <= 64), when C's columns directly follow B's in
+    one tensor (the mixer's x_proj slices of its projection output), one
+    copy of the 2N columns serves both (B, C: its two halves, rows 2N
+    apart); else (B, C, N), for _norm_inputs to make contiguous."""
+    if not (8 < N <= 64 and B.dtype == C.dtype and B.stride() == C.stride() and B.stride(2) == 1):
+        return B, C, N
+    es = B.element_size()
+    if C.data_ptr() != B.data_ptr() + N * es or B.stride(1) < 2 * N or B.stride(0) != B.shape[1] * B.stride(1):
+        return B, C, N
+    bc = torch.as_strided(B, (B.shape[0], B.shape[1], 2 * N), B.stride()).contiguous()
+    return bc[..., :N], bc[..., N:], 2 * N
+
+
 class NajuScanHip(torch.autograd.Function):
     """Autograd wrapper of naju_scan_fwd / naju_scan_bwd (include/naju_scan.h)."""
 
@@ -194,7 +212,12 @@ class NajuScanHip(torch.autograd.Function):
     def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False, ckpt_rows=0, du_skip=None):
         Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
         out_dtype = u.dtype
-        u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, B, C, D_skip, h0)
+        b_sinks = (sink_of(B), sink_of(C))
+        Bp, Cp, bc_ld = _bc_pair(B, C, N)
+        u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, Bp, Cp, D_skip, h0, bc_ld != N)
+        if bc_ld != N and (B_.data_ptr() != Bp.data_ptr() or C_.data_ptr() != Cp.data_ptr()):
+            # _norm_inputs converted their dtype: contiguous copies after all
+            B_, C_, bc_ld = B_.contiguous(), C_.contiguous(), N
         dts = (_DT[u_.dtype], _DT[fl_.dtype], _DT[B_.dtype])
         L = _lib.lib()
         dev = u_.device
@@ -214,9 +237,14 @@ class NajuScanHip(torch.autograd.Function):
         ws = _WS.get(dev, stream, nbytes)
         y = torch.empty((Bsz, T, D), dtype=u_.dtype, device=dev)
         hT = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_hT else None
-        _lib.check(L.naju_scan_fwd(
-            _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
-            _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
+        if bc_ld != N:
+            _lib.check(L.naju_scan_fwd_strided(
+                _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
+                _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, bc_ld, *dts, flags, ws.data_ptr(), ws.numel(), stream))
+        else:
+            _lib.check(L.naju_scan_fwd(
+                _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_), _ptr(h0_),
+                _ptr(y), _ptr(ckpt), _ptr(hT), Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
         if N == 1:
             _watch_status(dev, stream, ws)
         _check_status(dev)
@@ -230,6 +258,12 @@ class NajuScanHip(torch.autograd.Function):
             # u is a gradsink.fanout() alias: du goes into the fan-out's
             # buffer when it is the first gradient there
             ctx.u_acc = acc_sink_of(u) if u_ is u else None
+            ctx.bc_ld = bc_ld
+            # B and C are pieces of one gradsink.split (the mixer's
+            # projection output): dB and dC can go straight into its buffer
+            s0, s1 = b_sinks
+            ctx.bc_sinks = b_sinks if (bc_ld != N and s0 is not None and s1 is not None and s0[0] is s1[0]
+                                       and s0[0].dtype == B_.dtype) else None
         y = y if y.dtype == out_dtype else y.to(out_dtype)
         if want_hT:
             ctx.mark_non_differentiable(hT)
@@ -252,8 +286,25 @@ class NajuScanHip(torch.autograd.Function):
                 du = torch.empty_like(u_)
         dfl = torch.empty_like(fl_) if ng[1] else None
         dil = torch.empty_like(il_) if ng[2] else None
-        dB = torch.empty_like(B_) if ng[3] else None
-        dC = torch.empty_like(C_) if ng[4] else None
+        dB = dC = None
+        dbc_ld = N
+        if ctx.bc_ld != N and (ng[3] or ng[4]):
+            if ctx.bc_sinks is not None and not (flags & _lib.FLAG_OUT_F32):
+                # written in place into the split's gradient buffer, which its
+                # backward then takes as it is
+                (sb, cb), (sc, cc) = ctx.bc_sinks
+                dB, dC = sb.slice(cb, N), sc.slice(cc, N)
+            else:
+                dbc = torch.empty((Bsz, T, 2 * N), dtype=B_.dtype, device=dev)
+                dB, dC = dbc[..., :N], dbc[..., N:]
+            dbc_ld = dB.stride(1)
+            if dC.stride(1) != dbc_ld:
+                dbc = torch.empty((Bsz, T, 2 * N), dtype=B_.dtype, device=dev)
+                dB, dC, dbc_ld = dbc[..., :N], dbc[..., N:], 2 * N
+            dB, dC = (dB if ng[3] else None), (dC if ng[4] else None)
+        else:
+            dB = torch.empty_like(B_) if ng[3] else None
+            dC = torch.empty_like(C_) if ng[4] else None
         dD = torch.empty((D,), dtype=torch.float32, device=dev) if ng[5] else None
         want_h0 = has_h0 and len(ng) > 6 and ng[6]
         dh0 = torch.empty((Bsz, D, N), dtype=torch.float32, device=dev) if want_h0 else None
@@ -261,10 +312,16 @@ class NajuScanHip(torch.autograd.Function):
         stream = _stream_handle(dev)
         _raise_pending(dev, stream)
         ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags))
-        _lib.check(L.naju_scan_bwd(
-            _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_b), _ptr(ckpt), _ptr(dy),
-            _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
-            Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
+        if ctx.bc_ld != N or dbc_ld != N:
+            _lib.check(L.naju_scan_bwd_strided(
+                _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_b), _ptr(ckpt), _ptr(dy),
+                _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
+                Bsz, T, D, N, ctx.bc_ld, dbc_ld, *dts, flags, ws.data_ptr(), ws.numel(), stream))
+        else:
+            _lib.check(L.naju_scan_bwd(
+                _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_b), _ptr(ckpt), _ptr(dy),
+                _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
+                Bsz, T, D, N, *dts, flags, ws.data_ptr(), ws.numel(), stream))
         if N == 1:
             _watch_status(dev, stream, ws)
         _check_status(dev)

@@ -440,3 +440,20 @@ def test_env_checkpoint_interval_default(monkeypatch):
     assert scan_mod._default_ckpt_rows(1) == 0
     assert scan_mod._default_ckpt_rows(8) == 0
     assert scan_mod._default_ckpt_rows(65) == 0
+
+
+def test_strided_bc_rejections():
+    """Row strides the kernels do not serve return an error, not a wrong
+    answer (host checks only: nothing is launched)."""
+    L = _lib.lib()
+
+    def fwd(N, ld, B=256, C=256):
+        return L.naju_scan_fwd_strided(256, 256, 256, B, C, 256, None, 256, 256, None, 1, 8, 16, N, ld,
+                                       0, 0, 0, 0, 256, 1 << 20, None)
+
+    assert fwd(16, 8) == _lib.ERR_INVALID
+    assert fwd(1, 4) == _lib.ERR_UNSUPPORTED
+    assert fwd(128, 260) == _lib.ERR_UNSUPPORTED
+    assert fwd(16, 34) == _lib.ERR_UNSUPPORTED
+    assert fwd(16, 36, B=260) == _lib.ERR_UNSUPPORTED
+    assert fwd(16, (1 << 24) + 4) == _lib.ERR_UNSUPPORTED
