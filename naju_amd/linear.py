@@ -20,6 +20,7 @@ import torch.nn.functional as F
 
 from naju_amd import _lib
 from naju_amd.gradsink import acc_sink_of
+from naju_amd.xent import zero_padded_rows
 
 # output tiles (128 x 128) times parts kept at or below this: about two
 # waves of workgroups over the 256 compute units
@@ -96,6 +97,71 @@ class _Linear(torch.autograd.Function):
             if dw.dtype != ctx.w_dtype:
                 dw = dw.to(ctx.w_dtype)
         return dx, dw, None, None
+
+
+# the LM head's vocabulary rows are padded to a multiple of this
+HEAD_ALIGN = 128
+
+
+class _Head(torch.autograd.Function):
+    """logits = x W^T for a vocabulary-sized W [V, d], with W's 16-bit copy
+    padded by zero rows to Vp, a multiple of HEAD_ALIGN: the GEMMs then run on
+    aligned [rows, Vp] operands (a vocabulary of 50257 leaves every row of
+    the logits and of their gradient at an odd offset, which the library's
+    fast kernels do not take). The output is the [..., V] view of the
+    [rows, Vp] product, so it holds the same values as F.linear's logits. In
+    the backward, a gradient that naju_amd.xent.cross_entropy wrote in that
+    padded layout (padding columns zero) is used whole: dx = G W_pad over
+    K = Vp, dW = G^T x in float32 (the first V rows of the [Vp, d] product);
+    any other gradient takes the unpadded GEMMs (K = V). dW comes out in
+    float32, the parameter's dtype, as for the split-K weight gradients."""
+
+    @staticmethod
+    def forward(ctx, x, weight, dtype):
+        V, d = weight.shape
+        Vp = -(-V // HEAD_ALIGN) * HEAD_ALIGN
+        wp = torch.empty((Vp, d), dtype=dtype, device=weight.device)
+        if Vp > V:
+            wp[V:].zero_()
+        wp[:V].copy_(weight)
+        x2 = x.reshape(-1, d)
+        if x2.dtype != dtype:
+            x2 = x2.to(dtype)
+        out = torch.mm(x2, wp.t())
+        ctx.save_for_backward(x2, wp)
+        ctx.V, ctx.x_shape, ctx.x_dtype, ctx.w_dtype = V, x.shape, x.dtype, weight.dtype
+        return out[:, :V].view(*x.shape[:-1], V)
+
+    @staticmethod
+    def backward(ctx, dl):
+        x2, wp = ctx.saved_tensors
+        V, Vp = ctx.V, wp.shape[0]
+        rows = x2.shape[0]
+        g = dl.reshape(rows, V)
+        if g.dtype != wp.dtype:
+            g = g.to(wp.dtype)
+        full = zero_padded_rows(g, Vp) if Vp > V else None
+        gk, wk = (g, wp[:V]) if full is None else (full, wp)
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(gk, wk).view(ctx.x_shape)
+            if dx.dtype != ctx.x_dtype:
+                dx = dx.to(ctx.x_dtype)
+        if ctx.needs_input_grad[1]:
+            dw = torch.mm(gk.t(), x2, out_dtype=torch.float32)[:V]
+            if dw.dtype != ctx.w_dtype:
+                dw = dw.to(ctx.w_dtype)
+        return dx, dw, None
+
+
+def lm_head(x, weight):
+    """F.linear(x, weight) for the LM head (weight [V, d], no bias) in
+    compute_dtype(x) (which must not be None), through the padded GEMMs of
+    _Head; the logits are a [..., V] view with row stride Vp."""
+    dt = compute_dtype(x)
+    if dt is None:
+        raise ValueError("naju_amd.linear.lm_head serves CUDA tensors computed in float16 / bfloat16")
+    return _Head.apply(x, weight, dt)
 
 
 def compute_dtype(x):

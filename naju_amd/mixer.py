@@ -33,7 +33,7 @@ from torch.utils.checkpoint import checkpoint
 
 from naju_amd import gradsink
 from naju_amd.dwconv import dwconv, dwconv_pair, pair_supported
-from naju_amd.linear import compute_dtype, linear
+from naju_amd.linear import compute_dtype, linear, lm_head
 from naju_amd.optim import AdamW as NajuAdamW
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
@@ -287,7 +287,11 @@ class NajuLM(nn.Module):
         x = self.embed(ids)
         for blk in self.blocks:
             x = blk(x)
-        return self.head(self.norm(x, out_dtype=_out_dtype(x)))
+        h = self.norm(x, out_dtype=_out_dtype(x))
+        if compute_dtype(h) is not None:
+            # padded vocabulary rows: aligned GEMMs (logits: a strided view)
+            return lm_head(h, self.head.weight)
+        return self.head(h)
 
 
 def build_optimizer(model, lr, weight_decay=0.1, fused=None):

@@ -15,9 +15,16 @@ comes back in the logits' dtype, as autocast's cast would return it. The
 loss is float32 and deterministic. A target outside [0, V) that is not
 ignore_index gives a NaN loss instead of a device assertion.
 
+Logits whose rows are padded (a row stride a little above V, as the padded
+LM head of naju_amd.linear returns them) get their gradient in the same
+layout, the padding columns zero, so that the head's backward can read whole
+padded rows (``zero_padded_rows``).
+
 CUDA tensors only: there is no other implementation behind this function,
 and a missing library raises.
 """
+import weakref
+
 import torch
 
 from naju_amd import _lib
@@ -43,6 +50,40 @@ class _Workspace:
 
 _WS = _Workspace()
 
+# row strides up to this many elements above the class count are kept in the
+# gradient (padded rows); wider strides (a column slice of a wider tensor)
+# get a contiguous gradient
+_MAX_PAD = 512
+
+# gradient buffers [rows, ld] whose columns past the class count hold zeros,
+# by data pointer (an entry lives as long as its buffer)
+_ZERO_PADDED = weakref.WeakValueDictionary()
+
+
+def _grad_buffer(x, rows, cols):
+    """The logits' gradient [rows, cols]: with x's row stride when it pads
+    the rows by at most _MAX_PAD elements (a view of a [rows, stride] buffer
+    whose padding columns are zero), else contiguous."""
+    ld = x.stride(0)
+    if ld == cols or ld > cols + _MAX_PAD or rows == 0:
+        return torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+    buf = torch.empty((rows, ld), dtype=x.dtype, device=x.device)
+    buf[:, cols:].zero_()
+    _ZERO_PADDED[buf.data_ptr()] = buf
+    return buf[:, :cols]
+
+
+def zero_padded_rows(g, ld):
+    """The [rows, ld] buffer behind g [rows, cols] when g is a gradient this
+    module wrote with padded rows (columns cols .. ld of the buffer zero),
+    else None."""
+    if g.dim() != 2 or g.stride() != (ld, 1) or g.shape[1] >= ld:
+        return None
+    buf = _ZERO_PADDED.get(g.data_ptr())
+    if buf is None or tuple(buf.shape) != (g.shape[0], ld) or buf.dtype != g.dtype or buf.device != g.device:
+        return None
+    return buf
+
 
 class _CrossEntropy(torch.autograd.Function):
     @staticmethod
@@ -60,7 +101,7 @@ class _CrossEntropy(torch.autograd.Function):
         if want_grad:
             # the gradient (for dloss = 1) in the same pass over the logits;
             # the backward keeps it when dloss is 1
-            dx = torch.empty((rows, cols), dtype=x.dtype, device=dev)
+            dx = _grad_buffer(x, rows, cols)
             _lib.check_loss(L.naju_xent_fwd_grad(
                 x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype], ignore_index, lse.data_ptr(),
                 loss.data_ptr(), scale.data_ptr(), dx.data_ptr(), dx.stride(0), _DT[x.dtype], ws.data_ptr(),
@@ -87,7 +128,7 @@ class _CrossEntropy(torch.autograd.Function):
             dx, ctx.dx = ctx.dx, None
             bwd = L.naju_xent_bwd_if_scaled
         else:
-            dx = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+            dx = _grad_buffer(x, rows, cols)
             bwd = L.naju_xent_bwd
         _lib.check_loss(bwd(x.data_ptr(), x.stride(0), target.data_ptr(), rows, cols, _DT[x.dtype], ctx.ignore_index,
                             lse.data_ptr(), scale.data_ptr(), dloss.data_ptr(), dx.data_ptr(), dx.stride(0),

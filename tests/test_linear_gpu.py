@@ -69,3 +69,58 @@ def test_sum_parts_adds_in_part_order(gpu, n_parts, n, offset):
     assert torch.equal(out, ref)
     with pytest.raises(_lib.NajuScanError):
         _lib.check_mixer(L.naju_sum_parts(parts.data_ptr(), 17, n, out.data_ptr(), 0))
+
+
+def _rel64(a, b):
+    a, b = a.detach().double(), b.detach().double()
+    return float((a - b).norm() / b.norm())
+
+
+@pytest.mark.parametrize("V,d,rows,via", [
+    (1000, 64, (2, 96), "naju"),     # padded to 1024, gradient from naju_amd.xent
+    (1000, 64, (2, 96), "torch"),    # the same with torch's cross_entropy: unpadded GEMMs
+    (50257, 768, (1, 512), "naju"),  # the LM's vocabulary, padded to 50304
+    (1024, 32, (3, 50), "naju"),     # already aligned: no padding
+])
+def test_lm_head_padded_matches_float64(gpu, monkeypatch, V, d, rows, via):
+    """The padded LM head (naju_amd.linear.lm_head): logits equal F.linear's
+    on the bf16 operands (a [..., V] view with row stride Vp), and with the
+    loss on top the input and weight gradients agree with float64 autograd
+    of the same bf16-rounded operands to the bf16 rounding of the logits'
+    gradient; the padded backward GEMMs are taken exactly when the gradient
+    comes from naju_amd.xent.cross_entropy in the padded layout."""
+    from naju_amd import linear as lin
+    from naju_amd.xent import cross_entropy
+    hits = []
+    real = lin.zero_padded_rows
+
+    def spy(g, ld):
+        r = real(g, ld)
+        hits.append(r is not None)
+        return r
+
+    monkeypatch.setattr(lin, "zero_padded_rows", spy)
+    g = torch.Generator(device=gpu).manual_seed(V + d)
+    x = torch.randn(*rows, d, generator=g, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, d, generator=g, device=gpu) * 0.5 / d ** 0.5).requires_grad_(True)
+    tgt = torch.randint(0, V, (x.numel() // d,), generator=g, device=gpu)
+    logits = lin.lm_head(x, w)
+    Vp = -(-V // lin.HEAD_ALIGN) * lin.HEAD_ALIGN
+    assert logits.shape == (*rows, V) and logits.stride(-2) == Vp and logits.dtype == torch.bfloat16
+    wb = w.detach().to(torch.bfloat16)
+    ref = F.linear(x.detach(), wb)
+    assert _rel64(logits, ref) < 4e-3
+    if via == "naju":
+        loss = cross_entropy(logits.view(-1, V), tgt)
+    else:
+        loss = F.cross_entropy(logits.float().view(-1, V), tgt)
+    loss.backward()
+    torch.cuda.synchronize()
+    padded = Vp > V and via == "naju"
+    assert hits == ([padded] if Vp > V else []), hits
+    assert w.grad.dtype == torch.float32 and w.grad.shape == (V, d)
+    x64 = x.detach().double().requires_grad_(True)
+    w64 = wb.double().requires_grad_(True)
+    F.cross_entropy(F.linear(x64, w64).view(-1, V), tgt).backward()
+    assert _rel64(x.grad, x64.grad) < 1e-2
+    assert _rel64(w.grad, w64.grad) < 1e-2
