@@ -74,6 +74,16 @@ typedef struct naju_adamw_group {
   float eps;
 } naju_adamw_group;
 
+/* One float32 tensor of naju_cast_multi: numel elements from src (NULL:
+ * zeros) to element dst_offset of the destination; chunks as for
+ * naju_adamw_tensor. */
+typedef struct naju_cast_tensor {
+  const float* src;
+  int64_t dst_offset;
+  int64_t numel;
+  int64_t first_chunk;
+} naju_cast_tensor;
+
 /* Message of the last failed call of this thread ("" after a success). */
 const char* naju_optim_last_error(void);
 
@@ -93,6 +103,17 @@ int naju_grad_norm(const naju_adamw_tensor* tensors, const int32_t* chunk_tensor
  * by value; grad_coef a device float32 (the coef of naju_grad_norm) or NULL. */
 int naju_adamw_step(const naju_adamw_tensor* tensors, const int32_t* chunk_tensor, int n_tensors, int64_t n_chunks,
                     const naju_adamw_group* groups, int n_groups, const float* grad_coef, void* stream);
+
+/* Every tensor of the table rounded to dst_dtype (NAJU_DTYPE_BF16 or
+ * NAJU_DTYPE_F16; round to nearest even) into one destination buffer at its
+ * dst_offset, in one launch: the 16-bit weight copies that autocast makes
+ * one cast kernel each (and the concatenation of weights that share a
+ * GEMM, when their offsets are consecutive). Bitwise torch's .to(dtype) for
+ * finite and infinite values. table and chunk_tensor are device pointers; a
+ * chunk is moved as float4 when src is 16-byte and its destination 8-byte
+ * aligned. No reference counterpart (torch's autocast casts per tensor). */
+int naju_cast_multi(const naju_cast_tensor* tensors, const int32_t* chunk_tensor, int n_tensors, int64_t n_chunks,
+                    void* dst, int dst_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,7 @@ EXPORTED = (
     "naju_grad_norm_workspace_bytes",
     "naju_grad_norm",
     "naju_adamw_step",
+    "naju_cast_multi",
 )
 
 _lib = None
@@ -192,6 +193,9 @@ def lib():
     # tensors, chunk_tensor, n_tensors, n_chunks, groups (host), n_groups, grad_coef, stream
     L.naju_adamw_step.argtypes = [P, P, I, I64, P, I, P, P]
     L.naju_adamw_step.restype = I
+    # tensors, chunk_tensor, n_tensors, n_chunks, dst, dst_dtype, stream
+    L.naju_cast_multi.argtypes = [P, P, I, I64, P, I, P]
+    L.naju_cast_multi.restype = I
     _lib = L
     return _lib
 

@@ -57,9 +57,9 @@ __device__ __forceinline__ void adamw4(float4& p, const float4& g, float4& m, fl
 
 // The tensor of chunk c and the chunk's element range in it; false (the
 // chunk is skipped) when the table does not place c inside that tensor.
-__device__ __forceinline__ bool chunk_of(const naju_adamw_tensor* __restrict__ tab,
-                                         const int32_t* __restrict__ chunk_tensor, int n_tensors, int64_t c,
-                                         naju_adamw_tensor& t, int64_t& off, int& n) {
+template <typename Rec>
+__device__ __forceinline__ bool chunk_of(const Rec* __restrict__ tab, const int32_t* __restrict__ chunk_tensor,
+                                         int n_tensors, int64_t c, Rec& t, int64_t& off, int& n) {
   int ti = chunk_tensor[c];
   ti = ti < 0 ? 0 : (ti < n_tensors ? ti : n_tensors - 1);
   t = tab[ti];
@@ -189,6 +189,40 @@ __global__ __launch_bounds__(1024) void norm_final_kernel(const float* __restric
   }
 }
 
+template <typename TO>
+using out4_t = TO __attribute__((ext_vector_type(4)));
+
+// naju_cast_multi: one workgroup per chunk; a full aligned chunk issues all
+// eight float4 loads of a thread before its first store.
+template <typename TO>
+__global__ __launch_bounds__(kThreads) void cast_kernel(const naju_cast_tensor* __restrict__ tab,
+                                                        const int32_t* __restrict__ chunk_tensor, int n_tensors,
+                                                        TO* __restrict__ dst) {
+  naju_cast_tensor t;
+  int64_t off;
+  int n;
+  if (!chunk_of(tab, chunk_tensor, n_tensors, blockIdx.x, t, off, n)) return;
+  const float* __restrict__ S = t.src ? t.src + off : nullptr;
+  TO* __restrict__ D = dst + t.dst_offset + off;
+  const int tid = threadIdx.x;
+  if (n == kChunk && (!S || aligned16(S)) && ((uintptr_t)D & 7u) == 0) {
+    float4 v[kVec4];
+#pragma unroll
+    for (int k = 0; k < kVec4; ++k) v[k] = S ? ((const float4*)S)[k * kThreads + tid] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kVec4; ++k) {
+      out4_t<TO> o;
+      o.x = (TO)v[k].x;
+      o.y = (TO)v[k].y;
+      o.z = (TO)v[k].z;
+      o.w = (TO)v[k].w;
+      ((out4_t<TO>*)D)[k * kThreads + tid] = o;
+    }
+    return;
+  }
+  for (int i = tid; i < n; i += kThreads) D[i] = S ? (TO)S[i] : (TO)0.f;
+}
+
 thread_local char g_err[256] = "";
 
 int fail(int code, const char* fmt, ...) {
@@ -255,6 +289,28 @@ int naju_adamw_step(const naju_adamw_tensor* tensors, const int32_t* chunk_tenso
   for (int i = 0; i < n_groups; ++i) ga.g[i] = groups[i];
   hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)n_chunks), dim3(kThreads), 0, (hipStream_t)stream, tensors,
                      chunk_tensor, n_tensors, ga, grad_coef);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+int naju_cast_multi(const naju_cast_tensor* tensors, const int32_t* chunk_tensor, int n_tensors, int64_t n_chunks,
+                    void* dst, int dst_dtype, void* stream) {
+  g_err[0] = 0;
+  if (n_tensors < 0 || n_chunks < 0) return fail(NAJU_ERR_INVALID, "negative table size");
+  if (n_chunks > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "too many chunks (%lld)", (long long)n_chunks);
+  if (n_chunks > 0 && (!tensors || !chunk_tensor || n_tensors == 0 || !dst))
+    return fail(NAJU_ERR_INVALID, "null tensor table, chunk map or destination");
+  if (dst_dtype != NAJU_DTYPE_BF16 && dst_dtype != NAJU_DTYPE_F16)
+    return fail(NAJU_ERR_UNSUPPORTED, "destination dtype %d: bf16 or f16 only", dst_dtype);
+  if (n_chunks == 0) return NAJU_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dst_dtype == NAJU_DTYPE_BF16)
+    hipLaunchKernelGGL(cast_kernel<__bf16>, dim3((unsigned)n_chunks), dim3(kThreads), 0, st, tensors, chunk_tensor,
+                       n_tensors, (__bf16*)dst);
+  else
+    hipLaunchKernelGGL(cast_kernel<_Float16>, dim3((unsigned)n_chunks), dim3(kThreads), 0, st, tensors,
+                       chunk_tensor, n_tensors, (_Float16*)dst);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return NAJU_OK;

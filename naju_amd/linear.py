@@ -18,7 +18,7 @@ otherwise).
 import torch
 import torch.nn.functional as F
 
-from naju_amd import _lib
+from naju_amd import _lib, wcast
 from naju_amd.gradsink import acc_sink_of
 from naju_amd.xent import zero_padded_rows
 
@@ -60,12 +60,18 @@ def weight_grad(dy, x):
 
 
 class _Linear(torch.autograd.Function):
+    """x @ W^T with W the row-wise concatenation of weights (one GEMM for
+    layers that read the same x), wb its 16-bit copy when one is at hand
+    (naju_amd.wcast), else cast here."""
+
     @staticmethod
-    def forward(ctx, x, weight, dtype, x_acc):
+    def forward(ctx, x, dtype, x_acc, wb, *weights):
         xb = x if x.dtype == dtype else x.to(dtype)
-        wb = weight.to(dtype)
+        if wb is None:
+            wb = weights[0].to(dtype) if len(weights) == 1 else torch.cat([w.to(dtype) for w in weights], 0)
         ctx.save_for_backward(xb, wb)
-        ctx.x_dtype, ctx.w_dtype = x.dtype, weight.dtype
+        ctx.x_dtype, ctx.w_dtypes = x.dtype, [w.dtype for w in weights]
+        ctx.rows = [w.shape[0] for w in weights]
         # x is a gradsink.fanout() alias (in the compute dtype): dx is
         # written into, or added to, the fan-out's buffer
         ctx.x_acc = x_acc if xb is x else None
@@ -92,11 +98,14 @@ class _Linear(torch.autograd.Function):
                 dx = torch.mm(dy2, wb).view(*dy.shape[:-1], n_in)
                 if dx.dtype != ctx.x_dtype:
                     dx = dx.to(ctx.x_dtype)
-        if ctx.needs_input_grad[1]:
+        dws = [None] * len(ctx.rows)
+        if any(ctx.needs_input_grad[4:]):
             dw = weight_grad(dy2.contiguous(), xb.reshape(-1, n_in))
-            if dw.dtype != ctx.w_dtype:
-                dw = dw.to(ctx.w_dtype)
-        return dx, dw, None, None
+            # each weight's rows of the product (contiguous views)
+            for i, d in enumerate(dw.split(ctx.rows, 0) if len(ctx.rows) > 1 else (dw,)):
+                if ctx.needs_input_grad[4 + i]:
+                    dws[i] = d if d.dtype == ctx.w_dtypes[i] else d.to(ctx.w_dtypes[i])
+        return (dx, None, None, None, *dws)
 
 
 # the LM head's vocabulary rows are padded to a multiple of this
@@ -117,13 +126,14 @@ class _Head(torch.autograd.Function):
     float32, the parameter's dtype, as for the split-K weight gradients."""
 
     @staticmethod
-    def forward(ctx, x, weight, dtype):
+    def forward(ctx, x, weight, dtype, wp):
         V, d = weight.shape
         Vp = -(-V // HEAD_ALIGN) * HEAD_ALIGN
-        wp = torch.empty((Vp, d), dtype=dtype, device=weight.device)
-        if Vp > V:
-            wp[V:].zero_()
-        wp[:V].copy_(weight)
+        if wp is None or tuple(wp.shape) != (Vp, d):
+            wp = torch.empty((Vp, d), dtype=dtype, device=weight.device)
+            if Vp > V:
+                wp[V:].zero_()
+            wp[:V].copy_(weight)
         x2 = x.reshape(-1, d)
         if x2.dtype != dtype:
             x2 = x2.to(dtype)
@@ -151,7 +161,7 @@ class _Head(torch.autograd.Function):
             dw = torch.mm(gk.t(), x2, out_dtype=torch.float32)[:V]
             if dw.dtype != ctx.w_dtype:
                 dw = dw.to(ctx.w_dtype)
-        return dx, dw, None
+        return dx, dw, None, None
 
 
 def lm_head(x, weight):
@@ -161,7 +171,7 @@ def lm_head(x, weight):
     dt = compute_dtype(x)
     if dt is None:
         raise ValueError("naju_amd.linear.lm_head serves CUDA tensors computed in float16 / bfloat16")
-    return _Head.apply(x, weight, dt)
+    return _Head.apply(x, weight, dt, wcast.lookup((weight,), dt))
 
 
 def compute_dtype(x):
@@ -180,7 +190,18 @@ def linear(x, weight):
     dt = compute_dtype(x)
     if dt is None:
         raise ValueError("naju_amd.linear.linear serves CUDA tensors computed in float16 / bfloat16")
+    return linear_cat(x, (weight,))
+
+
+def linear_cat(x, weights):
+    """x @ cat(weights, 0)^T as linear() (one GEMM, one split-K weight
+    gradient), each weight getting its rows of the gradient; the 16-bit
+    concatenation comes from naju_amd.wcast when the group is active there."""
+    dt = compute_dtype(x)
+    if dt is None:
+        raise ValueError("naju_amd.linear.linear serves CUDA tensors computed in float16 / bfloat16")
     x_acc = acc_sink_of(x)
     if x_acc is not None and not x.is_contiguous():
         x_acc = None
-    return _Linear.apply(x, weight, dt, x_acc)
+    weights = tuple(weights)
+    return _Linear.apply(x, dt, x_acc, wcast.lookup(weights, dt), *weights)

@@ -31,9 +31,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
-from naju_amd import gradsink
+from naju_amd import gradsink, wcast
 from naju_amd.dwconv import dwconv, dwconv_pair, pair_supported
-from naju_amd.linear import compute_dtype, linear, lm_head
+from naju_amd.linear import HEAD_ALIGN, compute_dtype, linear, linear_cat, lm_head
 from naju_amd.optim import AdamW as NajuAdamW
 from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
@@ -86,6 +86,15 @@ def _linear(x, weight):
     if compute_dtype(x) is not None:
         return linear(x, weight)
     return F.linear(x, weight)
+
+
+def _linear_cat(x, weights):
+    """F.linear(x, torch.cat(weights, 0)); on CUDA in 16-bit compute one GEMM
+    whose 16-bit weight may come from naju_amd.wcast, with the split-K
+    float32 weight gradient."""
+    if compute_dtype(x) is not None:
+        return linear_cat(x, weights)
+    return F.linear(x, torch.cat(weights, 0))
 
 
 def _causal_dwconv(x, conv):
@@ -168,6 +177,16 @@ class NajuMixer(nn.Module):
             return dwconv(x, self.conv1d.weight, self.conv1d.bias, silu=True, out_dtype=_out_dtype(x))
         return F.silu(_causal_dwconv(x, self.conv1d))
 
+    def cast_groups(self):
+        """The weight groups this mixer's GEMMs look up in naju_amd.wcast
+        (on CUDA in 16-bit compute): in_proj, the fused f / i / x projection
+        (without gate_rank) and out_proj."""
+        g = [((self.in_proj.weight,), 0)]
+        if not self.gate_rank:
+            g.append(((self.f_proj.weight, self.i_proj.weight, self.x_proj.weight), 0))
+        g.append(((self.out_proj.weight,), 0))
+        return g
+
     def forward(self, u):
         xz = _linear(u, self.in_proj.weight)
         if xz.is_cuda:
@@ -202,8 +221,8 @@ class NajuMixer(nn.Module):
             # the three comes back as one GEMM instead of three plus two adds;
             # the convolutions read their slices in place
             di, N = self.d_inner, self.d_state
-            w = torch.cat([self.f_proj.weight, self.i_proj.weight, self.x_proj.weight], 0)
-            p_f, p_i, Bm, Cm = gradsink.split(_linear(h_g, w), [di, di, N, N])
+            w = (self.f_proj.weight, self.i_proj.weight, self.x_proj.weight)
+            p_f, p_i, Bm, Cm = gradsink.split(_linear_cat(h_g, w), [di, di, N, N])
             if pair and pair_supported(h_f, self.f_conv.weight, p_f, self.i_conv.weight, p_i):
                 f_logit, i_logit = dwconv_pair(
                     h_f, self.f_conv.weight, self.f_bias, p_f, self.i_conv.weight, self.i_bias, p_i,
@@ -283,15 +302,29 @@ class NajuLM(nn.Module):
         if tie_weights:
             self.head.weight = self.embed.weight
 
+    def _cast_groups(self, x):
+        """Every weight the forward's GEMMs take in 16-bit compute on CUDA
+        (the blocks' projections, the head padded to HEAD_ALIGN rows), for one
+        naju_cast_multi launch per forward; none otherwise."""
+        if not (x.is_cuda and torch.is_autocast_enabled("cuda")):
+            return []
+        groups = [g for blk in self.blocks for g in blk.mixer.cast_groups()]
+        return groups + [((self.head.weight,), HEAD_ALIGN)]
+
     def forward(self, ids):
         x = self.embed(ids)
-        for blk in self.blocks:
-            x = blk(x)
-        h = self.norm(x, out_dtype=_out_dtype(x))
-        if compute_dtype(h) is not None:
-            # padded vocabulary rows: aligned GEMMs (logits: a strided view)
-            return lm_head(h, self.head.weight)
-        return self.head(h)
+        groups = self._cast_groups(x)
+        if groups and getattr(self, "_wcopies", None) is None:
+            self._wcopies = wcast.WeightCopies()
+        with wcast.active(getattr(self, "_wcopies", None), groups,
+                          torch.get_autocast_dtype("cuda") if groups else None):
+            for blk in self.blocks:
+                x = blk(x)
+            h = self.norm(x, out_dtype=_out_dtype(x))
+            if compute_dtype(h) is not None:
+                # padded vocabulary rows: aligned GEMMs (logits: a strided view)
+                return lm_head(h, self.head.weight)
+            return self.head(h)
 
 
 def build_optimizer(model, lr, weight_decay=0.1, fused=None):

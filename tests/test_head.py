@@ -36,3 +36,25 @@ def test_registry_entry_ends_with_its_buffer():
     del g
     gc.collect()
     assert ptr not in xent._ZERO_PADDED
+
+
+def test_weight_copy_layout_and_table():
+    """naju_amd.wcast: a group's weights back to back, padding rows as
+    zero-fill entries (src 0), groups 64-element aligned, chunks per entry."""
+    from naju_amd import wcast
+    a, b, c = torch.empty(3, 8), torch.empty(5, 8), torch.empty(7, 16)
+    total, mats, entries = wcast.layout([((a, b), 0), ((c,), 4)])
+    assert mats == [(0, 8, 8), (64, 8, 16)]
+    assert total == 64 + 128
+    assert entries == [(a.data_ptr(), 0, 24), (b.data_ptr(), 24, 40), (c.data_ptr(), 64, 112), (0, 176, 16)]
+    rec, cmap = wcast.build_table([(1, 0, 8192), (2, 8192, 8193), (0, 20000, 5)])
+    assert list(rec["first_chunk"]) == [0, 1, 3] and list(cmap) == [0, 1, 1, 2]
+    assert not wcast.servable([((a,), 0)])  # CPU tensors
+
+
+def test_weight_copy_lookup_is_scoped():
+    from naju_amd import wcast
+    w = torch.empty(2, 2)
+    assert wcast.lookup((w,), torch.bfloat16) is None
+    with wcast.active(None, [], None):
+        assert wcast.lookup((w,), torch.bfloat16) is None

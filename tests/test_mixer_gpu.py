@@ -264,3 +264,41 @@ def test_mixer_gradient_fanout_matches_autograd_sums(gpu):
             assert _rel(pa.grad, pb.grad) < 1e-2, n
     finally:
         scan_mod._BACKEND_CACHE.pop("hip_plain", None)
+
+
+def test_lm_weight_copies_match_per_layer_casts(gpu, monkeypatch):
+    """NajuLM's forward under bf16 autocast writes every projection's and
+    the head's 16-bit weight with one naju_cast_multi launch
+    (naju_amd.wcast), which the GEMMs take in place of their own casts and
+    concatenations: logits, loss and every gradient are bitwise those of the
+    same model without it, and every lookup hits."""
+    import copy
+    from naju_amd import wcast
+    from naju_amd.xent import cross_entropy
+    torch.manual_seed(11)
+    V = 97
+    ma = NajuLM(V, d_model=64, n_layers=2, dropout=0.0, d_state=16, scan_backend="hip").to(gpu)
+    mb = copy.deepcopy(ma)
+    monkeypatch.setattr(mb, "_cast_groups", lambda x: [])
+    hits = []
+    real = wcast.lookup
+
+    def spy(weights, dtype):
+        r = real(weights, dtype)
+        hits.append(r is not None)
+        return r
+
+    monkeypatch.setattr(wcast, "lookup", spy)
+    ids = torch.randint(0, V, (2, 65), device=gpu)
+    outs = []
+    for m in (ma, mb):
+        hits.clear()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = m(ids[:, :-1])
+            loss = cross_entropy(logits.reshape(-1, V), ids[:, 1:].reshape(-1))
+        loss.backward()
+        outs.append((logits.detach().clone(), loss.detach(), [p.grad for p in m.parameters()], list(hits)))
+    assert outs[0][3] == [True] * (3 * 2 + 1) and not any(outs[1][3])
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    for (n, _), ga, gb in zip(ma.named_parameters(), outs[0][2], outs[1][2]):
+        assert torch.equal(ga, gb), n

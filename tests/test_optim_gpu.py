@@ -121,3 +121,40 @@ def test_adamw_rejects_what_it_does_not_serve(gpu):
     p.grad = torch.zeros_like(p)
     with pytest.raises(ValueError, match="float32"):
         AdamW([p]).step()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_weight_copies_are_torch_casts_bitwise(gpu, dtype):
+    """naju_cast_multi through naju_amd.wcast: every group's 16-bit matrix is
+    torch's .to(dtype) of its weights concatenated, bitwise (NaN as NaN),
+    over whole and partial chunks, an unaligned weight (element path),
+    special values (infinities, overflow, subnormals, ties of the rounding)
+    and zero padding rows; a second write after the weights change reuses the
+    table and shows the new values."""
+    from naju_amd import wcast
+    g = torch.Generator(device=gpu).manual_seed(3)
+    w1 = torch.randn(300, 1536, generator=g, device=gpu) * 0.02
+    bits = torch.randint(0, 1 << 31, (17, 1536), generator=g, device=gpu, dtype=torch.int64)
+    # exponents in a normal range, the low 16 bits an exact bf16 tie
+    bits = (bits & 0x807FFFFF) | (torch.randint(100, 150, (17, 1536), generator=g, device=gpu) << 23)
+    w2 = (bits.to(torch.int32) & ~0xFFFF | 0x8000).view(torch.float32).clone()
+    w2[0, :6] = torch.tensor([float("inf"), -float("inf"), 1e-40, -3.0e38, 65520.0, float("nan")], device=gpu)
+    base = torch.randn(5 * 1536 + 1, generator=g, device=gpu)
+    w3 = base[1:].view(5, 1536)
+    assert w3.data_ptr() % 16 == 4
+    w4 = torch.randn(1, 1536, generator=g, device=gpu)
+    groups = [((w1, w2), 0), ((w3,), 0), ((w4,), 128)]
+    copies = wcast.WeightCopies()
+    for rep in range(2):
+        mats = copies.write(groups, dtype)
+        torch.cuda.synchronize()
+        want = [torch.cat([w1, w2]).to(dtype), w3.to(dtype),
+                torch.cat([w4.to(dtype), torch.zeros(127, 1536, dtype=dtype, device=gpu)])]
+        for (ws, _), ref in zip(groups, want):
+            got = mats[tuple(id(w) for w in ws)]
+            assert got.shape == ref.shape and got.dtype == dtype
+            nan = torch.isnan(ref)
+            assert torch.equal(torch.isnan(got), nan)
+            assert torch.equal(got.view(torch.int16)[~nan], ref.view(torch.int16)[~nan]), rep
+        w1.mul_(-1.5)
+        w3.add_(0.25)
