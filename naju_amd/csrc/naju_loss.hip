@@ -16,6 +16,8 @@
 // at any 2-byte boundary) handled element by element.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -296,6 +298,204 @@ __global__ __launch_bounds__(kThreads) void xent_fwd_grad_kernel(const T* __rest
   grad_row<T, TD>(x + r * ld, dx + r * dld, t, n_cols, ignore, g, s_l, threadIdx.x);
 }
 
+// ---------------------------------------------- whole rows held in registers
+//
+// One workgroup of kRT threads per row for rows of kRegMin .. kRT * NV * E
+// classes: every 16-byte vector of the row is loaded once into registers
+// (NV per thread, all issued before the first is used), the row's maximum
+// and then its sum of exp(x - max) are formed from the registers, and with
+// GRAD the gradient for dloss = 1 is written from them too, so the row is
+// read from memory once instead of twice. The row's few elements before its
+// first 16-byte boundary and after its last whole vector are single loads.
+// Sums in a fixed order (per thread in vector order, the wave's lanes by
+// butterfly, the waves in wave order), so results repeat bitwise; the
+// forward-only and the forward-with-gradient forms run the same reduction,
+// so their lse (and with it the backward's gradient) agree bitwise.
+constexpr int kRT = 1024;
+constexpr int kRW = kRT / 64;
+constexpr int64_t kRegMin = 2048;
+
+// Element e of a 16-byte vector of T held as four raw 32-bit words.
+template <typename T>
+__device__ __forceinline__ float elem(const uint32_t (&w)[4], int e) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(w[e]);
+  } else if constexpr (std::is_same<T, bf16_t>::value) {
+    const uint32_t u = w[e >> 1];
+    return __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
+  } else {
+    const uint16_t h = (uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+    return (float)__builtin_bit_cast(f16_t, h);
+  }
+}
+
+// GRAD: the forward only, or with the gradient stored as vectors (dx rows of
+// T's size and the logits' alignment) or element by element.
+constexpr int kRegFwd = 0, kRegGradVec = 1, kRegGradElem = 2;
+
+template <typename T, typename TD, int NV, int GRAD>
+__global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(8))) void xent_row_reg_kernel(
+    const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ target, int64_t n_cols64, int64_t ignore,
+    float* __restrict__ lse, float* __restrict__ row_loss, float* __restrict__ row_valid,
+    const float* __restrict__ scale, TD* __restrict__ dx, int64_t dld) {
+  constexpr int E = 16 / sizeof(T);
+  __shared__ float s_red[kRW];
+  __shared__ float s_bc[2];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
+  // 32-bit column indices: rows of at most kRT * NV * E elements
+  const int n_cols = (int)n_cols64;
+  const T* p = x + r * ld;
+  const int head = (int)head_elems(p, n_cols64);
+  const int nvec = (n_cols - head) / E;
+  const int tail0 = head + nvec * E;
+  const uint4* q = reinterpret_cast<const uint4*>(p + head);
+  // the row as loaded (raw words, four per vector), converted where used:
+  // floats kept from one pass to the next would double the registers and
+  // leave room for one workgroup per compute unit
+  uint32_t a[NV][4];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = tid + k * kRT;
+    const uint4 v = q[i < nvec ? i : (nvec > 0 ? nvec - 1 : 0)];
+    a[k][0] = v.x, a[k][1] = v.y, a[k][2] = v.z, a[k][3] = v.w;
+  }
+  // keeps the compiler from carrying converted values across the passes
+  auto fence = [&]() {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) asm volatile("" : "+v"(a[k][0]), "+v"(a[k][1]), "+v"(a[k][2]), "+v"(a[k][3]));
+  };
+  const float hv = tid < head ? tof(p[tid]) : -INFINITY;
+  const float tv = tail0 + tid < n_cols ? tof(p[tail0 + tid]) : -INFINITY;
+  auto valid = [&](int k) { return tid + k * kRT < nvec; };
+
+  // the row's maximum
+  float m = fmaxf(hv, tv);
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (valid(k))
+#pragma unroll
+      for (int e = 0; e < E; ++e) m = fmaxf(m, elem<T>(a[k], e));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) s_red[wv] = m;
+  __syncthreads();
+  if (tid == 0) {
+    float M = s_red[0];
+    for (int w = 1; w < kRW; ++w) M = fmaxf(M, s_red[w]);
+    s_bc[0] = M;
+  }
+  __syncthreads();
+  const float M = s_bc[0];
+  fence();
+
+  // sum of exp(x - max); an all -inf row sums to 0 (lse -inf)
+  float sum = 0.f;
+  if (M != -INFINITY) {
+    auto ex = [&](float v) { return exp2_((v - M) * kLog2e); };
+    if (tid < head) sum += ex(hv);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (valid(k))
+#pragma unroll
+        for (int e = 0; e < E; ++e) sum += ex(elem<T>(a[k], e));
+    if (tail0 + tid < n_cols) sum += ex(tv);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (lane == 0) s_red[wv] = sum;  // thread 0 read the maxima before the last barrier
+  __syncthreads();
+  const int64_t t = target[r];
+  if (tid == 0) {
+    float S = s_red[0];
+    for (int w = 1; w < kRW; ++w) S += s_red[w];
+    const float l = M + logf(S);
+    lse[r] = l;
+    s_bc[1] = l;
+    float loss = 0.f, vld = 0.f;
+    if (t != ignore) {
+      vld = 1.f;
+      loss = (t >= 0 && t < n_cols64) ? l - tof(p[t]) : __builtin_nanf("");
+    }
+    row_loss[r] = loss;
+    row_valid[r] = vld;
+  }
+  if constexpr (GRAD != kRegFwd) {
+    fence();
+    __syncthreads();
+    const float l = s_bc[1];
+    TD* d = dx + r * dld;
+    // as grad_row: g * exp(x - lse), minus g at the target; an ignored row's
+    // gradient is 0 (selected, so that no branch splits the passes)
+    const bool ign = t == ignore;
+    const bool tin = t >= 0 && t < n_cols64;
+    const float g = tin ? 1.f * scale[0] : __builtin_nanf("");
+    const int t32 = tin ? (int)t : -1;  // the target's column (none: -1)
+    auto grad = [&](float v, int c) {
+      const float e = exp2_((v - l) * kLog2e) * g;
+      return ign ? 0.f : (c == t32 ? e - g : e);
+    };
+    if (tid < head) d[tid] = fromf<TD>(grad(hv, tid));
+    if (tail0 + tid < n_cols) d[tail0 + tid] = fromf<TD>(grad(tv, tail0 + tid));
+    typedef TD dvec_t __attribute__((ext_vector_type(E)));
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if (!valid(k)) continue;
+      const int i = tid + k * kRT;
+      const int c0 = head + i * E;
+      if constexpr (GRAD == kRegGradVec) {
+        dvec_t w;
+#pragma unroll
+        for (int e = 0; e < E; ++e) w[e] = fromf<TD>(grad(elem<T>(a[k], e), c0 + e));
+        reinterpret_cast<dvec_t*>(d + head)[i] = w;
+        // the later vectors' work stays after this store (computed ahead,
+        // their results would need registers of their own)
+#pragma unroll
+        for (int kk = k + 1; kk < NV; ++kk)
+          asm volatile("" : "+v"(a[kk][0]), "+v"(a[kk][1]), "+v"(a[kk][2]), "+v"(a[kk][3]));
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) d[c0 + e] = fromf<TD>(grad(elem<T>(a[k], e), c0 + e));
+      }
+    }
+  }
+}
+
+// Vectors per thread of the register kernel for rows of n_cols elements of
+// `size` bytes, or 0 when the row takes the two-pass kernels.
+int reg_nv(int64_t n_cols, int size) {
+  const int64_t e = 16 / size;
+  if (n_cols < kRegMin) return 0;
+  for (int nv : {2, 4, 7})
+    if (n_cols <= kRT * nv * e) return nv;
+  return 0;
+}
+
+template <typename T, typename TD, int GRAD>
+void launch_reg(int nv, const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
+                float* lse, float* rl, float* rv, const float* scale, void* dx, int64_t dld, hipStream_t st) {
+  const dim3 g((unsigned)rows), b(kRT);
+  if (nv == 2)
+    xent_row_reg_kernel<T, TD, 2, GRAD><<<g, b, 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse, rl, rv, scale,
+                                                         (TD*)dx, dld);
+  else if (nv == 4)
+    xent_row_reg_kernel<T, TD, 4, GRAD><<<g, b, 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse, rl, rv, scale,
+                                                         (TD*)dx, dld);
+  else
+    xent_row_reg_kernel<T, TD, 7, GRAD><<<g, b, 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse, rl, rv, scale,
+                                                         (TD*)dx, dld);
+}
+
+// Whether every row of dx starts at the same offset from a 16-byte boundary
+// as the same row of x (then the register kernel stores the gradient as
+// vectors): same element size, same base offset, row strides congruent.
+bool rows_match(const void* x, int64_t ld, int x_size, const void* dx, int64_t dld, int dx_size) {
+  if (x_size != dx_size) return false;
+  const int64_t e = 16 / x_size;
+  return ((uintptr_t)x & 15) == ((uintptr_t)dx & 15) && (ld - dld) % e == 0;
+}
+
 // ------------------------------------------------------------------ host side
 
 thread_local char g_err[256] = "";
@@ -330,6 +530,10 @@ int launched() {
 template <typename T>
 void launch_fwd(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
                 float* lse, float* rl, float* rv, hipStream_t st) {
+  if (const int nv = reg_nv(cols, sizeof(T))) {
+    launch_reg<T, T, kRegFwd>(nv, x, ld, tgt, rows, cols, ignore, lse, rl, rv, nullptr, nullptr, 0, st);
+    return;
+  }
   xent_fwd_kernel<T><<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>((const T*)x, ld, tgt, cols, ignore, lse, rl,
                                                                       rv);
 }
@@ -357,6 +561,13 @@ void launch_bwd_dt(int dx_dt, const void* x, int64_t ld, const int64_t* tgt, int
 template <typename T, typename TD>
 void launch_fwd_grad(const void* x, int64_t ld, const int64_t* tgt, int64_t rows, int64_t cols, int64_t ignore,
                      float* lse, float* rl, float* rv, const float* scale, void* dx, int64_t dld, hipStream_t st) {
+  if (const int nv = reg_nv(cols, sizeof(T))) {
+    if (rows_match(x, ld, sizeof(T), dx, dld, sizeof(TD)))
+      launch_reg<T, TD, kRegGradVec>(nv, x, ld, tgt, rows, cols, ignore, lse, rl, rv, scale, dx, dld, st);
+    else
+      launch_reg<T, TD, kRegGradElem>(nv, x, ld, tgt, rows, cols, ignore, lse, rl, rv, scale, dx, dld, st);
+    return;
+  }
   xent_fwd_grad_kernel<T, TD><<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>((const T*)x, ld, tgt, cols, ignore,
                                                                                lse, rl, rv, scale, (TD*)dx, dld);
 }
