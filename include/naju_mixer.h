@@ -159,12 +159,14 @@ size_t naju_dwconv_pair_workspace_bytes(int64_t batch, int64_t T, int64_t C, int
  * receives dx + that sum), dw0 / dbias0 / dw1 / dbias1 (each nullable; fixed
  * order, deterministic), and the adds' gradients dy0, dy1 written in x's
  * dtype into dadd0 / dadd1 (nullable, row stride dadd_ld). dy0, dy1 are
- * [batch, T, C] contiguous in x's dtype or float32. Same shapes served as
- * the forward. No reference counterpart as one call: the reference's two
- * Conv1d modules and autograd's sum of their input gradients
- * (naju/mixer.py:108-110). */
+ * [batch, T, C] in x's dtype or float32 with rows dy_ld apart (a multiple
+ * of 8: they may be the slices naju_scan_bwd_ex wrote into the projection's
+ * gradient buffer, whose adds' gradients then need no dadd). Same shapes
+ * served as the forward. No reference counterpart as one call: the
+ * reference's two Conv1d modules and autograd's sum of their input
+ * gradients (naju/mixer.py:108-110). */
 int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const float* w1, const void* dy0,
-                         const void* dy1, void* dx, int64_t dx_ld, float* dw0, float* dbias0, float* dw1,
+                         const void* dy1, int64_t dy_ld, void* dx, int64_t dx_ld, float* dw0, float* dbias0, float* dw1,
                          float* dbias1, void* dadd0, void* dadd1, int64_t dadd_ld, int64_t batch, int64_t T,
                          int64_t C, int K, int accumulate, int x_dtype, int dy_dtype, void* workspace,
                          size_t workspace_bytes, void* stream);

@@ -184,6 +184,46 @@ int naju_scan_bwd_strided(const void* u, const void* f_logit, const void* i_logi
                           int64_t bc_ld, int64_t dbc_ld, int x_dtype, int gate_dtype, int bc_dtype, int flags,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Output layout options of naju_scan_bwd_ex (initialise with
+ * NAJU_SCAN_BWD_LAYOUT_INIT, then set what differs from naju_scan_bwd; a
+ * stride <= 0 means the contiguous one):
+ *   bc_ld, dbc_ld  as bc_ld / dbc_ld of naju_scan_bwd_strided;
+ *   dg_ld          elements between rows of dfl and dil (D when <= 0);
+ *   dg_dtype       element type of dfl and dil (NAJU_DTYPE_*), or -1 for
+ *                  naju_scan_bwd's (the gates' type, or float32 with
+ *                  NAJU_FLAG_OUT_F32);
+ *   dfl_sum, dil_sum  [D] float32: dfl and dil summed over batch and time,
+ *                  from the float32 values before any rounding to dg_dtype
+ *                  (a bias added to the gate logits gets this gradient);
+ *                  NULL: not formed.
+ * Everything but the defaults is served on the matrix-core path
+ * (9 <= N <= 64) only, with strides that are multiples of 4 and pointers
+ * aligned to four elements; otherwise NAJU_ERR_UNSUPPORTED. */
+typedef struct naju_scan_bwd_layout {
+  int64_t bc_ld;
+  int64_t dbc_ld;
+  int64_t dg_ld;
+  int32_t dg_dtype;
+  int32_t reserved;
+  float* dfl_sum;
+  float* dil_sum;
+} naju_scan_bwd_layout;
+
+#define NAJU_SCAN_BWD_LAYOUT_INIT {0, 0, 0, -1, 0, NULL, NULL}
+
+/* naju_scan_bwd with the output layout above (layout NULL: naju_scan_bwd
+ * itself). The mixer's gate logits are a projection slice plus a
+ * convolution plus a bias: their gradient goes into the projection's
+ * gradient buffer in its 16-bit type (row stride of that buffer), and the
+ * bias gradient comes from the float32 sums, so neither needs a pass of its
+ * own. No reference counterpart (the reference's backends return contiguous
+ * gradients in the inputs' types). */
+int naju_scan_bwd_ex(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                     const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil,
+                     void* dB, void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N,
+                     int x_dtype, int gate_dtype, int bc_dtype, int flags, const naju_scan_bwd_layout* layout,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free forward: naju_scan_fwd with the caller's workspace
  * replaced by a static device array of NAJU_NOALLOC_SCRATCH_BYTES per GPU
  * (each GPU the library runs on holds it until the process ends; its

@@ -16,6 +16,19 @@ FLAG_OUT_F32, FLAG_DETERMINISTIC = 1, 2
 CKPT_SHIFT, CKPT_MASK = 8, 0xFF << 8
 
 
+class ScanBwdLayout(ctypes.Structure):
+    """naju_scan_bwd_layout (include/naju_scan.h); the defaults are
+    NAJU_SCAN_BWD_LAYOUT_INIT's."""
+    _fields_ = [("bc_ld", ctypes.c_int64), ("dbc_ld", ctypes.c_int64), ("dg_ld", ctypes.c_int64),
+                ("dg_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32), ("dfl_sum", ctypes.c_void_p),
+                ("dil_sum", ctypes.c_void_p)]
+
+    def __init__(self, **kw):
+        super().__init__(dg_dtype=-1)
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
 def ckpt_rows_flag(rows):
     """The NAJU_CKPT_ROWS(rows) flag bits (rows a multiple of 16 below 4096;
     0 or None = the default interval)."""
@@ -35,6 +48,7 @@ EXPORTED = (
     "naju_scan_bwd",
     "naju_scan_fwd_strided",
     "naju_scan_bwd_strided",
+    "naju_scan_bwd_ex",
     "naju_scan_workspace_status",
     "naju_scan_fwd_noalloc",
     "naju_scan_noalloc_status",
@@ -115,6 +129,9 @@ def lib():
     L.naju_scan_fwd_strided.restype = I
     L.naju_scan_bwd_strided.argtypes = [P] * 15 + [I64] * 6 + [I] * 4 + [P, SZ, P]
     L.naju_scan_bwd_strided.restype = I
+    # naju_scan_bwd's arguments with a naju_scan_bwd_layout pointer after the flags
+    L.naju_scan_bwd_ex.argtypes = [P] * 15 + [I64] * 4 + [I] * 4 + [P, P, SZ, P]
+    L.naju_scan_bwd_ex.restype = I
     # u, fl, il, B, C, D_skip, h0, y, ckpt, hT, batch, T, D, N, x_dt, g_dt, bc_dt, flags, stream
     L.naju_scan_fwd_noalloc.argtypes = [P] * 10 + [I64] * 4 + [I] * 4 + [P]
     L.naju_scan_fwd_noalloc.restype = I
@@ -165,7 +182,7 @@ def lib():
     L.naju_dwconv_pair_workspace_bytes.restype = SZ
     # x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dw0, db0, dw1, db1, dadd0, dadd1, dadd_ld, batch, T, C, K,
     # accumulate, x_dt, dy_dt, ws, ws_bytes, stream
-    L.naju_dwconv_pair_bwd.argtypes = ([P, I64] + [P] * 5 + [I64] + [P] * 6 + [I64] * 4 + [I] * 4
+    L.naju_dwconv_pair_bwd.argtypes = ([P, I64] + [P] * 4 + [I64, P, I64] + [P] * 6 + [I64] * 4 + [I] * 4
                                        + [P, SZ, P])
     L.naju_dwconv_pair_bwd.restype = I
     L.naju_loss_last_error.argtypes = []

@@ -537,7 +537,7 @@ __global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __res
                                                                  const float* __restrict__ w0,
                                                                  const float* __restrict__ w1,
                                                                  const TDY* __restrict__ dy0,
-                                                                 const TDY* __restrict__ dy1,
+                                                                 const TDY* __restrict__ dy1, int64_t ldy,
                                                                  TX* __restrict__ dx, int64_t ld_dx,
                                                                  TX* __restrict__ dadd0, TX* __restrict__ dadd1,
                                                                  int64_t ld_dadd, float* __restrict__ part0,
@@ -560,8 +560,8 @@ __global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __res
 #pragma unroll
   for (int i = 0; i < NZ; ++i) {
     const int64_t t = tw + i < T ? tw + i : T - 1;
-    g0[i] = ldc(dy0 + (b * T + t) * C + cc);
-    g1[i] = ldc(dy1 + (b * T + t) * C + cc);
+    g0[i] = ldc(dy0 + (b * T + t) * ldy + cc);
+    g1[i] = ldc(dy1 + (b * T + t) * ldy + cc);
   }
 #pragma unroll
   for (int i = 0; i < NX; ++i) {
@@ -1791,23 +1791,24 @@ void pair_fwd_dt(int y_dt, dim3 grid, hipStream_t st, const void* x, int64_t x_l
 
 template <typename TX, typename TDY>
 void pair_bwd_launch(dim3 grid, hipStream_t st, const void* x, int64_t x_ld, const float* w0, const float* w1,
-                     const void* dy0, const void* dy1, void* dx, int64_t dx_ld, void* dadd0, void* dadd1,
-                     int64_t dadd_ld, float* part0, float* part1, int64_t T, int64_t C, int acc) {
+                     const void* dy0, const void* dy1, int64_t dy_ld, void* dx, int64_t dx_ld, void* dadd0,
+                     void* dadd1, int64_t dadd_ld, float* part0, float* part1, int64_t T, int64_t C, int acc) {
   hipLaunchKernelGGL((dwconv4_pair_bwd_vec<TX, TDY>), grid, dim3(64 * kPW), 0, st, (const TX*)x, x_ld, w0, w1,
-                     (const TDY*)dy0, (const TDY*)dy1, (TX*)dx, dx_ld, (TX*)dadd0, (TX*)dadd1, dadd_ld, part0, part1,
-                     T, C, acc);
+                     (const TDY*)dy0, (const TDY*)dy1, dy_ld, (TX*)dx, dx_ld, (TX*)dadd0, (TX*)dadd1, dadd_ld, part0,
+                     part1, T, C, acc);
 }
 
 template <typename TX>
 void pair_bwd_dt(int dy_dt, dim3 grid, hipStream_t st, const void* x, int64_t x_ld, const float* w0,
-                 const float* w1, const void* dy0, const void* dy1, void* dx, int64_t dx_ld, void* dadd0,
-                 void* dadd1, int64_t dadd_ld, float* part0, float* part1, int64_t T, int64_t C, int acc) {
+                 const float* w1, const void* dy0, const void* dy1, int64_t dy_ld, void* dx, int64_t dx_ld,
+                 void* dadd0, void* dadd1, int64_t dadd_ld, float* part0, float* part1, int64_t T, int64_t C,
+                 int acc) {
   if (dy_dt == NAJU_DTYPE_F32 && !std::is_same<TX, float>::value)
-    pair_bwd_launch<TX, float>(grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0, part1,
-                               T, C, acc);
+    pair_bwd_launch<TX, float>(grid, st, x, x_ld, w0, w1, dy0, dy1, dy_ld, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
+                               part1, T, C, acc);
   else
-    pair_bwd_launch<TX, TX>(grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0, part1, T,
-                            C, acc);
+    pair_bwd_launch<TX, TX>(grid, st, x, x_ld, w0, w1, dy0, dy1, dy_ld, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
+                            part1, T, C, acc);
 }
 }  // namespace
 
@@ -1848,7 +1849,7 @@ size_t naju_dwconv_pair_workspace_bytes(int64_t batch, int64_t T, int64_t C, int
 }
 
 int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const float* w1, const void* dy0,
-                         const void* dy1, void* dx, int64_t dx_ld, float* dw0, float* dbias0, float* dw1,
+                         const void* dy1, int64_t dy_ld, void* dx, int64_t dx_ld, float* dw0, float* dbias0, float* dw1,
                          float* dbias1, void* dadd0, void* dadd1, int64_t dadd_ld, int64_t batch, int64_t T,
                          int64_t C, int K, int accumulate, int x_dtype, int dy_dtype, void* workspace,
                          size_t workspace_bytes, void* stream) {
@@ -1858,6 +1859,7 @@ int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const flo
   if (dx && dx_ld < C) return fail(NAJU_ERR_INVALID, "dx_ld (%lld) must be >= C (%lld)", (long long)dx_ld, (long long)C);
   if ((dadd0 || dadd1) && dadd_ld < C)
     return fail(NAJU_ERR_INVALID, "dadd_ld (%lld) must be >= C (%lld)", (long long)dadd_ld, (long long)C);
+  if (dy_ld < C) return fail(NAJU_ERR_INVALID, "dy_ld (%lld) must be >= C (%lld)", (long long)dy_ld, (long long)C);
   if (!dt_ok(x_dtype) || !dt_ok(dy_dtype)) return fail(NAJU_ERR_INVALID, "unknown dtype code");
   if (dy_dtype != x_dtype && dy_dtype != NAJU_DTYPE_F32)
     return fail(NAJU_ERR_UNSUPPORTED, "dy must have x's dtype or float32");
@@ -1873,7 +1875,7 @@ int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const flo
     return NAJU_OK;
   }
   if (!x || !w0 || !w1 || !dy0 || !dy1) return fail(NAJU_ERR_INVALID, "null pointer (x, weights and dy are required)");
-  if (!pair_ok(T, C, K, {x_ld, dx ? dx_ld : C, (dadd0 || dadd1) ? dadd_ld : C},
+  if (!pair_ok(T, C, K, {x_ld, dy_ld, dx ? dx_ld : C, (dadd0 || dadd1) ? dadd_ld : C},
                {x, w0, w1, dy0, dy1, dx, dadd0, dadd1}))
     return fail(NAJU_ERR_UNSUPPORTED,
                 "the pair kernels need K = 4, C and the row strides multiples of 8 and 16-byte aligned pointers");
@@ -1888,14 +1890,14 @@ int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const flo
   const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)ntb, (unsigned)batch);
   const int acc = accumulate ? 1 : 0;
   if (x_dtype == NAJU_DTYPE_BF16)
-    pair_bwd_dt<bf16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
-                        part1, T, C, acc);
+    pair_bwd_dt<bf16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dy_ld, dx, dx_ld, dadd0, dadd1, dadd_ld,
+                        part0, part1, T, C, acc);
   else if (x_dtype == NAJU_DTYPE_F16)
-    pair_bwd_dt<f16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
-                       part1, T, C, acc);
+    pair_bwd_dt<f16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dy_ld, dx, dx_ld, dadd0, dadd1, dadd_ld,
+                       part0, part1, T, C, acc);
   else
-    pair_bwd_dt<float>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dx, dx_ld, dadd0, dadd1, dadd_ld, part0,
-                       part1, T, C, acc);
+    pair_bwd_dt<float>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dy_ld, dx, dx_ld, dadd0, dadd1, dadd_ld,
+                       part0, part1, T, C, acc);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   const int64_t nblk = batch * ntb;

@@ -909,15 +909,22 @@ __device__ __forceinline__ float sum_parts(const float* __restrict__ p, int n_pa
 // identical), in one launch:
 //   blocks [0, n_bc_blocks): dB, dC [i] = sum over the channel tiles q of
 //     partB/partC[q*btn + i] (consecutive threads read consecutive i);
-//   blocks [n_bc_blocks, ...): dD[d] = sum over the n_rows rows of
-//     partD[row][d], 64 channels per block; wave w of 16 sums rows
-//     w, w+16, ... (32 loads in flight) with four interleaved
-//     accumulators, then the 16 wave sums are added in wave order.
+//   blocks [n_bc_blocks, ...): per-channel vectors v = 0 .. n_vec-1 (dD,
+//     and the gate gradients' sums when asked for), ceil(D / 64) blocks
+//     each: out_v[d] = sum over the n_rows rows of part_v[row][d], 64
+//     channels per block; wave w of 16 sums rows w, w+16, ... (32 loads in
+//     flight) with four interleaved accumulators, then the 16 wave sums are
+//     added in wave order.
+struct FoldVecs {
+  const float* part[3];
+  float* out[3];
+  int n;
+};
+
 __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ partB,
                                                     const float* __restrict__ partC, int n_parts, int64_t btn,
-                                                    void* dB, void* dC, int bc_dt, int n_bc_blocks,
-                                                    const float* __restrict__ partD, int64_t n_rows, int64_t D,
-                                                    float* __restrict__ dD, int bc_split, int64_t N,
+                                                    void* dB, void* dC, int bc_dt, int n_bc_blocks, FoldVecs fv,
+                                                    int64_t n_rows, int64_t D, int bc_split, int64_t N,
                                                     int64_t ld_out) {
   // entry i of the [batch * T][N] sums lands at row i / N, column i % N of
   // dB / dC, whose rows are ld_out elements apart
@@ -1019,7 +1026,15 @@ __global__ __launch_bounds__(1024) void fold_kernel(const float* __restrict__ pa
     return;
   }
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t d = (int64_t)(blockIdx.x - n_bc_blocks) * 64 + lane;
+  const int64_t per_vec = (D + 63) / 64;
+  const int64_t bi = (int64_t)blockIdx.x - n_bc_blocks;
+  const int vi = (int)(bi / per_vec);
+  if (vi >= fv.n) return;
+  // (selected, not indexed: a dynamic index into the argument would go
+  // through scratch memory)
+  const float* __restrict__ partD = vi == 0 ? fv.part[0] : (vi == 1 ? fv.part[1] : fv.part[2]);
+  float* __restrict__ dD = vi == 0 ? fv.out[0] : (vi == 1 ? fv.out[1] : fv.out[2]);
+  const int64_t d = (bi - vi * per_vec) * 64 + lane;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (d < D) {
     // 32 rows of a wave in flight per round: at N = 1 a wave's whole share
@@ -2294,7 +2309,7 @@ struct Layout {
   int V, CH, L, K, n_dtiles, n_tiles;
   int nseg, seg_sc;  // N > 1: time segments
   int ck_rows;       // the forward's checkpoint interval
-  size_t off_agg, off_incl, off_partB, off_partC, off_partD, off_segF, off_segZ, off_seg0, off_dense, total;
+  size_t off_agg, off_incl, off_partB, off_partC, off_partD, off_partG, off_segF, off_segZ, off_seg0, off_dense, total;
 };
 
 // N > 1: enough time segments that about kGnTargetWgs workgroups run per
@@ -2393,6 +2408,9 @@ void place_regions(Layout& l, int64_t batch, int64_t T, int64_t D, int64_t N, bo
   off = align_up(off + part_bc);
   l.off_partD = off;
   off = align_up(off + (bwd ? (size_t)batch * (N == 1 ? l.K : l.nseg) * D * sizeof(float) : 0));
+  // the matrix-core backward's per-segment sums of dfl and dil (when asked for)
+  l.off_partG = off;
+  off = align_up(off + (bwd && N > 1 && use_mc(N, true) ? (size_t)2 * batch * l.nseg * D * sizeof(float) : 0));
   const size_t seg_units = l.nseg > 1 ? (size_t)batch * l.nseg * D : 0;
   l.off_segF = off;
   off = align_up(off + seg_units * sizeof(float));
@@ -2911,11 +2929,32 @@ int naju_scan_fwd_noalloc(const void* u, const void* f_logit, const void* i_logi
                        bc_dtype, flags, ws, kScratchBytes, stream, kScratchBytes, N);
 }
 
+// The gate-gradient options of naju_scan_bwd_ex: dfl / dil rows ldg apart in
+// dg_req (-1: the default type), their sums over batch and time. Served on
+// the matrix-core path (9 <= N <= 64); a stride other than D needs a
+// multiple of 4 and pointers aligned to four elements.
+int check_gate_ext(const void* dfl, const void* dil, int64_t N, int64_t D, int64_t ldg, int dg_req, int dg_dt,
+                   bool sums) {
+  if (ldg == D && dg_req < 0 && !sums) return NAJU_OK;
+  if (N <= 1 || !use_mc(N, true))
+    return fail(NAJU_ERR_UNSUPPORTED, "gate-gradient strides, types and sums are served at 9 <= N <= 64");
+  if (ldg < D) return fail(NAJU_ERR_INVALID, "dfl / dil row stride (%lld) must be >= D (%lld)", (long long)ldg,
+                           (long long)D);
+  if (ldg > (1 << 24)) return fail(NAJU_ERR_UNSUPPORTED, "dfl / dil row stride (%lld) above 2^24", (long long)ldg);
+  if (dg_req >= 0 && !dt_ok(dg_req)) return fail(NAJU_ERR_INVALID, "unknown dtype code %d", dg_req);
+  const size_t a4 = 4 * dsize(dg_dt);
+  if (ldg != D && (ldg % 4 || (dfl && !aligned(dfl, a4)) || (dil && !aligned(dil, a4))))
+    return fail(NAJU_ERR_UNSUPPORTED, "strided dfl / dil need a row stride that is a multiple of 4 and %zu-byte "
+                "aligned pointers", a4);
+  return NAJU_OK;
+}
+
 static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
                          const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil,
                          void* dB, void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N,
                          int x_dtype, int gate_dtype, int bc_dtype, int flags, void* workspace,
-                         size_t workspace_bytes, void* stream, int64_t ldbc, int64_t lddbc) {
+                         size_t workspace_bytes, void* stream, int64_t ldbc, int64_t lddbc, int64_t ldg = -1,
+                         int dg_req = -1, float* dfl_sum = nullptr, float* dil_sum = nullptr) {
   g_err[0] = 0;
   int rc = check_common(batch, T, D, N, x_dtype, gate_dtype, bc_dtype);
   if (rc) return rc;
@@ -2924,6 +2963,10 @@ static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit
     return rc;
   if (lddbc != N && batch * T > 0 && D == 0)
     return fail(NAJU_ERR_UNSUPPORTED, "strided dB / dC need D > 0");
+  if (ldg < 0) ldg = D;
+  // the type dfl and dil are written in
+  const int dg_dt = dg_req >= 0 ? dg_req : ((flags & NAJU_FLAG_OUT_F32) ? (int)NAJU_DTYPE_F32 : gate_dtype);
+  if ((rc = check_gate_ext(dfl, dil, N, D, ldg, dg_req, dg_dt, dfl_sum || dil_sum))) return rc;
   if (flags & ~(NAJU_FLAG_OUT_F32 | NAJU_FLAG_DETERMINISTIC | NAJU_CKPT_MASK))
     return fail(NAJU_ERR_INVALID, "unknown flag bits 0x%x", flags);
   const int ck_rows = ckpt_rows(flags, N);
@@ -2935,6 +2978,10 @@ static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit
   if (batch == 0 || T == 0 || D == 0) {
     // Gradients of an empty scan: the reductions over the empty axes are 0.
     if (dD) hipLaunchKernelGGL(fill_kernel, dim3(small_grid(D)), dim3(256), 0, st, dD, (const float*)nullptr, D);
+    if (dfl_sum)
+      hipLaunchKernelGGL(fill_kernel, dim3(small_grid(D)), dim3(256), 0, st, dfl_sum, (const float*)nullptr, D);
+    if (dil_sum)
+      hipLaunchKernelGGL(fill_kernel, dim3(small_grid(D)), dim3(256), 0, st, dil_sum, (const float*)nullptr, D);
     if (dh0)
       hipLaunchKernelGGL(fill_kernel, dim3(small_grid(batch * D * N)), dim3(256), 0, st, dh0,
                          (const float*)nullptr, batch * D * N);
@@ -2977,9 +3024,11 @@ static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit
   a.partB = dB ? (float*)(ws + l.off_partB) : nullptr;
   a.partC = dC ? (float*)(ws + l.off_partC) : nullptr;
   a.partD = dD ? (float*)(ws + l.off_partD) : nullptr;
+  a.partG = (dfl_sum || dil_sum) ? (float*)(ws + l.off_partG) : nullptr;
   a.T = T;
   a.D = D;
   a.ldbc = ldbc;
+  a.ldg = ldg;
   a.N = (int)N;
   a.batch = (int)batch;
   a.bc_dt = bc_dtype;
@@ -2988,7 +3037,6 @@ static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit
   a.K = l.K;
   if (N > 1) {
     const int du_dt = out_f32 ? (int)NAJU_DTYPE_F32 : x_dtype;
-    const int dg_dt = out_f32 ? (int)NAJU_DTYPE_F32 : gate_dtype;
     a.nseg = l.nseg;
     a.seg_sc = l.seg_sc;
     a.segF = (float*)(ws + l.off_segF);
@@ -3054,7 +3102,7 @@ static int scan_bwd_impl(const void* u, const void* f_logit, const void* i_logit
     if (rc) return rc;
   }
 fold:
-  if (dB || dC || dD) {
+  if (dB || dC || dD || a.partG) {
     const int64_t btn = batch * T * N;
     // enough workgroups for about one pass of the threads over the entries
     // (four per thread when btn % 4 == 0), at most 1024
@@ -3065,10 +3113,20 @@ fold:
     const int bc_split = btn % 4 == 0 && n_plain < 128 ? 1 : 0;
     const int64_t n_bc64 = bc_split ? (btn / 4 + 63) / 64 : (n_plain < 1024 ? n_plain : 1024);
     const int n_bc = (dB || dC) ? (int)n_bc64 : 0;
-    const int n_d = dD ? (int)((D + 63) / 64) : 0;
+    const int64_t n_rows = batch * (int64_t)(N == 1 ? l.K : l.nseg);
+    FoldVecs fv{};
+    auto add_vec = [&](const float* part, float* out) {
+      fv.part[fv.n] = part;
+      fv.out[fv.n] = out;
+      ++fv.n;
+    };
+    if (dD) add_vec(a.partD, dD);
+    if (dfl_sum) add_vec(a.partG, dfl_sum);
+    if (dil_sum) add_vec(a.partG + n_rows * D, dil_sum);
+    const int n_d = fv.n * (int)((D + 63) / 64);
     hipLaunchKernelGGL(fold_kernel, dim3((unsigned)(n_bc + n_d)), dim3(1024), 0, st, a.partB, a.partC, l.n_dtiles,
-                       btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, a.partD,
-                       batch * (int64_t)(N == 1 ? l.K : l.nseg), D, dD, bc_split, N, lddbc);
+                       btn, dB, dC, out_f32 ? (int)NAJU_DTYPE_F32 : bc_dtype, n_bc, fv, n_rows, D, bc_split, N,
+                       lddbc);
     if (hipGetLastError() != hipSuccess) return fail(NAJU_ERR_LAUNCH, "fold launch failed");
   }
   return NAJU_OK;
@@ -3090,6 +3148,21 @@ int naju_scan_bwd_strided(const void* u, const void* f_logit, const void* i_logi
                           void* workspace, size_t workspace_bytes, void* stream) {
   return scan_bwd_impl(u, f_logit, i_logit, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N,
                        x_dtype, gate_dtype, bc_dtype, flags, workspace, workspace_bytes, stream, bc_ld, dbc_ld);
+}
+
+int naju_scan_bwd_ex(const void* u, const void* f_logit, const void* i_logit, const void* B, const void* C,
+                     const float* D_skip, const float* ckpt, const void* dy, void* du, void* dfl, void* dil,
+                     void* dB, void* dC, float* dD, float* dh0, int64_t batch, int64_t T, int64_t D, int64_t N,
+                     int x_dtype, int gate_dtype, int bc_dtype, int flags, const naju_scan_bwd_layout* layout,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!layout) return naju_scan_bwd(u, f_logit, i_logit, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0,
+                                    batch, T, D, N, x_dtype, gate_dtype, bc_dtype, flags, workspace,
+                                    workspace_bytes, stream);
+  const naju_scan_bwd_layout& o = *layout;
+  return scan_bwd_impl(u, f_logit, i_logit, B, C, D_skip, ckpt, dy, du, dfl, dil, dB, dC, dD, dh0, batch, T, D, N,
+                       x_dtype, gate_dtype, bc_dtype, flags, workspace, workspace_bytes, stream,
+                       o.bc_ld > 0 ? o.bc_ld : N, o.dbc_ld > 0 ? o.dbc_ld : N, o.dg_ld > 0 ? o.dg_ld : D,
+                       o.dg_dtype, o.dfl_sum, o.dil_sum);
 }
 
 int naju_scan_workspace_status(const void* workspace, void* stream, uint32_t* status) {

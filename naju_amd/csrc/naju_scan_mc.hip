@@ -962,6 +962,7 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
   }
   float Fseg = 1.f;
   float dDacc[4] = {0.f, 0.f, 0.f, 0.f};
+  float sgf = 0.f, sgi = 0.f;  // dfl, dil summed over this lane's rows (channel j)
 
   float (*Tf)[TP] = sh.gate[wv][0];
   float (*Tdy)[TP] = sh.gate[wv][1];
@@ -1355,6 +1356,8 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         const float dil = (1.f - i_o) * (dws * w_o);
         q1[r] = pfdy[r];
         q2[r] = w_o * pe[r];
+        sgf += dfl;
+        sgi += dil;
         Tf[j][4 * r + g] = dfl;
         Ti[j][4 * r + g] = du;
         Tw[j][4 * r + g] = dil;
@@ -1372,19 +1375,25 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
         const int64_t ob = ((int64_t)b * T + t0) * D;  // uniform
         const uint32_t o = (uint32_t)(rho * D + dw + cq);
         void* du_p = a.du ? (char*)a.du + ob * (du_dt == NAJU_DTYPE_F32 ? 4 : 2) : nullptr;
+        // dfl, dil: rows a.ldg elements apart, in dg_dt
+        const int64_t obg = ((int64_t)b * T + t0) * a.ldg;  // uniform
+        const uint32_t og = (uint32_t)(rho * a.ldg + dw + cq);
         const int gsz = dg_dt == NAJU_DTYPE_F32 ? 4 : 2;
-        void* dfl_p = a.dfl ? (char*)a.dfl + ob * gsz : nullptr;
-        void* dil_p = a.dil ? (char*)a.dil + ob * gsz : nullptr;
+        void* dfl_p = a.dfl ? (char*)a.dfl + obg * gsz : nullptr;
+        void* dil_p = a.dil ? (char*)a.dil + obg * gsz : nullptr;
         if (du_p) {
           if (du_dt == NAJU_DTYPE_F32) store_row4<float>(du_p, o, Ti, cq, rho, vec, ncq);
           else store_row4<TU>(du_p, o, Ti, cq, rho, vec, ncq);
         }
         if (dg_dt == NAJU_DTYPE_F32) {
-          if (dfl_p) store_row4<float>(dfl_p, o, Tf, cq, rho, vec, ncq);
-          if (dil_p) store_row4<float>(dil_p, o, Tw, cq, rho, vec, ncq);
+          if (dfl_p) store_row4<float>(dfl_p, og, Tf, cq, rho, vec, ncq);
+          if (dil_p) store_row4<float>(dil_p, og, Tw, cq, rho, vec, ncq);
+        } else if (dg_dt == NAJU_DTYPE_BF16) {
+          if (dfl_p) store_row4<bf16_t>(dfl_p, og, Tf, cq, rho, vec, ncq);
+          if (dil_p) store_row4<bf16_t>(dil_p, og, Tw, cq, rho, vec, ncq);
         } else {
-          if (dfl_p) store_row4<TG>(dfl_p, o, Tf, cq, rho, vec, ncq);
-          if (dil_p) store_row4<TG>(dil_p, o, Tw, cq, rho, vec, ncq);
+          if (dfl_p) store_row4<f16_t>(dfl_p, og, Tf, cq, rho, vec, ncq);
+          if (dil_p) store_row4<f16_t>(dil_p, og, Tw, cq, rho, vec, ncq);
         }
       }
       // ---- dC^T [n][t] and dB^T [n][t] per 16-entry tile of n (channel part:
@@ -1537,6 +1546,19 @@ __global__ __launch_bounds__(64 * kMcWB) void mc_bwd_kernel(const ScanArgs a, in
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (e < ncq) a.partD[((int64_t)b * a.nseg + seg) * D + dw + cq + e] = dDacc[e];
+    }
+    // the gate gradients' sums of the segment: channel j's four lane groups
+    // added (groups 0 + 1, 2 + 3, then the pairs)
+    if (a.partG) {
+      sgf += __shfl_xor(sgf, 16, 64);
+      sgi += __shfl_xor(sgi, 16, 64);
+      sgf += __shfl_xor(sgf, 32, 64);
+      sgi += __shfl_xor(sgi, 32, 64);
+      if (g == 0 && dok) {
+        const int64_t o = ((int64_t)b * a.nseg + seg) * D + d;
+        a.partG[o] = sgf;
+        a.partG[(int64_t)a.batch * a.nseg * D + o] = sgi;
+      }
     }
   }
 }

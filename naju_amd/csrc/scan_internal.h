@@ -96,6 +96,8 @@ struct ScanArgs {
   int64_t T;
   int64_t D;
   int64_t ldbc;  // elements between rows of B and C (N unless strided; the matrix-core path only)
+  int64_t ldg;   // elements between rows of dfl and dil (D unless strided; the matrix-core backward only)
+  float* partG;  // [2][batch * nseg][D]: per-segment sums of dfl, dil (matrix-core backward; NULL: none)
   int N;
   int batch;
   int bc_dt;

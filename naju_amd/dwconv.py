@@ -157,13 +157,56 @@ def dwconv(x, weight, bias=None, add=None, silu=False, out_dtype=None):
     return _DwConv.apply(x, w, bias, add, bool(silu), out_dtype, x_sink, add_sink, x_acc)
 
 
+class GateGrads:
+    """Hand-off of the two gate logits' gradients from the scan's backward
+    to the gate pair's backward (naju_amd.scan.naju_scan_hip(...,
+    gate_grads=)). The logits are add + bias + conv(x) with the adds pieces of
+    one gradsink.split (the mixer's projection output), so their gradients
+    are the adds' gradients: the scan writes them straight into the split's
+    gradient buffer in its type and row stride (naju_scan_bwd_ex), with
+    their float32 sums over batch and time (the biases' gradients). Autograd
+    then carries zero-stride markers in their place; the pair's backward
+    reads the buffer slices as its dy, writes no adds' gradients of its own,
+    and takes the sums as the biases' gradients. A scan backward that cannot
+    serve this returns ordinary gradients, and the pair's backward runs as
+    usual."""
+
+    def __init__(self, sinks, C):
+        self.sinks, self.C = sinks, C
+        self._result = None
+        self._markers = None
+
+    def targets(self):
+        """The two buffer slices the scan writes (the adds' gradients)."""
+        (s0, c0), (s1, c1) = self.sinks
+        return s0.slice(c0, self.C), s1.slice(c1, self.C)
+
+    def hand_over(self, g0, g1, sum0, sum1, shape, dtype0, dtype1):
+        """Record what the scan wrote; returns the markers for autograd."""
+        dev = g0.device
+        self._result = (g0, g1, sum0, sum1)
+        self._markers = (torch.zeros((), dtype=dtype0, device=dev).expand(shape),
+                         torch.zeros((), dtype=dtype1, device=dev).expand(shape))
+        return self._markers
+
+    def take(self, dy0, dy1):
+        """The scan's result when dy0, dy1 are its markers (taken once),
+        else None."""
+        r, m = self._result, self._markers
+        if r is None or not all(d.data_ptr() == k.data_ptr() and all(st == 0 for st in d.stride())
+                                for d, k in zip((dy0, dy1), m)):
+            return None
+        self._result = self._markers = None
+        return r
+
+
 class _DwConvPair(torch.autograd.Function):
     """The mixer's two gate convolutions over one input in one pass each way
     (naju_dwconv_pair_fwd / _bwd): y0 = add0 + b0 + conv(x, w0), y1 = add1 +
     b1 + conv(x, w1); x's gradient from both formed with one rounding."""
 
     @staticmethod
-    def forward(ctx, x, w0, b0, add0, w1, b1, add1, out_dtype, sinks, x_acc):
+    def forward(ctx, x, w0, b0, add0, w1, b1, add1, out_dtype, sinks, x_acc, gate_grads):
         B, T, C = x.shape
         K = w0.shape[1]
         ldx, ld_add = x.stride(1), add0.stride(1)
@@ -176,7 +219,7 @@ class _DwConvPair(torch.autograd.Function):
             B, T, C, K, _DT[x.dtype], _DT[out_dtype], stream))
         ctx.save_for_backward(x, w0, w1)
         ctx.has_b = (b0 is not None, b1 is not None)
-        ctx.sinks, ctx.x_acc = sinks, x_acc
+        ctx.sinks, ctx.x_acc, ctx.gate_grads = sinks, x_acc, gate_grads
         return y0, y1
 
     @staticmethod
@@ -184,10 +227,16 @@ class _DwConvPair(torch.autograd.Function):
         x, w0, w1 = ctx.saved_tensors
         B, T, C = x.shape
         K = w0.shape[1]
-        if dy1.dtype != dy0.dtype:
-            dy0, dy1 = dy0.float(), dy1.float()
-        dy0, dy1 = dy0.contiguous(), dy1.contiguous()
         need = ctx.needs_input_grad
+        gg = ctx.gate_grads.take(dy0, dy1) if ctx.gate_grads is not None else None
+        if gg is not None:
+            # the scan wrote dy0, dy1 as the adds' gradients into the split's
+            # buffer and summed them for the biases
+            dy0, dy1, gs0, gs1 = gg
+        else:
+            if dy1.dtype != dy0.dtype:
+                dy0, dy1 = dy0.float(), dy1.float()
+            dy0, dy1 = dy0.contiguous(), dy1.contiguous()
         dx = dx_ret = None
         acc = 0
         if need[0]:
@@ -199,25 +248,36 @@ class _DwConvPair(torch.autograd.Function):
                 dx = torch.empty((B, T, C), dtype=x.dtype, device=x.device)
         f32 = dict(dtype=torch.float32, device=x.device)
         dw0 = torch.empty((C, K), **f32) if need[1] else None
-        db0 = torch.empty((C,), **f32) if need[2] and ctx.has_b[0] else None
         dw1 = torch.empty((C, K), **f32) if need[4] else None
-        db1 = torch.empty((C,), **f32) if need[5] and ctx.has_b[1] else None
-        # the adds' gradients are dy0, dy1: written into the split's buffer
-        # in x's dtype (pair_supported checked that the adds are pieces of
-        # one gradsink.split with x's dtype)
-        (s0, col0), (s1, col1) = ctx.sinks
-        dadd0 = s0.slice(col0, C) if need[3] else None
-        dadd1 = s1.slice(col1, C) if need[6] else None
-        ld_dadd = (dadd0 if dadd0 is not None else dadd1).stride(1) if (dadd0 is not None or dadd1 is not None) else C
+        if gg is not None:
+            db0 = gs0 if need[2] and ctx.has_b[0] else None
+            db1 = gs1 if need[5] and ctx.has_b[1] else None
+            # already in the split's buffer: returned as they are, not written
+            dadd0 = dy0 if need[3] else None
+            dadd1 = dy1 if need[6] else None
+            wr0 = wr1 = wb0 = wb1 = None
+            ld_dadd = C
+        else:
+            db0 = torch.empty((C,), **f32) if need[2] and ctx.has_b[0] else None
+            db1 = torch.empty((C,), **f32) if need[5] and ctx.has_b[1] else None
+            # the adds' gradients are dy0, dy1: written into the split's
+            # buffer in x's dtype (pair_supported checked that the adds are
+            # pieces of one gradsink.split with x's dtype)
+            (s0, col0), (s1, col1) = ctx.sinks
+            dadd0 = s0.slice(col0, C) if need[3] else None
+            dadd1 = s1.slice(col1, C) if need[6] else None
+            wr0, wr1, wb0, wb1 = dadd0, dadd1, db0, db1
+            ld_dadd = (dadd0 if dadd0 is not None else dadd1).stride(1) if (dadd0 is not None
+                                                                           or dadd1 is not None) else C
         L = _lib.lib()
         stream = torch.cuda.current_stream(x.device).cuda_stream
         nbytes = L.naju_dwconv_pair_workspace_bytes(B, T, C, K)
         ws = _WS.get(x.device, stream, nbytes)
         _lib.check_mixer(L.naju_dwconv_pair_bwd(
-            _ptr(x), x.stride(1), _ptr(w0), _ptr(w1), _ptr(dy0), _ptr(dy1), _ptr(dx),
-            dx.stride(1) if dx is not None else C, _ptr(dw0), _ptr(db0), _ptr(dw1), _ptr(db1), _ptr(dadd0),
-            _ptr(dadd1), ld_dadd, B, T, C, K, acc, _DT[x.dtype], _DT[dy0.dtype], _ptr(ws), ws.numel(), stream))
-        return (dx if dx_ret is None else dx_ret, dw0, db0, dadd0, dw1, db1, dadd1, None, None, None)
+            _ptr(x), x.stride(1), _ptr(w0), _ptr(w1), _ptr(dy0), _ptr(dy1), dy0.stride(1), _ptr(dx),
+            dx.stride(1) if dx is not None else C, _ptr(dw0), _ptr(wb0), _ptr(dw1), _ptr(wb1), _ptr(wr0),
+            _ptr(wr1), ld_dadd, B, T, C, K, acc, _DT[x.dtype], _DT[dy0.dtype], _ptr(ws), ws.numel(), stream))
+        return (dx if dx_ret is None else dx_ret, dw0, db0, dadd0, dw1, db1, dadd1, None, None, None, None)
 
 
 def pair_supported(x, w0, add0, w1, add1):
@@ -240,10 +300,12 @@ def pair_supported(x, w0, add0, w1, add1):
     return True
 
 
-def dwconv_pair(x, w0, b0, add0, w1, b1, add1, out_dtype):
+def dwconv_pair(x, w0, b0, add0, w1, b1, add1, out_dtype, gate_grads=False):
     """(add0 + b0 + conv(x, w0), add1 + b1 + conv(x, w1)) in one pass each
     way, for what pair_supported accepts: the two gate logits of the mixer,
-    each as dwconv(x, w, b, add=add, out_dtype=out_dtype) computes it."""
+    each as dwconv(x, w, b, add=add, out_dtype=out_dtype) computes it.
+    gate_grads=True returns (y0, y1, GateGrads) for the logits' consumer
+    (naju_scan_hip(..., gate_grads=)) to hand their gradients over."""
     C = x.shape[2]
     ws = []
     for w in (w0, w1):
@@ -253,5 +315,7 @@ def dwconv_pair(x, w0, b0, add0, w1, b1, add1, out_dtype):
     x_acc = acc_sink_of(x)
     if x_acc is not None and x.stride(1) != C:
         x_acc = None
-    return _DwConvPair.apply(x, ws[0], bs[0], add0, ws[1], bs[1], add1, out_dtype,
-                             (sink_of(add0), sink_of(add1)), x_acc)
+    sinks = (sink_of(add0), sink_of(add1))
+    gg = GateGrads(sinks, C) if gate_grads else None
+    y0, y1 = _DwConvPair.apply(x, ws[0], bs[0], add0, ws[1], bs[1], add1, out_dtype, sinks, x_acc, gg)
+    return (y0, y1, gg) if gate_grads else (y0, y1)

@@ -215,6 +215,7 @@ class NajuMixer(nn.Module):
             h_g, h_f, h_i, h_s, h_r = gradsink.fanout(h, 5)
         else:
             h_g = h_f = h_i = h_s = h_r = h
+        gate_grads = None
         if h.is_cuda and not self.gate_rank:
             # f_proj, i_proj and x_proj in one GEMM over h (the same weights:
             # each output column is the same product), so h's gradient from
@@ -224,9 +225,12 @@ class NajuMixer(nn.Module):
             w = (self.f_proj.weight, self.i_proj.weight, self.x_proj.weight)
             p_f, p_i, Bm, Cm = gradsink.split(_linear_cat(h_g, w), [di, di, N, N])
             if pair and pair_supported(h_f, self.f_conv.weight, p_f, self.i_conv.weight, p_i):
-                f_logit, i_logit = dwconv_pair(
+                # with the HIP scan, the logits' gradients come back through
+                # gate_grads (written in place by the scan's backward)
+                f_logit, i_logit, *gg = dwconv_pair(
                     h_f, self.f_conv.weight, self.f_bias, p_f, self.i_conv.weight, self.i_bias, p_i,
-                    out_dtype=torch.promote_types(_out_dtype(h), self.f_bias.dtype))
+                    out_dtype=torch.promote_types(_out_dtype(h), self.f_bias.dtype), gate_grads=fold)
+                gate_grads = gg[0] if gg else None
             else:
                 f_logit = self._gate_logit(h_f, None, self.f_conv, self.f_bias, p=p_f)
                 i_logit = self._gate_logit(h_i, None, self.i_conv, self.i_bias, p=p_i)
@@ -237,7 +241,7 @@ class NajuMixer(nn.Module):
         # the scan reads out the state only; the D skip is applied here
         if fold:
             cx = naju_scan_hip(h_s, f_logit, i_logit, Bm, Cm, self.D_zero,
-                               du_skip=self.D.detach() * (1.0 / self._cx_scale))
+                               du_skip=self.D.detach() * (1.0 / self._cx_scale), gate_grads=gate_grads)
         else:
             cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
         if h.is_cuda:

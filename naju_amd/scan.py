@@ -38,6 +38,7 @@ never modified. ``y`` has u's dtype (the convention of the GPU training
 backends, chunk_triton.py:181 and chunk_affine_triton.py:288); each gradient
 has its input's dtype. Arithmetic and state are float32.
 """
+import ctypes
 import os
 
 import torch
@@ -209,7 +210,8 @@ class NajuScanHip(torch.autograd.Function):
     """Autograd wrapper of naju_scan_fwd / naju_scan_bwd (include/naju_scan.h)."""
 
     @staticmethod
-    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False, ckpt_rows=0, du_skip=None):
+    def forward(ctx, u, f_logit, i_logit, B, C, D_skip, h0=None, want_hT=False, ckpt_rows=0, du_skip=None,
+                gate_grads=None):
         Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
         out_dtype = u.dtype
         b_sinks = (sink_of(B), sink_of(C))
@@ -259,6 +261,9 @@ class NajuScanHip(torch.autograd.Function):
             # buffer when it is the first gradient there
             ctx.u_acc = acc_sink_of(u) if u_ is u else None
             ctx.bc_ld = bc_ld
+            # the gate logits' gradients may go straight to their consumer
+            # (naju_amd.dwconv.GateGrads: the gate convolutions' backward)
+            ctx.gate_grads = gate_grads
             # B and C are pieces of one gradsink.split (the mixer's
             # projection output): dB and dC can go straight into its buffer
             s0, s1 = b_sinks
@@ -284,8 +289,18 @@ class NajuScanHip(torch.autograd.Function):
                 du_ret = ctx.u_acc.marker()
             else:
                 du = torch.empty_like(u_)
-        dfl = torch.empty_like(fl_) if ng[1] else None
-        dil = torch.empty_like(il_) if ng[2] else None
+        # both gate gradients into the projection gradient buffer the gate
+        # logits' consumer names (its type and row stride), with the float32
+        # sums of both (the gate biases' gradients), on the matrix-core path
+        gg = getattr(ctx, "gate_grads", None)
+        gtgt = gg.targets() if (gg is not None and ng[1] and ng[2] and 8 < N <= 64
+                                and not (flags & _lib.FLAG_OUT_F32)) else None
+        if gtgt is not None:
+            dfl, dil = gtgt
+            gsum = torch.empty((2, D), dtype=torch.float32, device=dev)
+        else:
+            dfl = torch.empty_like(fl_) if ng[1] else None
+            dil = torch.empty_like(il_) if ng[2] else None
         dB = dC = None
         dbc_ld = N
         if ctx.bc_ld != N and (ng[3] or ng[4]):
@@ -312,7 +327,14 @@ class NajuScanHip(torch.autograd.Function):
         stream = _stream_handle(dev)
         _raise_pending(dev, stream)
         ws = _WS.get(dev, stream, L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags))
-        if ctx.bc_ld != N or dbc_ld != N:
+        if gtgt is not None:
+            lay = _lib.ScanBwdLayout(bc_ld=ctx.bc_ld, dbc_ld=dbc_ld, dg_ld=dfl.stride(1), dg_dtype=_DT[dfl.dtype],
+                                     dfl_sum=gsum.data_ptr(), dil_sum=gsum.data_ptr() + 4 * D)
+            _lib.check(L.naju_scan_bwd_ex(
+                _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_b), _ptr(ckpt), _ptr(dy),
+                _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
+                Bsz, T, D, N, *dts, flags, ctypes.byref(lay), ws.data_ptr(), ws.numel(), stream))
+        elif ctx.bc_ld != N or dbc_ld != N:
             _lib.check(L.naju_scan_bwd_strided(
                 _ptr(u_), _ptr(fl_), _ptr(il_), _ptr(B_), _ptr(C_), _ptr(D_b), _ptr(ckpt), _ptr(dy),
                 _ptr(du), _ptr(dfl), _ptr(dil), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dh0),
@@ -326,10 +348,13 @@ class NajuScanHip(torch.autograd.Function):
             _watch_status(dev, stream, ws)
         _check_status(dev)
         grads = [du, dfl, dil, dB, dC, dD]
+        if gtgt is not None:
+            # the consumer takes them from gg; autograd carries markers
+            grads[1], grads[2] = gg.hand_over(dfl, dil, gsum[0], gsum[1], fl_.shape, in_dtypes[1], in_dtypes[2])
         grads = [g if g is None or g.dtype == dt else g.to(dt) for g, dt in zip(grads, in_dtypes)]
         if du_ret is not None:
             grads[0] = du_ret
-        return (*grads, dh0, None, None, None)
+        return (*grads, dh0, None, None, None, None)
 
 
 def _default_ckpt_rows(N):
@@ -342,7 +367,7 @@ def _default_ckpt_rows(N):
 
 
 def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state=False, ckpt_rows=None,
-                  du_skip=None):
+                  du_skip=None, gate_grads=None):
     """y = scan(u, f_logit, i_logit, B, C, D_skip[, h0]) on the GPU (see module
     doc); (y, hT) with return_final_state=True. ckpt_rows: the checkpoint
     interval kept for the backward (None = NAJU_CKPT_ROWS from the
@@ -359,7 +384,7 @@ def naju_scan_hip(u, f_logit, i_logit, B, C, D_skip, h0=None, return_final_state
     if ckpt_rows is None:
         ckpt_rows = _default_ckpt_rows(B.shape[-1])
     return NajuScanHip.apply(u, f_logit, i_logit, B, C, D_skip, h0, bool(return_final_state), int(ckpt_rows),
-                             du_skip)
+                             du_skip, gate_grads)
 
 
 def resolve_backend(backend=None):

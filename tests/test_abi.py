@@ -457,3 +457,22 @@ def test_strided_bc_rejections():
     assert fwd(16, 34) == _lib.ERR_UNSUPPORTED
     assert fwd(16, 36, B=260) == _lib.ERR_UNSUPPORTED
     assert fwd(16, (1 << 24) + 4) == _lib.ERR_UNSUPPORTED
+
+
+def test_gate_gradient_layout_rejections():
+    """naju_scan_bwd_ex's gate-gradient options off the matrix-core path or
+    with a stride it cannot serve return an error (host checks only)."""
+    import ctypes
+    L = _lib.lib()
+
+    def bwd(N, **kw):
+        lay = _lib.ScanBwdLayout(**kw)
+        return L.naju_scan_bwd_ex(256, 256, 256, 256, 256, 256, 256, 256, 256, 256, 256, None, None, None, None,
+                                  1, 8, 16, N, 0, 0, 0, 0, ctypes.byref(lay), 256, 1 << 20, None)
+
+    assert bwd(1, dg_ld=20) == _lib.ERR_UNSUPPORTED
+    assert bwd(1, dfl_sum=256) == _lib.ERR_UNSUPPORTED
+    assert bwd(128, dg_dtype=_lib.DT_BF16) == _lib.ERR_UNSUPPORTED
+    assert bwd(16, dg_ld=8) == _lib.ERR_INVALID
+    assert bwd(16, dg_ld=18) == _lib.ERR_UNSUPPORTED
+    assert bwd(16, dg_dtype=7) == _lib.ERR_INVALID

@@ -299,3 +299,65 @@ def test_gate_pair_matches_two_single_convolutions(gpu, dtype, T):
         want = want + torch.autograd.grad(yr, xr, dy.double())[0]
     tol = 2.0 ** -7 if dtype == torch.bfloat16 else 1e-5
     assert _rel(dxp, want) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gate_pair_takes_handed_over_gradients(gpu, dtype):
+    """dwconv_pair(..., gate_grads=True): when the logits' consumer hands
+    their gradients over (written into the adds' split buffer in its type,
+    with their sums; naju_dwconv_pair_bwd reads them there, rows of the
+    buffer's stride apart), every gradient is bitwise the ordinary path's
+    for gradients of the same values, and the biases' gradients are the
+    handed-over sums."""
+    from naju_amd import gradsink
+    from naju_amd.dwconv import dwconv_pair, pair_supported
+    B, T, C, K = 2, 300, 264, 4
+    g = torch.Generator(device=gpu).manual_seed(5)
+    x0 = torch.randn(B, T, C, generator=g, device=gpu).to(dtype)
+    P0 = torch.randn(B, T, 2 * C + 16, generator=g, device=gpu).to(dtype)
+    ws = [torch.randn(C, 1, K, generator=g, device=gpu) / K for _ in range(2)]
+    bs = [torch.randn(C, generator=g, device=gpu) for _ in range(2)]
+    # gradients whose values the split buffer's type holds exactly
+    dys = [torch.randn(B, T, C, generator=g, device=gpu).to(dtype).float() for _ in range(2)]
+    sums = [d.sum((0, 1)) for d in dys]
+    g_prev = torch.randn(B, T, C, generator=g, device=gpu).to(dtype)
+
+    class Consumer(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, y0, y1, gg):
+            ctx.gg = gg
+            return y0.sum() + y1.sum()
+
+        @staticmethod
+        def backward(ctx, go):
+            if ctx.gg is None:
+                return dys[0], dys[1], None
+            t0, t1 = ctx.gg.targets()
+            t0.copy_(dys[0])
+            t1.copy_(dys[1])
+            m0, m1 = ctx.gg.hand_over(t0, t1, sums[0], sums[1], dys[0].shape, torch.float32, torch.float32)
+            return m0, m1, None
+
+    def run(handoff):
+        x = x0.clone().requires_grad_(True)
+        P = P0.clone().requires_grad_(True)
+        w = [t.clone().requires_grad_(True) for t in ws]
+        b = [t.clone().requires_grad_(True) for t in bs]
+        xa, xo = gradsink.fanout(x, 2)
+        p0, p1, _ = gradsink.split(P, [C, C, 16])
+        assert pair_supported(xa, w[0], p0, w[1], p1)
+        y0, y1, *gg = dwconv_pair(xa, w[0], b[0], p0, w[1], b[1], p1, out_dtype=torch.float32,
+                                  gate_grads=handoff)
+        loss = Consumer.apply(y0, y1, gg[0] if gg else None) + (xo.float() * g_prev.float()).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        return x.grad, P.grad, [t.grad for t in w], [t.grad for t in b]
+
+    dxh, dPh, dwh, dbh = run(True)
+    dxp, dPp, dwp, dbp = run(False)
+    assert torch.equal(dxh, dxp) and torch.equal(dPh, dPp)
+    for a, c in zip(dwh, dwp):
+        assert torch.equal(a, c)
+    for a, s, c in zip(dbh, sums, dbp):
+        assert torch.equal(a, s)
+        assert torch.allclose(a, c, rtol=1e-5, atol=1e-5)

@@ -302,3 +302,47 @@ def test_lm_weight_copies_match_per_layer_casts(gpu, monkeypatch):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     for (n, _), ga, gb in zip(ma.named_parameters(), outs[0][2], outs[1][2]):
         assert torch.equal(ga, gb), n
+
+
+def test_mixer_gate_gradients_handed_over_in_place(gpu, monkeypatch):
+    """With the HIP scan the mixer's gate logits' gradients go from the
+    scan's backward straight into the projection gradient buffer (bf16,
+    rounded once from float32, as autocast's backward rounds them) with
+    their float32 sums as the biases' gradients (naju_amd.dwconv.GateGrads):
+    the hand-off happens in every layer, and the gradients agree with the
+    same mixer reached through another backend name (no hand-off, float32
+    gate gradients into the convolutions) to bf16 rounding."""
+    import copy
+    from naju_amd import dwconv
+    from naju_amd import scan as scan_mod
+    from naju_amd.mixer import NajuMixer
+    taken = []
+    real = dwconv.GateGrads.take
+
+    def spy(self, dy0, dy1):
+        r = real(self, dy0, dy1)
+        taken.append(r is not None)
+        return r
+
+    monkeypatch.setattr(dwconv.GateGrads, "take", spy)
+    scan_mod._BACKEND_CACHE["hip_plain2"] = lambda *a: scan_mod.naju_scan_hip(*a)
+    try:
+        torch.manual_seed(4)
+        ma = NajuMixer(256, d_state=64, scan_backend="hip").to(gpu)
+        mb = copy.deepcopy(ma)
+        mb.scan_backend = "hip_plain2"
+        u = torch.randn(2, 384, 256, device=gpu)
+        gy = torch.randn(2, 384, 256, device=gpu)
+        outs = []
+        for m in (ma, mb):
+            ui = u.clone().requires_grad_(True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = m(ui)
+            y.float().backward(gy)
+            outs.append((ui.grad, {n: p.grad for n, p in m.named_parameters()}))
+        assert taken == [True], taken
+        assert _rel(outs[0][0], outs[1][0]) < 1e-2
+        for n, ga in outs[0][1].items():
+            assert _rel(ga, outs[1][1][n]) < 2e-2, n
+    finally:
+        scan_mod._BACKEND_CACHE.pop("hip_plain2", None)

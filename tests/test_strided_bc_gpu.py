@@ -138,3 +138,62 @@ def test_autograd_split_path_is_bitwise_the_plain_one(N, dtype):
     y1, g1 = _mixer_like(dev, sizes, N, dtype, True)
     assert torch.equal(y1, y0)
     assert torch.equal(g1, g0)
+
+
+@pytest.mark.parametrize("shape,dtype,gdt,dgt", [
+    ((2, 300, 96, 16), torch.bfloat16, torch.float32, torch.bfloat16),   # the mixer's: f32 gates, bf16 buffer
+    ((1, 1100, 192, 64), torch.bfloat16, torch.float32, torch.bfloat16),
+    ((2, 257, 128, 64), torch.float32, None, torch.float32),              # float32 model: f32 buffer
+    ((3, 77, 72, 12), torch.float16, torch.float32, torch.float16),
+])
+def test_gate_gradient_layout_and_sums(shape, dtype, gdt, dgt):
+    """naju_scan_bwd_ex with the gate-gradient options: dfl and dil written
+    into a wider buffer (row stride ld) in dg_dtype are torch's rounding of
+    naju_scan_bwd's float32 dfl, dil (bitwise); every other output is
+    bitwise naju_scan_bwd's; the sums over batch and time match float64 sums
+    of those float32 gradients; the buffer's other columns stay untouched."""
+    from naju_amd import _lib
+    dev = torch.device("cuda:0")
+    print(f"gate-gradient layout case {shape} {dtype} gates={gdt} -> {dgt}", flush=True)
+    Bsz, T, D, N = shape
+    ins = rand_inputs(*shape, seed=sum(shape) + 1, dtype=dtype, gate_dtype=gdt, h0_std=0.3)
+    t = {k: (v.to(dev).contiguous() if v is not None else None) for k, v in ins.items()}
+    flags = _lib.FLAG_OUT_F32
+    ref, _ = _abi(t, dev, flags)  # float32 outputs
+    L = _lib.lib()
+    u, fl, il, Bm, Cm, h0, dy = t["u"], t["f_logit"], t["i_logit"], t["B"], t["C"], t.get("h0"), t["dy"]
+    Dk = t["D_skip"].float().contiguous()
+    dts = (_DTC[u.dtype], _DTC[fl.dtype], _DTC[Bm.dtype])
+    ck = torch.empty(max(1, L.naju_scan_ckpt_elems(Bsz, T, D, N, *dts)), dtype=torch.float32, device=dev)
+    nb = L.naju_scan_workspace_bytes_ex(Bsz, T, D, N, *dts, flags)
+    ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    y = torch.empty(u.shape, dtype=torch.float32, device=dev)
+    _lib.check(L.naju_scan_fwd(_p(u), _p(fl), _p(il), _p(Bm), _p(Cm), _p(Dk), _p(h0), _p(y), _p(ck), None,
+                               Bsz, T, D, N, *dts, flags, _p(ws), ws.numel(), st))
+    ld = 2 * D + 40
+    buf = torch.full((Bsz, T, ld), float("nan"), dtype=dgt, device=dev)
+    dfl, dil = buf[..., 8:8 + D], buf[..., D + 40:2 * D + 40]
+    g = {k: torch.empty(u.shape, dtype=torch.float32, device=dev) for k in ("du",)}
+    g["dB"] = torch.empty(Bm.shape, dtype=torch.float32, device=dev)
+    g["dC"] = torch.empty(Bm.shape, dtype=torch.float32, device=dev)
+    g["dD"] = torch.empty(D, dtype=torch.float32, device=dev)
+    g["dh0"] = torch.empty(h0.shape, dtype=torch.float32, device=dev)
+    sums = torch.full((2, D), float("nan"), device=dev)
+    lay = _lib.ScanBwdLayout(dg_ld=ld, dg_dtype=_DTC[dgt], dfl_sum=sums.data_ptr(), dil_sum=sums.data_ptr() + 4 * D)
+    import ctypes
+    _lib.check(L.naju_scan_bwd_ex(_p(u), _p(fl), _p(il), _p(Bm), _p(Cm), _p(Dk), _p(ck), _p(dy), _p(g["du"]),
+                                  _p(dfl), _p(dil), _p(g["dB"]), _p(g["dC"]), _p(g["dD"]), _p(g["dh0"]),
+                                  Bsz, T, D, N, *dts, flags, ctypes.byref(lay), _p(ws), ws.numel(), st))
+    torch.cuda.synchronize()
+    for k in g:
+        assert torch.equal(g[k], ref[k]), k
+    assert torch.equal(dfl, ref["dfl"].to(dgt)) and torch.equal(dil, ref["dil"].to(dgt))
+    rest = torch.ones(ld, dtype=torch.bool, device=dev)
+    rest[8:8 + D] = False
+    rest[D + 40:2 * D + 40] = False
+    assert torch.isnan(buf[..., rest]).all()
+    for s, k in ((sums[0], "dfl"), (sums[1], "dil")):
+        want = ref[k].double().sum((0, 1))
+        scale = ref[k].double().abs().sum((0, 1)) + 1e-30
+        assert float(((s.double() - want).abs() / scale).max()) < 1e-5, k
