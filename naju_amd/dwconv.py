@@ -19,7 +19,7 @@ and a missing library raises.
 import torch
 
 from naju_amd import _lib
-from naju_amd.gradsink import acc_sink_of, sink_of
+from naju_amd.gradsink import _zero, acc_sink_of, sink_of
 
 _DT = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16}
 # naju_dwconv_bwd: dx += the gradient (include/naju_mixer.h)
@@ -182,22 +182,27 @@ class GateGrads:
         return s0.slice(c0, self.C), s1.slice(c1, self.C)
 
     def hand_over(self, g0, g1, sum0, sum1, shape, dtype0, dtype1):
-        """Record what the scan wrote; returns the markers for autograd."""
+        """Record what the scan wrote; returns the markers for autograd
+        (zeros of the logits' shape without storage of their own)."""
         dev = g0.device
         self._result = (g0, g1, sum0, sum1)
-        self._markers = (torch.zeros((), dtype=dtype0, device=dev).expand(shape),
-                         torch.zeros((), dtype=dtype1, device=dev).expand(shape))
+        self._markers = (_zero(dtype0, dev).expand(shape), _zero(dtype1, dev).expand(shape))
         return self._markers
 
     def take(self, dy0, dy1):
-        """The scan's result when dy0, dy1 are its markers (taken once),
-        else None."""
+        """(result, dy0, dy1) for the pair's backward, the hand-off taken
+        once: (the scan's result, None, None) when dy0, dy1 are its markers;
+        (None, dy0, dy1) when nothing was handed over; and when the logits
+        had another consumer too (autograd added its gradient to the
+        markers), (None, its gradient plus the scan's part, ...), which the
+        ordinary path then writes over the scan's part in the buffer."""
         r, m = self._result, self._markers
-        if r is None or not all(d.data_ptr() == k.data_ptr() and all(st == 0 for st in d.stride())
-                                for d, k in zip((dy0, dy1), m)):
-            return None
         self._result = self._markers = None
-        return r
+        if r is None:
+            return None, dy0, dy1
+        if all(d.data_ptr() == k.data_ptr() and all(st == 0 for st in d.stride()) for d, k in zip((dy0, dy1), m)):
+            return r, None, None
+        return None, dy0.float() + r[0].float(), dy1.float() + r[1].float()
 
 
 class _DwConvPair(torch.autograd.Function):
@@ -228,7 +233,9 @@ class _DwConvPair(torch.autograd.Function):
         B, T, C = x.shape
         K = w0.shape[1]
         need = ctx.needs_input_grad
-        gg = ctx.gate_grads.take(dy0, dy1) if ctx.gate_grads is not None else None
+        gg = None
+        if ctx.gate_grads is not None:
+            gg, dy0, dy1 = ctx.gate_grads.take(dy0, dy1)
         if gg is not None:
             # the scan wrote dy0, dy1 as the adds' gradients into the split's
             # buffer and summed them for the biases

@@ -301,14 +301,16 @@ def test_gate_pair_matches_two_single_convolutions(gpu, dtype, T):
     assert _rel(dxp, want) < tol
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_gate_pair_takes_handed_over_gradients(gpu, dtype):
+@pytest.mark.parametrize("dtype,extra", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True)])
+def test_gate_pair_takes_handed_over_gradients(gpu, dtype, extra):
     """dwconv_pair(..., gate_grads=True): when the logits' consumer hands
     their gradients over (written into the adds' split buffer in its type,
     with their sums; naju_dwconv_pair_bwd reads them there, rows of the
     buffer's stride apart), every gradient is bitwise the ordinary path's
     for gradients of the same values, and the biases' gradients are the
-    handed-over sums."""
+    handed-over sums. With a second consumer of the logits (extra), whose
+    gradient autograd adds to the hand-off's markers, the scan's part is
+    added back in and the result is bitwise the ordinary path's."""
     from naju_amd import gradsink
     from naju_amd.dwconv import dwconv_pair, pair_supported
     B, T, C, K = 2, 300, 264, 4
@@ -349,15 +351,21 @@ def test_gate_pair_takes_handed_over_gradients(gpu, dtype):
         y0, y1, *gg = dwconv_pair(xa, w[0], b[0], p0, w[1], b[1], p1, out_dtype=torch.float32,
                                   gate_grads=handoff)
         loss = Consumer.apply(y0, y1, gg[0] if gg else None) + (xo.float() * g_prev.float()).sum()
+        if extra:
+            loss = loss + (y0 * c0).sum() + (y1 * c1).sum()
         loss.backward()
         torch.cuda.synchronize()
         return x.grad, P.grad, [t.grad for t in w], [t.grad for t in b]
 
+    c0, c1 = (torch.randn(B, T, C, generator=g, device=gpu) for _ in range(2))
     dxh, dPh, dwh, dbh = run(True)
     dxp, dPp, dwp, dbp = run(False)
     assert torch.equal(dxh, dxp) and torch.equal(dPh, dPp)
     for a, c in zip(dwh, dwp):
         assert torch.equal(a, c)
     for a, s, c in zip(dbh, sums, dbp):
-        assert torch.equal(a, s)
-        assert torch.allclose(a, c, rtol=1e-5, atol=1e-5)
+        if extra:
+            assert torch.equal(a, c)
+        else:
+            assert torch.equal(a, s)
+            assert torch.allclose(a, c, rtol=1e-5, atol=1e-5)
