@@ -792,8 +792,16 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
 // wave 0 adds the 16 partial sums in wave order. The dw / dbias columns of
 // the conv partials ([C][K+1]) go to dw (j < K) and dbias (j == K); with
 // K = 0 every column is a dbias (the readout's dD).
-__global__ __launch_bounds__(1024) void fold_cols_kernel(const float* __restrict__ part, int64_t nblk, int64_t C,
-                                                         int K, float* __restrict__ dw, float* __restrict__ dbias) {
+__global__ __launch_bounds__(1024) void fold_cols_kernel(const float* __restrict__ part0, int64_t nblk, int64_t C,
+                                                         int K, float* __restrict__ dw0, float* __restrict__ dbias0,
+                                                         const float* __restrict__ part1, float* __restrict__ dw1,
+                                                         float* __restrict__ dbias1) {
+  // blockIdx.y selects one of two partial arrays of the same shape (the gate
+  // pair's two weights in one launch)
+  const bool second = blockIdx.y != 0;
+  const float* __restrict__ part = second ? part1 : part0;
+  float* __restrict__ dw = second ? dw1 : dw0;
+  float* __restrict__ dbias = second ? dbias1 : dbias0;
   __shared__ float s[16][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t ncol = C * (K + 1);
@@ -1000,10 +1008,13 @@ bool readout_vec_ok(int64_t n_rows, int64_t C, int64_t z_ld, std::initializer_li
   return true;
 }
 
-int launch_fold(const float* part, int64_t nblk, int64_t C, int K, float* dw, float* dbias, hipStream_t st) {
+// Folds part0 into dw0 / dbias0 and, when part1 is given, part1 into dw1 /
+// dbias1 in the same launch.
+int launch_fold(const float* part, int64_t nblk, int64_t C, int K, float* dw, float* dbias, hipStream_t st,
+                const float* part1 = nullptr, float* dw1 = nullptr, float* dbias1 = nullptr) {
   const int64_t ncol = C * (K + 1);
-  hipLaunchKernelGGL(fold_cols_kernel, dim3((unsigned)((ncol + 63) / 64)), dim3(1024), 0, st, part, nblk, C, K, dw,
-                     dbias);
+  hipLaunchKernelGGL(fold_cols_kernel, dim3((unsigned)((ncol + 63) / 64), part1 ? 2u : 1u), dim3(1024), 0, st, part,
+                     nblk, C, K, dw, dbias, part1, dw1, dbias1);
   return hipGetLastError() == hipSuccess ? NAJU_OK : fail(NAJU_ERR_LAUNCH, "fold launch failed");
 }
 
@@ -1901,7 +1912,8 @@ int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const flo
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   const int64_t nblk = batch * ntb;
-  if (part0 && (rc = launch_fold(part0, nblk, C, K, dw0, dbias0, st))) return rc;
+  if (part0 && part1) return launch_fold(part0, nblk, C, K, dw0, dbias0, st, part1, dw1, dbias1);
+  if (part0) return launch_fold(part0, nblk, C, K, dw0, dbias0, st);
   if (part1) return launch_fold(part1, nblk, C, K, dw1, dbias1, st);
   return NAJU_OK;
 }

@@ -39,7 +39,7 @@ from naju_amd.readout import readout
 from naju_amd.rmsnorm import rms_norm
 from naju_amd.rmsnorm import rms_norm_fork
 from naju_amd.rmsnorm import supported as rmsnorm_supported
-from naju_amd.residual import residual_dropout
+from naju_amd.residual import draw_seeds, residual_dropout
 from naju_amd.residual import supported as residual_supported
 from naju_amd import scan as _scan
 from naju_amd.scan import naju_scan, naju_scan_hip
@@ -240,8 +240,12 @@ class NajuMixer(nn.Module):
             i_logit = self._gate_logit(h, self.i_proj, self.i_conv, self.i_bias)
         # the scan reads out the state only; the D skip is applied here
         if fold:
-            cx = naju_scan_hip(h_s, f_logit, i_logit, Bm, Cm, self.D_zero,
-                               du_skip=self.D.detach() * (1.0 / self._cx_scale), gate_grads=gate_grads)
+            # D / s: formed for all layers in one launch by NajuLM.forward
+            # when it runs this mixer, else here
+            du_skip = self.__dict__.pop("_du_skip", None)
+            if du_skip is None:
+                du_skip = self.D.detach() * (1.0 / self._cx_scale)
+            cx = naju_scan_hip(h_s, f_logit, i_logit, Bm, Cm, self.D_zero, du_skip=du_skip, gate_grads=gate_grads)
         else:
             cx = naju_scan(h, f_logit, i_logit, Bm, Cm, self.D_zero, backend=self.scan_backend)
         if h.is_cuda:
@@ -267,7 +271,7 @@ class NajuBlock(nn.Module):
         # the norm's output feeds in_proj only: take it in that GEMM's dtype
         return self.drop(self.mixer(self.norm(u, out_dtype=_out_dtype(u))))
 
-    def _fused(self, u):
+    def _fused(self, u, seed=None):
         # the norm and the residual read u; their gradients meet in the
         # norm's backward pass, and the residual add and the dropout are one
         # pass each way (naju_amd.residual)
@@ -275,17 +279,23 @@ class NajuBlock(nn.Module):
         mix = self.mixer(h)
         if not residual_supported(u_res, mix):
             return u_res + self.drop(mix)
-        return residual_dropout(u_res, mix, self.drop.p if self.training else 0.0)
+        return residual_dropout(u_res, mix, self.drop.p if self.training else 0.0, seed=seed)
 
-    def forward(self, u):
-        # CUDA float32 residual streams that the fused kernels serve
-        fused = u.is_cuda and u.dtype == torch.float32 and rmsnorm_supported(u)
+    def fused_path(self, u):
+        """Whether forward(u) runs the fused norm / residual / dropout kernels
+        (CUDA float32 residual streams they serve)."""
+        return u.is_cuda and u.dtype == torch.float32 and rmsnorm_supported(u)
+
+    def forward(self, u, seed=None):
+        """seed: the fused path's dropout seed (a one-element int64 CUDA
+        tensor; NajuLM draws all its blocks' seeds at once), else drawn here."""
+        fused = self.fused_path(u)
         if self.use_ckpt and torch.is_grad_enabled():
             if fused:
-                return checkpoint(self._fused, u, use_reentrant=False)
+                return checkpoint(self._fused, u, seed, use_reentrant=False)
             return u + checkpoint(self._branch, u, use_reentrant=False)
         if fused:
-            return self._fused(u)
+            return self._fused(u, seed)
         return u + self._branch(u)
 
 
@@ -322,8 +332,26 @@ class NajuLM(nn.Module):
             self._wcopies = wcast.WeightCopies()
         with wcast.active(getattr(self, "_wcopies", None), groups,
                           torch.get_autocast_dtype("cuda") if groups else None):
-            for blk in self.blocks:
-                x = blk(x)
+            # every mixer's D / s (its scan's du_skip) in one multi-tensor
+            # launch; a mixer takes its own once during this forward, and what
+            # is not taken is dropped at its end (a recompute under
+            # activation checkpointing forms its own)
+            mixers = [blk.mixer for blk in self.blocks]
+            if x.is_cuda and mixers and all(m.D.is_cuda and m._cx_scale == mixers[0]._cx_scale for m in mixers):
+                for m, v in zip(mixers, torch._foreach_mul([m.D.detach() for m in mixers],
+                                                           1.0 / mixers[0]._cx_scale)):
+                    m.__dict__["_du_skip"] = v
+            try:
+                # the blocks' dropout seeds in one draw (one kernel, not one each)
+                seeds = None
+                if (self.training and self.blocks and self.blocks[0].drop.p > 0.0
+                        and self.blocks[0].fused_path(x)):
+                    seeds = draw_seeds(len(self.blocks), x.device)
+                for i, blk in enumerate(self.blocks):
+                    x = blk(x) if seeds is None else blk(x, seeds[i:i + 1])
+            finally:
+                for m in mixers:
+                    m.__dict__.pop("_du_skip", None)
             h = self.norm(x, out_dtype=_out_dtype(x))
             if compute_dtype(h) is not None:
                 # padded vocabulary rows: aligned GEMMs (logits: a strided view)

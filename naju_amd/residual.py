@@ -57,14 +57,27 @@ def supported(u, mix):
             and u.is_contiguous() and mix.is_contiguous())
 
 
-def residual_dropout(u, mix, p):
+def residual_dropout(u, mix, p, seed=None):
     """u + Dropout(p)(mix) (training-mode dropout; p = 0 is the plain sum)
-    for float32 u and mix of u's shape in float32 / bfloat16 / float16."""
+    for float32 u and mix of u's shape in float32 / bfloat16 / float16.
+    seed: a one-element int64 CUDA tensor to draw the mask from (a caller
+    with several dropouts draws all their seeds in one call), else drawn
+    here from torch's generator."""
     if not supported(u, mix):
         raise RuntimeError("naju_amd.residual_dropout: u must be a contiguous float32 CUDA tensor and mix a "
                            "contiguous CUDA tensor of u's shape in float32, bfloat16 or float16")
     p = float(p)
     if not 0.0 <= p < 1.0:
         raise ValueError(f"dropout probability must be in [0, 1), got {p}")
-    seed = torch.randint(0, 2 ** 62, (1,), device=u.device, dtype=torch.int64) if p > 0.0 else None
+    if p == 0.0:
+        seed = None
+    elif seed is None:
+        seed = draw_seeds(1, u.device)
+    elif not (seed.is_cuda and seed.dtype == torch.int64 and seed.numel() == 1):
+        raise ValueError("naju_amd.residual_dropout: seed must be a one-element int64 CUDA tensor")
     return _ResidualDropout.apply(u, mix, p, seed)
+
+
+def draw_seeds(n, device):
+    """n dropout seeds from torch's generator in one call (int64 [n])."""
+    return torch.randint(0, 2 ** 62, (n,), device=device, dtype=torch.int64)
