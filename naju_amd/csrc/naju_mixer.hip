@@ -265,16 +265,29 @@ static_assert(kCWB * kCRB == kVRowsB, "one partial row per kVRowsB rows");
 template <typename T>
 using cvec_t = T __attribute__((ext_vector_type(kCV)));
 
+template <typename T, int V>
+using pvec_t = T __attribute__((ext_vector_type(V)));
+
+#ifndef NAJU_CONV_BWD_V
+#define NAJU_CONV_BWD_V 2
+#endif
+constexpr int kBV = NAJU_CONV_BWD_V;  // single convolution backward: channels per thread
+#ifndef NAJU_CONV_FWD_V
+#define NAJU_CONV_FWD_V 2
+#endif
+constexpr int kFV4 = NAJU_CONV_FWD_V;  // forward kernels (single and pair): channels per thread
+
 template <typename T>
 __device__ __forceinline__ cvec_t<T> ldc(const T* p) {
   return *(const cvec_t<T>*)p;
 }
-template <typename T>
-__device__ __forceinline__ void stc(T* p, const float (&x)[kCV]) {
-  cvec_t<T> v;
+template <typename T, int V>
+__device__ __forceinline__ void stc(T* p, const float (&x)[V]) {
+  typedef T v_t __attribute__((ext_vector_type(V)));
+  v_t v;
 #pragma unroll
-  for (int j = 0; j < kCV; ++j) v[j] = (T)x[j];
-  *(cvec_t<T>*)p = v;
+  for (int j = 0; j < V; ++j) v[j] = (T)x[j];
+  *(v_t*)p = v;
 }
 
 // grid: (ceil(C / (64 * kCV)), ceil(T / kCRF), batch), 64 threads: rows
@@ -286,24 +299,24 @@ __global__ __launch_bounds__(64) void dwconv4_fwd_vec(const TX* __restrict__ x, 
                                                       const float* __restrict__ w, const float* __restrict__ bias,
                                                       const TX* __restrict__ add, int64_t ld_add,
                                                       TY* __restrict__ y, int64_t T, int64_t C) {
-  constexpr int K = 4, V = kCV, R = kCRF;
+  constexpr int K = 4, V = kFV4, R = kCRF;
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * V;
   if (c0 >= C) return;
   const int64_t b = blockIdx.z;
   const int64_t t0 = (int64_t)blockIdx.y * R;
   const TX* xb = x + b * T * ldx + c0;
-  cvec_t<TX> xr[R + K - 1], ar[R];
+  pvec_t<TX, V> xr[R + K - 1], ar[R];
 #pragma unroll
   for (int i = 0; i < R + K - 1; ++i) {
     int64_t t = t0 - (K - 1) + i;
     t = t < 0 ? 0 : (t < T ? t : T - 1);
-    xr[i] = ldc(xb + t * ldx);
+    xr[i] = *(const pvec_t<TX, V>*)(xb + t * ldx);
   }
   if (ADD) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t t = t0 + r < T ? t0 + r : T - 1;
-      ar[r] = ldc(add + (b * T + t) * ld_add + c0);
+      ar[r] = *(const pvec_t<TX, V>*)(add + (b * T + t) * ld_add + c0);
     }
   }
   float wr[V][K], bc[V];
@@ -345,7 +358,7 @@ __global__ __launch_bounds__(64 * kCWB) void dwconv4_bwd_vec(const TX* __restric
                                                              const TDY* __restrict__ dy, TX* __restrict__ dx,
                                                              int64_t ld_dx, TX* __restrict__ dadd, int64_t ld_dadd,
                                                              float* __restrict__ part, int64_t T, int64_t C, int acc) {
-  constexpr int K = 4, V = kCV, R = kCRB;
+  constexpr int K = 4, V = kBV, R = kCRB;
   constexpr int NZ = R + K - 1;                 // dz rows tw .. tw + R + 2
   constexpr int NX = SILU ? R + 2 * (K - 1) : R + K - 1;  // x rows tw - 3 ..
   __shared__ float s_red[kCWB][(K + 1) * V][64];
@@ -357,24 +370,24 @@ __global__ __launch_bounds__(64 * kCWB) void dwconv4_bwd_vec(const TX* __restric
   const int64_t b = blockIdx.z;
   const int64_t tw = (int64_t)blockIdx.y * (kCWB * R) + wv * R;
   const TX* xb = x + b * T * ldx + cc;
-  cvec_t<TDY> gr[NZ];
-  cvec_t<TX> xr[NX], dr[R];
+  pvec_t<TDY, V> gr[NZ];
+  pvec_t<TX, V> xr[NX], dr[R];
 #pragma unroll
   for (int i = 0; i < NZ; ++i) {
     const int64_t t = tw + i < T ? tw + i : T - 1;
-    gr[i] = ldc(dy + (b * T + t) * C + cc);
+    gr[i] = *(const pvec_t<TDY, V>*)(dy + (b * T + t) * C + cc);
   }
 #pragma unroll
   for (int i = 0; i < NX; ++i) {
     int64_t t = tw - (K - 1) + i;
     t = t < 0 ? 0 : (t < T ? t : T - 1);
-    xr[i] = ldc(xb + t * ldx);
+    xr[i] = *(const pvec_t<TX, V>*)(xb + t * ldx);
   }
   if (dx && acc) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t t = tw + r < T ? tw + r : T - 1;
-      dr[r] = ldc(dx + (b * T + t) * ld_dx + cc);
+      dr[r] = *(const pvec_t<TX, V>*)(dx + (b * T + t) * ld_dx + cc);
     }
   }
   float wr[V][K], bc[V];
@@ -468,6 +481,11 @@ __global__ __launch_bounds__(64 * kCWB) void dwconv4_bwd_vec(const TX* __restric
 // array.
 constexpr int kPR = 8;  // backward rows per wave
 constexpr int kPW = 4;  // backward waves per workgroup
+#ifndef NAJU_PAIR_BWD_V
+#define NAJU_PAIR_BWD_V 2
+#endif
+constexpr int kPV = NAJU_PAIR_BWD_V;  // backward channels per thread
+
 static_assert(kPW * kPR == kVRowsB, "one partial row per kVRowsB rows");
 
 template <typename TX, typename TY>
@@ -479,24 +497,24 @@ __global__ __launch_bounds__(64) void dwconv4_pair_fwd_vec(const TX* __restrict_
                                                            const TX* __restrict__ add0, const TX* __restrict__ add1,
                                                            int64_t ld_add, TY* __restrict__ y0, TY* __restrict__ y1,
                                                            int64_t T, int64_t C) {
-  constexpr int K = 4, V = kCV, R = kCRF;
+  constexpr int K = 4, V = kFV4, R = kCRF;
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * V;
   if (c0 >= C) return;
   const int64_t b = blockIdx.z;
   const int64_t t0 = (int64_t)blockIdx.y * R;
   const TX* xb = x + b * T * ldx + c0;
-  cvec_t<TX> xr[R + K - 1], a0[R], a1[R];
+  pvec_t<TX, V> xr[R + K - 1], a0[R], a1[R];
 #pragma unroll
   for (int i = 0; i < R + K - 1; ++i) {
     int64_t t = t0 - (K - 1) + i;
     t = t < 0 ? 0 : (t < T ? t : T - 1);
-    xr[i] = ldc(xb + t * ldx);
+    xr[i] = *(const pvec_t<TX, V>*)(xb + t * ldx);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t = t0 + r < T ? t0 + r : T - 1;
-    a0[r] = ldc(add0 + (b * T + t) * ld_add + c0);
-    a1[r] = ldc(add1 + (b * T + t) * ld_add + c0);
+    a0[r] = *(const pvec_t<TX, V>*)(add0 + (b * T + t) * ld_add + c0);
+    a1[r] = *(const pvec_t<TX, V>*)(add1 + (b * T + t) * ld_add + c0);
   }
   float wr0[V][K], wr1[V][K], bc0[V], bc1[V];
 #pragma unroll
@@ -543,7 +561,7 @@ __global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __res
                                                                  int64_t ld_dadd, float* __restrict__ part0,
                                                                  float* __restrict__ part1, int64_t T, int64_t C,
                                                                  int acc) {
-  constexpr int K = 4, V = kCV, R = kPR;
+  constexpr int K = 4, V = kPV, R = kPR;
   constexpr int NZ = R + K - 1;  // dy rows tw .. tw + R + 2
   constexpr int NX = R + K - 1;  // x rows tw - 3 .. tw + R - 1
   __shared__ float s_red[kPW][(K + 1) * V][64];
@@ -555,25 +573,25 @@ __global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __res
   const int64_t b = blockIdx.z;
   const int64_t tw = (int64_t)blockIdx.y * (kPW * R) + wv * R;
   const TX* xb = x + b * T * ldx + cc;
-  cvec_t<TDY> g0[NZ], g1[NZ];
-  cvec_t<TX> xr[NX], dr[R];
+  pvec_t<TDY, V> g0[NZ], g1[NZ];
+  pvec_t<TX, V> xr[NX], dr[R];
 #pragma unroll
   for (int i = 0; i < NZ; ++i) {
     const int64_t t = tw + i < T ? tw + i : T - 1;
-    g0[i] = ldc(dy0 + (b * T + t) * ldy + cc);
-    g1[i] = ldc(dy1 + (b * T + t) * ldy + cc);
+    g0[i] = *(const pvec_t<TDY, V>*)(dy0 + (b * T + t) * ldy + cc);
+    g1[i] = *(const pvec_t<TDY, V>*)(dy1 + (b * T + t) * ldy + cc);
   }
 #pragma unroll
   for (int i = 0; i < NX; ++i) {
     int64_t t = tw - (K - 1) + i;
     t = t < 0 ? 0 : (t < T ? t : T - 1);
-    xr[i] = ldc(xb + t * ldx);
+    xr[i] = *(const pvec_t<TX, V>*)(xb + t * ldx);
   }
   if (dx && acc) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t t = tw + r < T ? tw + r : T - 1;
-      dr[r] = ldc(dx + (b * T + t) * ld_dx + cc);
+      dr[r] = *(const pvec_t<TX, V>*)(dx + (b * T + t) * ld_dx + cc);
     }
   }
   float wr0[V][K], wr1[V][K];
@@ -1454,7 +1472,7 @@ int naju_dwconv_fwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (batch == 0 || T == 0 || C == 0) return NAJU_OK;
   if (!x || !w || !y) return fail(NAJU_ERR_INVALID, "null pointer (x, w and y are required)");
   if (dwf_vec_t kv = pick_fwd_vec(x, x_ld, w, bias, add, add_ld, y, T, C, K, act, x_dtype, add_dtype, y_dtype)) {
-    const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)((T + kCRF - 1) / kCRF),
+    const dim3 grid((unsigned)((C + 64 * kFV4 - 1) / (64 * kFV4)), (unsigned)((T + kCRF - 1) / kCRF),
                     (unsigned)batch);
     hipLaunchKernelGGL(kv, grid, dim3(64), 0, (hipStream_t)stream, x, x_ld, w, bias, add, add_ld, y, T, C);
   } else {
@@ -1508,7 +1526,7 @@ int naju_dwconv_bwd(const void* x, int64_t x_ld, const float* w, const float* bi
   if (dwb_vec_t kv = pick_bwd_vec(x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, T, C, K, act, x_dtype, dy_dtype,
                                   dx_dtype, dadd_dtype)) {
     const int64_t ntb = (T + kVRowsB - 1) / kVRowsB;
-    const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)ntb, (unsigned)batch);
+    const dim3 grid((unsigned)((C + 64 * kBV - 1) / (64 * kBV)), (unsigned)ntb, (unsigned)batch);
     hipLaunchKernelGGL(kv, grid, dim3(64 * kCWB), 0, st, x, x_ld, w, bias, dy, dx, dx_ld, dadd, dadd_ld, part, T, C, acc);
     nblk = batch * ntb;
   } else {
@@ -1841,7 +1859,7 @@ int naju_dwconv_pair_fwd(const void* x, int64_t x_ld, const float* w0, const flo
   if (!pair_ok(T, C, K, {x_ld, add_ld}, {x, w0, w1, bias0, bias1, add0, add1, y0, y1}))
     return fail(NAJU_ERR_UNSUPPORTED,
                 "the pair kernels need K = 4, C and the row strides multiples of 8 and 16-byte aligned pointers");
-  const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)((T + kCRF - 1) / kCRF), (unsigned)batch);
+  const dim3 grid((unsigned)((C + 64 * kFV4 - 1) / (64 * kFV4)), (unsigned)((T + kCRF - 1) / kCRF), (unsigned)batch);
   hipStream_t st = (hipStream_t)stream;
   if (x_dtype == NAJU_DTYPE_BF16)
     pair_fwd_dt<bf16_t>(y_dtype, grid, st, x, x_ld, w0, bias0, w1, bias1, add0, add1, add_ld, y0, y1, T, C);
@@ -1898,7 +1916,7 @@ int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const flo
   float* part0 = (dw0 || dbias0) ? (float*)workspace : nullptr;
   float* part1 = (dw1 || dbias1) ? (float*)((char*)workspace + one) : nullptr;
   const int64_t ntb = (T + kVRowsB - 1) / kVRowsB;
-  const dim3 grid((unsigned)((C + 64 * kCV - 1) / (64 * kCV)), (unsigned)ntb, (unsigned)batch);
+  const dim3 grid((unsigned)((C + 64 * kPV - 1) / (64 * kPV)), (unsigned)ntb, (unsigned)batch);
   const int acc = accumulate ? 1 : 0;
   if (x_dtype == NAJU_DTYPE_BF16)
     pair_bwd_dt<bf16_t>(dy_dtype, grid, st, x, x_ld, w0, w1, dy0, dy1, dy_ld, dx, dx_ld, dadd0, dadd1, dadd_ld,
