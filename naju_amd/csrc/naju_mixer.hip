@@ -686,20 +686,25 @@ __global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __res
 constexpr int kRB = 8;
 static_assert(kVRows % kRB == 0, "whole row batches per block");
 
-template <typename T>
-using v8_t = T __attribute__((ext_vector_type(kVec)));
+#ifndef NAJU_READOUT_V
+#define NAJU_READOUT_V 4
+#endif
+constexpr int kRV = NAJU_READOUT_V;  // readout: channels per thread
 
 template <typename T>
-__device__ __forceinline__ v8_t<T> ld8r(const T* p) {
-  return *(const v8_t<T>*)p;
+using rvec_t = T __attribute__((ext_vector_type(kRV)));
+
+template <typename T>
+__device__ __forceinline__ rvec_t<T> ldrv(const T* p) {
+  return *(const rvec_t<T>*)p;
 }
 
 // An empty asm that takes v's registers as in-out operands: every load
 // feeding v is complete there, and nothing that uses v moves above it.
 template <typename T>
-__device__ __forceinline__ void pin8(v8_t<T>& v) {
-  static_assert(sizeof(v8_t<T>) % 4 == 0, "whole registers");
-  uint32_t w[sizeof(v8_t<T>) / 4];
+__device__ __forceinline__ void pinv(rvec_t<T>& v) {
+  static_assert(sizeof(rvec_t<T>) % 4 == 0, "whole registers");
+  uint32_t w[sizeof(rvec_t<T>) / 4];
   __builtin_memcpy(w, &v, sizeof(w));
 #pragma unroll
   for (int i = 0; i < (int)(sizeof(w) / 4); ++i) asm volatile("" : "+v"(w[i]));
@@ -711,36 +716,37 @@ __global__ __launch_bounds__(64) void readout_fwd_vec(const T* __restrict__ cx, 
                                                       const T* __restrict__ z, int64_t z_ld,
                                                       const float* __restrict__ Dv, float scale, T* __restrict__ y,
                                                       int64_t n_rows, int64_t C) {
-  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kRV;
   if (c0 >= C) return;
   const int64_t r0 = (int64_t)blockIdx.y * kVRows;
-  float dv[kVec];
-  ld8f(Dv + c0, dv);
-  auto one = [&](const v8_t<T>& xa, const v8_t<T>& xh, const v8_t<T>& xz, int64_t row) {
-    float a[kVec];
+  float dv[kRV];
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) a[j] = fmaf((float)xa[j], scale, dv[j] * (float)xh[j]) * silu((float)xz[j]);
-    st8(y + row * C + c0, a);
+  for (int j = 0; j < kRV; ++j) dv[j] = Dv[c0 + j];
+  auto one = [&](const rvec_t<T>& xa, const rvec_t<T>& xh, const rvec_t<T>& xz, int64_t row) {
+    float a[kRV];
+#pragma unroll
+    for (int j = 0; j < kRV; ++j) a[j] = fmaf((float)xa[j], scale, dv[j] * (float)xh[j]) * silu((float)xz[j]);
+    stc(y + row * C + c0, a);
   };
   for (int rb = 0; rb < kVRows; rb += kRB) {
     const int64_t b0 = r0 + rb;
     if (b0 + kRB <= n_rows) {
       // a whole batch: straight-line loads, then the rows
-      v8_t<T> xa[kRB], xh[kRB], xz[kRB];
+      rvec_t<T> xa[kRB], xh[kRB], xz[kRB];
 #pragma unroll
       for (int r = 0; r < kRB; ++r) {
-        xa[r] = ld8r(cx + (b0 + r) * C + c0);
-        xh[r] = ld8r(h + (b0 + r) * C + c0);
-        xz[r] = ld8r(z + (b0 + r) * z_ld + c0);
+        xa[r] = ldrv(cx + (b0 + r) * C + c0);
+        xh[r] = ldrv(h + (b0 + r) * C + c0);
+        xz[r] = ldrv(z + (b0 + r) * z_ld + c0);
       }
       // (keeps the compiler from sinking the loads into the rows' code)
 #pragma unroll
-      for (int r = 0; r < kRB; ++r) pin8(xa[r]), pin8(xh[r]), pin8(xz[r]);
+      for (int r = 0; r < kRB; ++r) pinv(xa[r]), pinv(xh[r]), pinv(xz[r]);
 #pragma unroll
       for (int r = 0; r < kRB; ++r) one(xa[r], xh[r], xz[r], b0 + r);
     } else {
       for (int64_t row = b0; row < n_rows; ++row)
-        one(ld8r(cx + row * C + c0), ld8r(h + row * C + c0), ld8r(z + row * z_ld + c0), row);
+        one(ldrv(cx + row * C + c0), ldrv(h + row * C + c0), ldrv(z + row * z_ld + c0), row);
       break;
     }
   }
@@ -753,17 +759,18 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
                                                       const T* __restrict__ dy, T* __restrict__ dcx,
                                                       T* __restrict__ dh, T* __restrict__ dz, int64_t dz_ld,
                                                       float* __restrict__ part, int64_t n_rows, int64_t C) {
-  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kVec;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kRV;
   if (c0 >= C) return;
   const int64_t r0 = (int64_t)blockIdx.y * kVRows;
-  float dv[kVec], dd[kVec];
-  ld8f(Dv + c0, dv);
+  float dv[kRV], dd[kRV];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) dd[j] = 0.f;
-  auto one = [&](const v8_t<T>& xc, const v8_t<T>& xh, const v8_t<T>& xz, const v8_t<T>& xg, int64_t row) {
-    float o0[kVec], o1[kVec], o2[kVec];
+  for (int j = 0; j < kRV; ++j) dv[j] = Dv[c0 + j];
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
+  for (int j = 0; j < kRV; ++j) dd[j] = 0.f;
+  auto one = [&](const rvec_t<T>& xc, const rvec_t<T>& xh, const rvec_t<T>& xz, const rvec_t<T>& xg, int64_t row) {
+    float o0[kRV], o1[kRV], o2[kRV];
+#pragma unroll
+    for (int j = 0; j < kRV; ++j) {
       const float zz = (float)xz[j], g = (float)xg[j], hh = (float)xh[j];
       const float sg = sigmoid_f(zz);
       const float gs = g * (zz * sg);
@@ -773,35 +780,35 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
       const float a = fmaf((float)xc[j], scale, dv[j] * hh);
       o2[j] = g * a * sg * fmaf(zz, 1.f - sg, 1.f);
     }
-    if (dcx) st8(dcx + row * C + c0, o0);
-    if (dh) st8(dh + row * C + c0, o1);
-    if (dz) st8(dz + row * dz_ld + c0, o2);
+    if (dcx) stc(dcx + row * C + c0, o0);
+    if (dh) stc(dh + row * C + c0, o1);
+    if (dz) stc(dz + row * dz_ld + c0, o2);
   };
   for (int rb = 0; rb < kVRows; rb += kRB) {
     const int64_t b0 = r0 + rb;
     if (b0 + kRB <= n_rows) {
       // a whole batch: straight-line loads, then the rows
-      v8_t<T> xc[kRB], xh[kRB], xz[kRB], xg[kRB];
+      rvec_t<T> xc[kRB], xh[kRB], xz[kRB], xg[kRB];
 #pragma unroll
       for (int r = 0; r < kRB; ++r) {
-        xc[r] = ld8r(cx + (b0 + r) * C + c0);
-        xh[r] = ld8r(h + (b0 + r) * C + c0);
-        xz[r] = ld8r(z + (b0 + r) * z_ld + c0);
-        xg[r] = ld8r(dy + (b0 + r) * C + c0);
+        xc[r] = ldrv(cx + (b0 + r) * C + c0);
+        xh[r] = ldrv(h + (b0 + r) * C + c0);
+        xz[r] = ldrv(z + (b0 + r) * z_ld + c0);
+        xg[r] = ldrv(dy + (b0 + r) * C + c0);
       }
 #pragma unroll
       for (int r = 0; r < kRB; ++r) one(xc[r], xh[r], xz[r], xg[r], b0 + r);
     } else {
       for (int64_t row = b0; row < n_rows; ++row)
-        one(ld8r(cx + row * C + c0), ld8r(h + row * C + c0), ld8r(z + row * z_ld + c0), ld8r(dy + row * C + c0),
+        one(ldrv(cx + row * C + c0), ldrv(h + row * C + c0), ldrv(z + row * z_ld + c0), ldrv(dy + row * C + c0),
             row);
       break;
     }
   }
   if (part) {
     float* pp = part + (int64_t)blockIdx.y * C + c0;
-    *(float4*)pp = make_float4(dd[0], dd[1], dd[2], dd[3]);
-    *(float4*)(pp + 4) = make_float4(dd[4], dd[5], dd[6], dd[7]);
+#pragma unroll
+    for (int q = 0; q < kRV; q += 4) *(float4*)(pp + q) = make_float4(dd[q], dd[q + 1], dd[q + 2], dd[q + 3]);
   }
 }
 
@@ -1554,7 +1561,7 @@ int naju_readout_fwd(const void* cx, const void* h, const void* z, int64_t z_ld,
   if (n_rows == 0 || C == 0) return NAJU_OK;
   if (!cx || !h || !z || !Dv || !y) return fail(NAJU_ERR_INVALID, "null pointer (cx, h, z, Dv and y are required)");
   if (readout_vec_ok(n_rows, C, z_ld, {cx, h, z, Dv, y}, {cx_dtype, h_dtype, z_dtype, y_dtype})) {
-    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)((n_rows + kVRows - 1) / kVRows));
+    const dim3 grid((unsigned)((C + 64 * kRV - 1) / (64 * kRV)), (unsigned)((n_rows + kVRows - 1) / kVRows));
     hipStream_t st = (hipStream_t)stream;
     if (cx_dtype == NAJU_DTYPE_BF16)
       hipLaunchKernelGGL(readout_fwd_vec<bf16_t>, grid, dim3(64), 0, st, (const bf16_t*)cx, (const bf16_t*)h,
@@ -1613,7 +1620,7 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
                       dh ? dh_dtype : h_dtype, dz ? dz_dtype : h_dtype},
                      dz ? dz_ld : 0)) {
     nblk = (n_rows + kVRows - 1) / kVRows;
-    const dim3 grid((unsigned)((C + 64 * kVec - 1) / (64 * kVec)), (unsigned)nblk);
+    const dim3 grid((unsigned)((C + 64 * kRV - 1) / (64 * kRV)), (unsigned)nblk);
     if (h_dtype == NAJU_DTYPE_BF16)
       hipLaunchKernelGGL(readout_bwd_vec<bf16_t>, grid, dim3(64), 0, st, (const bf16_t*)cx, (const bf16_t*)h,
                          (const bf16_t*)z, z_ld, Dv, scale, (const bf16_t*)dy, (bf16_t*)dcx, (bf16_t*)dh, (bf16_t*)dz,
