@@ -177,6 +177,18 @@ int naju_dwconv_pair_bwd(const void* x, int64_t x_ld, const float* w0, const flo
  * forms the weight gradient as one GEMM. */
 int naju_sum_parts(const float* parts, int n_parts, int64_t n, float* out, void* stream);
 
+/* dw[id] += the rows dy[order[q]] of every q with sorted_ids[q] == id, for
+ * the n ids sorted with a stable sort (sorted_ids = ids[order]); dy is
+ * [n_ids_before_sorting, d] float32, dw [V, d] float32, both row-major; ids
+ * outside [0, V) are skipped. Each row of dw gets its rows added in sorted
+ * order, one workgroup per run of equal ids: deterministic. The embedding's
+ * backward (nn.Embedding without padding_idx, max_norm or
+ * scale_grad_by_freq) added in place into a gradient already there (a tied
+ * LM head's). Reference counterpart: torch's embedding backward under
+ * naju/lm.py:13-33's tied weights, which autograd then adds to the head's. */
+int naju_embedding_bwd_add(const int64_t* sorted_ids, const int64_t* order, const float* dy, int64_t n, int64_t d,
+                           float* dw, int64_t V, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,7 @@ EXPORTED = (
     "naju_residual_dropout_fwd",
     "naju_dropout_bwd",
     "naju_sum_parts",
+    "naju_embedding_bwd_add",
     "naju_dwconv_pair_fwd",
     "naju_dwconv_pair_workspace_bytes",
     "naju_dwconv_pair_bwd",
@@ -175,6 +176,9 @@ def lib():
     L.naju_dropout_bwd.restype = I
     L.naju_sum_parts.argtypes = [P, I, I64, P, P]
     L.naju_sum_parts.restype = I
+    # sorted_ids, order, dy, n, d, dw, V, stream
+    L.naju_embedding_bwd_add.argtypes = [P, P, P, I64, I64, P, I64, P]
+    L.naju_embedding_bwd_add.restype = I
     # x, x_ld, w0, bias0, add0, w1, bias1, add1, add_ld, y0, y1, batch, T, C, K, x_dt, y_dt, stream
     L.naju_dwconv_pair_fwd.argtypes = [P, I64] + [P] * 6 + [I64, P, P] + [I64] * 3 + [I] * 3 + [P]
     L.naju_dwconv_pair_fwd.restype = I

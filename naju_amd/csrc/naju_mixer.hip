@@ -1461,6 +1461,45 @@ typedef void (*dropbwd_t)(const float*, const int64_t*, DropKeep, void*, int64_t
 
 }  // namespace
 
+namespace {
+
+// Embedding gradient added into dW [V, d] (float32): workgroup p serves the
+// run of equal ids that starts at position p of the sorted ids (the other
+// workgroups return at once) and adds the dy rows of that run, in sorted
+// order (a stable sort keeps the original order of equal ids), to the row
+// dW[id]: dW[id] + dy[r1] + dy[r2] + ..., a fixed order. Threads take
+// columns 4 at a time.
+__global__ __launch_bounds__(256) void embed_bwd_add_kernel(const int64_t* __restrict__ sorted,
+                                                            const int64_t* __restrict__ order,
+                                                            const float* __restrict__ dy, int64_t n, int64_t d,
+                                                            float* __restrict__ dw, int64_t V) {
+  const int64_t p = blockIdx.x;
+  const int64_t id = sorted[p];
+  if ((p > 0 && sorted[p - 1] == id) || id < 0 || id >= V) return;
+  int64_t end = p + 1;
+  while (end < n && sorted[end] == id) ++end;
+  float* __restrict__ row = dw + id * d;
+  const bool vec = d % 4 == 0 && ((uintptr_t)dw & 15) == 0 && ((uintptr_t)dy & 15) == 0;
+  if (vec) {
+    for (int64_t c = 4 * (int64_t)threadIdx.x; c < d; c += 4 * 256) {
+      float4 acc = *(const float4*)(row + c);
+      for (int64_t q = p; q < end; ++q) {
+        const float4 v = *(const float4*)(dy + order[q] * d + c);
+        acc.x += v.x, acc.y += v.y, acc.z += v.z, acc.w += v.w;
+      }
+      *(float4*)(row + c) = acc;
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < d; c += 256) {
+      float acc = row[c];
+      for (int64_t q = p; q < end; ++q) acc += dy[order[q] * d + c];
+      row[c] = acc;
+    }
+  }
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* naju_mixer_last_error(void) { return g_err; }
@@ -1789,6 +1828,20 @@ int naju_sum_parts(const float* parts, int n_parts, int64_t n, float* out, void*
   } else {
     hipLaunchKernelGGL(sum_parts_any, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, parts, n_parts, n, out);
   }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return NAJU_OK;
+}
+
+int naju_embedding_bwd_add(const int64_t* sorted_ids, const int64_t* order, const float* dy, int64_t n, int64_t d,
+                           float* dw, int64_t V, void* stream) {
+  g_err[0] = 0;
+  if (n < 0 || d < 0 || V < 0) return fail(NAJU_ERR_INVALID, "negative size");
+  if (n == 0 || d == 0) return NAJU_OK;
+  if (!sorted_ids || !order || !dy || !dw) return fail(NAJU_ERR_INVALID, "null pointer");
+  if (n > 0x7fffffff) return fail(NAJU_ERR_UNSUPPORTED, "too many ids (%lld)", (long long)n);
+  hipLaunchKernelGGL(embed_bwd_add_kernel, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream, sorted_ids, order,
+                     dy, n, d, dw, V);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NAJU_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return NAJU_OK;

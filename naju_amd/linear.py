@@ -126,7 +126,8 @@ class _Head(torch.autograd.Function):
     float32, the parameter's dtype, as for the split-K weight gradients."""
 
     @staticmethod
-    def forward(ctx, x, weight, dtype, wp):
+    def forward(ctx, x, weight, dtype, wp, tied):
+        ctx.tied = tied
         V, d = weight.shape
         Vp = -(-V // HEAD_ALIGN) * HEAD_ALIGN
         if wp is None or tuple(wp.shape) != (Vp, d):
@@ -161,17 +162,24 @@ class _Head(torch.autograd.Function):
             dw = torch.mm(gk.t(), x2, out_dtype=torch.float32)[:V]
             if dw.dtype != ctx.w_dtype:
                 dw = dw.to(ctx.w_dtype)
-        return dx, dw, None, None
+            if ctx.tied is not None and dw.dtype == torch.float32:
+                # the tied embedding's backward adds its rows into it and
+                # returns the sum (naju_amd.embed.TiedGrad)
+                ctx.tied.put(dw)
+                dw = None
+        return dx, dw, None, None, None
 
 
-def lm_head(x, weight):
+def lm_head(x, weight, tied=None):
     """F.linear(x, weight) for the LM head (weight [V, d], no bias) in
     compute_dtype(x) (which must not be None), through the padded GEMMs of
-    _Head; the logits are a [..., V] view with row stride Vp."""
+    _Head; the logits are a [..., V] view with row stride Vp. tied: a
+    naju_amd.embed.TiedGrad that takes the weight's gradient for the tied
+    embedding's backward."""
     dt = compute_dtype(x)
     if dt is None:
         raise ValueError("naju_amd.linear.lm_head serves CUDA tensors computed in float16 / bfloat16")
-    return _Head.apply(x, weight, dt, wcast.lookup((weight,), dt))
+    return _Head.apply(x, weight, dt, wcast.lookup((weight,), dt), tied)
 
 
 def compute_dtype(x):

@@ -31,7 +31,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
-from naju_amd import gradsink, wcast
+from naju_amd import embed, gradsink, wcast
 from naju_amd.dwconv import dwconv, dwconv_pair, pair_supported
 from naju_amd.linear import HEAD_ALIGN, compute_dtype, linear, linear_cat, lm_head
 from naju_amd.optim import AdamW as NajuAdamW
@@ -326,7 +326,14 @@ class NajuLM(nn.Module):
         return groups + [((self.head.weight,), HEAD_ALIGN)]
 
     def forward(self, ids):
-        x = self.embed(ids)
+        # tied weights under 16-bit autocast on the GPU: the head's gradient
+        # goes to the embedding's backward, which adds its rows in place
+        w = self.embed.weight
+        tied = None
+        if (self.head.weight is w and torch.is_grad_enabled() and w.requires_grad
+                and torch.is_autocast_enabled("cuda") and embed.supported(ids, w)):
+            tied = embed.TiedGrad(w)
+        x = embed.embedding(ids, w, tied) if tied is not None else self.embed(ids)
         groups = self._cast_groups(x)
         if groups and getattr(self, "_wcopies", None) is None:
             self._wcopies = wcast.WeightCopies()
@@ -355,7 +362,7 @@ class NajuLM(nn.Module):
             h = self.norm(x, out_dtype=_out_dtype(x))
             if compute_dtype(h) is not None:
                 # padded vocabulary rows: aligned GEMMs (logits: a strided view)
-                return lm_head(h, self.head.weight)
+                return lm_head(h, self.head.weight, tied)
             return self.head(h)
 
 
