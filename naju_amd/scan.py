@@ -191,17 +191,23 @@ def _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0):
     return Bsz, T, D, N
 
 
-def _bc_pair(B, C, N):
+def _bc_pair(B, C, N, in_place=True):
     """B and C as the scan reads them, and their row stride: on the
     matrix-core path (9 <= N <= 64), when C's columns directly follow B's in
-    one tensor (the mixer's x_proj slices of its projection output), one
-    copy of the 2N columns serves both (B, C: its two halves, rows 2N
-    apart); else (B, C, N), for _norm_inputs to make contiguous."""
+    one tensor (the mixer's x_proj slices of its projection output), the
+    scan reads them in place (rows B.stride(1) apart; the saved tensors then
+    keep that whole output alive until the backward) when in_place and the
+    stride and addresses are 4-element aligned, else from one copy of the 2N
+    columns (B, C: its two halves, rows 2N apart); otherwise (B, C, N), for
+    _norm_inputs to make contiguous."""
     if not (8 < N <= 64 and B.dtype == C.dtype and B.stride() == C.stride() and B.stride(2) == 1):
         return B, C, N
     es = B.element_size()
-    if C.data_ptr() != B.data_ptr() + N * es or B.stride(1) < 2 * N or B.stride(0) != B.shape[1] * B.stride(1):
+    ld = B.stride(1)
+    if C.data_ptr() != B.data_ptr() + N * es or ld < 2 * N or B.stride(0) != B.shape[1] * ld:
         return B, C, N
+    if in_place and ld % 4 == 0 and B.data_ptr() % (4 * es) == 0 and C.data_ptr() % (4 * es) == 0 and ld <= 1 << 24:
+        return B, C, ld
     bc = torch.as_strided(B, (B.shape[0], B.shape[1], 2 * N), B.stride()).contiguous()
     return bc[..., :N], bc[..., N:], 2 * N
 
@@ -215,7 +221,9 @@ class NajuScanHip(torch.autograd.Function):
         Bsz, T, D, N = _check_shapes(u, f_logit, i_logit, B, C, D_skip, h0)
         out_dtype = u.dtype
         b_sinks = (sink_of(B), sink_of(C))
-        Bp, Cp, bc_ld = _bc_pair(B, C, N)
+        # a memory-light checkpoint interval keeps B and C as a copy, so the
+        # projection output is not held until the backward
+        Bp, Cp, bc_ld = _bc_pair(B, C, N, in_place=int(ckpt_rows or 0) <= 16)
         u_, fl_, il_, B_, C_, D_, h0_ = _norm_inputs(u, f_logit, i_logit, Bp, Cp, D_skip, h0, bc_ld != N)
         if bc_ld != N and (B_.data_ptr() != Bp.data_ptr() or C_.data_ptr() != Cp.data_ptr()):
             # _norm_inputs converted their dtype: contiguous copies after all
