@@ -225,8 +225,8 @@ __global__ __launch_bounds__(kThreads) void readout_bwd_kernel(const void* cx, c
 // ------------------------------------------------ vector fast paths (K = 4)
 //
 // The same operations on several channels per thread with 8- or 16-byte
-// accesses (the readout: 8 channels, kVRows rows per thread, one wave per
-// block; the convolutions: kCV channels, below). Used when C and the row
+// accesses (the readout: kRV channels, kVRows or kVRowsR rows per thread,
+// one wave per block; the convolutions: kCV channels, below). Used when C and the row
 // strides are multiples of 8 and the pointers 16-byte aligned; the scalar
 // kernels above serve every other case.
 constexpr int kVec = 8;
@@ -678,13 +678,16 @@ __global__ __launch_bounds__(64 * kPW) void dwconv4_pair_bwd_vec(const TX* __res
 }
 
 
-// grid: (ceil(C / (64 * kVec)), ceil(n_rows / kVRows)), 64 threads
+// grid: (ceil(C / (64 * kRV)), ceil(n_rows / kVRows)) (kVRowsR in the
+// backward), 64 threads
 // Rows of a readout block are taken kRB at a time: in a whole batch every
 // load of the kRB rows is issued before the first is used, so a wave waits
 // for memory once per kRB rows (the block's last, partial batch goes row by
 // row).
 constexpr int kRB = 8;
-static_assert(kVRows % kRB == 0, "whole row batches per block");
+// rows per block of the readout backward (its dD partial rows: one per block)
+constexpr int kVRowsR = 32;
+static_assert(kVRows % kRB == 0 && kVRowsR % kRB == 0 && kVRowsR >= kVRows, "whole row batches per block");
 
 #ifndef NAJU_READOUT_V
 #define NAJU_READOUT_V 4
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
                                                       float* __restrict__ part, int64_t n_rows, int64_t C) {
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * kRV;
   if (c0 >= C) return;
-  const int64_t r0 = (int64_t)blockIdx.y * kVRows;
+  const int64_t r0 = (int64_t)blockIdx.y * kVRowsR;
   float dv[kRV], dd[kRV];
 #pragma unroll
   for (int j = 0; j < kRV; ++j) dv[j] = Dv[c0 + j];
@@ -784,7 +787,7 @@ __global__ __launch_bounds__(64) void readout_bwd_vec(const T* __restrict__ cx, 
     if (dh) stc(dh + row * C + c0, o1);
     if (dz) stc(dz + row * dz_ld + c0, o2);
   };
-  for (int rb = 0; rb < kVRows; rb += kRB) {
+  for (int rb = 0; rb < kVRowsR; rb += kRB) {
     const int64_t b0 = r0 + rb;
     if (b0 + kRB <= n_rows) {
       // a whole batch: straight-line loads, then the rows
@@ -1658,7 +1661,7 @@ int naju_readout_bwd(const void* cx, const void* h, const void* z, int64_t z_ld,
                      {h_dtype, z_dtype, dy_dtype, cx ? cx_dtype : h_dtype, dcx ? dcx_dtype : h_dtype,
                       dh ? dh_dtype : h_dtype, dz ? dz_dtype : h_dtype},
                      dz ? dz_ld : 0)) {
-    nblk = (n_rows + kVRows - 1) / kVRows;
+    nblk = (n_rows + kVRowsR - 1) / kVRowsR;
     const dim3 grid((unsigned)((C + 64 * kRV - 1) / (64 * kRV)), (unsigned)nblk);
     if (h_dtype == NAJU_DTYPE_BF16)
       hipLaunchKernelGGL(readout_bwd_vec<bf16_t>, grid, dim3(64), 0, st, (const bf16_t*)cx, (const bf16_t*)h,
