@@ -10,7 +10,8 @@ embedding's backward adds its rows into that buffer in place
 equal ids in a stable sort, a fixed order) and returns it as the weight's
 whole gradient. A head gradient that no embedding backward takes in the same
 backward pass (a loss that does not reach the embedding) is added to the
-weight's ``.grad`` when the pass ends, so no gradient is lost.
+weight's ``.grad`` when the pass ends, so no gradient is lost; a
+torch.autograd.grad pass leaves ``.grad`` alone, as autograd does.
 
 CUDA float32 weights and input gradients only; ``embedding`` raises for
 anything else (NajuLM then keeps nn.Embedding).
@@ -28,6 +29,9 @@ class TiedGrad:
     def __init__(self, weight):
         self.weight = weight
         self._dw = None
+        # the weight's gradient accumulator: the end-of-pass fallback adds
+        # to .grad only in a pass that runs it (not torch.autograd.grad)
+        self._acc = weight.view_as(weight).grad_fn.next_functions[0][0] if weight.requires_grad else None
 
     def put(self, dw):
         """From the head's backward (which then returns no gradient for the
@@ -39,9 +43,18 @@ class TiedGrad:
         dw, self._dw = self._dw, None
         return dw
 
+    def _accumulates(self):
+        probe = getattr(torch._C, "_will_engine_execute_node", None)
+        if self._acc is None or probe is None:
+            return self._acc is not None
+        try:
+            return bool(probe(self._acc))
+        except RuntimeError:  # torch.autograd.grad with the weight among its inputs
+            return False
+
     def _flush(self):
         dw = self.take()
-        if dw is None:
+        if dw is None or not self._accumulates():
             return
         w = self.weight
         with torch.no_grad():

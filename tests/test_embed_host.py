@@ -65,3 +65,16 @@ def test_taken_head_gradient_is_not_added_twice():
     dy = torch.randn_like(y)
     y.backward(dy)
     torch.testing.assert_close(w.grad, dy.t() @ h.detach())
+
+
+def test_autograd_grad_pass_leaves_grad_alone():
+    """torch.autograd.grad over the head's input: the untaken head gradient
+    is dropped, as autograd drops the weight's gradient there."""
+    torch.manual_seed(2)
+    w = torch.nn.Parameter(torch.randn(5, 3))
+    x = torch.randn(4, 3, requires_grad=True)
+    y = _Head.apply(x, w, embed.TiedGrad(w))
+    dy = torch.randn_like(y)
+    (dx,) = torch.autograd.grad(y, [x], dy)
+    torch.testing.assert_close(dx, dy @ w.detach())
+    assert w.grad is None
